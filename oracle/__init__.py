@@ -1,0 +1,220 @@
+"""CPU oracle for the attention and gated-delta-rule hot path (TEST INFRASTRUCTURE ONLY).
+
+A ctypes front end over ``oracle/liboracle.so``, the plain-C restatement of dash-ops' reference
+implementations (``crates/dash-ops/src/attention/reference.rs``,
+``crates/dash-ops/src/gated_delta/chunk/reference.rs``,
+``crates/dash-ops/src/gated_delta/recurrent.rs:309-404``). Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this module: as the
+checker of the HIP path, and as the timed CPU baseline. The product package ``dashmag_amd`` never
+imports it.
+
+Every function takes and returns numpy float32 arrays in the contract's layouts
+(``[B, T, H, D]``, states ``[S, H, Dk, Dv]``); ``precision`` picks the C body compiled in f32 (the
+reference's precision) or in f64.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compiles the oracle with the committed Makefile; returns the library's path."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+class _Attention(ctypes.Structure):
+    _fields_ = [
+        ("b", ctypes.c_int64), ("tq", ctypes.c_int64), ("tk", ctypes.c_int64),
+        ("hq", ctypes.c_int64), ("hkv", ctypes.c_int64), ("d", ctypes.c_int64),
+        ("causal", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("left", ctypes.c_int64), ("right", ctypes.c_int64),
+        ("mask_kind", ctypes.c_int32),
+        ("padding", ctypes.c_void_p), ("cu_q", ctypes.c_void_p), ("cu_k", ctypes.c_void_p),
+        ("nseq", ctypes.c_int64),
+    ]
+
+
+class _Gdr(ctypes.Structure):
+    _fields_ = [
+        ("b", ctypes.c_int64), ("t", ctypes.c_int64), ("h", ctypes.c_int64),
+        ("dk", ctypes.c_int64), ("dv", ctypes.c_int64),
+        ("cu", ctypes.c_void_p), ("nseq", ctypes.c_int64),
+        ("qk_l2norm", ctypes.c_int32), ("scale", ctypes.c_float),
+    ]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _lib.dmo_attention_visible.restype = ctypes.c_int
+        _lib.dmo_attention_visible.argtypes = [ctypes.POINTER(_Attention), ctypes.c_int64,
+                                               ctypes.c_int64, ctypes.c_int64]
+    return _lib
+
+
+def set_threads(n: int) -> None:
+    lib().dmo_set_threads(int(n))
+
+
+def threads() -> int:
+    return int(lib().dmo_threads())
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _i64(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int64))
+
+
+def _p(x):
+    return None if x is None else x.ctypes.data_as(ctypes.c_void_p)
+
+
+def _side(x):
+    return -1 if x is None else int(x)
+
+
+class AttentionCall:
+    """The arguments of one attention call, as the C oracle takes them.
+
+    ``mask`` is ``None``, ``("padding", bool[B, Tk])`` or ``("packed", cu_q, cu_k)``;
+    ``left``/``right`` are window sides (``None`` unbounded).
+    """
+
+    def __init__(self, q, k, v, mask=None, causal=False, scale=None, left=None, right=None):
+        self.q, self.k, self.v = _f32(q), _f32(k), _f32(v)
+        b, tq, hq, d = self.q.shape
+        _, tk, hkv, _ = self.k.shape
+        self.keep = []
+        s = _Attention(b=b, tq=tq, tk=tk, hq=hq, hkv=hkv, d=d, causal=int(bool(causal)),
+                       scale=float(np.float32(1.0 / math.sqrt(d)) if scale is None else scale),
+                       left=_side(left), right=_side(right), mask_kind=0)
+        if mask is not None and mask[0] == "padding":
+            pad = np.ascontiguousarray(np.asarray(mask[1], dtype=np.uint8))
+            self.keep.append(pad)
+            s.mask_kind, s.padding = 1, pad.ctypes.data
+        elif mask is not None and mask[0] == "packed":
+            cq, ck = _i64(mask[1]), _i64(mask[2])
+            self.keep += [cq, ck]
+            s.mask_kind, s.cu_q, s.cu_k, s.nseq = 2, cq.ctypes.data, ck.ctypes.data, len(cq) - 1
+        self.s = s
+
+    def visible(self, b, i, j) -> bool:
+        return bool(lib().dmo_attention_visible(ctypes.byref(self.s), b, i, j))
+
+    def visible_matrix(self, b=0) -> np.ndarray:
+        tq, tk = self.s.tq, self.s.tk
+        return np.array([[self.visible(b, i, j) for j in range(tk)] for i in range(tq)], bool)
+
+
+def attention_fwd(call: AttentionCall, precision="f32"):
+    """Output ``[B, Tq, Hq, D]`` and natural log-sum-exp ``[B, Tq, Hq]`` (reference.rs:305-348)."""
+    s = call.s
+    o = np.zeros((s.b, s.tq, s.hq, s.d), np.float32)
+    lse = np.zeros((s.b, s.tq, s.hq), np.float32)
+    getattr(lib(), f"dmo_attention_fwd_{precision}")(
+        ctypes.byref(s), _p(call.q), _p(call.k), _p(call.v), _p(o), _p(lse))
+    return o, lse
+
+
+def attention_bwd(call: AttentionCall, o, lse, d_o, precision="f32"):
+    """Gradients ``(dq, dk, dv)`` from the forward's output and lse (reference.rs:352-431)."""
+    s = call.s
+    o, lse, d_o = _f32(o), _f32(lse), _f32(d_o)
+    dq = np.zeros_like(call.q)
+    dk = np.zeros_like(call.k)
+    dv = np.zeros_like(call.v)
+    getattr(lib(), f"dmo_attention_bwd_{precision}")(
+        ctypes.byref(s), _p(call.q), _p(call.k), _p(call.v), _p(o), _p(lse), _p(d_o),
+        _p(dq), _p(dk), _p(dv))
+    return dq, dk, dv
+
+
+def attention_decode(q, k, v, lengths=None, left=None, scale=None, precision="f32"):
+    """One query per sequence ``[B, Hq, D]`` against ``[B, S, Hkv, D]`` (reference.rs:433-467)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, hq, d = q.shape
+    _, s, hkv, _ = k.shape
+    ln = None if lengths is None else _i64(lengths)
+    sc = float(np.float32(1.0 / math.sqrt(d)) if scale is None else scale)
+    o = np.zeros_like(q)
+    f = getattr(lib(), f"dmo_attention_decode_{precision}")
+    f.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_float,
+                                                                  ctypes.c_void_p]
+    f(b, s, hq, hkv, d, _p(q), _p(k), _p(v), _p(ln), _side(left), sc, _p(o))
+    return o
+
+
+def _gdr(q, v, cu, l2norm, scale):
+    b, t, h, dk = q.shape[0], q.shape[1], q.shape[2], q.shape[3]
+    dv = v.shape[3]
+    cu = None if cu is None else _i64(cu)
+    sc = float(np.float32(1.0 / math.sqrt(dk)) if scale is None else scale)
+    s = _Gdr(b=b, t=t, h=h, dk=dk, dv=dv, cu=None if cu is None else cu.ctypes.data,
+             nseq=0 if cu is None else len(cu) - 1, qk_l2norm=int(bool(l2norm)), scale=sc)
+    return s, cu
+
+
+def gdr_chunk_fwd(q, k, v, g, beta, h0=None, cu=None, l2norm=False, scale=None,
+                  precision="f32"):
+    """Chunked gated delta rule forward (chunk/reference.rs:481-509, packed :697-735): output
+    ``[B, T, H, Dv]`` and final states ``[S, H, Dk, Dv]``."""
+    q, k, v, g, beta = map(_f32, (q, k, v, g, beta))
+    s, cu = _gdr(q, v, cu, l2norm, scale)
+    nseq = s.nseq if cu is not None else s.b
+    h0 = None if h0 is None else _f32(h0)
+    out = np.zeros(q.shape[:3] + (s.dv,), np.float32)
+    fin = np.zeros((nseq, s.h, s.dk, s.dv), np.float32)
+    rc = getattr(lib(), f"dmo_gdr_chunk_fwd_{precision}")(
+        ctypes.byref(s), _p(q), _p(k), _p(v), _p(g), _p(beta), _p(h0), _p(out), _p(fin))
+    assert rc == 0
+    return out, fin
+
+
+def gdr_chunk_bwd(q, k, v, g, beta, h0, d_out, d_final, cu=None, l2norm=False, scale=None,
+                  precision="f32"):
+    """Chunked gated delta rule backward (chunk/reference.rs:519-695, packed :737-780):
+    ``(dq, dk, dv, dg, dbeta, dh0)``."""
+    q, k, v, g, beta, d_out = map(_f32, (q, k, v, g, beta, d_out))
+    s, cu = _gdr(q, v, cu, l2norm, scale)
+    nseq = s.nseq if cu is not None else s.b
+    h0 = None if h0 is None else _f32(h0)
+    d_final = None if d_final is None else _f32(d_final)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    dg, db = np.zeros_like(g), np.zeros_like(beta)
+    dh0 = np.zeros((nseq, s.h, s.dk, s.dv), np.float32)
+    rc = getattr(lib(), f"dmo_gdr_chunk_bwd_{precision}")(
+        ctypes.byref(s), _p(q), _p(k), _p(v), _p(g), _p(beta), _p(h0), _p(d_out), _p(d_final),
+        _p(dq), _p(dk), _p(dv), _p(dg), _p(db), _p(dh0))
+    assert rc == 0
+    return dq, dk, dv, dg, db, dh0
+
+
+def gdr_step(q, k, v, g, beta, state, cu=None, l2norm=False, scale=None, precision="f32"):
+    """The recurrent step (recurrent.rs:309-404): ``q``, ``k`` ``[B, H, Dk]`` (packed: ``[T, H,
+    Dk]``), state ``[S, H, Dk, Dv]``; returns ``(out, new_state)``."""
+    q, k, v, g, beta = map(_f32, (q, k, v, g, beta))
+    st = _f32(state).copy()
+    # the step's rows as a batch of one of T tokens
+    s, cu = _gdr(q[None], v[None], cu, l2norm, scale)
+    s.b = q.shape[0]
+    out = np.zeros(v.shape, np.float32)
+    rc = getattr(lib(), f"dmo_gdr_step_{precision}")(
+        ctypes.byref(s), _p(q), _p(k), _p(v), _p(g), _p(beta), _p(st), _p(out))
+    assert rc == 0
+    return out, st
