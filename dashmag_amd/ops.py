@@ -1,0 +1,348 @@
+"""The hot path's operations on device tensors, mirroring dash-ops' public functions (same names,
+argument meaning and refusals): ``attention``, ``attention_with_lse``, ``attention_backward``,
+``attention_decode`` (crates/dash-ops/src/attention.rs:648-806), ``chunk_gated_delta_rule``
+(gated_delta/chunk.rs:856-981) with its explicit backward ``chunk_gated_delta_rule_backward``,
+and ``gated_delta_step`` (gated_delta/recurrent.rs:158).
+
+Tensors are torch tensors on the GPU (PyTorch is the device-memory and stream plumbing); every
+computation runs in ``libdashmi.so`` through its C ABI, on torch's current stream. A call
+outside the contract raises :class:`~dashmag_amd.contract.Unsupported` whose message starts
+``"<operation>: "``, as a ``Result``-returning implementation reports it (dash-mlx's convention).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .contract import (AttentionMask, AttentionOptions, ChunkGatedDeltaOptions,
+                       GatedDeltaStepOptions, UNBOUNDED, Unsupported)
+
+_DT = {torch.float32: _lib.DM_F32, torch.bfloat16: _lib.DM_BF16, torch.float16: _lib.DM_F16}
+
+
+def _dtype(op, t):
+    if t.dtype not in _DT:
+        raise Unsupported(f"{op}: dtype {t.dtype} is not f32, bf16 or f16")
+    return _DT[t.dtype]
+
+
+def _device(op, *ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise Unsupported(f"{op}: the tensors must be on the GPU (got {t.device})")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(op, rc):
+    if rc == _lib.DM_OK:
+        return
+    msg = _lib.last_error()
+    if rc == _lib.DM_ERR_REFUSED:
+        raise Unsupported(msg if msg.startswith(op) else f"{op}: {msg}")
+    raise RuntimeError(msg)
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _offsets(t, device):
+    """Offsets of any int dtype as the int32 device array the kernels read."""
+    t = torch.as_tensor(t)
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+# ------------------------------------------------------------------------------------------
+# Attention
+# ------------------------------------------------------------------------------------------
+
+def _attention_desc(op, q, k, v, mask: AttentionMask, options: AttentionOptions, keep):
+    if q.dim() != 4:
+        raise Unsupported(f"{op}: query is [B, Tq, Hq, D]")
+    if k.dim() != 4:
+        raise Unsupported(f"{op}: key is [B, Tk, Hkv, D]")
+    b, tq, hq, d = q.shape
+    bk, tk, hkv, dk = k.shape
+    if tuple(k.shape) != tuple(v.shape):
+        raise Unsupported(f"{op}: key and value must have one shape")
+    if b != bk:
+        raise Unsupported(f"{op}: query and key must have one batch size")
+    if d != dk:
+        raise Unsupported(f"{op}: query and key must have one head dimension")
+    if hkv == 0 or hq % hkv != 0:
+        raise Unsupported(f"{op}: the query heads ({hq}) must be a multiple of the key-value "
+                          f"heads ({hkv})")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise Unsupported(f"{op}: query, key and value must share one dtype")
+    desc = _lib.AttentionDesc(b=b, tq=tq, tk=tk, hq=hq, hkv=hkv, d=d, dtype=_dtype(op, q),
+                              mask_kind=_lib.DM_MASK_NONE)
+    if mask.kind == AttentionMask.KEY_PADDING:
+        pad = torch.as_tensor(mask.padding)
+        if tuple(pad.shape) != (b, tk):
+            raise Unsupported(f"{op}: the key padding mask is [B, Tk] = [{b}, {tk}]")
+        pad = pad.to(device=q.device, dtype=torch.uint8).contiguous()
+        keep.append(pad)
+        desc.mask_kind, desc.key_padding = _lib.DM_MASK_KEY_PADDING, pad.data_ptr()
+    elif mask.kind == AttentionMask.PACKED:
+        cq, ck = torch.as_tensor(mask.cu_seqlens_q), torch.as_tensor(mask.cu_seqlens_k)
+        if b != 1:
+            raise Unsupported(f"{op}: packed sequences lie along the time, B = 1")
+        if cq.dim() != 1 or ck.dim() != 1 or cq.shape != ck.shape or cq.shape[0] < 1:
+            raise Unsupported(f"{op}: cu_seqlens_q and cu_seqlens_k are [S + 1], one S, got "
+                              f"{list(cq.shape)}, {list(ck.shape)}")
+        cq, ck = _offsets(cq, q.device), _offsets(ck, q.device)
+        keep += [cq, ck]
+        desc.mask_kind = _lib.DM_MASK_PACKED
+        desc.cu_seqlens_q, desc.cu_seqlens_k = cq.data_ptr(), ck.data_ptr()
+        desc.nseq = cq.shape[0] - 1
+    o = desc.options
+    o.causal = int(bool(options.causal))
+    o.has_scale = int(options.scale is not None)
+    o.scale = float(options.scale) if options.scale is not None else 0.0
+    o.has_window = int(options.window is not None)
+    if options.window is not None:
+        o.window_left = min(int(options.window.left), UNBOUNDED)
+        o.window_right = min(int(options.window.right), UNBOUNDED)
+    o.deterministic = int(bool(options.deterministic))
+    return desc
+
+
+def attention_with_lse(query, key, value, mask: Optional[AttentionMask] = None,
+                       options: Optional[AttentionOptions] = None):
+    """``(output [B, Tq, Hq, D] in the queries' dtype, lse [B, Tq, Hq] f32)``
+    (crates/dash-ops/src/attention.rs:660)."""
+    op = "attention"
+    mask = mask or AttentionMask.none()
+    options = options or AttentionOptions()
+    _device(op, query, key, value)
+    keep = []
+    desc = _attention_desc(op, query, key, value, mask, options, keep)
+    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    nbytes = _lib.lib().dm_attention_fwd_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_attention_fwd(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
+                                           _ptr(out), _ptr(lse), _ptr(ws), nbytes, _stream()))
+    return out, lse
+
+
+def attention(query, key, value, mask=None, options=None):
+    """The output alone (attention.rs:648)."""
+    return attention_with_lse(query, key, value, mask, options)[0]
+
+
+def attention_backward(query, key, value, output, lse, grad_output, mask=None, options=None):
+    """``(dq, dk, dv)`` in their inputs' dtype and shape, from the forward's output and lse
+    (attention.rs:689). The output's gradient is read in the output's dtype."""
+    op = "attention_backward"
+    mask = mask or AttentionMask.none()
+    options = options or AttentionOptions()
+    _device(op, query, key, value, output, lse, grad_output)
+    keep = []
+    desc = _attention_desc(op, query, key, value, mask, options, keep)
+    if tuple(output.shape) != tuple(query.shape) or tuple(grad_output.shape) != tuple(query.shape):
+        raise Unsupported(f"{op}: the output and its gradient are [B, Tq, Hq, D]")
+    if tuple(lse.shape) != tuple(query.shape[:3]):
+        raise Unsupported(f"{op}: the log-sum-exp is [B, Tq, Hq]")
+    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
+    o = output.to(q.dtype).contiguous()
+    g = grad_output.to(q.dtype).contiguous()
+    ls = lse.to(torch.float32).contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    nbytes = _lib.lib().dm_attention_bwd_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_attention_bwd(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
+                                           _ptr(o), _ptr(ls), _ptr(g), _ptr(dq), _ptr(dk),
+                                           _ptr(dv), _ptr(ws), nbytes, _stream()))
+    return dq, dk, dv
+
+
+def attention_decode(query, key, value, lengths=None, options=None):
+    """One query per sequence ``[B, Hq, D]`` against the cache ``[B, S, Hkv, D]``, sequence ``b``
+    holding its first ``lengths[b]`` keys (attention.rs:732); ``[B, Hq, D]`` in the queries'
+    dtype."""
+    op = "attention_decode"
+    options = options or AttentionOptions()
+    _device(op, query, key, value)
+    if query.dim() != 3:
+        raise Unsupported(f"{op}: query is [B, Hq, D]")
+    if key.dim() != 4:
+        raise Unsupported(f"{op}: key is [B, S, Hkv, D]")
+    b, hq, d = query.shape
+    keep = []
+    desc = _attention_desc(op, query.unsqueeze(1), key, value, AttentionMask.none(), options,
+                           keep)
+    ln = None
+    if lengths is not None:
+        lt = torch.as_tensor(lengths)
+        if tuple(lt.shape) != (b,):
+            raise Unsupported(f"{op}: the cache lengths are [B] = [{b}]")
+        ln = _offsets(lt, query.device)
+    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
+    out = torch.empty_like(q)
+    nbytes = _lib.lib().dm_attention_decode_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_attention_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
+                                              _ptr(ln), _ptr(out), _ptr(ws), nbytes, _stream()))
+    return out
+
+
+# ------------------------------------------------------------------------------------------
+# Gated delta rule
+# ------------------------------------------------------------------------------------------
+
+def _gdr_desc(op, q, k, v, g, beta, cu_seqlens, qk_l2norm, scale, step, keep):
+    if step:
+        if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+            raise Unsupported(f"{op}: q, k and v are [B, H, D], got {list(q.shape)}, "
+                              f"{list(k.shape)}, {list(v.shape)}")
+        b, h, dk = q.shape
+        t = 1
+        dv = v.shape[2]
+        if tuple(k.shape) != (b, h, dk):
+            raise Unsupported(f"{op}: k must match q [B, H, Dk]")
+        if tuple(v.shape[:2]) != (b, h):
+            raise Unsupported(f"{op}: v must be [B, H, Dv] with q's B, H")
+        if tuple(g.shape) != (b, h):
+            raise Unsupported(f"{op}: g must be [B, H]")
+        if tuple(beta.shape) != (b, h):
+            raise Unsupported(f"{op}: beta must be [B, H]")
+    else:
+        if q.dim() != 4:
+            raise Unsupported(f"{op}: queries are [B, T, H, Dk]")
+        b, t, h, dk = q.shape
+        dv = v.shape[3]
+        if tuple(k.shape) != (b, t, h, dk):
+            raise Unsupported(f"{op}: keys must have the queries' shape [B, T, H, Dk]")
+        if tuple(v.shape) != (b, t, h, dv):
+            raise Unsupported(f"{op}: values must be [B, T, H, Dv] with the queries' B, T, H")
+        if tuple(g.shape) != (b, t, h):
+            raise Unsupported(f"{op}: g must be [B, T, H]")
+        if tuple(beta.shape) != (b, t, h):
+            raise Unsupported(f"{op}: beta must be [B, T, H]")
+        if t == 0:
+            raise Unsupported(f"{op}: the sequence must not be empty")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise Unsupported(f"{op}: queries, keys and values must share one dtype, got "
+                          f"{q.dtype}, {k.dtype}, {v.dtype}")
+    dt = _dtype(op, q)
+    for name, x in (("g", g), ("beta", beta)):
+        if x.dtype not in (torch.float32, q.dtype):
+            raise Unsupported(f"{op}: {name} must be f32 or the queries' dtype")
+    desc = _lib.GdrDesc(b=b, t=t, h=h, dk=dk, dv=dv, dtype=dt, g_dtype=_DT[g.dtype],
+                        beta_dtype=_DT[beta.dtype], qk_l2norm=int(bool(qk_l2norm)),
+                        has_scale=int(scale is not None),
+                        scale=float(scale) if scale is not None else 0.0)
+    nseq = b
+    if cu_seqlens is not None:
+        cu = torch.as_tensor(cu_seqlens)
+        if not step and b != 1:
+            raise Unsupported(f"{op}: packed sequences lie along T of a batch of one, got B = {b}")
+        if cu.dim() != 1 or cu.shape[0] < 2:
+            raise Unsupported(f"{op}: cu_seqlens must hold S + 1 >= 2 offsets, got "
+                              f"{cu.shape[0] if cu.dim() == 1 else list(cu.shape)}")
+        cu = _offsets(cu, q.device)
+        keep.append(cu)
+        desc.cu_seqlens, desc.nseq = cu.data_ptr(), cu.shape[0] - 1
+        nseq = cu.shape[0] - 1
+    return desc, nseq, (b, t, h, dk, dv)
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, initial_state=None, cu_seqlens=None,
+                           options: Optional[ChunkGatedDeltaOptions] = None):
+    """The chunked gated delta rule (gated_delta/chunk.rs:856): ``(out [B, T, H, Dv] in the
+    queries' dtype, final states [S, H, Dk, Dv] f32 if asked else None)``."""
+    op = "chunk_gated_delta_rule"
+    options = options or ChunkGatedDeltaOptions()
+    _device(op, q, k, v, g, beta, initial_state)
+    keep = []
+    desc, nseq, (b, t, h, dk, dv) = _gdr_desc(op, q, k, v, g, beta, cu_seqlens,
+                                              options.qk_l2norm, options.scale, False, keep)
+    if initial_state is not None and tuple(initial_state.shape) != (nseq, h, dk, dv):
+        raise Unsupported(f"{op}: the initial state must be [S, H, Dk, Dv], one per sequence")
+    qc, kc, vc, gc, bc = (x.contiguous() for x in (q, k, v, g, beta))
+    h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    out = torch.empty((b, t, h, dv), dtype=q.dtype, device=q.device)
+    fin = torch.empty((nseq, h, dk, dv), dtype=torch.float32, device=q.device) \
+        if options.output_final_state else None
+    nbytes = _lib.lib().dm_gdr_chunk_fwd_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_gdr_chunk_fwd(ctypes.byref(desc), _ptr(qc), _ptr(kc), _ptr(vc),
+                                           _ptr(gc), _ptr(bc), _ptr(h0), _ptr(out), _ptr(fin),
+                                           _ptr(ws), nbytes, _stream()))
+    return out, fin
+
+
+def chunk_gated_delta_rule_backward(q, k, v, g, beta, initial_state, cu_seqlens, d_out,
+                                    d_final_state=None,
+                                    options: Optional[ChunkGatedDeltaOptions] = None):
+    """The written-out backward of :func:`chunk_gated_delta_rule` (gated_delta/chunk.rs:542-767,
+    chunk/reference.rs:519-695): ``(dq, dk, dv, dg, dbeta, dh0)``, each in its input's dtype,
+    ``dh0`` f32 (``None`` without an initial state)."""
+    op = "chunk_gated_delta_rule_backward"
+    options = options or ChunkGatedDeltaOptions()
+    _device(op, q, k, v, g, beta, initial_state, d_out, d_final_state)
+    keep = []
+    desc, nseq, (b, t, h, dk, dv) = _gdr_desc(op, q, k, v, g, beta, cu_seqlens,
+                                              options.qk_l2norm, options.scale, False, keep)
+    if tuple(d_out.shape) != (b, t, h, dv):
+        raise Unsupported(f"{op}: the output's gradient is [B, T, H, Dv]")
+    if d_final_state is not None and tuple(d_final_state.shape) != (nseq, h, dk, dv):
+        raise Unsupported(f"{op}: the final state's gradient is [S, H, Dk, Dv]")
+    qc, kc, vc, gc, bc = (x.contiguous() for x in (q, k, v, g, beta))
+    h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    do = d_out.to(q.dtype).contiguous()
+    dfin = None if d_final_state is None else d_final_state.to(torch.float32).contiguous()
+    dq, dk_, dv_ = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+    dg, db = torch.empty_like(gc), torch.empty_like(bc)
+    dh0 = torch.empty((nseq, h, dk, dv), dtype=torch.float32, device=q.device) \
+        if initial_state is not None else None
+    nbytes = _lib.lib().dm_gdr_chunk_bwd_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_gdr_chunk_bwd(
+        ctypes.byref(desc), _ptr(qc), _ptr(kc), _ptr(vc), _ptr(gc), _ptr(bc), _ptr(h0),
+        _ptr(do), _ptr(dfin), _ptr(dq), _ptr(dk_), _ptr(dv_), _ptr(dg), _ptr(db), _ptr(dh0),
+        _ptr(ws), nbytes, _stream()))
+    return dq, dk_, dv_, dg, db, dh0
+
+
+def gated_delta_step(q, k, v, g, beta, state, cu_seqlens=None,
+                     options: Optional[GatedDeltaStepOptions] = None, in_place: bool = False):
+    """A step of the recurrent gated delta rule (gated_delta/recurrent.rs:158): ``(out [B, H,
+    Dv] in q's dtype, new states shaped as ``state`` in f32)``. With ``in_place`` the new states
+    are written over ``state`` (which must then be contiguous f32), as the kernel path does when
+    it owns the state (recurrent/kernel.rs:355-377)."""
+    op = "gated_delta_step"
+    options = options or GatedDeltaStepOptions()
+    _device(op, q, k, v, g, beta, state)
+    keep = []
+    desc, nseq, (b, _, h, dk, dv) = _gdr_desc(op, q, k, v, g, beta, cu_seqlens,
+                                              options.qk_l2norm, options.scale, True, keep)
+    if tuple(state.shape) != (nseq, h, dk, dv):
+        raise Unsupported(f"{op}: state must be [S, H, Dk, Dv], one per sequence")
+    if state.dtype != torch.float32:
+        raise Unsupported(f"{op}: the state is f32")
+    qc, kc, vc, gc, bc = (x.contiguous() for x in (q, k, v, g, beta))
+    if in_place:
+        if not state.is_contiguous():
+            raise Unsupported(f"{op}: an in-place state must be contiguous")
+        st_in = st_out = state
+    else:
+        st_in = state.contiguous()
+        st_out = torch.empty_like(st_in)
+    out = torch.empty((b, h, dv), dtype=q.dtype, device=q.device)
+    _check(op, _lib.lib().dm_gdr_step(ctypes.byref(desc), _ptr(qc), _ptr(kc), _ptr(vc),
+                                      _ptr(gc), _ptr(bc), _ptr(st_in), _ptr(st_out), _ptr(out),
+                                      _stream()))
+    return out, st_out

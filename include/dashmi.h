@@ -1,0 +1,172 @@
+/* dashmi: the MI355X (gfx950) attention and gated-delta-rule hot path behind a C ABI.
+ *
+ * Each entry point replaces one operation of dash-ops' backend-extension traits, which the
+ * reference's callers (dash-mag's Arm, dash-conformance's Adapter) reach through:
+ *
+ *   dm_attention_fwd     AttentionBackend::attention_forward   crates/dash-ops/src/attention.rs:289-352
+ *                        (public fn attention_with_lse          crates/dash-ops/src/attention.rs:660)
+ *   dm_attention_bwd     AttentionBackend::attention_backward   crates/dash-ops/src/attention.rs:689
+ *   dm_attention_decode  AttentionBackend::attention_decode     crates/dash-ops/src/attention.rs:732
+ *   dm_gdr_chunk_fwd     ChunkGatedDeltaBackend::chunk_gated_delta_forward
+ *                                                               crates/dash-ops/src/gated_delta/chunk.rs:340-425, :856
+ *   dm_gdr_chunk_bwd     ChunkGatedDeltaBackend::chunk_gated_delta_backward (the Autodiff node's
+ *                        backward, chunk.rs:542-767, as an explicit entry point)
+ *   dm_gdr_step          GatedDeltaStepBackend::gated_delta_step crates/dash-ops/src/gated_delta/recurrent.rs:52-81, :158
+ *
+ * Conventions (crates/dash-contract/src/lib.rs:38-91):
+ *   - Every tensor is a device pointer to a contiguous array in the contract's layout:
+ *     [B, T, H, D] for queries/keys/values/outputs, [B, T, H] for lse, g and beta,
+ *     [S, H, Dk, Dv] f32 for states. The caller makes strided inputs contiguous.
+ *   - Floating inputs of a call share one dtype (dm_dtype); lse and states are f32; g and beta
+ *     of the gated delta rule may each be f32 or the inputs' dtype.
+ *   - Sequence boundaries (cu_seqlens) and cache lengths are int32 device arrays.
+ *   - A call outside the contract is refused before any launch: the call returns
+ *     DM_ERR_REFUSED and dm_last_error() holds "<operation>: <reason>" (thread-local).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL for the default stream) and nothing
+ *     synchronises the host, except where stated.
+ *   - Scratch memory is the caller's: each entry point that needs any has a *_workspace query
+ *     returning the bytes it needs, and takes that buffer (device memory, 256-byte aligned).
+ */
+#ifndef DASHMI_H
+#define DASHMI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DM_OK 0
+#define DM_ERR_REFUSED 1 /* outside the contract, or an input this library does not take */
+#define DM_ERR_HIP 2     /* a HIP runtime error */
+
+#define DM_UNBOUNDED UINT64_MAX /* a window side that does not bind (usize::MAX) */
+
+typedef enum { DM_F32 = 0, DM_BF16 = 1, DM_F16 = 2 } dm_dtype;
+
+typedef enum {
+    DM_MASK_NONE = 0,        /* every key */
+    DM_MASK_KEY_PADDING = 1, /* uint8 [B, Tk], nonzero where a key is left out */
+    DM_MASK_PACKED = 2       /* cu_seqlens_q, cu_seqlens_k int32 [nseq + 1], B = 1 */
+} dm_mask_kind;
+
+/* AttentionOptions (crates/dash-contract/src/attention.rs:83-115). */
+typedef struct {
+    int32_t causal;
+    int32_t has_scale; /* 0: scale = 1/sqrt(D) */
+    float scale;
+    int32_t has_window;
+    uint64_t window_left, window_right; /* DM_UNBOUNDED for an open side */
+    int32_t deterministic;              /* 1: the query gradient in a fixed summation order */
+} dm_attention_options;
+
+/* One attention call's shapes, dtype and mask (check_shapes, attention.rs:551-590). */
+typedef struct {
+    int64_t b, tq, tk, hq, hkv, d;
+    int32_t dtype; /* dm_dtype of q, k, v, o, d_o and the gradients */
+    int32_t mask_kind;
+    const uint8_t *key_padding;
+    const int32_t *cu_seqlens_q, *cu_seqlens_k;
+    int64_t nseq;
+    dm_attention_options options;
+} dm_attention_desc;
+
+/* The gated delta rule's shapes and options (chunk.rs:771 check_inputs, recurrent.rs:258). */
+typedef struct {
+    int64_t b, t, h, dk, dv;  /* step: b = rows (tokens), t = 1 */
+    int32_t dtype;            /* q, k, v, the output and their gradients */
+    int32_t g_dtype;          /* DM_F32 or dtype */
+    int32_t beta_dtype;       /* DM_F32 or dtype */
+    const int32_t *cu_seqlens; /* packed: [nseq + 1] over a batch of one; NULL: a sequence per row */
+    int64_t nseq;
+    int32_t qk_l2norm;
+    int32_t has_scale;
+    float scale;
+} dm_gdr_desc;
+
+/* The message of this thread's last refusal or error. */
+const char *dm_last_error(void);
+
+/* Library and device facts: "gfx950, 256 CUs, ..." (the capability probe of
+ * crates/dash-ops/src/cube.rs:27-151). Returns DM_OK, or DM_ERR_REFUSED on a device the kernels
+ * are not built for. */
+int dm_describe(char *buf, size_t len);
+
+/* Launch counters, the probes of attention.rs:158-221, chunk.rs:119-163 and recurrent.rs:41-50:
+ * how many kernels of each kind this process launched. */
+typedef enum {
+    DM_PROBE_ATTN_FWD_MFMA = 0,
+    DM_PROBE_ATTN_FWD_GENERIC,
+    DM_PROBE_ATTN_BWD_MFMA,
+    DM_PROBE_ATTN_BWD_GENERIC,
+    DM_PROBE_DECODE_SPLIT,
+    DM_PROBE_DECODE_MERGE,
+    DM_PROBE_GDR_CHUNK_FWD,
+    DM_PROBE_GDR_CHUNK_BWD,
+    DM_PROBE_GDR_STEP,
+    DM_PROBE_COUNT
+} dm_probe;
+uint64_t dm_probe_count(int probe);
+void dm_probe_reset(void);
+
+/* The keys query `i` of batch row `b` sees, as the half-open interval [*lo, *hi) of key indices
+ * (empty when *lo >= *hi), before key padding, which is per key: the closed form of
+ * crates/dash-ops/src/attention/kernels.rs:416-523 (row_bounds, query_range) and of the
+ * reference's materialised mask, reference.rs:163-272. Host-only; reads host copies of the
+ * offsets (desc->cu_seqlens_* must point to host memory for this call). */
+int dm_attention_row_bounds(const dm_attention_desc *desc, int64_t b, int64_t i, int64_t *lo,
+                            int64_t *hi);
+
+/* Attention forward: o [B, Tq, Hq, D] in dtype, lse [B, Tq, Hq] f32 (natural log, -inf for a
+ * query that sees no key, whose output is 0). Replaces attention.rs:660 / cube.rs:562. */
+size_t dm_attention_fwd_workspace(const dm_attention_desc *desc);
+int dm_attention_fwd(const dm_attention_desc *desc, const void *q, const void *k, const void *v,
+                     void *o, float *lse, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Attention backward from the forward's o and lse and the output's gradient d_o: dq, dk, dv in
+ * dtype (dk, dv summed over each key-value head's group). Replaces attention.rs:689 /
+ * cube.rs:850. */
+size_t dm_attention_bwd_workspace(const dm_attention_desc *desc);
+int dm_attention_bwd(const dm_attention_desc *desc, const void *q, const void *k, const void *v,
+                     const void *o, const float *lse, const void *d_o, void *dq, void *dk,
+                     void *dv, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Decoding: q [B, Hq, D] against the cache k, v [B, S, Hkv, D], sequence b holding its first
+ * lengths[b] keys (all S when lengths is NULL); the options' scale and window left apply.
+ * o [B, Hq, D] in dtype. Replaces attention.rs:732 / cube.rs:1126. `desc->tq` is unused,
+ * desc->tk is S. */
+size_t dm_attention_decode_workspace(const dm_attention_desc *desc);
+int dm_attention_decode(const dm_attention_desc *desc, const void *q, const void *k,
+                        const void *v, const int32_t *lengths, void *o, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/* The chunked gated delta rule forward: out [B, T, H, Dv] in dtype and, if final_state is not
+ * NULL, each sequence's final state [S, H, Dk, Dv] f32; h0 [S, H, Dk, Dv] f32 or NULL (zeros).
+ * Replaces chunk.rs:856 / chunk/cube.rs:4757. */
+size_t dm_gdr_chunk_fwd_workspace(const dm_gdr_desc *desc);
+int dm_gdr_chunk_fwd(const dm_gdr_desc *desc, const void *q, const void *k, const void *v,
+                     const void *g, const void *beta, const float *h0, void *out,
+                     float *final_state, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Its backward: from d_out [B, T, H, Dv] (dtype) and d_final [S, H, Dk, Dv] f32 (NULL: zeros),
+ * the gradients dq, dk [B, T, H, Dk], dv (dtype), dg (g_dtype), dbeta (beta_dtype) and
+ * dh0 [S, H, Dk, Dv] f32 (NULL: not wanted). Replaces chunk.rs:545 / chunk/cube.rs:3623. */
+size_t dm_gdr_chunk_bwd_workspace(const dm_gdr_desc *desc);
+int dm_gdr_chunk_bwd(const dm_gdr_desc *desc, const void *q, const void *k, const void *v,
+                     const void *g, const void *beta, const float *h0, const void *d_out,
+                     const float *d_final, void *dq, void *dk, void *dv, void *dg, void *dbeta,
+                     float *dh0, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The recurrent step: rows q, k [B, H, Dk], v [B, H, Dv], g, beta [B, H] advance the states
+ * [S, H, Dk, Dv] f32 (S = B, or cu_seqlens' sequences token by token); out [B, H, Dv] in
+ * dtype. state_out may equal state_in (in place). Replaces recurrent.rs:158 /
+ * recurrent/kernel.rs:294. */
+int dm_gdr_step(const dm_gdr_desc *desc, const void *q, const void *k, const void *v,
+                const void *g, const void *beta, const float *state_in, float *state_out,
+                void *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
