@@ -1,0 +1,300 @@
+"""Benchmark of the attention and gated-delta-rule hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+A step is one pass of the hot path over one batch of synthetic input (dashmag_amd/synthetic.py).
+The headline (``value``) is BASELINE.json's first metric on its config 2: causal packed-varlen
+attention forward + backward, bf16, Hq=32, Hkv=8, D=128, 16384 tokens, as algorithmic TFLOP/s
+(14 P D Hq per step, P the visible pairs). The other metrics of the same line, under
+``secondary``: the north-star T=4096 single sequence, KV-cache decode (config 3, HBM GB/s),
+the chunked gated delta rule forward and backward (config 4, tokens/s and TFLOP/s) and the
+recurrent step (config 5, HBM GB/s). Inputs are resident in HBM before the timed region; every
+call goes through libdashmi.so's C ABI with descriptors and buffers prepared beforehand, timed
+with HIP events on the stream the kernels run on.
+
+``cpu_baseline`` is the CPU oracle (the C restatement of dash-ops' reference, OpenMP) on a
+bounded sample of the same workload, on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step")
+    return p.parse_args()
+
+
+class Timed:
+    """Times a C-ABI call on the current stream: `steps` back-to-back calls between two HIP
+    events, after `warmup` untimed ones."""
+
+    def __init__(self, torch, fn):
+        self.torch, self.fn = torch, fn
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            self.fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            self.fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps  # ms per call
+
+
+def check(rc, lib):
+    if rc != 0:
+        raise RuntimeError(lib.dm_last_error().decode())
+
+
+def bench_attention(torch, dm, ops, lib, data, steps, warmup, cu=None):
+    """Forward + backward of one batch; returns (ms_step, ms_fwd, ms_bwd)."""
+    from dashmag_amd import _lib
+    q, k, v, do = data["q"], data["k"], data["v"], data["do"]
+    mask = dm.AttentionMask.none() if cu is None else dm.AttentionMask.packed(cu, cu)
+    opts = dm.AttentionOptions(causal=True)
+    keep = []
+    desc = ops._attention_desc("attention", q, k, v, mask, opts, keep)
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    fws = lib.dm_attention_fwd_workspace(ctypes.byref(desc))
+    bws = lib.dm_attention_bwd_workspace(ctypes.byref(desc))
+    ws = torch.empty(max(fws, bws, 1), dtype=torch.uint8, device=q.device)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    P = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o, lse, do, dq, dk, dv, ws)]
+    d = ctypes.byref(desc)
+
+    def fwd():
+        check(lib.dm_attention_fwd(d, P[0], P[1], P[2], P[3], P[4], P[9], fws, st), lib)
+
+    def bwd():
+        check(lib.dm_attention_bwd(d, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8],
+                                   P[9], bws, st), lib)
+
+    def step():
+        fwd()
+        bwd()
+
+    ms_fwd = Timed(torch, fwd).run(steps, warmup)
+    ms_bwd = Timed(torch, bwd).run(steps, warmup)
+    ms_step = Timed(torch, step).run(steps, warmup)
+    return ms_step, ms_fwd, ms_bwd, _lib.probe_counts()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (every GPU "
+              "box here has one GPU, and the hot path shards with no exchange: see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import dashmag_amd as dm
+    from dashmag_amd import _lib, ops, synthetic as syn
+
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    only = set(filter(None, args.only.split(",")))
+    want = lambda name: not only or name in only  # noqa: E731
+    secondary = {}
+    print(f"device: {_lib.describe()}", file=sys.stderr, flush=True)
+
+    # ---- headline: attention fwd+bwd, config 2 ----
+    c2 = syn.config2(dev)
+    P2 = syn.visible_pairs(c2["lengths"])
+    flop2 = 14 * P2 * 128 * 32
+    head = None
+    if want("attn"):
+        ms, mf, mb, probes = bench_attention(torch, dm, ops, lib, c2, args.steps, args.warmup,
+                                             c2["cu_seqlens"])
+        head = dict(ms=ms, ms_fwd=mf, ms_bwd=mb, probes=probes)
+        print(f"attention config 2: {ms:.3f} ms/step (fwd {mf:.3f}, bwd {mb:.3f}), "
+              f"{flop2 / ms / 1e9:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    del c2
+    if want("attn4096"):
+        c = syn.config2_single(dev)
+        ms, mf, mb, _ = bench_attention(torch, dm, ops, lib, c, args.steps, args.warmup)
+        P = syn.visible_pairs([4096])
+        secondary["attention_fwd_bwd_T4096"] = dict(
+            unit="TFLOP/s", value=14 * P * 128 * 32 / ms / 1e9, ms_per_step=ms,
+            fwd_tflops=4 * P * 128 * 32 / mf / 1e9, bwd_tflops=10 * P * 128 * 32 / mb / 1e9,
+            frac_of_bf16_peak=14 * P * 128 * 32 / ms / 1e9 / BF16_PEAK_TFLOPS)
+        print(f"attention T=4096: {ms:.3f} ms/step, "
+              f"{secondary['attention_fwd_bwd_T4096']['value']:.1f} TFLOP/s", file=sys.stderr,
+              flush=True)
+        del c
+
+    # ---- decode, config 3 ----
+    if want("decode"):
+        c = syn.config3(dev)
+        q, k, v, lens = c["q"], c["k"], c["v"], c["lengths"]
+        keep = []
+        desc = ops._attention_desc("attention_decode", q.unsqueeze(1), k, v,
+                                   dm.AttentionMask.none(), dm.AttentionOptions(), keep)
+        o = torch.empty_like(q)
+        nb = lib.dm_attention_decode_workspace(ctypes.byref(desc))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        ptrs = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, lens, o, ws)]
+        fn = lambda: check(lib.dm_attention_decode(ctypes.byref(desc), *ptrs[:5], ptrs[5], nb,  # noqa
+                                                   st), lib)
+        ms = Timed(torch, fn).run(max(args.steps, 50), args.warmup)
+        sum_l = int(lens.sum())
+        nbytes = 4 * 8 * 128 * sum_l + 4 * 64 * 32 * 128 + 4 * 64
+        secondary["decode"] = dict(unit="GB/s", value=nbytes / ms / 1e6, us_per_call=ms * 1e3,
+                                   bytes=nbytes, frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS)
+        print(f"decode: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
+              flush=True)
+        del c, k, v
+
+    # ---- gated delta rule chunked, config 4 ----
+    if want("gdr"):
+        c = syn.config4(dev)
+        opts = dm.ChunkGatedDeltaOptions(output_final_state=True)
+        keep = []
+        args_t = [c[x] for x in ("q", "k", "v", "g", "beta")]
+        desc, nseq, (b, t, h, dk, dv) = ops._gdr_desc("chunk_gated_delta_rule", *args_t,
+                                                      c["cu_seqlens"], False, None, False, keep)
+        out = torch.empty_like(c["v"])
+        fin = torch.empty_like(c["h0"])
+        nb = lib.dm_gdr_chunk_fwd_workspace(ctypes.byref(desc))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [c["h0"], out, fin, ws]]
+        fn = lambda: check(lib.dm_gdr_chunk_fwd(ctypes.byref(desc), *p[:8], p[8], nb, st), lib)  # noqa
+        ms = Timed(torch, fn).run(max(3, args.steps // 4), 1)
+        cu = c["cu_seqlens"].tolist()
+        nch = h * sum((cu[i + 1] - cu[i] + 63) // 64 for i in range(len(cu) - 1))
+        flop = 11534336 * nch
+        secondary["gdr_chunk_fwd"] = dict(unit="tokens/s", value=t / ms * 1e3, ms_per_call=ms,
+                                          tflops=flop / ms / 1e9,
+                                          frac_of_bf16_peak=flop / ms / 1e9 / BF16_PEAK_TFLOPS)
+        print(f"gdr chunk fwd: {ms:.3f} ms, {t / ms * 1e3:.3e} tokens/s, "
+              f"{flop / ms / 1e9:.2f} TFLOP/s", file=sys.stderr, flush=True)
+        # backward (reported)
+        dq, dk_, dv_ = (torch.empty_like(x) for x in args_t[:3])
+        dg, db = torch.empty_like(c["g"]), torch.empty_like(c["beta"])
+        dh0 = torch.empty_like(c["h0"])
+        nbb = lib.dm_gdr_chunk_bwd_workspace(ctypes.byref(desc))
+        wsb = torch.empty(max(nbb, 1), dtype=torch.uint8, device=dev)
+        pb = [ctypes.c_void_p(x.data_ptr()) for x in
+              args_t + [c["h0"], c["do"], fin, dq, dk_, dv_, dg, db, dh0, wsb]]
+        fnb = lambda: check(lib.dm_gdr_chunk_bwd(ctypes.byref(desc), *pb[:14], pb[14], nbb, st),  # noqa
+                            lib)
+        msb = Timed(torch, fnb).run(2, 1)
+        secondary["gdr_chunk_bwd"] = dict(unit="tokens/s", value=t / msb * 1e3, ms_per_call=msb,
+                                          tflops=32.5e6 * nch / msb / 1e9)
+        print(f"gdr chunk bwd: {msb:.3f} ms", file=sys.stderr, flush=True)
+        del c, ws, wsb
+
+    # ---- gated delta step, config 5 ----
+    if want("step"):
+        c = syn.config5(dev)
+        keep = []
+        args_t = [c[x] for x in ("q", "k", "v", "g", "beta")]
+        desc, nseq, (b, _, h, dk, dv) = ops._gdr_desc("gated_delta_step", *args_t, None, False,
+                                                      None, True, keep)
+        st_in = c["state"]
+        out = torch.empty_like(c["v"])
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [st_in, st_in, out]]
+        fn = lambda: check(lib.dm_gdr_step(ctypes.byref(desc), *p, st), lib)  # noqa
+        ms = Timed(torch, fn).run(max(args.steps, 100), args.warmup)
+        nbytes = 8 * b * h * dk * dv + (3 * 2 * h * 128 + 2 * 4 * h) * b
+        secondary["gdr_step"] = dict(unit="GB/s", value=nbytes / ms / 1e6, us_per_call=ms * 1e3,
+                                     bytes=nbytes,
+                                     frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS)
+        print(f"gdr step: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
+              flush=True)
+        del c
+
+    # ---- CPU baseline: the oracle on a bounded sample of config 2 ----
+    cpu = None
+    if not args.no_cpu_baseline and want("attn"):
+        import numpy as np
+
+        import oracle
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        oracle.set_threads(threads)
+        c = syn.config2("cpu", dtype=torch.float32)
+        lens = c["lengths"]
+        s = 1  # sequence 1 of config 2
+        a, e = sum(lens[:s]), sum(lens[:s + 1])
+        sl = lambda x: np.ascontiguousarray(x[:, a:e].numpy())  # noqa: E731
+        q, k, v, do = (sl(c[x].to(torch.bfloat16).float()) for x in ("q", "k", "v", "do"))
+        call = oracle.AttentionCall(q, k, v, None, True)
+        t0 = time.time()
+        o, l = oracle.attention_fwd(call)
+        oracle.attention_bwd(call, o, l, do)
+        sec = time.time() - t0
+        L = e - a
+        flop = 14 * syn.visible_pairs([L]) * 128 * 32
+        cpu = dict(value=flop / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                   sample=f"config 2 sequence {s} alone ({L} tokens, causal, Hq=32, Hkv=8, "
+                          f"D=128, f32 values of the bf16 inputs), forward + backward, "
+                          f"{sec:.1f} s")
+        print(f"cpu baseline: {cpu['value'] * 1e3:.2f} GFLOP/s on {threads} threads "
+              f"({sec:.1f} s)", file=sys.stderr, flush=True)
+
+    if head is None:
+        print(json.dumps({"secondary": secondary}))
+        return
+    ms = head["ms"]
+    value = flop2 / ms / 1e9
+    # dominant kernel: the backward entry point (the larger share of the step)
+    dom_ms, dom_flop, dom = (head["ms_bwd"], 10 * P2 * 128 * 32, "attention backward") \
+        if head["ms_bwd"] >= head["ms_fwd"] else (head["ms_fwd"], 4 * P2 * 128 * 32,
+                                                  "attention forward")
+    achieved = dom_flop / dom_ms / 1e9
+    line = {
+        "metric": "attn fwd+bwd TFLOP/s; GDR chunk tokens/s; decode HBM GB/s (% of roofline)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (splitmix64 + Box-Muller, BASELINE.md seeds)",
+        "config": {"workload": "attention fwd+bwd, packed varlen causal, 16384 tokens in "
+                               f"{len(syn.attention_lengths()[0])} sequences, Hq=32, Hkv=8, "
+                               "D=128 (BASELINE config 2)",
+                   "tokens": 16384, "hq": 32, "hkv": 8, "d": 128,
+                   "visible_pairs": P2, "flop_per_step": flop2},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
