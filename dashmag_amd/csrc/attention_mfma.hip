@@ -21,17 +21,29 @@ namespace dm {
 
 constexpr int kFwdM = 128;  // queries per workgroup
 constexpr int kFwdN = 64;   // keys per tile
+// A row-major LDS tile read along its rows by ds_read_b128 (16 lanes on 16 consecutive rows) is
+// conflict-free with a row stride of 16 mod 256 bytes; one read transposed by
+// ds_read_b64_tr_b16 (a 16-lane group on 4 consecutive rows x 32 bytes, the two groups of a half
+// wave side by side) with a stride of 64 mod 256 bytes.
+template <int D>
+struct Strides {
+    static constexpr int ROW = D + 8;   // elements: 272 bytes at D = 128, 144 at D = 64
+    static constexpr int TR = D + 32;   // elements: 320 bytes at D = 128, 192 at D = 64
+};
 
 template <int D>
 struct FwdSmem {
-    static constexpr int KS = D + 8;   // K row stride (elements): 16-byte pad against conflicts
-    static constexpr int VS = kFwdN + 4;  // V^T row stride: 136 bytes, conflict-free 8-byte reads
-    uint16_t k[kFwdN * KS];
-    uint16_t vt[D * VS];
+    uint4 k[kFwdN * Strides<D>::ROW / 8];
+    uint4 v[kFwdN * Strides<D>::TR / 8];
     int32_t lo[4], hi[4], flo[4], fhi[4];
 };
 
-template <int DT, int D>
+// The per-tile rescale is skipped until a row's maximum grows by more than 2^8 over the one its
+// exponentials are taken against: p stays below 256, exact in f32 and bf16 range, and the
+// normalisation at the end uses the same reference.
+constexpr float kRescaleThreshold = 8.f;
+
+template <int DT, int D, bool PAD>
 __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, int64_t Hq,
                                                         int64_t Hkv, float scale,
                                                         const uint16_t *__restrict__ q,
@@ -40,6 +52,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
                                                         uint16_t *__restrict__ o,
                                                         float *__restrict__ lse) {
     using Sm = FwdSmem<D>;
+    constexpr int KS = Strides<D>::ROW, VS = Strides<D>::TR;
     __shared__ Sm sm;
     constexpr int KSTEPS = D / 16;  // k-steps of S^T over the head dimension
     constexpr int DT32 = D / 32;    // 32-row tiles of O^T
@@ -56,22 +69,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     const int64_t kh = h / (Hq / Hkv);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
-    const int64_t m0 = tile * kFwdM;
-    const int64_t qi = m0 + wave * 32 + col;  // this lane's query row
+    const int64_t qi = tile * kFwdM + wave * 32 + col;  // this lane's query row
     const bool qvalid = qi < Tq;
 
     // visibility interval of this lane's query
-    int64_t lo = 0, hi = 0;
-    if (qvalid) row_bounds(m, qi, &lo, &hi);
-    // workgroup range: union of the rows' intervals; the keys every row sees
+    int64_t lo64 = 0, hi64 = 0;
+    if (qvalid) row_bounds(m, qi, &lo64, &hi64);
+    const int32_t lo = (int32_t)lo64, hi = (int32_t)hi64;
     {
-        int32_t wl = lo < hi ? (int32_t)lo : INT32_MAX, wh = lo < hi ? (int32_t)hi : INT32_MIN;
-        // rows that see nothing force masking on every tile
-        int32_t fl = lo < hi ? (int32_t)lo : INT32_MAX, fh = lo < hi ? (int32_t)hi : INT32_MIN;
-        int32_t rfl = (qvalid && lo < hi) ? (int32_t)lo : (qvalid ? INT32_MAX : INT32_MIN);
-        int32_t rfh = (qvalid && lo < hi) ? (int32_t)hi : (qvalid ? INT32_MIN : INT32_MAX);
-        (void)fl;
-        (void)fh;
+        // workgroup range (union of the rows' intervals) and the keys every row sees; a row
+        // that sees nothing forces masking on every tile
+        int32_t wl = lo < hi ? lo : INT32_MAX, wh = lo < hi ? hi : INT32_MIN;
+        int32_t rfl = (qvalid && lo < hi) ? lo : (qvalid ? INT32_MAX : INT32_MIN);
+        int32_t rfh = (qvalid && lo < hi) ? hi : (qvalid ? INT32_MIN : INT32_MAX);
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
             wl = min(wl, __shfl_xor(wl, off, 64));
@@ -93,7 +103,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     const int32_t full_hi = min(min(sm.fhi[0], sm.fhi[1]), min(sm.fhi[2], sm.fhi[3]));
 
     // this wavefront's queries as the B operand: col = query, k = head dimension
-    const int64_t qstride = Hq * D;  // elements between consecutive query rows
     Frag8 qf[KSTEPS];
     {
         const uint16_t *qp = q + ((b * Tq + qi) * Hq + h) * D + half * 8;
@@ -101,125 +110,101 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
         for (int s = 0; s < KSTEPS; s++)
             qf[s].u = qvalid ? *(const uint4 *)(qp + s * 16) : make_uint4(0, 0, 0, 0);
     }
-    (void)qstride;
 
     f32x16_t acc[DT32];
 #pragma unroll
     for (int t = 0; t < DT32; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[t][i] = 0.f;
-    float mrow = -INFINITY, lrow = 0.f;  // running max of the raw scores, this lane's partial sum
-    const float qk_scale = scale * 1.4426950408889634f;
+    // mc: the reference the exponentials are taken against, max raw score x scale x log2(e);
+    // lrow: this lane's partial sum of the exponentials
+    float mc = -INFINITY, lrow = 0.f;
+    const float c2 = scale * 1.4426950408889634f;
 
-    const int64_t kvstride = Hkv * D;  // elements between consecutive key rows
-    const uint16_t *kbase = k + (b * Tk * Hkv + kh) * D;
-    const uint16_t *vbase = v + (b * Tk * Hkv + kh) * D;
-    const uint8_t *pad = m.pad ? m.pad + b * Tk : nullptr;
-
-    // global -> register staging of one K tile (16-byte chunks) and one V tile (4x4 blocks)
-    constexpr int KCH = kFwdN * D / 8 / 256;       // K chunks per thread
-    constexpr int VBL = kFwdN * D / 16 / 256;      // V 4x4 blocks per thread
-    uint4 kreg[KCH];
-    uint2 vreg[VBL][4];
-    auto load_tile = [&](int64_t j0) {
+    // staging of one K and one V tile: 16-byte chunks at per-thread byte offsets, loaded through
+    // buffer resources whose range ends at the last key (rows past it read as zeros)
+    const int32_t kvstride = (int32_t)(Hkv * D);
+    const uint32_t kvbytes = (uint32_t)(((Tk - 1) * Hkv + 1) * D * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + (b * Tk * Hkv + kh) * D, kvbytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + (b * Tk * Hkv + kh) * D, kvbytes);
+    const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
+    constexpr int CPR = D / 8;                 // chunks per row
+    constexpr int NCH = kFwdN * CPR / 256;     // chunks per thread per tensor
+    constexpr int RSTEP = 256 / CPR;           // rows between a thread's chunks
+    const int crow = tid / CPR, ccol = tid % CPR;
+    const uint32_t goff = (uint32_t)(crow * kvstride + ccol * 8) * 2;
+    uint4 kreg[NCH], vreg[NCH];
+    auto load_tile = [&](int32_t j0) {
+        const uint32_t base = (uint32_t)j0 * (uint32_t)kvstride * 2 + goff;
 #pragma unroll
-        for (int u = 0; u < KCH; u++) {
-            const int c = tid + 256 * u;
-            const int r = c / (D / 8), c8 = c % (D / 8);
-            const int64_t j = j0 + r;
-            kreg[u] = j < Tk ? *(const uint4 *)(kbase + j * kvstride + c8 * 8)
-                             : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < VBL; u++) {
-            const int c = tid + 256 * u;
-            const int dq = c % (D / 4), kq = c / (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int64_t j = j0 + kq * 4 + r;
-                vreg[u][r] = j < Tk ? *(const uint2 *)(vbase + j * kvstride + dq * 4)
-                                    : make_uint2(0, 0);
-            }
+        for (int u = 0; u < NCH; u++) {
+            const uint32_t off = base + (uint32_t)(u * RSTEP * kvstride * 2);
+            kreg[u] = buf_load16(krs, off);
+            vreg[u] = buf_load16(vrs, off);
         }
     };
     auto store_tile = [&]() {
 #pragma unroll
-        for (int u = 0; u < KCH; u++) {
-            const int c = tid + 256 * u;
-            const int r = c / (D / 8), c8 = c % (D / 8);
-            *(uint4 *)(sm.k + r * Sm::KS + c8 * 8) = kreg[u];
-        }
-#pragma unroll
-        for (int u = 0; u < VBL; u++) {
-            const int c = tid + 256 * u;
-            const int dq = c % (D / 4), kq = c / (D / 4);
-            const uint2 *x = vreg[u];
-            // 4 keys x 4 dims -> 4 dims x 4 keys
-            uint2 t0, t1, t2, t3;
-            t0.x = (x[0].x & 0xffffu) | (x[1].x << 16);
-            t0.y = (x[2].x & 0xffffu) | (x[3].x << 16);
-            t1.x = (x[0].x >> 16) | (x[1].x & 0xffff0000u);
-            t1.y = (x[2].x >> 16) | (x[3].x & 0xffff0000u);
-            t2.x = (x[0].y & 0xffffu) | (x[1].y << 16);
-            t2.y = (x[2].y & 0xffffu) | (x[3].y << 16);
-            t3.x = (x[0].y >> 16) | (x[1].y & 0xffff0000u);
-            t3.y = (x[2].y >> 16) | (x[3].y & 0xffff0000u);
-            uint16_t *dst = sm.vt + (dq * 4) * Sm::VS + kq * 4;
-            *(uint2 *)(dst) = t0;
-            *(uint2 *)(dst + Sm::VS) = t1;
-            *(uint2 *)(dst + 2 * Sm::VS) = t2;
-            *(uint2 *)(dst + 3 * Sm::VS) = t3;
+        for (int u = 0; u < NCH; u++) {
+            sm.k[(crow + u * RSTEP) * (KS / 8) + ccol] = kreg[u];
+            sm.v[(crow + u * RSTEP) * (VS / 8) + ccol] = vreg[u];
         }
     };
+    const uint16_t *sk = (const uint16_t *)sm.k, *sv = (const uint16_t *)sm.v;
 
     if (kv_lo < kv_hi) load_tile(kv_lo);
-    for (int64_t j0 = kv_lo; j0 < kv_hi; j0 += kFwdN) {
+    for (int32_t j0 = kv_lo; j0 < kv_hi; j0 += kFwdN) {
         __syncthreads();
         store_tile();
         __syncthreads();
         if (j0 + kFwdN < kv_hi) load_tile(j0 + kFwdN);
 
-        // S^T for keys [j0, j0 + 64): two 32-key row tiles
+        // S^T for keys [j0, j0 + 64): two 32-key row tiles, their accumulation chains
+        // interleaved
         f32x16_t s[2];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) s[t][i] = 0.f;
-            const uint16_t *kr = sm.k + (t * 32 + col) * Sm::KS + half * 8;
 #pragma unroll
-            for (int st = 0; st < KSTEPS; st++) {
+        for (int st = 0; st < KSTEPS; st++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
                 Frag8 a;
-                a.u = *(const uint4 *)(kr + st * 16);
+                a.u = *(const uint4 *)(sk + (t * 32 + col) * KS + half * 8 + st * 16);
                 s[t] = mfma32<DT>(a, qf[st], s[t]);
             }
+        // mask where the tile is cut
+        if (PAD || j0 < full_lo || j0 + kFwdN > full_hi) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int32_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                    bool vis = j >= lo && j < hi;
+                    if constexpr (PAD) vis = vis && !pad[j];
+                    s[t][i] = vis ? s[t][i] : -INFINITY;
+                }
         }
-        // mask where the tile is cut; the row statistics are kept on the raw scores, so that
-        // p = exp2((s - m) * scale * log2(e)) rounds once after an exact subtraction
-        const bool masked = pad || j0 < full_lo || j0 + kFwdN > full_hi;
         float tmax = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float x = s[t][i];
-                if (masked) {
-                    const int64_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                    const bool vis = j >= lo && j < hi && (!pad || !pad[j]);
-                    x = vis ? x : -INFINITY;
-                }
-                s[t][i] = x;
-                tmax = fmaxf(tmax, x);
-            }
+            for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[t][i]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(mrow, tmax);
-        const float mbase = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = exp2f((mrow - mbase) * qk_scale);
-        mrow = mnew;
-        lrow *= alpha;
+        const float tmc = tmax * c2;
+        const bool grow = tmc - mc > kRescaleThreshold;  // false while both are -inf
+        if (__any(grow)) {
+            const float mnew = grow ? tmc : mc;
+            const float alpha = grow ? fast_exp2(mc - mnew) : 1.f;  // 0 from -inf
+            mc = mnew;
+            lrow *= alpha;
 #pragma unroll
-        for (int t = 0; t < DT32; t++)
+            for (int t = 0; t < DT32; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[t][i] *= alpha;
+                for (int i = 0; i < 16; i++) acc[t][i] *= alpha;
+        }
+        const float mneg = mc == -INFINITY ? 0.f : -mc;
         // P^T as B fragments: tile t, step u takes the lane's values i in [8u, 8u + 8)
         Frag8 pf[2][2];
 #pragma unroll
@@ -229,29 +214,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
                 float p[8];
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    p[e] = exp2f((s[t][8 * u + e] - mbase) * qk_scale);
+                    p[e] = fast_exp2(fmaf(s[t][8 * u + e], c2, mneg));
                     lrow += p[e];
                 }
                 pf[t][u].u = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
                                         pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
             }
-        // O^T += V^T P^T: key order of slot e of lane half h in step (t, u):
-        //   32 t + 16 u + 8 (e / 4) + 4 h + e % 4
+        // O^T += V^T P^T: A = V^T from the row-major V tile by transposed reads, key order
+        //   32 t + 16 u + 8 (e / 4) + 4 h + e % 4 in slot e of lane half h of step (t, u);
+        // the four output tiles' chains interleaved
 #pragma unroll
-        for (int dt = 0; dt < DT32; dt++) {
-            const uint16_t *vr = sm.vt + (dt * 32 + col) * Sm::VS + half * 4;
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int u = 0; u < 2; u++)
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const uint16_t *p0 = vr + t * 32 + u * 16;
-                    const uint2 lo4 = *(const uint2 *)(p0);
-                    const uint2 hi4 = *(const uint2 *)(p0 + 8);
-                    Frag8 a;
-                    a.u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                for (int dt = 0; dt < DT32; dt++) {
+                    const Frag8 a = lds_tr_frag(sv, VS, t * 32 + u * 16, dt * 32, lane);
                     acc[dt] = mfma32<DT>(a, pf[t][u], acc[dt]);
                 }
-        }
     }
 
     // finish: l over both halves, normalise, write O and lse
@@ -271,13 +251,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
         }
     if (half == 0)
         lse[(b * Tq + qi) * Hq + h] =
-            ltot > 0.f ? (float)((double)mrow * (double)scale + log((double)ltot)) : -INFINITY;
+            ltot > 0.f ? (float)((double)mc * 0.6931471805599453 + log((double)ltot)) : -INFINITY;
 }
 
 bool mfma_fwd_takes(const dm_attention_desc *d) {
     // a positive scale keeps the maximum of the raw scores the maximum of the scaled ones
+    // buffer loads take 32-bit byte offsets within one batch row's keys and values
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) && (d->d == 64 || d->d == 128) &&
-           d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f;
+           d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
+           d->tk * d->hkv * d->d * 2 < (1ll << 31);
 }
 
 int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float scale,
@@ -290,12 +272,17 @@ int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     dim3 grid((unsigned)nblocks), block(256);
     const uint16_t *qq = (const uint16_t *)q, *kk = (const uint16_t *)k, *vv = (const uint16_t *)v;
     uint16_t *oo = (uint16_t *)o;
-#define FWD(DT, DD) \
-    attn_fwd_mfma<DT, DD><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, kk, vv, oo, lse)
+#define FWD(DT, DD)                                                                            \
+    if (m.pad)                                                                                 \
+        attn_fwd_mfma<DT, DD, true><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
+                                                            kk, vv, oo, lse);                 \
+    else                                                                                       \
+        attn_fwd_mfma<DT, DD, false><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale,   \
+                                                             qq, kk, vv, oo, lse)
     if (d->dtype == DM_BF16) {
-        if (d->d == 64) FWD(DM_BF16, 64); else FWD(DM_BF16, 128);
+        if (d->d == 64) { FWD(DM_BF16, 64); } else { FWD(DM_BF16, 128); }
     } else {
-        if (d->d == 64) FWD(DM_F16, 64); else FWD(DM_F16, 128);
+        if (d->d == 64) { FWD(DM_F16, 64); } else { FWD(DM_F16, 128); }
     }
 #undef FWD
     probe_add(DM_PROBE_ATTN_FWD_MFMA);

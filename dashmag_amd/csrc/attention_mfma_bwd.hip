@@ -130,35 +130,27 @@ __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) 
     }
 }
 
-// 4 rows x 4 columns of 16-bit values (4 uint2, one per row) -> 4 columns x 4 rows.
-__device__ __forceinline__ void transpose4(const uint2 *x, uint2 *t) {
-    t[0].x = (x[0].x & 0xffffu) | (x[1].x << 16);
-    t[0].y = (x[2].x & 0xffffu) | (x[3].x << 16);
-    t[1].x = (x[0].x >> 16) | (x[1].x & 0xffff0000u);
-    t[1].y = (x[2].x >> 16) | (x[3].x & 0xffff0000u);
-    t[2].x = (x[0].y & 0xffffu) | (x[1].y << 16);
-    t[2].y = (x[2].y & 0xffffu) | (x[3].y << 16);
-    t[3].x = (x[0].y >> 16) | (x[1].y & 0xffff0000u);
-    t[3].y = (x[2].y >> 16) | (x[3].y & 0xffff0000u);
-}
-
 // ------------------------------------------------------------------------------------------
 // dK, dV
 // ------------------------------------------------------------------------------------------
 
 template <int D>
+struct BwdStrides {
+    static constexpr int ROW = D + 8;  // rows read by ds_read_b128
+    static constexpr int TR = D + 32;  // rows read by ds_read_b64_tr_b16
+};
+
+template <int D>
 struct DkdvSmem {
-    static constexpr int RS = D + 8;       // row-major stride (elements)
-    static constexpr int TS = kQTile + 4;  // transposed stride: 136 bytes
-    uint16_t q[kQTile * RS];
-    uint16_t qt[D * TS];
-    uint16_t g[kQTile * RS];
-    uint16_t gt[D * TS];
+    uint4 q[kQTile * BwdStrides<D>::ROW / 8];
+    uint4 qt[kQTile * BwdStrides<D>::TR / 8];
+    uint4 g[kQTile * BwdStrides<D>::ROW / 8];
+    uint4 gt[kQTile * BwdStrides<D>::TR / 8];
     float lse2[kQTile], delta[kQTile];
     int32_t rlo[kQTile], rhi[kQTile];
 };
 
-template <int DT, int D>
+template <int DT, int D, bool PAD>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_t Hq,
                                                    int64_t Hkv, float scale,
                                                    const uint16_t *__restrict__ q,
@@ -169,6 +161,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
                                                    BwdWs w, uint16_t *__restrict__ dk,
                                                    uint16_t *__restrict__ dv) {
     using Sm = DkdvSmem<D>;
+    constexpr int RS = BwdStrides<D>::ROW, TS = BwdStrides<D>::TR;
     __shared__ Sm sm;
     constexpr int KSTEPS = D / 16, DT32 = D / 32;
     const int64_t Tq = m.tq, Tk = m.tk;
@@ -180,11 +173,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     const int64_t group = Hq / Hkv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
-    const int64_t j0 = kb * kKvBlock;
-    const int64_t key = j0 + wave * 32 + col;  // this lane's key
+    const int32_t j0 = (int32_t)(kb * kKvBlock);
+    const int32_t key = j0 + wave * 32 + col;  // this lane's key
     const bool kvalid = key < Tk;
-    const bool kpad = m.pad && kvalid && m.pad[b * Tk + key];
-    const int64_t kvstride = Hkv * D, qstride = Hq * D;
+    const bool kpad = PAD && kvalid && m.pad[b * Tk + key];
     const float c2 = scale * 1.4426950408889634f;
 
     // K and V of this lane's key as B operands (col = key, k = head dimension)
@@ -206,26 +198,27 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
 
     const int64_t ntiles = (Tq + kQTile - 1) / kQTile;
     const int32_t *tr = w.trange + b * ntiles * 4;
-    const int64_t j1 = j0 + kKvBlock < Tk ? j0 + kKvBlock : Tk;
+    const int32_t j1 = j0 + kKvBlock < Tk ? j0 + kKvBlock : (int32_t)Tk;
     auto sees = [&](int64_t t) -> bool { return tr[t * 4] < j1 && tr[t * 4 + 1] > j0; };
 
-    // staging: Q and dO tiles as 4x4 blocks (row-major and transposed copies come from them)
-    constexpr int NB = kQTile * D / 16 / 256;  // 4x4 blocks per thread per tensor
-    uint2 qreg[NB][4], greg[NB][4];
+    // staging: Q and dO tiles in 16-byte chunks (buffer loads whose range ends at the last
+    // query row), written to a row copy and a transposed-read copy
+    constexpr int CPR = D / 8, NCH = kQTile * CPR / 256, RSTEP = 256 / CPR;
+    const int crow = tid / CPR, ccol = tid % CPR;
+    const uint32_t qrow_bytes = (uint32_t)(Hq * D * 2);
+    const uint32_t qbytes = (uint32_t)(((Tq - 1) * Hq + 1) * D * 2);
+    const uint32_t goff = crow * qrow_bytes + ccol * 16;
+    uint4 qreg[NCH], greg[NCH];
+    __amdgpu_buffer_rsrc_t qrs, grs;
     auto load = [&](int64_t h, int64_t t) {
-        const int64_t i0 = t * kQTile;
+        qrs = make_rsrc(q + (b * Tq * Hq + h) * D, qbytes);
+        grs = make_rsrc(d_o + (b * Tq * Hq + h) * D, qbytes);
+        const uint32_t base = (uint32_t)(t * kQTile) * qrow_bytes + goff;
 #pragma unroll
-        for (int u = 0; u < NB; u++) {
-            const int c = tid + 256 * u;
-            const int dq = c % (D / 4), rq = c / (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int64_t i = i0 + rq * 4 + r;
-                const bool ok = i < Tq;
-                const int64_t off = ((b * Tq + i) * Hq + h) * D + dq * 4;
-                qreg[u][r] = ok ? *(const uint2 *)(q + off) : make_uint2(0, 0);
-                greg[u][r] = ok ? *(const uint2 *)(d_o + off) : make_uint2(0, 0);
-            }
+        for (int u = 0; u < NCH; u++) {
+            const uint32_t off = base + u * RSTEP * qrow_bytes;
+            qreg[u] = buf_load16(qrs, off);
+            greg[u] = buf_load16(grs, off);
         }
     };
     float st_lse = 0.f, st_delta = 0.f;
@@ -242,21 +235,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     };
     auto store = [&]() {
 #pragma unroll
-        for (int u = 0; u < NB; u++) {
-            const int c = tid + 256 * u;
-            const int dq = c % (D / 4), rq = c / (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                *(uint2 *)(sm.q + (rq * 4 + r) * Sm::RS + dq * 4) = qreg[u][r];
-                *(uint2 *)(sm.g + (rq * 4 + r) * Sm::RS + dq * 4) = greg[u][r];
-            }
-            uint2 t4[4];
-            transpose4(qreg[u], t4);
-#pragma unroll
-            for (int e = 0; e < 4; e++) *(uint2 *)(sm.qt + (dq * 4 + e) * Sm::TS + rq * 4) = t4[e];
-            transpose4(greg[u], t4);
-#pragma unroll
-            for (int e = 0; e < 4; e++) *(uint2 *)(sm.gt + (dq * 4 + e) * Sm::TS + rq * 4) = t4[e];
+        for (int u = 0; u < NCH; u++) {
+            const int r = crow + u * RSTEP;
+            sm.q[r * (RS / 8) + ccol] = qreg[u];
+            sm.qt[r * (TS / 8) + ccol] = qreg[u];
+            sm.g[r * (RS / 8) + ccol] = greg[u];
+            sm.gt[r * (TS / 8) + ccol] = greg[u];
         }
         if (tid < kQTile) {
             sm.lse2[tid] = st_lse;
@@ -265,12 +249,14 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
             sm.rhi[tid] = st_hi;
         }
     };
+    const uint16_t *sq = (const uint16_t *)sm.q, *sqt = (const uint16_t *)sm.qt;
+    const uint16_t *sg = (const uint16_t *)sm.g, *sgt = (const uint16_t *)sm.gt;
 
     // the (head, tile) steps: the group's query heads, each over the tiles that see the keys
     int64_t hh = kh * group, tt = 0;
+    const int64_t hend = (kh + 1) * group;
     auto advance = [&](int64_t &h, int64_t &t) {
-        // from (h, t) to the next step that sees the keys, or h = end
-        while (h < (kh + 1) * group) {
+        while (h < hend) {
             while (t < ntiles && !sees(t)) t++;
             if (t < ntiles) return;
             h++;
@@ -279,32 +265,32 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     };
     const bool any_key = j0 < Tk;
     if (any_key) advance(hh, tt);
-    if (any_key && hh < (kh + 1) * group) {
+    if (any_key && hh < hend) {
         load(hh, tt);
         load_rows(hh, tt);
     }
-    while (any_key && hh < (kh + 1) * group) {
-        const int64_t h = hh, t = tt;
+    while (any_key && hh < hend) {
+        const int64_t t = tt;
         __syncthreads();
         store();
         __syncthreads();
         // next step's loads, in flight during this step's products
         tt++;
         advance(hh, tt);
-        if (hh < (kh + 1) * group) {
+        if (hh < hend) {
             load(hh, tt);
             load_rows(hh, tt);
         }
         const int32_t *r = tr + t * 4;
-        const bool masked = m.pad != nullptr || r[2] > j0 || r[3] < j0 + kKvBlock;
+        const bool masked = PAD || r[2] > j0 || r[3] < j0 + kKvBlock;
 #pragma unroll
         for (int qs = 0; qs < kQTile / 32; qs++) {
             // S and dP for 32 queries x this wavefront's 32 keys
             f32x16_t s, dp;
 #pragma unroll
             for (int i = 0; i < 16; i++) s[i] = dp[i] = 0.f;
-            const uint16_t *qa = sm.q + (qs * 32 + col) * Sm::RS + half * 8;
-            const uint16_t *ga = sm.g + (qs * 32 + col) * Sm::RS + half * 8;
+            const uint16_t *qa = sq + (qs * 32 + col) * RS + half * 8;
+            const uint16_t *ga = sg + (qs * 32 + col) * RS + half * 8;
 #pragma unroll
             for (int st = 0; st < KSTEPS; st++) {
                 Frag8 a;
@@ -313,48 +299,48 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
                 a.u = *(const uint4 *)(ga + st * 16);
                 dp = mfma32<DT>(a, vf[st], dp);
             }
-            // P = exp2(S c - lse2), dS = P (dP - delta), element (query row, this lane's key)
+            // P = exp2(S c - lse2), dS = P (dP - delta); element i is query
+            //   32 qs + 8 (i / 4) + 4 h + i % 4, four consecutive rows per i / 4
             Frag8 pf[2], df[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 float p[8], ds[8];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int i = 8 * u + e;
-                    const int qr = qs * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                    float x = exp2f(s[i] * c2 - sm.lse2[qr]);
-                    if (masked) {
-                        const bool vis = key >= sm.rlo[qr] && key < sm.rhi[qr] && !kpad;
-                        x = vis ? x : 0.f;
+                for (int g4 = 0; g4 < 2; g4++) {
+                    const int r0 = qs * 32 + (2 * u + g4) * 8 + half * 4;
+                    const float4 l4 = *(const float4 *)(sm.lse2 + r0);
+                    const float4 d4 = *(const float4 *)(sm.delta + r0);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                    const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int i = 8 * u + 4 * g4 + e;
+                        float x = fast_exp2(fmaf(s[i], c2, -lv[e]));
+                        if (masked) {
+                            const bool vis = key >= sm.rlo[r0 + e] && key < sm.rhi[r0 + e] && !kpad;
+                            x = vis ? x : 0.f;
+                        }
+                        p[4 * g4 + e] = x;
+                        ds[4 * g4 + e] = x * (dp[i] - dl[e]);
                     }
-                    p[e] = x;
-                    ds[e] = x * (dp[i] - sm.delta[qr]);
                 }
                 pf[u].u = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
                                      pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
                 df[u].u = make_uint4(pack2<DT>(ds[0], ds[1]), pack2<DT>(ds[2], ds[3]),
                                      pack2<DT>(ds[4], ds[5]), pack2<DT>(ds[6], ds[7]));
             }
-            // dV += P^T dO, dK += dS^T Q: A = (row key, k = query), B = (k = query, col = d)
-            // from the transposed copies; slot e of lane half h in step u is query
-            //   32 qs + 16 u + 8 (e / 4) + 4 h + e % 4
+            // dV += P^T dO, dK += dS^T Q: A = (row key, k = query) from the products' output,
+            // B = (k = query, col = d) by transposed reads of the row-major tiles
 #pragma unroll
-            for (int dt = 0; dt < DT32; dt++) {
-                const uint16_t *gp = sm.gt + (dt * 32 + col) * Sm::TS + qs * 32 + half * 4;
-                const uint16_t *qp = sm.qt + (dt * 32 + col) * Sm::TS + qs * 32 + half * 4;
+            for (int u = 0; u < 2; u++)
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    Frag8 bg, bq;
-                    const uint2 g0 = *(const uint2 *)(gp + u * 16), g1 = *(const uint2 *)(gp + u * 16 + 8);
-                    const uint2 q0 = *(const uint2 *)(qp + u * 16), q1 = *(const uint2 *)(qp + u * 16 + 8);
-                    bg.u = make_uint4(g0.x, g0.y, g1.x, g1.y);
-                    bq.u = make_uint4(q0.x, q0.y, q1.x, q1.y);
+                for (int dt = 0; dt < DT32; dt++) {
+                    const Frag8 bg = lds_tr_frag(sgt, TS, qs * 32 + u * 16, dt * 32, lane);
+                    const Frag8 bq = lds_tr_frag(sqt, TS, qs * 32 + u * 16, dt * 32, lane);
                     dva[dt] = mfma32<DT>(pf[u], bg, dva[dt]);
                     dka[dt] = mfma32<DT>(df[u], bq, dka[dt]);
                 }
-            }
         }
-        (void)h;
     }
     // write dK (scaled), dV: lane holds column d = 32 dt + col, rows = keys of this wavefront
     //   32 w + 8 (i / 4) + 4 h + i % 4
@@ -365,18 +351,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
             const int64_t j = j0 + wave * 32 + (i / 4) * 8 + half * 4 + (i % 4);
             if (j >= Tk) continue;
             const int64_t off = ((b * Tk + j) * Hkv + kh) * D + dt * 32 + col;
-            const float kv = dka[dt][i] * scale, vv = dva[dt][i];
-            if constexpr (DT == DM_BF16) {
-                dk[off] = f32_to_bf16(kv);
-                dv[off] = f32_to_bf16(vv);
-            } else {
-                _Float16 a = (_Float16)kv, c = (_Float16)vv;
-                dk[off] = *(uint16_t *)&a;
-                dv[off] = *(uint16_t *)&c;
-            }
+            const uint32_t kv2 = pack2<DT>(dka[dt][i] * scale, dva[dt][i]);
+            dk[off] = (uint16_t)(kv2 & 0xffffu);
+            dv[off] = (uint16_t)(kv2 >> 16);
         }
-    (void)kvstride;
-    (void)qstride;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -385,15 +363,13 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
 
 template <int D>
 struct DqSmem {
-    static constexpr int RS = D + 8;
-    static constexpr int TS = kDqN + 4;
-    uint16_t k[kDqN * RS];
-    uint16_t v[kDqN * RS];
-    uint16_t kt[D * TS];
+    uint4 k[kDqN * BwdStrides<D>::ROW / 8];
+    uint4 v[kDqN * BwdStrides<D>::ROW / 8];
+    uint4 kt[kDqN * BwdStrides<D>::TR / 8];
     int32_t lo[4], hi[4], flo[4], fhi[4];
 };
 
-template <int DT, int D>
+template <int DT, int D, bool PAD>
 __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t Hq, int64_t Hkv,
                                                  float scale, const uint16_t *__restrict__ q,
                                                  const uint16_t *__restrict__ k,
@@ -402,6 +378,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
                                                  const float *__restrict__ delta, BwdWs w,
                                                  uint16_t *__restrict__ dq) {
     using Sm = DqSmem<D>;
+    constexpr int RS = BwdStrides<D>::ROW, TS = BwdStrides<D>::TR;
     __shared__ Sm sm;
     constexpr int KSTEPS = D / 16, DT32 = D / 32;
     const int64_t Tq = m.tq, Tk = m.tk;
@@ -417,7 +394,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     const int col = lane & 31, half = lane >> 5;
     const int64_t qi = tile * kDqM + wave * 32 + col;
     const bool qvalid = qi < Tq;
-    int64_t lo = 0, hi = 0;
+    int32_t lo = 0, hi = 0;
     float lse2 = INFINITY, dl = 0.f;
     if (qvalid) {
         lo = w.rlo[b * Tq + qi];
@@ -427,9 +404,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     }
     if (lse2 == INFINITY) hi = lo;  // a query that sees no key: dq = 0
     {
-        int32_t wl = lo < hi ? (int32_t)lo : INT32_MAX, wh = lo < hi ? (int32_t)hi : INT32_MIN;
-        int32_t rfl = (qvalid && lo < hi) ? (int32_t)lo : (qvalid ? INT32_MAX : INT32_MIN);
-        int32_t rfh = (qvalid && lo < hi) ? (int32_t)hi : (qvalid ? INT32_MIN : INT32_MAX);
+        int32_t wl = lo < hi ? lo : INT32_MAX, wh = lo < hi ? hi : INT32_MIN;
+        int32_t rfl = (qvalid && lo < hi) ? lo : (qvalid ? INT32_MAX : INT32_MIN);
+        int32_t rfh = (qvalid && lo < hi) ? hi : (qvalid ? INT32_MIN : INT32_MAX);
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
             wl = min(wl, __shfl_xor(wl, off, 64));
@@ -465,59 +442,53 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[t][i] = 0.f;
     const float c2 = scale * 1.4426950408889634f;
-    const int64_t kvstride = Hkv * D;
-    const uint16_t *kbase = k + (b * Tk * Hkv + kh) * D;
-    const uint16_t *vbase = v + (b * Tk * Hkv + kh) * D;
-    const uint8_t *pad = m.pad ? m.pad + b * Tk : nullptr;
+    const float nlse = -lse2;
+    const int32_t kvstride = (int32_t)(Hkv * D);
+    const uint32_t kvbytes = (uint32_t)(((Tk - 1) * Hkv + 1) * D * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + (b * Tk * Hkv + kh) * D, kvbytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + (b * Tk * Hkv + kh) * D, kvbytes);
+    const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
 
-    constexpr int NB = kDqN * D / 16 / 256;
-    uint2 kreg[NB][4], vreg[NB][4];
-    auto load_tile = [&](int64_t j0) {
+    constexpr int CPR = D / 8, NCH = kDqN * CPR / 256, RSTEP = 256 / CPR;
+    const int crow = tid / CPR, ccol = tid % CPR;
+    const uint32_t goff = (uint32_t)(crow * kvstride + ccol * 8) * 2;
+    uint4 kreg[NCH], vreg[NCH];
+    auto load_tile = [&](int32_t j0) {
+        const uint32_t base = (uint32_t)j0 * (uint32_t)kvstride * 2 + goff;
 #pragma unroll
-        for (int u = 0; u < NB; u++) {
-            const int c = tid + 256 * u;
-            const int dq4 = c % (D / 4), kq = c / (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int64_t j = j0 + kq * 4 + r;
-                const bool ok = j < Tk;
-                kreg[u][r] = ok ? *(const uint2 *)(kbase + j * kvstride + dq4 * 4) : make_uint2(0, 0);
-                vreg[u][r] = ok ? *(const uint2 *)(vbase + j * kvstride + dq4 * 4) : make_uint2(0, 0);
-            }
+        for (int u = 0; u < NCH; u++) {
+            const uint32_t off = base + (uint32_t)(u * RSTEP * kvstride * 2);
+            kreg[u] = buf_load16(krs, off);
+            vreg[u] = buf_load16(vrs, off);
         }
     };
     auto store_tile = [&]() {
 #pragma unroll
-        for (int u = 0; u < NB; u++) {
-            const int c = tid + 256 * u;
-            const int dq4 = c % (D / 4), kq = c / (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                *(uint2 *)(sm.k + (kq * 4 + r) * Sm::RS + dq4 * 4) = kreg[u][r];
-                *(uint2 *)(sm.v + (kq * 4 + r) * Sm::RS + dq4 * 4) = vreg[u][r];
-            }
-            uint2 t4[4];
-            transpose4(kreg[u], t4);
-#pragma unroll
-            for (int e = 0; e < 4; e++) *(uint2 *)(sm.kt + (dq4 * 4 + e) * Sm::TS + kq * 4) = t4[e];
+        for (int u = 0; u < NCH; u++) {
+            const int r = crow + u * RSTEP;
+            sm.k[r * (RS / 8) + ccol] = kreg[u];
+            sm.kt[r * (TS / 8) + ccol] = kreg[u];
+            sm.v[r * (RS / 8) + ccol] = vreg[u];
         }
     };
+    const uint16_t *sk = (const uint16_t *)sm.k, *sv = (const uint16_t *)sm.v;
+    const uint16_t *skt = (const uint16_t *)sm.kt;
 
     if (kv_lo < kv_hi) load_tile(kv_lo);
-    for (int64_t j0 = kv_lo; j0 < kv_hi; j0 += kDqN) {
+    for (int32_t j0 = kv_lo; j0 < kv_hi; j0 += kDqN) {
         __syncthreads();
         store_tile();
         __syncthreads();
         if (j0 + kDqN < kv_hi) load_tile(j0 + kDqN);
-        const bool masked = pad || j0 < full_lo || j0 + kDqN > full_hi;
+        const bool masked = PAD || j0 < full_lo || j0 + kDqN > full_hi;
         Frag8 df[2][2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             f32x16_t s, dp;
 #pragma unroll
             for (int i = 0; i < 16; i++) s[i] = dp[i] = 0.f;
-            const uint16_t *ka = sm.k + (t * 32 + col) * Sm::RS + half * 8;
-            const uint16_t *va = sm.v + (t * 32 + col) * Sm::RS + half * 8;
+            const uint16_t *ka = sk + (t * 32 + col) * RS + half * 8;
+            const uint16_t *va = sv + (t * 32 + col) * RS + half * 8;
 #pragma unroll
             for (int st = 0; st < KSTEPS; st++) {
                 Frag8 a;
@@ -532,10 +503,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int i = 8 * u + e;
-                    float p = exp2f(s[i] * c2 - lse2);
+                    float p = fast_exp2(fmaf(s[i], c2, nlse));
                     if (masked) {
-                        const int64_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                        const bool vis = j >= lo && j < hi && (!pad || !pad[j]);
+                        const int32_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                        bool vis = j >= lo && j < hi;
+                        if constexpr (PAD) vis = vis && !pad[j];
                         p = vis ? p : 0.f;
                     }
                     ds[e] = p * (dp[i] - dl);
@@ -544,21 +516,16 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
                                         pack2<DT>(ds[4], ds[5]), pack2<DT>(ds[6], ds[7]));
             }
         }
-        // dQ^T += K^T dS^T
+        // dQ^T += K^T dS^T: A = K^T by transposed reads of the row-major K tile
 #pragma unroll
-        for (int dt = 0; dt < DT32; dt++) {
-            const uint16_t *kr = sm.kt + (dt * 32 + col) * Sm::TS + half * 4;
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int u = 0; u < 2; u++)
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const uint16_t *p0 = kr + t * 32 + u * 16;
-                    const uint2 lo4 = *(const uint2 *)(p0), hi4 = *(const uint2 *)(p0 + 8);
-                    Frag8 a;
-                    a.u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                for (int dt = 0; dt < DT32; dt++) {
+                    const Frag8 a = lds_tr_frag(skt, TS, t * 32 + u * 16, dt * 32, lane);
                     acc[dt] = mfma32<DT>(a, df[t][u], acc[dt]);
                 }
-        }
     }
     if (!qvalid) return;
     uint16_t *op = dq + ((b * Tq + qi) * Hq + h) * D;
@@ -580,7 +547,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 
 bool mfma_bwd_takes(const dm_attention_desc *d) {
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) && (d->d == 64 || d->d == 128) &&
-           d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f;
+           d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
+           d->tk * d->hkv * d->d * 2 < (1ll << 31) && d->tq * d->hq * d->d * 2 < (1ll << 31);
 }
 
 size_t mfma_bwd_workspace(const dm_attention_desc *d) {
@@ -606,11 +574,21 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, oo, gg, lse, \
                                                                    delta, w);                  \
     bwd_tiles<<<(unsigned)(d->b * ntiles64), 64, 0, st>>>(d->b, d->tq, w);                     \
-    bwd_dkdv<DT, DD><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, kk,   \
-                                                      vv, gg, delta, w, (uint16_t *)dk,        \
-                                                      (uint16_t *)dv);                         \
-    bwd_dq<DT, DD><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, kk, vv,  \
-                                                   gg, delta, w, (uint16_t *)dq)
+    if (m.pad) {                                                                               \
+        bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
+                                                                qq, kk, vv, gg, delta, w,      \
+                                                                (uint16_t *)dk, (uint16_t *)dv); \
+        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq,  \
+                                                             kk, vv, gg, delta, w,             \
+                                                             (uint16_t *)dq);                  \
+    } else {                                                                                   \
+        bwd_dkdv<DT, DD, false><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
+                                                                 qq, kk, vv, gg, delta, w,     \
+                                                                 (uint16_t *)dk, (uint16_t *)dv); \
+        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
+                                                              kk, vv, gg, delta, w,            \
+                                                              (uint16_t *)dq);                 \
+    }
     if (d->dtype == DM_BF16) {
         if (d->d == 64) { BWD(DM_BF16, 64); } else { BWD(DM_BF16, 128); }
     } else {

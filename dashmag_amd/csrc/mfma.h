@@ -10,7 +10,7 @@
 //   D: lane l holds col (l % 16), rows 4 * (l / 16) + i, i in [0, 4)
 // Which hardware k a lane's slot is does not matter to a product as long as A and B agree; the
 // kernels use that freedom to feed a product's output fragment back in as the next one's operand.
-// tests/test_gpu_mfma.py checks these layouts on the device.
+// The attention and gated-delta-rule parity tests check these layouts on the device.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -60,23 +60,53 @@ __device__ __forceinline__ f32x4_t mfma16(const Frag8 &a, const Frag8 &b, const 
     }
 }
 
-// f32 -> 16-bit bits (bf16 round to nearest even, or f16), two at a time.
+// f32 -> 16-bit bits, two at a time: v_cvt_pk_bf16_f32 (round to nearest even) or
+// v_cvt_pk_f16_f32.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    f32x2_t x = {a, b};
+    uint32_t u;
     if constexpr (DT == DM_BF16) {
-        uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
-        ua += 0x7fffu + ((ua >> 16) & 1u);
-        ub += 0x7fffu + ((ub >> 16) & 1u);
-        return (ua >> 16) | (ub & 0xffff0000u);
+        bf16x2_t y = __builtin_convertvector(x, bf16x2_t);
+        __builtin_memcpy(&u, &y, 4);
     } else {
-        union {
-            _Float16 h[2];
-            uint32_t u;
-        } c;
-        c.h[0] = (_Float16)a;
-        c.h[1] = (_Float16)b;
-        return c.u;
+        f16x2_t y = __builtin_convertvector(x, f16x2_t);
+        __builtin_memcpy(&u, &y, 4);
     }
+    return u;
+}
+
+// 2^x on v_exp_f32 directly (the arguments here are finite or -inf; no range reduction).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// The transposed operand of a 32x32x16 product from a row-major LDS tile (rows = the product's
+// k, 16-bit elements along the other index), by two ds_read_b64_tr_b16. ds_read_b64_tr_b16 hands
+// lane i of each 16-lane group element i % 4 of the 8-byte row that lane 4 e + i / 4 of the group
+// addressed, in slot e. With the rows addressed below, lane l receives, for index c = l % 32 of
+// the operand's 32 rows/columns, the tile's elements (k0 + 8 j + 4 (l / 32) + e, c0 + c) for
+// e in [0, 4) in slots 4 j + e: the k order the 32x32 products' output layout has, so a product's
+// output fragment can be the other operand.
+//   tile: LDS base of the row-major tile, stride: its row stride in elements.
+__device__ __forceinline__ Frag8 lds_tr_frag(const uint16_t *tile, int stride, int k0, int c0,
+                                             int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int row = k0 + 4 * (g >> 1) + (i >> 2);
+    const int colx = c0 + 16 * (g & 1) + 4 * (i & 3);
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    const uint16_t *p0 = tile + row * stride + colx;
+    const uint16_t *p1 = p0 + 8 * stride;
+    s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0));
+    s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p1));
+    Frag8 f;
+    __builtin_memcpy(&f.u.x, &a, 8);
+    __builtin_memcpy(&f.u.z, &b, 8);
+    return f;
 }
 
 template <int DT>
@@ -105,6 +135,17 @@ __device__ __forceinline__ float unpack_hi(uint32_t w) {
         c.u = w;
         return (float)c.h[1];
     }
+}
+
+// Raw buffer loads: out-of-range offsets (>= the resource's byte count) return zeros, so tile
+// loads need no bounds branches. The offsets are 32-bit byte offsets from the resource's base.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(x[0], x[1], x[2], x[3]);
 }
 
 // Linear block index remapped so that consecutive logical work items land on one XCD (block
