@@ -712,13 +712,17 @@ GdrArgs gdr_args(const dm_gdr_desc *d, const void *q, const void *k, const void 
     return a;
 }
 
-int launch_gdr_plan(const dm_gdr_desc *d, GdrWs &w, hipStream_t st) {
+int launch_plan(const dm_gdr_desc *d, int32_t *seq_chunk0, int32_t *chunk_seq,
+                int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st) {
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
-    const int64_t T = d->cu_seqlens ? d->t : d->t;
-    gdr_plan<<<1, 256, 0, st>>>(S, T, nc, d->cu_seqlens, w.seq_chunk0, w.chunk_seq,
-                                w.chunk_tok0, w.chunk_len);
+    gdr_plan<<<1, 256, 0, st>>>(S, d->t, nc, d->cu_seqlens, seq_chunk0, chunk_seq, chunk_tok0,
+                                chunk_len);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule: plan");
     return DM_OK;
+}
+
+int launch_gdr_plan(const dm_gdr_desc *d, GdrWs &w, hipStream_t st) {
+    return launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st);
 }
 
 }  // namespace dm

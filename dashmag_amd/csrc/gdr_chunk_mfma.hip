@@ -1,14 +1,670 @@
-// MFMA chunked gated delta rule forward (placeholder until the gfx950 kernels land).
+// The chunked gated delta rule forward on gfx950 MFMA: bf16/f16 inputs, Dk = Dv = 128, f32 state
+// and accumulation, the intermediates that only feed products rounded to the inputs' dtype (W, U,
+// T, S, V' and Q K^T o decay, as fla's and the reference's tensor-core kernels round them,
+// crates/dash-ops/src/gated_delta/chunk/cube/tc.rs:1-12).
+//
+//   gdr_mfma_prep    per (chunk, head), parallel: G = cumsum g; K K^T and Q K^T (MFMA); A and
+//                    T = (I + A)^-1 in f32 by 16 x 16 blocks (each diagonal block by column
+//                    forward substitution, the rest by block forward substitution); W = T (beta
+//                    gamma K), U = T (beta V) (MFMA); Aqk = scale (Q K^T o decay).
+//   gdr_mfma_state   per (sequence, head), serial over the sequence's chunks: the state S lives
+//                    in registers in the 32x32 products' output layout, which is also the
+//                    operand layout of the next product, so it never leaves the wavefronts;
+//                    V' = U - W S; S <- exp(G_last) S + K^T (lam V'); S and V' are stored as
+//                    ready-made operand fragments for the output kernel.
+//   gdr_mfma_output  per (chunk, head), parallel: O^T = scale gamma (S^T Q^T) + V'^T Aqk^T.
+// Notation as chunk/reference.rs:11-18 (Q scaled, G_last the chunk's last cumulative gate).
+#include <string>
+#include <type_traits>
+
+#include "attention_kernels.h"
 #include "gdr_common.h"
+#include "mfma.h"
 
 namespace dm {
 
-bool gdr_mfma_takes(const dm_gdr_desc *d) { (void)d; return false; }
-size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { (void)d; return 0; }
-int launch_gdr_mfma_fwd(const dm_gdr_desc *, const void *, const void *, const void *,
-                        const void *, const void *, const float *, void *, float *, void *,
-                        hipStream_t) {
-    return refuse("chunk_gated_delta_rule: no MFMA kernel");
+constexpr int kD = 128;         // Dk = Dv of this kernel set
+constexpr int kC = kChunk;      // 64 tokens
+constexpr int kRowS = kD + 8;   // row stride read by ds_read_b128 rows
+constexpr int kRowB = kD + 4;   // row stride read by ds_read_b64 rows (32 rows per half wave)
+constexpr int kTrS = kD + 32;   // row stride read by ds_read_b64_tr_b16
+
+struct MfmaWs {
+    int32_t *seq_chunk0, *chunk_seq, *chunk_tok0, *chunk_len;
+    float *G;          // [ch][64]
+    uint16_t *W, *U;   // [ch][64][128] row-major
+    uint16_t *Aqk;     // [ch][64][64] row-major, scale included
+    uint16_t *Sf;      // [ch][4 dv tiles][8 dk steps][64 lanes][8]: S entering the chunk
+    uint16_t *Vf;      // [ch][4 dv tiles][4 token steps][64 lanes][8]: V'
+    uint16_t *Qn, *Kn; // [ch][64][128] normalised queries and keys (with the l2 normalisation)
+};
+
+static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w) {
+    const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d), ch = nc * d->h;
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> char * {
+        char *p = base ? base + off : nullptr;
+        off += align_up(bytes);
+        return p;
+    };
+    MfmaWs x{};
+    x.seq_chunk0 = (int32_t *)take((S + 1) * 4);
+    x.chunk_seq = (int32_t *)take(nc * 4);
+    x.chunk_tok0 = (int32_t *)take(nc * 4);
+    x.chunk_len = (int32_t *)take(nc * 4);
+    x.G = (float *)take(ch * kC * 4);
+    x.W = (uint16_t *)take(ch * kC * kD * 2);
+    x.U = (uint16_t *)take(ch * kC * kD * 2);
+    x.Aqk = (uint16_t *)take(ch * kC * kC * 2);
+    x.Sf = (uint16_t *)take(ch * kD * kD * 2);
+    x.Vf = (uint16_t *)take(ch * kC * kD * 2);
+    if (d->qk_l2norm) {
+        x.Qn = (uint16_t *)take(ch * kC * kD * 2);
+        x.Kn = (uint16_t *)take(ch * kC * kD * 2);
+    }
+    if (w) *w = x;
+    return off;
+}
+
+// ------------------------------------------------------------------------------------------
+// Prep
+// ------------------------------------------------------------------------------------------
+
+// 73.6 KB: two workgroups per CU. The query tile's space later holds T, and the key tile's the
+// block products; both then stage the W and U rows for coalesced stores. One buffer holds
+// beta gamma K for W, then beta V for U.
+struct PrepSmem {
+    uint4 k[kC * kRowS / 8];  // keys, rows; later block products; later W rows
+    uint4 q[kC * kRowS / 8];  // queries, rows; later T (f32); later U rows
+    uint4 x[kC * kTrS / 8];   // beta gamma K, then beta V: rows read transposed
+    float a[kC][kC + 4];      // A (strictly lower), f32, 16-byte aligned rows
+    float g[kC], gam[kC], bet[kC];
+};
+static_assert(sizeof(float) * kC * (kC + 4) <= sizeof(uint4) * kC * kRowS / 8, "T in q");
+static_assert(sizeof(float) * 3 * 16 * 20 <= sizeof(uint4) * kC * kRowS / 8, "M in k");
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
+    __shared__ PrepSmem sm;
+    const int64_t ch = blockIdx.x, n = ch / a.H, h = ch % a.H;
+    const int len = w.chunk_len[n];
+    if (len == 0) return;
+    const int64_t tok0 = w.chunk_tok0[n];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    uint16_t *ks = (uint16_t *)sm.k, *qs = (uint16_t *)sm.q, *xs = (uint16_t *)sm.x;
+    float(*tt)[kC + 4] = (float(*)[kC + 4])sm.q;  // T, in the query tile's space
+    float(*mm)[16][20] = (float(*)[16][20])sm.k;  // block products, in the key tile's
+
+    // gates; the values, in registers until U (16 lanes per row, 4 rows per thread)
+    if (tid < kC) {
+        const bool ok = tid < len;
+        sm.g[tid] = ok ? ld_any(a.g_dt, a.g, (tok0 + tid) * a.H + h) : 0.f;
+        sm.bet[tid] = ok ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
+    }
+    uint4 vreg[4];
+    {
+        const uint16_t *vin = (const uint16_t *)a.v;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
+            vreg[u] = r < len ? *(const uint4 *)(vin + ((tok0 + r) * a.H + h) * kD + c * 8)
+                              : make_uint4(0, 0, 0, 0);
+        }
+    }
+    // queries and keys: 16 lanes per row, zero past the chunk's tokens; normalised in f32 and
+    // rounded back to the dtype when asked
+    const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k;
+    for (int r = tid / 16; r < kC; r += 16) {
+        const int c = tid % 16;
+        const bool ok = r < len;
+        const int64_t off = ((tok0 + r) * a.H + h) * kD + c * 8;
+        uint4 qv = ok ? *(const uint4 *)(qin + off) : make_uint4(0, 0, 0, 0);
+        uint4 kv = ok ? *(const uint4 *)(kin + off) : make_uint4(0, 0, 0, 0);
+        if (a.l2norm) {
+            float qf[8], kf[8];
+            const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, kw[4] = {kv.x, kv.y, kv.z, kv.w};
+            float sq = 0.f, sk = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                qf[2 * e] = unpack_lo<DT>(qw[e]);
+                qf[2 * e + 1] = unpack_hi<DT>(qw[e]);
+                kf[2 * e] = unpack_lo<DT>(kw[e]);
+                kf[2 * e + 1] = unpack_hi<DT>(kw[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                sq += qf[e] * qf[e];
+                sk += kf[e] * kf[e];
+            }
+#pragma unroll
+            for (int o = 8; o >= 1; o >>= 1) {
+                sq += __shfl_xor(sq, o, 64);
+                sk += __shfl_xor(sk, o, 64);
+            }
+            const float qi = 1.f / sqrtf(sq + 1e-6f), ki = 1.f / sqrtf(sk + 1e-6f);
+            qv = make_uint4(pack2<DT>(qf[0] * qi, qf[1] * qi), pack2<DT>(qf[2] * qi, qf[3] * qi),
+                            pack2<DT>(qf[4] * qi, qf[5] * qi), pack2<DT>(qf[6] * qi, qf[7] * qi));
+            kv = make_uint4(pack2<DT>(kf[0] * ki, kf[1] * ki), pack2<DT>(kf[2] * ki, kf[3] * ki),
+                            pack2<DT>(kf[4] * ki, kf[5] * ki), pack2<DT>(kf[6] * ki, kf[7] * ki));
+            *(uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8) = qv;
+            *(uint4 *)(w.Kn + (ch * kC + r) * kD + c * 8) = kv;
+        }
+        sm.q[r * (kRowS / 8) + c] = qv;
+        sm.k[r * (kRowS / 8) + c] = kv;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // G = cumsum(g) by an inclusive scan across the wavefront (one token per lane)
+        float x = sm.g[lane];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        sm.g[lane] = x;
+        sm.gam[lane] = __expf(x);
+        w.G[ch * kC + lane] = x;
+    }
+    __syncthreads();
+    // beta gamma K rows for the transposed reads of W's product
+    for (int xx = tid; xx < kC * 16; xx += 256) {
+        const int r = xx / 16, c = xx % 16;
+        const uint4 kv = sm.k[r * (kRowS / 8) + c];
+        const float fk = sm.bet[r] * sm.gam[r];
+        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+        uint32_t ko[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            ko[e] = pack2<DT>(unpack_lo<DT>(kw[e]) * fk, unpack_hi<DT>(kw[e]) * fk);
+        sm.x[r * (kTrS / 8) + c] = make_uint4(ko[0], ko[1], ko[2], ko[3]);
+    }
+
+    // K K^T and Q K^T on the lower tiles (0,0), (1,0), (1,1) (waves 0-2); A = beta (K K^T) o
+    // decay strictly below the diagonal, Aqk = scale (Q K^T) o decay on and below it. Output
+    // element i of tile (ti, tj): row 32 ti + 8 (i / 4) + 4 h + i % 4, column 32 tj + col.
+    uint16_t *aq_out = w.Aqk + ch * kC * kC;
+    if (wave < 3) {
+        const int ti = wave == 0 ? 0 : 1, tj = wave == 2 ? 1 : 0;
+        f32x16_t kk, qk;
+#pragma unroll
+        for (int i = 0; i < 16; i++) kk[i] = qk[i] = 0.f;
+#pragma unroll
+        for (int st = 0; st < kD / 16; st++) {
+            Frag8 ak, aq, bk;
+            ak.u = *(const uint4 *)(ks + (ti * 32 + col) * kRowS + half * 8 + st * 16);
+            aq.u = *(const uint4 *)(qs + (ti * 32 + col) * kRowS + half * 8 + st * 16);
+            bk.u = *(const uint4 *)(ks + (tj * 32 + col) * kRowS + half * 8 + st * 16);
+            kk = mfma32<DT>(ak, bk, kk);
+            qk = mfma32<DT>(aq, bk, qk);
+        }
+        const int j = tj * 32 + col;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+            // masked before the exponential (above the diagonal G_i - G_j > 0)
+            const float dec = r >= j ? __expf(sm.g[r] - sm.g[j]) : 0.f;
+            sm.a[r][j] = r > j ? sm.bet[r] * kk[i] * dec : 0.f;
+            const uint32_t p2 = pack2<DT>(r >= j ? qk[i] * dec * a.scale : 0.f, 0.f);
+            aq_out[r * kC + j] = (uint16_t)(p2 & 0xffffu);
+        }
+    } else {
+        for (int xx = lane; xx < 32 * 32; xx += 64) {
+            const int r = xx / 32, j = 32 + xx % 32;
+            sm.a[r][j] = 0.f;
+            aq_out[r * kC + j] = 0;
+        }
+    }
+    __syncthreads();  // the query and key tiles are dead from here
+
+    // T = (I + A)^-1 by 16 x 16 blocks. Diagonal block b (wave b), row by row, lane c holding
+    // column c in registers: T[i][c] = [i == c] - sum_{x < i} A[i][x] T[x][c] (rows of A read
+    // as broadcasts; T[x][c] = 0 for x < c makes the sum start at c).
+    {
+        const int b = wave, c = lane & 15;
+        float tc[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float s = 0.f;
+#pragma unroll
+            for (int x4 = 0; x4 < i; x4 += 4) {
+                const float4 a4 = *(const float4 *)&sm.a[16 * b + i][16 * b + x4];
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (x4 + e < i) s += av[e] * tc[x4 + e];
+            }
+            tc[i] = (i == c ? 1.f : 0.f) - s;
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) tt[16 * b + i][16 * b + c] = tc[i];
+        }
+        // the strictly upper blocks of T are zero
+        for (int xx = lane; xx < 256; xx += 64) {
+            const int r = xx / 16, cc = xx % 16;
+            for (int bj = b + 1; bj < 4; bj++) tt[16 * b + r][16 * bj + cc] = 0.f;
+        }
+    }
+    __syncthreads();
+    // Off-diagonal blocks, one block diagonal (lev = i - j) at a time, wave j taking block
+    // (j + lev, j): M = sum_{k = j}^{i - 1} A_ik T_kj, then T_ij = -T_ii M. Lane: column
+    // cc = lane % 16 and rows 4 (lane / 16) + e.
+    {
+        const int cc = lane & 15, r0 = 4 * (lane >> 4);
+        auto level = [&](auto levc) {
+            constexpr int lev = decltype(levc)::value;
+            const int bj = wave, bi = wave + lev;
+            if (wave < 4 - lev) {
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < lev; kk++) {
+                    const int kb_ = bj + kk;
+                    float tcol[16];
+#pragma unroll
+                    for (int y = 0; y < 16; y++) tcol[y] = tt[16 * kb_ + y][16 * bj + cc];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+#pragma unroll
+                        for (int y4 = 0; y4 < 16; y4 += 4) {
+                            const float4 a4 = *(const float4 *)&sm.a[16 * bi + r0 + e][16 * kb_ + y4];
+                            acc[e] += a4.x * tcol[y4] + a4.y * tcol[y4 + 1] + a4.z * tcol[y4 + 2] +
+                                      a4.w * tcol[y4 + 3];
+                        }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) mm[wave][r0 + e][cc] = acc[e];
+            }
+            __syncthreads();
+            if (wave < 4 - lev) {
+                float mcol[16];
+#pragma unroll
+                for (int y = 0; y < 16; y++) mcol[y] = mm[wave][y][cc];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int y4 = 0; y4 < 16; y4 += 4) {
+                        const float4 t4 = *(const float4 *)&tt[16 * bi + r0 + e][16 * bi + y4];
+                        s += t4.x * mcol[y4] + t4.y * mcol[y4 + 1] + t4.z * mcol[y4 + 2] +
+                             t4.w * mcol[y4 + 3];
+                    }
+                    tt[16 * bi + r0 + e][16 * bj + cc] = -s;
+                }
+            }
+            __syncthreads();
+        };
+        level(std::integral_constant<int, 1>{});
+        level(std::integral_constant<int, 2>{});
+        level(std::integral_constant<int, 3>{});
+    }
+
+    // W = T (beta gamma K), then U = T (beta V): 8 output tiles each (2 token rows x 4 columns
+    // of 32), wave w taking column tile w. A = T rows (f32 -> dtype) with k slots
+    // 16 st + 8 j + 4 h + e, B = the scaled rows read transposed (k = token, col = column).
+    auto product = [&](f32x16_t *res) {
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) res[ti][i] = 0.f;
+#pragma unroll
+            for (int st = 0; st < kC / 16; st++) {
+                Frag8 at;
+                const float *tr = &tt[ti * 32 + col][st * 16 + half * 4];
+                at.u = make_uint4(pack2<DT>(tr[0], tr[1]), pack2<DT>(tr[2], tr[3]),
+                                  pack2<DT>(tr[8], tr[9]), pack2<DT>(tr[10], tr[11]));
+                const Frag8 bx = lds_tr_frag(xs, kTrS, st * 16, wave * 32, lane);
+                res[ti] = mfma32<DT>(at, bx, res[ti]);
+            }
+        }
+    };
+    f32x16_t wt[2], ut[2];
+    product(wt);
+    __syncthreads();
+    // beta V rows in the same buffer
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
+        const float fv = sm.bet[r];
+        const uint32_t vw[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+        uint32_t vo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            vo[e] = pack2<DT>(unpack_lo<DT>(vw[e]) * fv, unpack_hi<DT>(vw[e]) * fv);
+        sm.x[r * (kTrS / 8) + c] = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+    }
+    __syncthreads();
+    product(ut);
+    __syncthreads();
+    // stage W and U as rows (element i: row 32 ti + 8 (i / 4) + 4 h + i % 4, column
+    // 32 wave + col), then store whole rows
+    {
+        uint16_t *wrows = (uint16_t *)sm.k, *urows = (uint16_t *)sm.q;
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                const uint32_t p2 = pack2<DT>(wt[ti][i], ut[ti][i]);
+                wrows[r * kRowS + wave * 32 + col] = (uint16_t)(p2 & 0xffffu);
+                urows[r * kRowS + wave * 32 + col] = (uint16_t)(p2 >> 16);
+            }
+        __syncthreads();
+        uint16_t *Wout = w.W + ch * kC * kD, *Uout = w.U + ch * kC * kD;
+        for (int xx = tid; xx < kC * 16; xx += 256) {
+            const int r = xx / 16, c = xx % 16;
+            *(uint4 *)(Wout + r * kD + c * 8) = sm.k[r * (kRowS / 8) + c];
+            *(uint4 *)(Uout + r * kD + c * 8) = sm.q[r * (kRowS / 8) + c];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// State pass
+// ------------------------------------------------------------------------------------------
+
+struct StateSmem {
+    uint4 w[kC * kRowB / 8 + 1];  // W rows (8-byte reads), +1: kRowB is not a multiple of 8
+    uint4 k[kC * kTrS / 8];       // K rows read transposed
+    uint4 u[kC * kTrS / 8];       // U rows read transposed
+    float g[kC];
+};
+
+// One workgroup of 4 wavefronts per (sequence, head); wavefront w owns state columns
+// [32 w, 32 w + 32) over all 128 rows: 4 output tiles of 32 x 32 in f32.
+template <int DT>
+__global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, const float *h0,
+                                                         float *final_state) {
+    __shared__ StateSmem sm;
+    const int64_t sh = blockIdx.x, s = sh / a.H, h = sh % a.H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
+    const int dv = wave * 32 + col;  // this lane's state column
+    uint16_t *ws_ = (uint16_t *)sm.w, *kss = (uint16_t *)sm.k, *uss = (uint16_t *)sm.u;
+    const int64_t seq_t0 = c0 < c1 ? w.chunk_tok0[c0] : 0;
+    const int64_t seq_end = c0 < c1 ? (int64_t)w.chunk_tok0[c1 - 1] + w.chunk_len[c1 - 1] : 0;
+
+    // S: tile r holds rows 32 r + 8 (i / 4) + 4 h + i % 4 of column dv
+    f32x16_t S[4];
+    {
+        const float *src = h0 ? h0 + sh * kD * kD : nullptr;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                S[r][i] = src ? src[row * kD + dv] : 0.f;
+            }
+    }
+    // staging of a chunk's W, U and K (rows of 16 16-byte chunks), two chunks ahead: set A for
+    // even steps, set B for odd ones
+    auto load = [&](int c, uint4 *r_, float &g_) {
+        const int64_t ch = (int64_t)c * a.H + h;
+        const uint16_t *W = w.W + ch * kC * kD, *U = w.U + ch * kC * kD;
+        if (tid < kC) g_ = w.G[ch * kC + tid];
+        // a sequence's chunks are consecutive, kC tokens apart
+        const int64_t tok0 = seq_t0 + (int64_t)(c - c0) * kC;
+        const int len = (int)min((int64_t)kC, seq_end - tok0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int x = tid + 256 * u, r = x / 16, cc = x % 16;
+            r_[u] = *(const uint4 *)(W + r * kD + cc * 8);
+            r_[4 + u] = *(const uint4 *)(U + r * kD + cc * 8);
+            // keys: the normalised chunk-major copy, or the inputs' rows
+            if (a.l2norm)
+                r_[8 + u] = *(const uint4 *)(w.Kn + (ch * kC + r) * kD + cc * 8);
+            else
+                r_[8 + u] = r < len ? *(const uint4 *)((const uint16_t *)a.k +
+                                                       ((tok0 + r) * a.H + h) * kD + cc * 8)
+                                    : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](const uint4 *r_, float g_) {
+        if (tid < kC) sm.g[tid] = g_;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int x = tid + 256 * u, r = x / 16, cc = x % 16;
+            uint2 *wp = (uint2 *)(ws_ + r * kRowB + cc * 8);
+            wp[0] = make_uint2(r_[u].x, r_[u].y);
+            wp[1] = make_uint2(r_[u].z, r_[u].w);
+            sm.u[r * (kTrS / 8) + cc] = r_[4 + u];
+            sm.k[r * (kTrS / 8) + cc] = r_[8 + u];
+        }
+    };
+    auto step = [&](int c, uint4 *r_, float &g_) {
+        const int64_t ch = (int64_t)c * a.H + h;
+        __syncthreads();
+        store(r_, g_);
+        __syncthreads();
+        if (c + 2 < c1) load(c + 2, r_, g_);
+
+        // S as operand fragments (k = state row, col = dv), in the dtype; also stored for the
+        // output kernel in fragment order [dv tile][k step][lane]
+        Frag8 sf[8];
+        uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const int r = st / 2, u = st % 2;
+            sf[st].u = make_uint4(pack2<DT>(S[r][8 * u + 0], S[r][8 * u + 1]),
+                                  pack2<DT>(S[r][8 * u + 2], S[r][8 * u + 3]),
+                                  pack2<DT>(S[r][8 * u + 4], S[r][8 * u + 5]),
+                                  pack2<DT>(S[r][8 * u + 6], S[r][8 * u + 7]));
+            *(uint4 *)(sfo + (st * 64 + lane) * 8) = sf[st].u;
+        }
+        // V' = U - W S: 2 token tiles; A = W rows (k slots in the fragments' state-row order:
+        // 16 st + 8 j + 4 h + e), B = S fragments
+        f32x16_t vp[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) vp[t][i] = 0.f;
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint16_t *wrow = ws_ + (t * 32 + col) * kRowB + st * 16 + half * 4;
+                const uint2 lo4 = *(const uint2 *)(wrow), hi4 = *(const uint2 *)(wrow + 8);
+                Frag8 aw;
+                aw.u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                vp[t] = mfma32<DT>(aw, sf[st], vp[t]);
+            }
+        // U in the same layout by transposed reads of the U rows (token t 32 + 16 u + ...)
+        const float glast = sm.g[kC - 1];
+        Frag8 vlf[4];
+        uint16_t *vfo = w.Vf + ch * kC * kD + (size_t)wave * 4 * 64 * 8;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const Frag8 uf = lds_tr_frag(uss, kTrS, t * 32 + u * 16, wave * 32, lane);
+                const uint32_t uw[4] = {uf.u.x, uf.u.y, uf.u.z, uf.u.w};
+                float v8[8], l8[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int i = 8 * u + e;
+                    const float uu = (e & 1) ? unpack_hi<DT>(uw[e / 2]) : unpack_lo<DT>(uw[e / 2]);
+                    v8[e] = uu - vp[t][i];
+                    const int tok = t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                    l8[e] = v8[e] * __expf(glast - sm.g[tok]);
+                }
+                const int st = t * 2 + u;
+                const uint4 vf = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
+                                            pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
+                vlf[st].u = make_uint4(pack2<DT>(l8[0], l8[1]), pack2<DT>(l8[2], l8[3]),
+                                       pack2<DT>(l8[4], l8[5]), pack2<DT>(l8[6], l8[7]));
+                *(uint4 *)(vfo + (st * 64 + lane) * 8) = vf;
+            }
+        // S <- exp(G_last) S + K^T (lam V'): A = K^T by transposed reads of the K rows
+        const float gl = __expf(glast);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) S[r][i] *= gl;
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const Frag8 ak = lds_tr_frag(kss, kTrS, st * 16, r * 32, lane);
+                S[r] = mfma32<DT>(ak, vlf[st], S[r]);
+            }
+    };
+    uint4 ra[12], rb[12];
+    float ga = 0.f, gb = 0.f;
+    if (c0 < c1) load(c0, ra, ga);
+    if (c0 + 1 < c1) load(c0 + 1, rb, gb);
+    for (int c = c0; c < c1; c += 2) {
+        step(c, ra, ga);
+        if (c + 1 < c1) step(c + 1, rb, gb);
+    }
+    if (final_state) {
+        float *dst = final_state + sh * kD * kD;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                dst[row * kD + dv] = S[r][i];
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Output
+// ------------------------------------------------------------------------------------------
+
+// O^T = scale gamma (S^T Q^T) + V'^T Aqk^T per (chunk, head): 8 output tiles (4 of 32 state
+// columns x 2 of 32 tokens); wave w takes column tile w for both token tiles. A = S^T and V'^T
+// fragments as the state pass stored them (the operand layouts of A and B are the same); B = Q^T
+// and Aqk^T from rows (k slots 16 st + 8 j + 4 h + e). Each lane then holds one token's 4
+// consecutive columns per group: 8-byte stores along the output row.
+struct OutSmem {
+    uint4 q[kC * kRowB / 8 + 1];      // queries, rows (8-byte reads)
+    uint4 aq[kC * (kC + 4) / 8 + 1];  // Aqk, rows (8-byte reads)
+    float g[kC];
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void *out) {
+    __shared__ OutSmem sm;
+    const int64_t ch = blockIdx.x, n = ch / a.H, h = ch % a.H;
+    const int len = w.chunk_len[n];
+    if (len == 0) return;
+    const int64_t tok0 = w.chunk_tok0[n];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
+    const uint16_t *vfo = w.Vf + ch * kC * kD + (size_t)wave * 4 * 64 * 8;
+    const uint16_t *aqg = w.Aqk + ch * kC * kC;
+    uint16_t *qs = (uint16_t *)sm.q, *as = (uint16_t *)sm.aq;
+    constexpr int AS = kC + 4;
+    // the chunk's queries (the normalised chunk-major copy, or the inputs' rows) and Aqk
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        uint4 qv;
+        if (a.l2norm)
+            qv = *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8);
+        else
+            qv = r < len ? *(const uint4 *)((const uint16_t *)a.q + ((tok0 + r) * a.H + h) * kD + c * 8)
+                         : make_uint4(0, 0, 0, 0);
+        uint2 *qp = (uint2 *)(qs + r * kRowB + c * 8);
+        qp[0] = make_uint2(qv.x, qv.y);
+        qp[1] = make_uint2(qv.z, qv.w);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int x = tid + 256 * u, r = x / 8, c = x % 8;
+        const uint4 av = *(const uint4 *)(aqg + r * kC + c * 8);
+        uint2 *ap = (uint2 *)(as + r * AS + c * 8);
+        ap[0] = make_uint2(av.x, av.y);
+        ap[1] = make_uint2(av.z, av.w);
+    }
+    if (tid < kC) sm.g[tid] = w.G[ch * kC + tid];
+    Frag8 sf[8], vf[4];
+#pragma unroll
+    for (int st = 0; st < 8; st++) sf[st].u = *(const uint4 *)(sfo + (st * 64 + lane) * 8);
+#pragma unroll
+    for (int st = 0; st < 4; st++) vf[st].u = *(const uint4 *)(vfo + (st * 64 + lane) * 8);
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        const int tok = tt * 32 + col;  // this lane's token (column of O^T)
+        f32x16_t inter, intra;
+#pragma unroll
+        for (int i = 0; i < 16; i++) inter[i] = intra[i] = 0.f;
+        const uint16_t *qr = qs + tok * kRowB + half * 4;
+        const uint16_t *ar = as + tok * AS + half * 4;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            Frag8 bq;
+            const uint2 lo4 = *(const uint2 *)(qr + st * 16), hi4 = *(const uint2 *)(qr + st * 16 + 8);
+            bq.u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+            inter = mfma32<DT>(sf[st], bq, inter);
+            if (st < 4) {
+                Frag8 ba;
+                const uint2 l2 = *(const uint2 *)(ar + st * 16), h2 = *(const uint2 *)(ar + st * 16 + 8);
+                ba.u = make_uint4(l2.x, l2.y, h2.x, h2.y);
+                intra = mfma32<DT>(vf[st], ba, intra);
+            }
+        }
+        if (tok >= len) continue;
+        const float f = a.scale * __expf(sm.g[tok]);
+        uint16_t *op = (uint16_t *)out + ((tok0 + tok) * a.H + h) * kD + wave * 32;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            uint2 v2;
+            v2.x = pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]);
+            v2.y = pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]);
+            *(uint2 *)(op + g4 * 8 + half * 4) = v2;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------
+
+bool gdr_mfma_takes(const dm_gdr_desc *d) {
+    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk == kD && d->dv == kD;
+}
+
+size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { return mfma_layout(d, nullptr, nullptr); }
+
+int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
+                        const void *g, const void *beta, const float *h0, void *out,
+                        float *final_state, void *workspace, hipStream_t st) {
+    MfmaWs w;
+    mfma_layout(d, (char *)workspace, &w);
+    GdrArgs a;
+    a.H = d->h;
+    a.Dk = d->dk;
+    a.Dv = d->dv;
+    a.g_dt = d->g_dtype;
+    a.beta_dt = d->beta_dtype;
+    a.l2norm = d->qk_l2norm;
+    a.scale = d->has_scale ? d->scale : (float)(1.0 / std::sqrt((double)d->dk));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.g = g;
+    a.beta = beta;
+    const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
+    int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st);
+    if (rc) return rc;
+    const unsigned chunks = (unsigned)(nc * d->h), seqs = (unsigned)(S * d->h);
+    if (d->dtype == DM_BF16) {
+        if (chunks) gdr_mfma_prep<DM_BF16><<<chunks, 256, 0, st>>>(a, w);
+        gdr_mfma_state<DM_BF16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
+        if (chunks) gdr_mfma_output<DM_BF16><<<chunks, 256, 0, st>>>(a, w, out);
+    } else {
+        if (chunks) gdr_mfma_prep<DM_F16><<<chunks, 256, 0, st>>>(a, w);
+        gdr_mfma_state<DM_F16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
+        if (chunks) gdr_mfma_output<DM_F16><<<chunks, 256, 0, st>>>(a, w, out);
+    }
+    probe_add(DM_PROBE_GDR_CHUNK_FWD, 4);
+    DM_LAUNCH_CHECK("chunk_gated_delta_rule: MFMA launch");
+    return DM_OK;
 }
 
 }  // namespace dm

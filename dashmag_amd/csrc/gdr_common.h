@@ -22,6 +22,9 @@ struct GdrWs {
 };
 
 int check_gdr(const dm_gdr_desc *d, const char *op, bool step);
+// The chunk plan over the call's sequences (gdr_chunk.hip).
+int launch_plan(const dm_gdr_desc *d, int32_t *seq_chunk0, int32_t *chunk_seq,
+                int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st);
 int64_t gdr_nseq(const dm_gdr_desc *d);
 int64_t gdr_chunk_bound(const dm_gdr_desc *d);
 
