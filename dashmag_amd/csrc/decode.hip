@@ -11,10 +11,13 @@
 
 #include "attention_kernels.h"
 #include "dm_common.h"
+#include "mfma.h"
 
 namespace dm {
 
-constexpr int kDecodeSpan = 256;  // keys per workgroup (split)
+constexpr int kDecodeRows = 4;        // K/V rows each lane group loads per step
+constexpr int kDecodeMinSpan = 512;    // fewest keys a workgroup takes
+constexpr int kDecodeWorkgroups = 1024;  // the split count aims at about this many workgroups
 
 struct Bf16x8 {
     uint4 raw;
@@ -40,12 +43,53 @@ __device__ __forceinline__ void unpack8(const uint4 &r, float *x) {
     }
 }
 
+typedef __bf16 dec_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 dec_f16x2 __attribute__((ext_vector_type(2)));
+
+// The dot product of 8 16-bit pairs in f32: v_dot2_f32_bf16 / v_dot2_f32_f16.
+template <int DT>
+__device__ __forceinline__ float dot8(const uint4 &a, const uint4 &b) {
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+    float t = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if constexpr (DT == DM_BF16) {
+            dec_bf16x2 x, y;
+            __builtin_memcpy(&x, &aw[e], 4);
+            __builtin_memcpy(&y, &bw[e], 4);
+            t = __builtin_amdgcn_fdot2_f32_bf16(x, y, t, false);
+        } else {
+            dec_f16x2 x, y;
+            __builtin_memcpy(&x, &aw[e], 4);
+            __builtin_memcpy(&y, &bw[e], 4);
+            t = __builtin_amdgcn_fdot2(x, y, t, false);
+        }
+    }
+    return t;
+}
+
+// Sum over aligned groups of N lanes (N = 8, 16 or 32) by DPP moves within 16-lane rows: quad
+// swaps, then the half-row mirror (lane i with 7 - i) and the row mirror (lane i with 15 - i)
+// pair lanes from the other half each time, so every lane ends with its group's sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float t) {
+#define DM_DPP(x, ctrl) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xf, 0xf, false))
+    t += DM_DPP(t, 0xB1);   // quad_perm [1, 0, 3, 2]
+    t += DM_DPP(t, 0x4E);   // quad_perm [2, 3, 0, 1]
+    t += DM_DPP(t, 0x141);  // row_half_mirror
+    if constexpr (N >= 16) t += DM_DPP(t, 0x140);  // row_mirror
+#undef DM_DPP
+    if constexpr (N >= 32) t += __shfl_xor(t, 16, 64);
+    return t;
+}
+
 // One split of one (sequence, key-value head): keys [base + split * span, ...) of the keys the
 // sequence's query sees, [lo, hi). Writes part_o [B, Hq, nsplit, D] (normalised) and part_lse
 // [B, Hq, nsplit] (-inf for a split that sees nothing).
 template <int DT, int D, int G>
 __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64_t Hkv,
-                                                    int64_t left, float scale, int nsplit,
+                                                    int64_t left, float scale, int nsplit, int span,
                                                     const void *__restrict__ q,
                                                     const void *__restrict__ k,
                                                     const void *__restrict__ v,
@@ -55,10 +99,10 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
     constexpr int LPR = D / 8;       // lanes per K/V row
     constexpr int RPW = 64 / LPR;    // rows per wavefront per step
     constexpr int NW = 4;            // wavefronts
-    constexpr int GROUPS = RPW * NW; // independent partial states in the workgroup
     const int split = blockIdx.x, kh = blockIdx.y;
     const int64_t b = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane / LPR, seg = lane % LPR;
 
     int64_t len = lengths ? (int64_t)lengths[b] : S;
@@ -66,20 +110,18 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
     if (len < 0) len = 0;
     int64_t lo = left >= 0 ? len - 1 - left : 0;
     if (lo < 0) lo = 0;
-    const int64_t start = lo + (int64_t)split * kDecodeSpan;
-    int64_t end = start + kDecodeSpan;
+    const int64_t start = lo + (int64_t)split * span;
+    int64_t end = start + span;
     if (end > len) end = len;
 
-    // queries of the group, this lane's 8 elements, pre-scaled by scale * log2(e)
+    // queries of the group, this lane's 8 elements as 4 packed pairs (the dot products run on
+    // v_dot2_f32_{bf16,f16} with f32 accumulation); scale * log2(e) applied to the f32 sum
     const float qscale = scale * 1.4426950408889634f;
-    float qv[G][8];
+    uint4 qp[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const int64_t h = kh * G + g;
-        const uint4 raw = *(const uint4 *)((const char *)q + ((b * Hq + h) * D + seg * 8) * 2);
-        unpack8<DT>(raw, qv[g]);
-#pragma unroll
-        for (int e = 0; e < 8; e++) qv[g][e] *= qscale;
+        qp[g] = *(const uint4 *)((const char *)q + ((b * Hq + h) * D + seg * 8) * 2);
     }
 
     float mx[G], l[G], acc[G][8];
@@ -95,79 +137,112 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
     const char *kb = (const char *)k + (b * S * Hkv + kh) * D * 2 + seg * 16;
     const char *vb = (const char *)v + (b * S * Hkv + kh) * D * 2 + seg * 16;
 
-    for (int64_t j0 = start + wave * RPW; j0 < end; j0 += NW * RPW * 2) {
-        // two rows per lane group per step, loads issued before use
-        const int64_t ja = j0 + r, jb = j0 + NW * RPW + r;
-        const bool va = ja < end, vbv = jb < end;
-        uint4 ka = make_uint4(0, 0, 0, 0), vra = ka, kbr = ka, vrb = ka;
-        if (va) {
-            ka = *(const uint4 *)(kb + ja * row_stride);
-            vra = *(const uint4 *)(vb + ja * row_stride);
-        }
-        if (vbv) {
-            kbr = *(const uint4 *)(kb + jb * row_stride);
-            vrb = *(const uint4 *)(vb + jb * row_stride);
-        }
-        float kf[2][8], vf[2][8];
-        unpack8<DT>(ka, kf[0]);
-        unpack8<DT>(kbr, kf[1]);
-        unpack8<DT>(vra, vf[0]);
-        unpack8<DT>(vrb, vf[1]);
-        float s[2][G];
+    // each wavefront sweeps a contiguous quarter of the split, kDecodeRows rows per lane group
+    // per step; the next step's rows are loaded before this step's are used
+    constexpr int ROWS = kDecodeRows;
+    const int64_t per_wave = span / NW;
+    const int64_t w0 = start + wave * per_wave;
+    const int64_t w1 = min(w0 + per_wave, end);
+    uint4 kr[ROWS], vr[ROWS], kn[ROWS], vn[ROWS];
+    // rows past the wavefront's range load row w1 - 1 again (a visible row, so the loads need no
+    // branch and the compiler can keep the next step's loads in flight); their scores are -inf.
+    // Buffer loads from the wavefront's first row keep the two register sets' loads apart (plain
+    // loads of both sets get merged into one load at the loop head, which waits at once).
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb - seg * 16 + w0 * row_stride, 0xffffffffu);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb - seg * 16 + w0 * row_stride, 0xffffffffu);
+    auto load = [&](int64_t j0, uint4 *kk, uint4 *vv) {
 #pragma unroll
-        for (int u = 0; u < 2; u++)
+        for (int u = 0; u < ROWS; u++) {
+            const uint32_t off =
+                (uint32_t)((min(j0 + u * RPW + r, w1 - 1) - w0) * row_stride) + seg * 16;
+            kk[u] = buf_load16_nt(krs, off);
+            vv[u] = buf_load16_nt(vrs, off);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // issue the loads here, ahead of the math
+    };
+    auto consume = [&](int64_t j0, const uint4 *kk, const uint4 *vv) {
+        float s[ROWS][G];
+#pragma unroll
+        for (int u = 0; u < ROWS; u++) {
+            const bool ok = j0 + u * RPW + r < w1;
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                float t = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) t += qv[g][e] * kf[u][e];
-#pragma unroll
-                for (int o = LPR / 2; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
-                s[u][g] = t;
+                const float t = group_sum<LPR>(dot8<DT>(qp[g], kk[u]));
+                s[u][g] = ok ? t * qscale : -INFINITY;
             }
-        if (!va) {
-#pragma unroll
-            for (int g = 0; g < G; g++) s[0][g] = -INFINITY;
-        }
-        if (!vbv) {
-#pragma unroll
-            for (int g = 0; g < G; g++) s[1][g] = -INFINITY;
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float mn = fmaxf(mx[g], fmaxf(s[0][g], s[1][g]));
-            if (mn == -INFINITY) continue;
-            const float alpha = exp2f(mx[g] - mn);
-            const float p0 = exp2f(s[0][g] - mn), p1 = exp2f(s[1][g] - mn);
-            l[g] = l[g] * alpha + p0 + p1;
+            float mn = mx[g];
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] * alpha + p0 * vf[0][e] + p1 * vf[1][e];
+            for (int u = 0; u < ROWS; u++) mn = fmaxf(mn, s[u][g]);
+            // with nothing visible yet (mn = -inf) every factor below is exp2(-inf) = 0
+            const float ref = mn == -INFINITY ? 0.f : mn;
+            const float alpha = __builtin_amdgcn_exp2f(mx[g] - ref);
+            l[g] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] *= alpha;
+#pragma unroll
+            for (int u = 0; u < ROWS; u++) {
+                float vf[8];
+                unpack8<DT>(vv[u], vf);
+                const float p = __builtin_amdgcn_exp2f(s[u][g] - ref);
+                l[g] += p;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] += p * vf[e];
+            }
             mx[g] = mn;
         }
+    };
+    // two register sets in turn, so no copies wait on loads still in flight
+    constexpr int STEP = RPW * ROWS;
+    if (w0 < w1) load(w0, kr, vr);
+    for (int64_t j0 = w0; j0 < w1; j0 += 2 * STEP) {
+        load(j0 + STEP, kn, vn);
+        consume(j0, kr, vr);
+        if (j0 + STEP >= w1) break;
+        load(j0 + 2 * STEP, kr, vr);
+        consume(j0 + STEP, kn, vn);
     }
 
-    // Combine the GROUPS partial states through LDS: [GROUPS][G] (m, l), [GROUPS][G][D] acc.
-    __shared__ float sm_m[GROUPS][G], sm_l[GROUPS][G];
-    __shared__ float sm_acc[GROUPS][G][D];
-    const int grp = wave * RPW + r;
+    // Combine the RPW lane groups of each wavefront by shuffles, then the NW wavefronts through
+    // LDS: [NW][G] (m, l), [NW][G][D] acc.
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        if (seg == 0) {
-            sm_m[grp][g] = mx[g];
-            sm_l[grp][g] = l[g];
-        }
 #pragma unroll
-        for (int e = 0; e < 8; e++) sm_acc[grp][g][seg * 8 + e] = acc[g][e];
+        for (int o = LPR; o < 64; o <<= 1) {
+            const float mo = __shfl_xor(mx[g], o, 64);
+            const float M = fmaxf(mx[g], mo);
+            const float wa = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx[g] - M);
+            const float wb = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - M);
+            l[g] = l[g] * wa + __shfl_xor(l[g], o, 64) * wb;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] * wa + __shfl_xor(acc[g][e], o, 64) * wb;
+            mx[g] = M;
+        }
+    }
+    __shared__ float sm_m[NW][G], sm_l[NW][G];
+    __shared__ float sm_acc[NW][G][D];
+    if (r == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (seg == 0) {
+                sm_m[wave][g] = mx[g];
+                sm_l[wave][g] = l[g];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) sm_acc[wave][g][seg * 8 + e] = acc[g][e];
+        }
     }
     __syncthreads();
     for (int x = threadIdx.x; x < G * D; x += 256) {
         const int g = x / D, d = x % D;
         float M = -INFINITY;
-        for (int t = 0; t < GROUPS; t++) M = fmaxf(M, sm_m[t][g]);
+        for (int t = 0; t < NW; t++) M = fmaxf(M, sm_m[t][g]);
         float L = 0.f, A = 0.f;
         if (M != -INFINITY) {
-            for (int t = 0; t < GROUPS; t++) {
-                const float w = exp2f(sm_m[t][g] - M);
+            for (int t = 0; t < NW; t++) {
+                const float w = __builtin_amdgcn_exp2f(sm_m[t][g] - M);
                 L += sm_l[t][g] * w;
                 A += sm_acc[t][g][d] * w;
             }
@@ -262,8 +337,19 @@ static bool split_takes(const dm_attention_desc *d) {
            (d->d == 64 || d->d == 128 || d->d == 256) && (g == 1 || g == 2 || g == 4 || g == 8);
 }
 
+// Keys per split: the smallest power of two from kDecodeMinSpan up that keeps the grid within
+// about kDecodeWorkgroups workgroups (long streams per workgroup keep the loads in flight; a
+// small batch still gets enough workgroups to cover the chip).
+static int span_of(const dm_attention_desc *d) {
+    int64_t span = kDecodeMinSpan;
+    const int64_t heads = d->b * d->hkv;
+    while (span < d->tk && heads * ((d->tk + span - 1) / span) > kDecodeWorkgroups) span *= 2;
+    return (int)span;
+}
+
 static int nsplit_of(const dm_attention_desc *d) {
-    return (int)((d->tk + kDecodeSpan - 1) / kDecodeSpan);
+    const int64_t span = span_of(d);
+    return (int)((d->tk + span - 1) / span);
 }
 
 static int64_t left_of(const dm_attention_desc *d) {
@@ -327,14 +413,14 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         DM_LAUNCH_CHECK("attention_decode: launch");
         return DM_OK;
     }
-    const int nsplit = nsplit_of(d);
+    const int nsplit = nsplit_of(d), span = span_of(d);
     const size_t parts = (size_t)rows * nsplit;
     float *part_o = (float *)workspace;
     float *part_lse = (float *)((char *)workspace + align_up(parts * d->d * sizeof(float)));
     dim3 grid(nsplit, (unsigned)d->hkv, (unsigned)d->b);
     const int g = (int)(d->hq / d->hkv);
 #define DEC_SPLIT(DT, DD, GG)                                                               \
-    decode_split<DT, DD, GG><<<grid, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, \
+    decode_split<DT, DD, GG><<<grid, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, span, \
                                                    q, k, v, lengths, part_o, part_lse)
 #define DEC_G(DT, DD)                                \
     switch (g) {                                     \

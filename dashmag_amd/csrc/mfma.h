@@ -147,6 +147,12 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     return make_uint4(x[0], x[1], x[2], x[3]);
 }
+// The same with the non-temporal hint (cache policy bit 1): for data read once and streamed past,
+// such as a key-value cache during decode.
+__device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+    return make_uint4(x[0], x[1], x[2], x[3]);
+}
 
 // Linear block index remapped so that consecutive logical work items land on one XCD (block
 // b runs on XCD b % 8): XCD x takes logical items [x * per, (x + 1) * per).
