@@ -38,21 +38,29 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="also run a plain 1 GiB device copy (torch copy_), 5 times: the known-size "
+                        "kernel that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
     return p.parse_args()
 
 
 class Timed:
     """Times a C-ABI call on the current stream: `steps` back-to-back calls between two HIP
-    events, after `warmup` untimed ones."""
+    events, after `warmup` untimed ones. Over the same timed region the library's kernel timers
+    (HIP event pairs around each launch, on the launch stream) give each kernel's average launch
+    duration, in ``kernel_ms`` {name: (ms per launch, launches)}."""
 
     def __init__(self, torch, fn):
         self.torch, self.fn = torch, fn
+        self.kernel_ms = {}
 
     def run(self, steps, warmup):
+        from dashmag_amd import _lib
         torch = self.torch
         for _ in range(warmup):
             self.fn()
         torch.cuda.synchronize()
+        _lib.kernel_timing(True)
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
@@ -60,7 +68,22 @@ class Timed:
             self.fn()
         end.record()
         torch.cuda.synchronize()
+        self.kernel_ms = {k: (ms / n, n) for k, (ms, n) in _lib.kernel_times().items() if n}
+        _lib.kernel_timing(False)
         return start.elapsed_time(end) / steps  # ms per call
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (a line ``traffic_bytes_per_launch <kernel>: N``), or None when it has none."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_attention_decode_step.md")
+    try:
+        for line in open(path):
+            if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def check(rc, lib):
@@ -99,8 +122,9 @@ def bench_attention(torch, dm, ops, lib, data, steps, warmup, cu=None):
 
     ms_fwd = Timed(torch, fwd).run(steps, warmup)
     ms_bwd = Timed(torch, bwd).run(steps, warmup)
-    ms_step = Timed(torch, step).run(steps, warmup)
-    return ms_step, ms_fwd, ms_bwd, _lib.probe_counts()
+    t = Timed(torch, step)
+    ms_step = t.run(steps, warmup)
+    return ms_step, ms_fwd, ms_bwd, _lib.probe_counts(), t.kernel_ms
 
 
 def main():
@@ -121,6 +145,15 @@ def main():
     want = lambda name: not only or name in only  # noqa: E731
     secondary = {}
     print(f"device: {_lib.describe()}", file=sys.stderr, flush=True)
+    if args.copy_probe:
+        x = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print("copy probe: 5 copies of 1 GiB (read 1048576 KiB, write 1048576 KiB each)",
+              file=sys.stderr, flush=True)
+        del x, y
 
     # ---- headline: attention fwd+bwd, config 2 ----
     c2 = syn.config2(dev)
@@ -128,15 +161,17 @@ def main():
     flop2 = 14 * P2 * 128 * 32
     head = None
     if want("attn"):
-        ms, mf, mb, probes = bench_attention(torch, dm, ops, lib, c2, args.steps, args.warmup,
+        ms, mf, mb, probes, kms = bench_attention(torch, dm, ops, lib, c2, args.steps, args.warmup,
                                              c2["cu_seqlens"])
-        head = dict(ms=ms, ms_fwd=mf, ms_bwd=mb, probes=probes)
+        head = dict(ms=ms, ms_fwd=mf, ms_bwd=mb, probes=probes, kernel_ms=kms)
+        print("attention config 2 kernels: " + ", ".join(
+            f"{k} {v[0] * 1e3:.1f} us" for k, v in kms.items()), file=sys.stderr, flush=True)
         print(f"attention config 2: {ms:.3f} ms/step (fwd {mf:.3f}, bwd {mb:.3f}), "
               f"{flop2 / ms / 1e9:.1f} TFLOP/s", file=sys.stderr, flush=True)
     del c2
     if want("attn4096"):
         c = syn.config2_single(dev)
-        ms, mf, mb, _ = bench_attention(torch, dm, ops, lib, c, args.steps, args.warmup)
+        ms, mf, mb, _, _ = bench_attention(torch, dm, ops, lib, c, args.steps, args.warmup)
         P = syn.visible_pairs([4096])
         secondary["attention_fwd_bwd_T4096"] = dict(
             unit="TFLOP/s", value=14 * P * 128 * 32 / ms / 1e9, ms_per_step=ms,
@@ -161,11 +196,16 @@ def main():
         ptrs = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, lens, o, ws)]
         fn = lambda: check(lib.dm_attention_decode(ctypes.byref(desc), *ptrs[:5], ptrs[5], nb,  # noqa
                                                    st), lib)
-        ms = Timed(torch, fn).run(max(args.steps, 50), args.warmup)
+        tm = Timed(torch, fn)
+        ms = tm.run(max(args.steps, 50), args.warmup)
         sum_l = int(lens.sum())
         nbytes = 4 * 8 * 128 * sum_l + 4 * 64 * 32 * 128 + 4 * 64
         secondary["decode"] = dict(unit="GB/s", value=nbytes / ms / 1e6, us_per_call=ms * 1e3,
-                                   bytes=nbytes, frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS)
+                                   bytes=nbytes, frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS,
+                                   kernel_us={k: round(v[0] * 1e3, 2) for k, v in tm.kernel_ms.items()})
+        if "decode_split" in tm.kernel_ms:
+            ks = tm.kernel_ms["decode_split"][0]
+            secondary["decode"]["split_kernel_GBps"] = nbytes / ks / 1e6
         print(f"decode: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
               flush=True)
         del c, k, v
@@ -185,13 +225,16 @@ def main():
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [c["h0"], out, fin, ws]]
         fn = lambda: check(lib.dm_gdr_chunk_fwd(ctypes.byref(desc), *p[:8], p[8], nb, st), lib)  # noqa
-        ms = Timed(torch, fn).run(max(3, args.steps // 4), 1)
+        tm = Timed(torch, fn)
+        ms = tm.run(max(3, args.steps // 4), 1)
         cu = c["cu_seqlens"].tolist()
         nch = h * sum((cu[i + 1] - cu[i] + 63) // 64 for i in range(len(cu) - 1))
         flop = 11534336 * nch
         secondary["gdr_chunk_fwd"] = dict(unit="tokens/s", value=t / ms * 1e3, ms_per_call=ms,
                                           tflops=flop / ms / 1e9,
-                                          frac_of_bf16_peak=flop / ms / 1e9 / BF16_PEAK_TFLOPS)
+                                          frac_of_bf16_peak=flop / ms / 1e9 / BF16_PEAK_TFLOPS,
+                                          kernel_us={k: round(v[0] * 1e3, 2)
+                                                     for k, v in tm.kernel_ms.items()})
         print(f"gdr chunk fwd: {ms:.3f} ms, {t / ms * 1e3:.3e} tokens/s, "
               f"{flop / ms / 1e9:.2f} TFLOP/s", file=sys.stderr, flush=True)
         # backward (reported)
@@ -222,11 +265,14 @@ def main():
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [st_in, st_in, out]]
         fn = lambda: check(lib.dm_gdr_step(ctypes.byref(desc), *p, st), lib)  # noqa
-        ms = Timed(torch, fn).run(max(args.steps, 100), args.warmup)
+        tm = Timed(torch, fn)
+        ms = tm.run(max(args.steps, 100), args.warmup)
         nbytes = 8 * b * h * dk * dv + (3 * 2 * h * 128 + 2 * 4 * h) * b
         secondary["gdr_step"] = dict(unit="GB/s", value=nbytes / ms / 1e6, us_per_call=ms * 1e3,
                                      bytes=nbytes,
-                                     frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS)
+                                     frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS,
+                                     kernel_us={k: round(v[0] * 1e3, 2)
+                                                for k, v in tm.kernel_ms.items()})
         print(f"gdr step: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
               flush=True)
         del c
@@ -264,11 +310,16 @@ def main():
         return
     ms = head["ms"]
     value = flop2 / ms / 1e9
-    # dominant kernel: the backward entry point (the larger share of the step)
-    dom_ms, dom_flop, dom = (head["ms_bwd"], 10 * P2 * 128 * 32, "attention backward") \
-        if head["ms_bwd"] >= head["ms_fwd"] else (head["ms_fwd"], 4 * P2 * 128 * 32,
-                                                  "attention forward")
+    # dominant kernel: the one with the most time per step, with the GEMMs it performs as its
+    # algorithmic work (2 P D Hq FLOP per GEMM): forward QK^T and PV (2 GEMMs); dk/dv kernel
+    # QK^T, dO V^T, P^T dO, dS^T Q (4); dq kernel QK^T, dO V^T, dS K (3)
+    gemms = {"attn_fwd": 2, "attn_bwd_dkdv": 4, "attn_bwd_dq": 3}
+    kms = {k: v for k, v in head["kernel_ms"].items() if k in gemms}
+    dom = max(kms, key=lambda k: kms[k][0] * kms[k][1])
+    dom_ms = kms[dom][0]
+    dom_flop = gemms[dom] * 2 * P2 * 128 * 32
     achieved = dom_flop / dom_ms / 1e9
+    traffic = measured_traffic(dom)
     line = {
         "metric": "attn fwd+bwd TFLOP/s; GDR chunk tokens/s; decode HBM GB/s (% of roofline)",
         "value": round(value, 3),
@@ -287,9 +338,10 @@ def main():
                                "D=128 (BASELINE config 2)",
                    "tokens": 16384, "hq": 32, "hkv": 8, "d": 128,
                    "visible_pairs": P2, "flop_per_step": flop2},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": dom, "kernel_us": round(dom_ms * 1e3, 2),
+                     "flop_per_launch": dom_flop, "achieved": round(achieved, 2),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -51,6 +51,9 @@ SIGNATURES = {
     "dm_describe": (ctypes.c_int, [ctypes.c_char_p, _SZ]),
     "dm_probe_count": (ctypes.c_uint64, [ctypes.c_int]),
     "dm_probe_reset": (None, []),
+    "dm_kernel_timing": (ctypes.c_int, [ctypes.c_int]),
+    "dm_kernel_time": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_uint64)]),
     "dm_attention_row_bounds": (ctypes.c_int, [_AD, _I64, _I64, ctypes.POINTER(_I64),
                                                ctypes.POINTER(_I64)]),
     "dm_attention_fwd_workspace": (_SZ, [_AD]),
@@ -102,6 +105,25 @@ def probe_counts() -> dict:
 
 def probe_reset() -> None:
     lib().dm_probe_reset()
+
+
+KERNELS = ["attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "decode_split", "gdr_prep", "gdr_state",
+           "gdr_output", "gdr_step"]
+
+
+def kernel_timing(enable: bool) -> None:
+    """Starts (and zeroes) or stops the library's per-kernel HIP event timers."""
+    lib().dm_kernel_timing(1 if enable else 0)
+
+
+def kernel_times() -> dict:
+    """{kernel: (total ms, launches)} since timing was enabled; waits for the recorded events."""
+    out = {}
+    for i, name in enumerate(KERNELS):
+        ms, n = ctypes.c_double(), ctypes.c_uint64()
+        lib().dm_kernel_time(i, ctypes.byref(ms), ctypes.byref(n))
+        out[name] = (ms.value, int(n.value))
+    return out
 
 
 def describe() -> str:

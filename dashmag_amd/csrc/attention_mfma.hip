@@ -279,10 +279,13 @@ int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     else                                                                                       \
         attn_fwd_mfma<DT, DD, false><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale,   \
                                                              qq, kk, vv, oo, lse)
-    if (d->dtype == DM_BF16) {
-        if (d->d == 64) { FWD(DM_BF16, 64); } else { FWD(DM_BF16, 128); }
-    } else {
-        if (d->d == 64) { FWD(DM_F16, 64); } else { FWD(DM_F16, 128); }
+    {
+        KernelTimer timer(DM_KERNEL_ATTN_FWD, st);
+        if (d->dtype == DM_BF16) {
+            if (d->d == 64) { FWD(DM_BF16, 64); } else { FWD(DM_BF16, 128); }
+        } else {
+            if (d->d == 64) { FWD(DM_F16, 64); } else { FWD(DM_F16, 128); }
+        }
     }
 #undef FWD
     probe_add(DM_PROBE_ATTN_FWD_MFMA);

@@ -575,19 +575,23 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
                                                                    delta, w);                  \
     bwd_tiles<<<(unsigned)(d->b * ntiles64), 64, 0, st>>>(d->b, d->tq, w);                     \
     if (m.pad) {                                                                               \
+        { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
                                                                 qq, kk, vv, gg, delta, w,      \
-                                                                (uint16_t *)dk, (uint16_t *)dv); \
+                                                                (uint16_t *)dk, (uint16_t *)dv); } \
+        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
         bwd_dq<DT, DD, true><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq,  \
                                                              kk, vv, gg, delta, w,             \
-                                                             (uint16_t *)dq);                  \
+                                                             (uint16_t *)dq); }                \
     } else {                                                                                   \
+        { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, false><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
                                                                  qq, kk, vv, gg, delta, w,     \
-                                                                 (uint16_t *)dk, (uint16_t *)dv); \
+                                                                 (uint16_t *)dk, (uint16_t *)dv); } \
+        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
         bwd_dq<DT, DD, false><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
                                                               kk, vv, gg, delta, w,            \
-                                                              (uint16_t *)dq);                 \
+                                                              (uint16_t *)dq); }               \
     }
     if (d->dtype == DM_BF16) {
         if (d->d == 64) { BWD(DM_BF16, 64); } else { BWD(DM_BF16, 128); }

@@ -435,11 +435,13 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         case 128: DEC_G(DT, 128); break;             \
         default: DEC_G(DT, 256); break;              \
     }
+    {
+        KernelTimer timer(DM_KERNEL_DECODE_SPLIT, st);
+        if (d->dtype == DM_BF16) { DEC_D(DM_BF16); } else { DEC_D(DM_F16); }
+    }
     if (d->dtype == DM_BF16) {
-        DEC_D(DM_BF16);
         decode_merge<DM_BF16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
     } else {
-        DEC_D(DM_F16);
         decode_merge<DM_F16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
     }
 #undef DEC_D

@@ -21,6 +21,19 @@ void set_error(const std::string &msg);
 int refuse(const std::string &msg);  // sets the message, returns DM_ERR_REFUSED
 int hip_status(hipError_t e, const char *what);
 void probe_add(int probe, uint64_t n = 1);
+
+// Records a HIP event pair around the launches in its scope while kernel timing is enabled
+// (dm_kernel_timing); does nothing otherwise.
+class KernelTimer {
+  public:
+    KernelTimer(int kernel, hipStream_t stream);
+    ~KernelTimer();
+
+  private:
+    int kernel_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+};
 bool device_ok(std::string *why);
 
 #define DM_LAUNCH_CHECK(what)                                                   \

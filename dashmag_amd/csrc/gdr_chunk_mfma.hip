@@ -654,13 +654,31 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
     if (rc) return rc;
     const unsigned chunks = (unsigned)(nc * d->h), seqs = (unsigned)(S * d->h);
     if (d->dtype == DM_BF16) {
-        if (chunks) gdr_mfma_prep<DM_BF16><<<chunks, 256, 0, st>>>(a, w);
-        gdr_mfma_state<DM_BF16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
-        if (chunks) gdr_mfma_output<DM_BF16><<<chunks, 256, 0, st>>>(a, w, out);
+        {
+            KernelTimer t(DM_KERNEL_GDR_PREP, st);
+            if (chunks) gdr_mfma_prep<DM_BF16><<<chunks, 256, 0, st>>>(a, w);
+        }
+        {
+            KernelTimer t(DM_KERNEL_GDR_STATE, st);
+            gdr_mfma_state<DM_BF16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
+        }
+        {
+            KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
+            if (chunks) gdr_mfma_output<DM_BF16><<<chunks, 256, 0, st>>>(a, w, out);
+        }
     } else {
-        if (chunks) gdr_mfma_prep<DM_F16><<<chunks, 256, 0, st>>>(a, w);
-        gdr_mfma_state<DM_F16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
-        if (chunks) gdr_mfma_output<DM_F16><<<chunks, 256, 0, st>>>(a, w, out);
+        {
+            KernelTimer t(DM_KERNEL_GDR_PREP, st);
+            if (chunks) gdr_mfma_prep<DM_F16><<<chunks, 256, 0, st>>>(a, w);
+        }
+        {
+            KernelTimer t(DM_KERNEL_GDR_STATE, st);
+            gdr_mfma_state<DM_F16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
+        }
+        {
+            KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
+            if (chunks) gdr_mfma_output<DM_F16><<<chunks, 256, 0, st>>>(a, w, out);
+        }
     }
     probe_add(DM_PROBE_GDR_CHUNK_FWD, 4);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule: MFMA launch");

@@ -210,12 +210,15 @@ extern "C" int dm_gdr_step(const dm_gdr_desc *d, const void *q, const void *k, c
     else if (rows <= 32) STEP(DT, 32);              \
     else STEP(DT, 64);
     if (rows > 64) return refuse("gated_delta_step: state shape not implemented");
-    if (d->dtype == DM_F32) {
-        STEP_R(DM_F32)
-    } else if (d->dtype == DM_BF16) {
-        STEP_R(DM_BF16)
-    } else {
-        STEP_R(DM_F16)
+    {
+        KernelTimer timer(DM_KERNEL_GDR_STEP, st);
+        if (d->dtype == DM_F32) {
+            STEP_R(DM_F32)
+        } else if (d->dtype == DM_BF16) {
+            STEP_R(DM_BF16)
+        } else {
+            STEP_R(DM_F16)
+        }
     }
 #undef STEP_R
 #undef STEP

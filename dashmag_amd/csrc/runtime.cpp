@@ -4,7 +4,10 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "dm_common.h"
 
@@ -27,6 +30,69 @@ int hip_status(hipError_t e, const char *what) {
 
 void probe_add(int probe, uint64_t n) {
     if (probe >= 0 && probe < DM_PROBE_COUNT) g_probes[probe].fetch_add(n);
+}
+
+// Kernel timers: event pairs still to be read, per kernel, and the totals read so far. Events are
+// pooled; at most kMaxPending pairs are kept per kernel (older ones are read first).
+static std::mutex g_timing_mu;
+static std::atomic<bool> g_timing{false};
+struct TimerSlot {
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    double ms = 0.0;
+    uint64_t launches = 0;
+};
+static TimerSlot g_timers[DM_KERNEL_COUNT];
+static std::vector<hipEvent_t> g_event_pool;
+constexpr size_t kMaxPending = 4096;
+
+static hipEvent_t take_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+static void drain(TimerSlot &t) {
+    for (auto &pr : t.pending) {
+        float ms = 0.f;
+        if (hipEventSynchronize(pr.second) == hipSuccess &&
+            hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess) {
+            t.ms += ms;
+            t.launches += 1;
+        }
+        g_event_pool.push_back(pr.first);
+        g_event_pool.push_back(pr.second);
+    }
+    t.pending.clear();
+}
+
+KernelTimer::KernelTimer(int kernel, hipStream_t stream) : kernel_(kernel), stream_(stream) {
+    if (!g_timing.load(std::memory_order_relaxed) || kernel < 0 || kernel >= DM_KERNEL_COUNT)
+        return;
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    start_ = take_event();
+    if (start_ && hipEventRecord(start_, stream_) != hipSuccess) {
+        g_event_pool.push_back(start_);
+        start_ = nullptr;
+    }
+}
+
+KernelTimer::~KernelTimer() {
+    if (!start_) return;
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    hipEvent_t end = take_event();
+    if (!end || hipEventRecord(end, stream_) != hipSuccess) {
+        g_event_pool.push_back(start_);
+        if (end) g_event_pool.push_back(end);
+        return;
+    }
+    TimerSlot &t = g_timers[kernel_];
+    if (t.pending.size() >= kMaxPending) drain(t);
+    t.pending.emplace_back(start_, end);
 }
 
 // The kernels are built for gfx950 (wave64, MFMA with the 16-deep bf16 forms, 160 KiB of LDS);
@@ -62,6 +128,26 @@ uint64_t dm_probe_count(int probe) {
 
 void dm_probe_reset(void) {
     for (auto &p : dm::g_probes) p.store(0);
+}
+
+int dm_kernel_timing(int enable) {
+    std::lock_guard<std::mutex> lock(dm::g_timing_mu);
+    for (auto &t : dm::g_timers) {
+        dm::drain(t);
+        t.ms = 0.0;
+        t.launches = 0;
+    }
+    dm::g_timing.store(enable != 0);
+    return DM_OK;
+}
+
+int dm_kernel_time(int kernel, double *ms, uint64_t *launches) {
+    if (kernel < 0 || kernel >= DM_KERNEL_COUNT) return dm::refuse("kernel_time: no such kernel");
+    std::lock_guard<std::mutex> lock(dm::g_timing_mu);
+    dm::drain(dm::g_timers[kernel]);
+    if (ms) *ms = dm::g_timers[kernel].ms;
+    if (launches) *launches = dm::g_timers[kernel].launches;
+    return DM_OK;
 }
 
 int dm_describe(char *buf, size_t len) {

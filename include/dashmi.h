@@ -110,6 +110,24 @@ typedef enum {
 uint64_t dm_probe_count(int probe);
 void dm_probe_reset(void);
 
+/* Kernel timers (no counterpart in the reference; a measurement hook for benchmarks and
+ * profilers): while enabled, the library records a HIP event pair around each launch of the
+ * kernels below, on the stream it launches them on. dm_kernel_time waits for the recorded events
+ * and returns the summed duration in ms and the launch count since timing was last enabled. */
+typedef enum {
+    DM_KERNEL_ATTN_FWD = 0,   /* MFMA attention forward */
+    DM_KERNEL_ATTN_BWD_DKDV,  /* MFMA attention backward, dk and dv */
+    DM_KERNEL_ATTN_BWD_DQ,    /* MFMA attention backward, dq */
+    DM_KERNEL_DECODE_SPLIT,   /* decode, pass 1 */
+    DM_KERNEL_GDR_PREP,       /* chunked gated delta rule: per-chunk preparation */
+    DM_KERNEL_GDR_STATE,      /* chunked gated delta rule: the state pass */
+    DM_KERNEL_GDR_OUTPUT,     /* chunked gated delta rule: the output */
+    DM_KERNEL_GDR_STEP,       /* gated delta rule step */
+    DM_KERNEL_COUNT
+} dm_kernel;
+int dm_kernel_timing(int enable);
+int dm_kernel_time(int kernel, double *ms, uint64_t *launches);
+
 /* The keys query `i` of batch row `b` sees, as the half-open interval [*lo, *hi) of key indices
  * (empty when *lo >= *hi), before key padding, which is per key: the closed form of
  * crates/dash-ops/src/attention/kernels.rs:416-523 (row_bounds, query_range) and of the
