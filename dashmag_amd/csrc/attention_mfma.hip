@@ -181,8 +181,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int32_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                    bool vis = j >= lo && j < hi;
-                    if constexpr (PAD) vis = vis && !pad[j];
+                    bool vis = (j >= lo) & (j < hi);
+                    if constexpr (PAD) vis = vis & (pad[j < Tk ? j : Tk - 1] == 0);
                     s[t][i] = vis ? s[t][i] : -INFINITY;
                 }
         }

@@ -14,15 +14,15 @@
 //   bwd_dq     per (tile of 128 queries, query head): sweeps the key tiles as the forward does,
 //              recomputing S^T and dP^T, dQ^T += K^T dS^T.
 #include <string>
+#include <type_traits>
 
 #include "attention_kernels.h"
 #include "mfma.h"
 
 namespace dm {
 
-constexpr int kRowTile = 64;   // rows per tile of the prep's tile ranges
-constexpr int kKvBlock = 128;  // keys per dK/dV workgroup (32 per wavefront)
-constexpr int kQTile = 64;     // queries per step of the dK/dV sweep
+constexpr int kRowTile = 32;   // rows per tile of the prep's tile ranges (= the dK/dV step)
+constexpr int kKvBlock = 128;  // keys per dK/dV workgroup (32 per wavefront pair)
 constexpr int kDqM = 128;      // queries per dQ workgroup
 constexpr int kDqN = 64;       // keys per step of the dQ sweep
 
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
     (void)b;
 }
 
-// Per tile of 64 rows: [union lo, union hi) of the rows' intervals, and [full lo, full hi), the
+// Per tile of kRowTile rows: [union lo, union hi) of the rows' intervals, and [full lo, full hi), the
 // keys every row of the tile sees (empty when a row of the tile sees nothing).
 __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) {
     const int64_t ntiles = (Tq + kRowTile - 1) / kRowTile;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) 
     const int64_t b = t / ntiles, tile = t % ntiles;
     const int64_t i = tile * kRowTile + threadIdx.x;
     int32_t ul = INT32_MAX, uh = INT32_MIN, fl = INT32_MIN, fh = INT32_MAX;
-    if (i < Tq) {
+    if (threadIdx.x < kRowTile && i < Tq) {
         const int32_t lo = w.rlo[b * Tq + i], hi = w.rhi[b * Tq + i];
         if (lo < hi) {
             ul = lo;
@@ -140,18 +140,51 @@ struct BwdStrides {
     static constexpr int TR = D + 32;  // rows read by ds_read_b64_tr_b16
 };
 
+// Wave pairs: a workgroup of 8 wavefronts takes 128 keys of one key-value head; wavefronts w and
+// w + 4 (one SIMD) share the keys j0 + 32 w + [0, 32). Per 32-query step, wavefront w holds K
+// and computes S = Q K^T, P = exp2(S c - lse2) (masked), hands P (f32) over through LDS and
+// accumulates dV += P^T dO; wavefront w + 4 holds V and, one step behind, computes
+// dP = dO V^T, dS = P (dP - delta) and accumulates dK += dS^T Q. The two halves carry equal
+// MFMA work, and one's exp / pack work overlaps the other's products on the shared SIMD. All
+// 512 threads stage Q / dO tiles from HBM two steps ahead through registers into three
+// rotating LDS slots; one barrier per step.
+constexpr int kDkdvStep = 32;  // queries per step
+constexpr int kDkdvSlots = 3;
+
+template <int D>
+struct DkdvSlot {
+    uint4 q[kDkdvStep * BwdStrides<D>::ROW / 8];
+    uint4 qt[kDkdvStep * BwdStrides<D>::TR / 8];
+    uint4 g[kDkdvStep * BwdStrides<D>::ROW / 8];
+    uint4 gt[kDkdvStep * BwdStrides<D>::TR / 8];
+    float lse2[kDkdvStep], delta[kDkdvStep];
+    int32_t rlo[kDkdvStep], rhi[kDkdvStep];
+};
+
+#ifdef DM_TRACE_DKDV
+// profiling aid (built only with -DDM_TRACE_DKDV): per-step clock stamps of one workgroup
+__device__ uint64_t dm_trace[2][256][4];
+#define DM_STAMP(role, step, k)                                                                  \
+    do {                                                                                        \
+        if (work == DM_TRACE_DKDV && kw == 0 && lane == 0 && (step) < 256)                      \
+            dm_trace[role][step][k] = __builtin_readcyclecounter();                             \
+    } while (0)
+#else
+#define DM_STAMP(role, step, k) \
+    do {                        \
+    } while (0)
+#endif
+constexpr int kDkdvRing = 8;  // schedule entries in flight (steps n - 1 .. n + 5)
+
 template <int D>
 struct DkdvSmem {
-    uint4 q[kQTile * BwdStrides<D>::ROW / 8];
-    uint4 qt[kQTile * BwdStrides<D>::TR / 8];
-    uint4 g[kQTile * BwdStrides<D>::ROW / 8];
-    uint4 gt[kQTile * BwdStrides<D>::TR / 8];
-    float lse2[kQTile], delta[kQTile];
-    int32_t rlo[kQTile], rhi[kQTile];
+    DkdvSlot<D> slot[kDkdvSlots];
+    float4 p[2][4][4][64];  // [step parity][key block][i / 4][lane]: P in the products' layout
+    int4 sched[kDkdvRing];  // step k: {query head, tile, needs the mask, exists}
 };
 
 template <int DT, int D, bool PAD>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_t Hq,
+__global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_t Hq,
                                                    int64_t Hkv, float scale,
                                                    const uint16_t *__restrict__ q,
                                                    const uint16_t *__restrict__ k,
@@ -171,189 +204,364 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     if (work >= nwork) return;
     const int64_t kh = work % Hkv, kb = (work / Hkv) % nkb, b = work / (Hkv * nkb);
     const int64_t group = Hq / Hkv;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool pwave = wave < 4;  // computes P and dV; the other half dS and dK
+    const int kw = wave & 3;      // the key sub-block of this wavefront
     const int col = lane & 31, half = lane >> 5;
     const int32_t j0 = (int32_t)(kb * kKvBlock);
-    const int32_t key = j0 + wave * 32 + col;  // this lane's key
+    const int32_t key = j0 + kw * 32 + col;  // this lane's key
     const bool kvalid = key < Tk;
     const bool kpad = PAD && kvalid && m.pad[b * Tk + key];
+    const int32_t mkey = kpad ? -1 : key;  // a padded key is seen by no query (intervals >= 0)
     const float c2 = scale * 1.4426950408889634f;
 
-    // K and V of this lane's key as B operands (col = key, k = head dimension)
-    Frag8 kf[KSTEPS], vf[KSTEPS];
+    // K (P waves) or V (dS waves) of this lane's key as B operands (col = key, k = head dim)
+    Frag8 bf[KSTEPS];
     {
-        const uint16_t *kp = k + ((b * Tk + key) * Hkv + kh) * D + half * 8;
-        const uint16_t *vp = v + ((b * Tk + key) * Hkv + kh) * D + half * 8;
+        const uint16_t *src = pwave ? k : v;
+        const uint16_t *bp = src + ((b * Tk + key) * Hkv + kh) * D + half * 8;
 #pragma unroll
-        for (int s = 0; s < KSTEPS; s++) {
-            kf[s].u = kvalid ? *(const uint4 *)(kp + s * 16) : make_uint4(0, 0, 0, 0);
-            vf[s].u = kvalid ? *(const uint4 *)(vp + s * 16) : make_uint4(0, 0, 0, 0);
-        }
+        for (int s = 0; s < KSTEPS; s++)
+            bf[s].u = kvalid ? *(const uint4 *)(bp + s * 16) : make_uint4(0, 0, 0, 0);
     }
-    f32x16_t dka[DT32], dva[DT32];
+    // P waves accumulate dV, dS waves dK
+    f32x16_t acc[DT32];
 #pragma unroll
     for (int t = 0; t < DT32; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) dka[t][i] = dva[t][i] = 0.f;
+        for (int i = 0; i < 16; i++) acc[t][i] = 0.f;
 
-    const int64_t ntiles = (Tq + kQTile - 1) / kQTile;
+    const int64_t ntiles = (Tq + kDkdvStep - 1) / kDkdvStep;
     const int32_t *tr = w.trange + b * ntiles * 4;
     const int32_t j1 = j0 + kKvBlock < Tk ? j0 + kKvBlock : (int32_t)Tk;
-    auto sees = [&](int64_t t) -> bool { return tr[t * 4] < j1 && tr[t * 4 + 1] > j0; };
+    // The (head, tile) steps: the group's query heads, each over the tiles that see the keys.
+    // A wavefront walks them 64 tiles at a time: one vector load of the tiles' ranges and two
+    // ballots give the seeing tiles and the ones needing the per-element mask as bit masks, so
+    // a step costs no memory round trip.
+    const int32_t hend = (int32_t)((kh + 1) * group);
+    struct TileIter {
+        int32_t h, t;       // current step (h == hend: done)
+        int32_t c0;         // first tile of the current 64-tile chunk
+        uint64_t pending;   // seeing tiles of the chunk after t
+        uint64_t cut;       // tiles of the chunk needing the per-element mask
+        bool masked;        // whether step t needs it
+    };
+    auto scan = [&](TileIter &it) {
+        const int32_t tt = it.c0 + lane;
+        const int4 r = *(const int4 *)(tr + (tt < ntiles ? tt : ntiles - 1) * 4);
+        const bool in = tt < ntiles;
+        const bool see = in & (r.x < j1) & (r.y > j0);
+        const bool part = PAD | (r.z > j0) | (r.w < j0 + kKvBlock);
+        it.pending = __ballot(see);
+        it.cut = __ballot(part);
+    };
+    // moves `it` to its next step (the first one when it.t < 0)
+    auto next = [&](TileIter &it) {
+        while (it.h < hend) {
+            if (it.pending) {
+                const int bit = __builtin_ctzll(it.pending);
+                it.pending &= it.pending - 1;
+                it.t = __builtin_amdgcn_readfirstlane(it.c0 + bit);
+                it.masked = (it.cut >> bit) & 1;
+                return;
+            }
+            it.c0 += 64;
+            if (it.c0 >= ntiles) {
+                it.h++;
+                it.c0 = 0;
+                if (it.h >= hend) return;
+            }
+            scan(it);
+        }
+    };
+    auto start = [&](TileIter &it) {
+        it.h = (int32_t)(kh * group);
+        it.c0 = 0;
+        it.t = -1;
+        if (j0 >= Tk) {
+            it.h = hend;
+            return;
+        }
+        scan(it);
+        next(it);
+    };
 
-    // staging: Q and dO tiles in 16-byte chunks (buffer loads whose range ends at the last
-    // query row), written to a row copy and a transposed-read copy
-    constexpr int CPR = D / 8, NCH = kQTile * CPR / 256, RSTEP = 256 / CPR;
-    const int crow = tid / CPR, ccol = tid % CPR;
+    // staging: a step's Q and dO rows in 16-byte chunks (2 per thread) by buffer loads whose
+    // range ends at the last query row, then a row copy and a transposed-read copy of each;
+    // two register sets, a step's loads issued two steps before its store
+    constexpr int CPR = D / 8, NCH = (kDkdvStep * CPR + 511) / 512, RSTEP = 512 / CPR;
+    const int crow = tid / CPR, ccol = tid % CPR;  // crow >= kDkdvStep: no chunk (D = 64)
     const uint32_t qrow_bytes = (uint32_t)(Hq * D * 2);
     const uint32_t qbytes = (uint32_t)(((Tq - 1) * Hq + 1) * D * 2);
     const uint32_t goff = crow * qrow_bytes + ccol * 16;
-    uint4 qreg[NCH], greg[NCH];
-    __amdgpu_buffer_rsrc_t qrs, grs;
-    auto load = [&](int64_t h, int64_t t) {
-        qrs = make_rsrc(q + (b * Tq * Hq + h) * D, qbytes);
-        grs = make_rsrc(d_o + (b * Tq * Hq + h) * D, qbytes);
-        const uint32_t base = (uint32_t)(t * kQTile) * qrow_bytes + goff;
+    struct Stage {
+        uint4 q[NCH], g[NCH];
+        float lse, delta;
+        int32_t lo, hi;
+    };
+    Stage stg0, stg1;
+    // Every call issues the same loads (so the compiler's count of loads in flight is exact and
+    // a store waits only for its own set): rows past the tile's last valid row read zeros or a
+    // repeated row, and every thread reads a row's lse / delta / interval (only 32 store them).
+    // Zeros are harmless: a row whose interval is empty gets P = 0.
+    const uint32_t mbytes = (uint32_t)(((Tq - 1) * Hq + 1) * 4);
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(w.rlo + b * Tq, (uint32_t)(Tq * 4));
+    const __amdgpu_buffer_rsrc_t hrs = make_rsrc(w.rhi + b * Tq, (uint32_t)(Tq * 4));
+    auto load = [&](Stage &x, int64_t h, int64_t t) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t qrs = make_rsrc(q + (b * Tq * Hq + h) * D, qbytes);
+        const __amdgpu_buffer_rsrc_t grs = make_rsrc(d_o + (b * Tq * Hq + h) * D, qbytes);
+        const uint32_t base = (uint32_t)(t * kDkdvStep) * qrow_bytes + ccol * 16;
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            const uint32_t off = base + u * RSTEP * qrow_bytes;
-            qreg[u] = buf_load16(qrs, off);
-            greg[u] = buf_load16(grs, off);
+            const int r = (crow + u * RSTEP) & (kDkdvStep - 1);
+            const uint32_t off = base + r * qrow_bytes;
+            x.q[u] = buf_load16(qrs, off);
+            x.g[u] = buf_load16(grs, off);
         }
+        const uint32_t i = (uint32_t)(t * kDkdvStep) + (tid & (kDkdvStep - 1));
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(w.lse2 + b * Tq * Hq + h, mbytes);
+        const __amdgpu_buffer_rsrc_t drs = make_rsrc(delta + b * Tq * Hq + h, mbytes);
+        x.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, i * (uint32_t)Hq * 4, 0, 0));
+        x.delta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drs, i * (uint32_t)Hq * 4, 0, 0));
+        x.lo = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, i * 4, 0, 0);
+        x.hi = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(hrs, i * 4, 0, 0);
     };
-    float st_lse = 0.f, st_delta = 0.f;
-    int32_t st_lo = 0, st_hi = 0;
-    auto load_rows = [&](int64_t h, int64_t t) {
-        if (tid < kQTile) {
-            const int64_t i = t * kQTile + tid;
-            const bool ok = i < Tq;
-            st_lse = ok ? w.lse2[(b * Tq + i) * Hq + h] : INFINITY;
-            st_delta = ok ? delta[(b * Tq + i) * Hq + h] : 0.f;
-            st_lo = ok ? w.rlo[b * Tq + i] : 0;
-            st_hi = ok ? w.rhi[b * Tq + i] : 0;
-        }
-    };
-    auto store = [&]() {
+    auto store = [&](const Stage &x, DkdvSlot<D> &sl) {
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
             const int r = crow + u * RSTEP;
-            sm.q[r * (RS / 8) + ccol] = qreg[u];
-            sm.qt[r * (TS / 8) + ccol] = qreg[u];
-            sm.g[r * (RS / 8) + ccol] = greg[u];
-            sm.gt[r * (TS / 8) + ccol] = greg[u];
+            if (r >= kDkdvStep) break;  // (head width 64: half the threads stage nothing)
+            sl.q[r * (RS / 8) + ccol] = x.q[u];
+            sl.qt[r * (TS / 8) + ccol] = x.q[u];
+            sl.g[r * (RS / 8) + ccol] = x.g[u];
+            sl.gt[r * (TS / 8) + ccol] = x.g[u];
         }
-        if (tid < kQTile) {
-            sm.lse2[tid] = st_lse;
-            sm.delta[tid] = st_delta;
-            sm.rlo[tid] = st_lo;
-            sm.rhi[tid] = st_hi;
+        if (tid < kDkdvStep) {
+            sl.lse2[tid] = x.lse;
+            sl.delta[tid] = x.delta;
+            sl.rlo[tid] = x.lo;
+            sl.rhi[tid] = max(x.hi - x.lo, 0);  // stored as the span hi - lo
         }
     };
-    const uint16_t *sq = (const uint16_t *)sm.q, *sqt = (const uint16_t *)sm.qt;
-    const uint16_t *sg = (const uint16_t *)sm.g, *sgt = (const uint16_t *)sm.gt;
 
-    // the (head, tile) steps: the group's query heads, each over the tiles that see the keys
-    int64_t hh = kh * group, tt = 0;
-    const int64_t hend = (kh + 1) * group;
-    auto advance = [&](int64_t &h, int64_t &t) {
-        while (h < hend) {
-            while (t < ntiles && !sees(t)) t++;
-            if (t < ntiles) return;
-            h++;
-            t = 0;
-        }
+    // The schedule: wavefront 0 walks the steps and writes step k's entry into the ring
+    // sm.sched five steps ahead of its use (entries 0 .. 4 up front, entry n + 5 in iteration
+    // n); every wavefront reads the entries it needs, so a step costs the others no walk.
+    TileIter it;
+    auto publish = [&](const int k) __attribute__((always_inline)) {
+        if (lane == 0)
+            sm.sched[k % kDkdvRing] = make_int4(it.h, it.t, it.masked ? 1 : 0, it.h < hend ? 1 : 0);
+        if (it.h < hend) next(it);
     };
-    const bool any_key = j0 < Tk;
-    if (any_key) advance(hh, tt);
-    if (any_key && hh < hend) {
-        load(hh, tt);
-        load_rows(hh, tt);
+    if (wave == 0) {
+        start(it);
+        for (int k = 0; k < 5; k++) publish(k);
     }
-    while (any_key && hh < hend) {
-        const int64_t t = tt;
-        __syncthreads();
-        store();
-        __syncthreads();
-        // next step's loads, in flight during this step's products
-        tt++;
-        advance(hh, tt);
-        if (hh < hend) {
-            load(hh, tt);
-            load_rows(hh, tt);
+    __syncthreads();
+    struct Entry {
+        int32_t h, t;
+        bool masked, valid;
+    };
+    auto entry = [&](const int k) __attribute__((always_inline)) -> Entry {
+        const int4 e = sm.sched[k % kDkdvRing];
+        Entry x;
+        x.h = __builtin_amdgcn_readfirstlane(e.x);
+        x.t = __builtin_amdgcn_readfirstlane(e.y);
+        x.masked = __builtin_amdgcn_readfirstlane(e.z) != 0;
+        x.valid = __builtin_amdgcn_readfirstlane(e.w) != 0;
+        return x;
+    };
+    // prologue: step 0 into slot 0, steps 1 and 2 loading into the two register sets
+    {
+        const Entry e0 = entry(0), e1 = entry(1), e2 = entry(2);
+        load(stg0, e0.valid ? e0.h : kh * group, e0.valid ? e0.t : 0);
+        if (e0.valid) store(stg0, sm.slot[0]);
+        load(stg0, e1.valid ? e1.h : kh * group, e1.valid ? e1.t : 0);
+        load(stg1, e2.valid ? e2.h : kh * group, e2.valid ? e2.t : 0);
+    }
+    __syncthreads();
+
+    // stage step n + 1 (held by this step's register set) into slot `nslot`; the set then
+    // loads step n + 3
+    auto restage = [&](const int n, const int nslot, Stage &x) __attribute__((always_inline)) {
+        if (entry(n + 1).valid) store(x, sm.slot[nslot]);
+        const Entry e = entry(n + 3);
+        // a step past the last loads the group's first tile again (the same loads every call)
+        load(x, e.valid ? e.h : kh * group, e.valid ? e.t : 0);
+    };
+    // P waves, step n: S = Q K^T, P (handed over in LDS), dV += P^T dO
+    auto pstep = [&](const int n, const int cslot, auto masked_c) __attribute__((always_inline)) {
+        constexpr bool MASKED = decltype(masked_c)::value;
+        const DkdvSlot<D> &sl = sm.slot[cslot];
+        const uint16_t *sq = (const uint16_t *)sl.q, *sgt = (const uint16_t *)sl.gt;
+        f32x16_t s;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[i] = 0.f;
+        const uint16_t *qa = sq + col * RS + half * 8;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(qa + st * 16);
+            s = mfma32<DT>(a, bf[st], s);
         }
-        const int32_t *r = tr + t * 4;
-        const bool masked = PAD || r[2] > j0 || r[3] < j0 + kKvBlock;
+        // P = exp2(S c - lse2); element i is query 8 (i / 4) + 4 h + i % 4
+        float p[16];
 #pragma unroll
-        for (int qs = 0; qs < kQTile / 32; qs++) {
-            // S and dP for 32 queries x this wavefront's 32 keys
-            f32x16_t s, dp;
-#pragma unroll
-            for (int i = 0; i < 16; i++) s[i] = dp[i] = 0.f;
-            const uint16_t *qa = sq + (qs * 32 + col) * RS + half * 8;
-            const uint16_t *ga = sg + (qs * 32 + col) * RS + half * 8;
-#pragma unroll
-            for (int st = 0; st < KSTEPS; st++) {
-                Frag8 a;
-                a.u = *(const uint4 *)(qa + st * 16);
-                s = mfma32<DT>(a, kf[st], s);
-                a.u = *(const uint4 *)(ga + st * 16);
-                dp = mfma32<DT>(a, vf[st], dp);
+        for (int j = 0; j < 4; j++) {
+            const int r0 = j * 8 + half * 4;
+            const float4 l4 = *(const float4 *)(sl.lse2 + r0);
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+            int lo4[4] = {0, 0, 0, 0}, hi4[4] = {0, 0, 0, 0};
+            if constexpr (MASKED) {
+                // rows hold lo and hi - lo: key visible iff (key - lo) < (hi - lo) unsigned
+                const int4 a4 = *(const int4 *)(sl.rlo + r0);
+                const int4 b4 = *(const int4 *)(sl.rhi + r0);
+                lo4[0] = a4.x; lo4[1] = a4.y; lo4[2] = a4.z; lo4[3] = a4.w;
+                hi4[0] = b4.x; hi4[1] = b4.y; hi4[2] = b4.z; hi4[3] = b4.w;
             }
-            // P = exp2(S c - lse2), dS = P (dP - delta); element i is query
-            //   32 qs + 8 (i / 4) + 4 h + i % 4, four consecutive rows per i / 4
-            Frag8 pf[2], df[2];
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                float p[8], ds[8];
-#pragma unroll
-                for (int g4 = 0; g4 < 2; g4++) {
-                    const int r0 = qs * 32 + (2 * u + g4) * 8 + half * 4;
-                    const float4 l4 = *(const float4 *)(sm.lse2 + r0);
-                    const float4 d4 = *(const float4 *)(sm.delta + r0);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                    const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int i = 8 * u + 4 * g4 + e;
-                        float x = fast_exp2(fmaf(s[i], c2, -lv[e]));
-                        if (masked) {
-                            const bool vis = key >= sm.rlo[r0 + e] && key < sm.rhi[r0 + e] && !kpad;
-                            x = vis ? x : 0.f;
-                        }
-                        p[4 * g4 + e] = x;
-                        ds[4 * g4 + e] = x * (dp[i] - dl[e]);
-                    }
+            for (int e = 0; e < 4; e++) {
+                float x = fast_exp2(fmaf(s[4 * j + e], c2, -lv[e]));
+                if constexpr (MASKED) {
+                    const bool vis = (uint32_t)(mkey - lo4[e]) < (uint32_t)hi4[e];
+                    x = vis ? x : 0.f;
                 }
-                pf[u].u = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
-                                     pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
-                df[u].u = make_uint4(pack2<DT>(ds[0], ds[1]), pack2<DT>(ds[2], ds[3]),
-                                     pack2<DT>(ds[4], ds[5]), pack2<DT>(ds[6], ds[7]));
+                p[4 * j + e] = x;
             }
-            // dV += P^T dO, dK += dS^T Q: A = (row key, k = query) from the products' output,
-            // B = (k = query, col = d) by transposed reads of the row-major tiles
+            sm.p[n & 1][kw][j][lane] =
+                make_float4(p[4 * j], p[4 * j + 1], p[4 * j + 2], p[4 * j + 3]);
+        }
+        DM_STAMP(0, n, 2);
+        Frag8 pf[2];
 #pragma unroll
-            for (int u = 0; u < 2; u++)
+        for (int u = 0; u < 2; u++)
+            pf[u].u = make_uint4(pack2<DT>(p[8 * u], p[8 * u + 1]),
+                                 pack2<DT>(p[8 * u + 2], p[8 * u + 3]),
+                                 pack2<DT>(p[8 * u + 4], p[8 * u + 5]),
+                                 pack2<DT>(p[8 * u + 6], p[8 * u + 7]));
+        // dV += P^T dO: A = (row key, k = query) from the product's output, B = dO (k = query,
+        // col = d) by transposed reads of the row-major tile
 #pragma unroll
-                for (int dt = 0; dt < DT32; dt++) {
-                    const Frag8 bg = lds_tr_frag(sgt, TS, qs * 32 + u * 16, dt * 32, lane);
-                    const Frag8 bq = lds_tr_frag(sqt, TS, qs * 32 + u * 16, dt * 32, lane);
-                    dva[dt] = mfma32<DT>(pf[u], bg, dva[dt]);
-                    dka[dt] = mfma32<DT>(df[u], bq, dka[dt]);
-                }
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int dt = 0; dt < DT32; dt++) {
+                const Frag8 bg = lds_tr_frag(sgt, TS, u * 16, dt * 32, lane);
+                acc[dt] = mfma32<DT>(pf[u], bg, acc[dt]);
+            }
+    };
+    // dS waves, step m: dP = dO V^T, dS = P (dP - delta), dK += dS^T Q
+    auto dsstep = [&](const int m, const int mslot) __attribute__((always_inline)) {
+        const DkdvSlot<D> &sl = sm.slot[mslot];
+        const uint16_t *sg = (const uint16_t *)sl.g, *sqt = (const uint16_t *)sl.qt;
+        f32x16_t dp;
+#pragma unroll
+        for (int i = 0; i < 16; i++) dp[i] = 0.f;
+        const uint16_t *ga = sg + col * RS + half * 8;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(ga + st * 16);
+            dp = mfma32<DT>(a, bf[st], dp);
+        }
+        float ds[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 p4 = sm.p[m & 1][kw][j][lane];
+            const float4 d4 = *(const float4 *)(sl.delta + j * 8 + half * 4);
+            ds[4 * j + 0] = p4.x * (dp[4 * j + 0] - d4.x);
+            ds[4 * j + 1] = p4.y * (dp[4 * j + 1] - d4.y);
+            ds[4 * j + 2] = p4.z * (dp[4 * j + 2] - d4.z);
+            ds[4 * j + 3] = p4.w * (dp[4 * j + 3] - d4.w);
+        }
+        DM_STAMP(1, m + 1, 2);
+        Frag8 df[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            df[u].u = make_uint4(pack2<DT>(ds[8 * u], ds[8 * u + 1]),
+                                 pack2<DT>(ds[8 * u + 2], ds[8 * u + 3]),
+                                 pack2<DT>(ds[8 * u + 4], ds[8 * u + 5]),
+                                 pack2<DT>(ds[8 * u + 6], ds[8 * u + 7]));
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int dt = 0; dt < DT32; dt++) {
+                const Frag8 bq = lds_tr_frag(sqt, TS, u * 16, dt * 32, lane);
+                acc[dt] = mfma32<DT>(df[u], bq, acc[dt]);
+            }
+    };
+
+    // The steps run as iterations n = 0 .. N (N steps), one barrier each: the P waves compute
+    // step n in iterations 0 .. N - 1, the dS waves step n - 1 in iterations 1 .. N. Each half
+    // runs its own loop (the same barriers), unrolled by two so that each register set keeps
+    // its own registers and its loads stay in flight across a step (a set chosen at run time
+    // would be copied, and the copy waits for the loads).
+    // slot indices rotate with n: cs = n % 3 (step n), ns = (n + 1) % 3, ps = (n + 2) % 3
+    // = (n - 1) % 3
+    int cs = 0, ns = 1, ps = 2;
+    auto rotate = [&]() __attribute__((always_inline)) {
+        const int t = ps;
+        ps = cs;
+        cs = ns;
+        ns = t;
+    };
+    if (pwave) {
+        int n = 0;
+        auto one = [&](Stage &x) __attribute__((always_inline)) {
+            DM_STAMP(0, n, 0);
+            restage(n, ns, x);
+            DM_STAMP(0, n, 1);
+            // one code path for every tile (a branch here would split the accumulators'
+            // registers); the per-element test costs three VALU operations per score
+            pstep(n, cs, std::true_type{});
+            DM_STAMP(0, n, 3);
+            if (wave == 0) publish(n + 5);
+            __syncthreads();
+            n++;
+            rotate();
+        };
+        for (;;) {
+            if (!entry(n).valid) break;
+            one(stg0);
+            if (!entry(n).valid) break;
+            one(stg1);
+        }
+        __syncthreads();  // iteration N
+    } else {
+        restage(0, ns, stg0);
+        __syncthreads();
+        int n = 1;
+        rotate();
+        auto one = [&](Stage &x) __attribute__((always_inline)) {
+            DM_STAMP(1, n, 0);
+            restage(n, ns, x);
+            DM_STAMP(1, n, 1);
+            dsstep(n - 1, ps);
+            DM_STAMP(1, n, 3);
+            __syncthreads();
+            n++;
+            rotate();
+        };
+        for (;;) {
+            if (!entry(n - 1).valid) break;
+            one(stg1);
+            if (!entry(n - 1).valid) break;
+            one(stg0);
         }
     }
-    // write dK (scaled), dV: lane holds column d = 32 dt + col, rows = keys of this wavefront
-    //   32 w + 8 (i / 4) + 4 h + i % 4
+    // write dV (P waves) or dK (scaled, dS waves): lane holds column d = 32 dt + col, rows =
+    // keys 32 kw + 8 (i / 4) + 4 h + i % 4
+    uint16_t *out = pwave ? dv : dk;
+    const float f = pwave ? 1.f : scale;
 #pragma unroll
     for (int dt = 0; dt < DT32; dt++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int64_t j = j0 + wave * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-            if (j >= Tk) continue;
-            const int64_t off = ((b * Tk + j) * Hkv + kh) * D + dt * 32 + col;
-            const uint32_t kv2 = pack2<DT>(dka[dt][i] * scale, dva[dt][i]);
-            dk[off] = (uint16_t)(kv2 & 0xffffu);
-            dv[off] = (uint16_t)(kv2 >> 16);
+        for (int i = 0; i < 16; i += 2) {
+            const int64_t ja = j0 + kw * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+            const uint32_t x2 = pack2<DT>(acc[dt][i] * f, acc[dt][i + 1] * f);
+            const int64_t off = ((b * Tk + ja) * Hkv + kh) * D + dt * 32 + col;
+            if (ja < Tk) out[off] = (uint16_t)(x2 & 0xffffu);
+            if (ja + 1 < Tk) out[off + Hkv * D] = (uint16_t)(x2 >> 16);
         }
 }
 
@@ -482,40 +690,48 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         if (j0 + kDqN < kv_hi) load_tile(j0 + kDqN);
         const bool masked = PAD || j0 < full_lo || j0 + kDqN > full_hi;
         Frag8 df[2][2];
+        // straight-line bodies for unmasked tiles and for tiles with the visibility test
+        auto sweep = [&](auto masked_c) {
+            constexpr bool MASKED = decltype(masked_c)::value;
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            f32x16_t s, dp;
+            for (int t = 0; t < 2; t++) {
+                f32x16_t s, dp;
 #pragma unroll
-            for (int i = 0; i < 16; i++) s[i] = dp[i] = 0.f;
-            const uint16_t *ka = sk + (t * 32 + col) * RS + half * 8;
-            const uint16_t *va = sv + (t * 32 + col) * RS + half * 8;
+                for (int i = 0; i < 16; i++) s[i] = dp[i] = 0.f;
+                const uint16_t *ka = sk + (t * 32 + col) * RS + half * 8;
+                const uint16_t *va = sv + (t * 32 + col) * RS + half * 8;
 #pragma unroll
-            for (int st = 0; st < KSTEPS; st++) {
-                Frag8 a;
-                a.u = *(const uint4 *)(ka + st * 16);
-                s = mfma32<DT>(a, qf[st], s);
-                a.u = *(const uint4 *)(va + st * 16);
-                dp = mfma32<DT>(a, gf[st], dp);
-            }
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                float ds[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int i = 8 * u + e;
-                    float p = fast_exp2(fmaf(s[i], c2, nlse));
-                    if (masked) {
-                        const int32_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                        bool vis = j >= lo && j < hi;
-                        if constexpr (PAD) vis = vis && !pad[j];
-                        p = vis ? p : 0.f;
-                    }
-                    ds[e] = p * (dp[i] - dl);
+                for (int st = 0; st < KSTEPS; st++) {
+                    Frag8 a;
+                    a.u = *(const uint4 *)(ka + st * 16);
+                    s = mfma32<DT>(a, qf[st], s);
+                    a.u = *(const uint4 *)(va + st * 16);
+                    dp = mfma32<DT>(a, gf[st], dp);
                 }
-                df[t][u].u = make_uint4(pack2<DT>(ds[0], ds[1]), pack2<DT>(ds[2], ds[3]),
-                                        pack2<DT>(ds[4], ds[5]), pack2<DT>(ds[6], ds[7]));
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    float ds[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const int i = 8 * u + e;
+                        float p = fast_exp2(fmaf(s[i], c2, nlse));
+                        if constexpr (MASKED) {
+                            const int32_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                            bool vis = (j >= lo) & (j < hi);
+                            if constexpr (PAD) vis = vis & (pad[j < Tk ? j : Tk - 1] == 0);
+                            p = vis ? p : 0.f;
+                        }
+                        ds[e] = p * (dp[i] - dl);
+                    }
+                    df[t][u].u = make_uint4(pack2<DT>(ds[0], ds[1]), pack2<DT>(ds[2], ds[3]),
+                                            pack2<DT>(ds[4], ds[5]), pack2<DT>(ds[6], ds[7]));
+                }
             }
-        }
+        };
+        if (masked)
+            sweep(std::true_type{});
+        else
+            sweep(std::false_type{});
         // dQ^T += K^T dS^T: A = K^T by transposed reads of the row-major K tile
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -555,6 +771,12 @@ size_t mfma_bwd_workspace(const dm_attention_desc *d) {
     return mfma_bwd_takes(d) ? bwd_layout(d, nullptr, nullptr) : 0;
 }
 
+#ifdef DM_TRACE_DKDV
+extern "C" int dm_debug_trace(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(dm_trace), bytes) == hipSuccess ? 0 : 1;
+}
+#endif
+
 int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float scale,
                          const void *q, const void *k, const void *v, const void *o,
                          const float *lse, const void *d_o, void *dq, void *dk, void *dv,
@@ -562,7 +784,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     BwdWs w;
     bwd_layout(d, (char *)workspace, &w);
     const int64_t qrows = d->b * d->tq;
-    const int64_t ntiles64 = (d->tq + kRowTile - 1) / kRowTile;
+    const int64_t ntiles_r = (d->tq + kRowTile - 1) / kRowTile;
     const int64_t nkb = (d->tk + kKvBlock - 1) / kKvBlock;
     const int64_t nq = (d->tq + kDqM - 1) / kDqM;
     const int64_t nb_kv = (nkb * d->hkv * d->b + 7) / 8 * 8;
@@ -573,10 +795,10 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
 #define BWD(DT, DD)                                                                            \
     bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, oo, gg, lse, \
                                                                    delta, w);                  \
-    bwd_tiles<<<(unsigned)(d->b * ntiles64), 64, 0, st>>>(d->b, d->tq, w);                     \
+    bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
     if (m.pad) {                                                                               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
-        bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
+        bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
                                                                 qq, kk, vv, gg, delta, w,      \
                                                                 (uint16_t *)dk, (uint16_t *)dv); } \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
@@ -585,7 +807,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
                                                              (uint16_t *)dq); }                \
     } else {                                                                                   \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
-        bwd_dkdv<DT, DD, false><<<(unsigned)nb_kv, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
+        bwd_dkdv<DT, DD, false><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
                                                                  qq, kk, vv, gg, delta, w,     \
                                                                  (uint16_t *)dk, (uint16_t *)dv); } \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
