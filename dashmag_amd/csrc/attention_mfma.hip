@@ -32,9 +32,14 @@ struct Strides {
 };
 
 template <int D>
-struct FwdSmem {
+struct FwdSlot {
     uint4 k[kFwdN * Strides<D>::ROW / 8];
     uint4 v[kFwdN * Strides<D>::TR / 8];
+};
+
+template <int D>
+struct FwdSmem {
+    FwdSlot<D> slot[2];  // key / value tiles, double-buffered
     int32_t lo[4], hi[4], flo[4], fhi[4];
 };
 
@@ -133,31 +138,36 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     constexpr int RSTEP = 256 / CPR;           // rows between a thread's chunks
     const int crow = tid / CPR, ccol = tid % CPR;
     const uint32_t goff = (uint32_t)(crow * kvstride + ccol * 8) * 2;
-    uint4 kreg[NCH], vreg[NCH];
-    auto load_tile = [&](int32_t j0) {
+    // Tiles go HBM -> registers -> LDS: two register sets, a tile's loads issued two steps
+    // before its store (every call issues the same loads; tiles past the range re-read the
+    // first), two LDS slots, one barrier per step.
+    struct KvStage {
+        uint4 k[NCH], v[NCH];
+    };
+    KvStage st0, st1;
+    auto load_tile = [&](KvStage &x, int32_t j0) __attribute__((always_inline)) {
         const uint32_t base = (uint32_t)j0 * (uint32_t)kvstride * 2 + goff;
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
             const uint32_t off = base + (uint32_t)(u * RSTEP * kvstride * 2);
-            kreg[u] = buf_load16(krs, off);
-            vreg[u] = buf_load16(vrs, off);
+            x.k[u] = buf_load16(krs, off);
+            x.v[u] = buf_load16(vrs, off);
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](const KvStage &x, FwdSlot<D> &sl) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            sm.k[(crow + u * RSTEP) * (KS / 8) + ccol] = kreg[u];
-            sm.v[(crow + u * RSTEP) * (VS / 8) + ccol] = vreg[u];
+            sl.k[(crow + u * RSTEP) * (KS / 8) + ccol] = x.k[u];
+            sl.v[(crow + u * RSTEP) * (VS / 8) + ccol] = x.v[u];
         }
     };
-    const uint16_t *sk = (const uint16_t *)sm.k, *sv = (const uint16_t *)sm.v;
+    auto clampj = [&](int32_t j) { return j < kv_hi ? j : kv_lo; };
 
-    if (kv_lo < kv_hi) load_tile(kv_lo);
-    for (int32_t j0 = kv_lo; j0 < kv_hi; j0 += kFwdN) {
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (j0 + kFwdN < kv_hi) load_tile(j0 + kFwdN);
+    auto one = [&](const int32_t j0, const int sl_cur, KvStage &x) __attribute__((always_inline)) {
+        if (j0 + kFwdN < kv_hi) store_tile(x, sm.slot[sl_cur ^ 1]);
+        load_tile(x, clampj(j0 + 3 * kFwdN));
+        const uint16_t *sk = (const uint16_t *)sm.slot[sl_cur].k;
+        const uint16_t *sv = (const uint16_t *)sm.slot[sl_cur].v;
 
         // S^T for keys [j0, j0 + 64): two 32-key row tiles, their accumulation chains
         // interleaved
@@ -232,6 +242,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
                     const Frag8 a = lds_tr_frag(sv, VS, t * 32 + u * 16, dt * 32, lane);
                     acc[dt] = mfma32<DT>(a, pf[t][u], acc[dt]);
                 }
+        __syncthreads();
+    };
+    if (kv_lo < kv_hi) {
+        load_tile(st0, kv_lo);
+        store_tile(st0, sm.slot[0]);
+        load_tile(st0, clampj(kv_lo + kFwdN));
+        load_tile(st1, clampj(kv_lo + 2 * kFwdN));
+    }
+    __syncthreads();
+    for (int32_t j0 = kv_lo; j0 < kv_hi; j0 += 2 * kFwdN) {
+        one(j0, 0, st0);
+        if (j0 + kFwdN >= kv_hi) break;
+        one(j0 + kFwdN, 1, st1);
     }
 
     // finish: l over both halves, normalise, write O and lse

@@ -24,7 +24,6 @@ namespace dm {
 constexpr int kRowTile = 32;   // rows per tile of the prep's tile ranges (= the dK/dV step)
 constexpr int kKvBlock = 128;  // keys per dK/dV workgroup (32 per wavefront pair)
 constexpr int kDqM = 128;      // queries per dQ workgroup
-constexpr int kDqN = 64;       // keys per step of the dQ sweep
 
 struct BwdWs {
     float *lse2;      // [B, Tq, Hq]
@@ -569,16 +568,30 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
 // dQ
 // ------------------------------------------------------------------------------------------
 
+// Wave pairs, as the dK/dV kernel: a workgroup of 8 wavefronts takes 128 queries of one query
+// head; wavefronts w and w + 4 (one SIMD) share the queries 32 w + [0, 32). Per 32-key step,
+// wavefront w holds Q and computes S^T = K Q^T and P (masked), handing P (f32) over through LDS;
+// wavefront w + 4 holds dO and, one step behind, computes dP^T = V dO^T, dS = P (dP - delta)
+// and accumulates dQ^T += K^T dS^T. Key / value tiles rotate through three LDS slots, staged
+// two steps ahead through two register sets; one barrier per step.
+constexpr int kDqStep = 32;  // keys per step
+
+template <int D>
+struct DqSlot {
+    uint4 k[kDqStep * BwdStrides<D>::ROW / 8];
+    uint4 kt[kDqStep * BwdStrides<D>::TR / 8];
+    uint4 v[kDqStep * BwdStrides<D>::ROW / 8];
+};
+
 template <int D>
 struct DqSmem {
-    uint4 k[kDqN * BwdStrides<D>::ROW / 8];
-    uint4 v[kDqN * BwdStrides<D>::ROW / 8];
-    uint4 kt[kDqN * BwdStrides<D>::TR / 8];
+    DqSlot<D> slot[3];
+    float4 p[2][4][4][64];  // [step parity][query block][i / 4][lane]
     int32_t lo[4], hi[4], flo[4], fhi[4];
 };
 
 template <int DT, int D, bool PAD>
-__global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t Hq, int64_t Hkv,
+__global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t Hq, int64_t Hkv,
                                                  float scale, const uint16_t *__restrict__ q,
                                                  const uint16_t *__restrict__ k,
                                                  const uint16_t *__restrict__ v,
@@ -598,9 +611,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     const int64_t tile = ntiles - 1 - (work / Hq) % ntiles;
     const int64_t b = work / (Hq * ntiles);
     const int64_t kh = h / (Hq / Hkv);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool pwave = wave < 4;  // computes P; the other half dS and dQ
+    const int qw = wave & 3;      // the query block of this wavefront
     const int col = lane & 31, half = lane >> 5;
-    const int64_t qi = tile * kDqM + wave * 32 + col;
+    const int64_t qi = tile * kDqM + qw * 32 + col;
     const bool qvalid = qi < Tq;
     int32_t lo = 0, hi = 0;
     float lse2 = INFINITY, dl = 0.f;
@@ -611,7 +627,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         dl = delta[(b * Tq + qi) * Hq + h];
     }
     if (lse2 == INFINITY) hi = lo;  // a query that sees no key: dq = 0
-    {
+    if (pwave) {
         int32_t wl = lo < hi ? lo : INT32_MAX, wh = lo < hi ? hi : INT32_MIN;
         int32_t rfl = (qvalid && lo < hi) ? lo : (qvalid ? INT32_MAX : INT32_MIN);
         int32_t rfh = (qvalid && lo < hi) ? hi : (qvalid ? INT32_MIN : INT32_MAX);
@@ -623,26 +639,25 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
             rfh = min(rfh, __shfl_xor(rfh, off, 64));
         }
         if (lane == 0) {
-            sm.lo[wave] = wl;
-            sm.hi[wave] = wh;
-            sm.flo[wave] = rfl;
-            sm.fhi[wave] = rfh;
+            sm.lo[qw] = wl;
+            sm.hi[qw] = wh;
+            sm.flo[qw] = rfl;
+            sm.fhi[qw] = rfh;
         }
     }
     __syncthreads();
     const int32_t kv_lo = min(min(sm.lo[0], sm.lo[1]), min(sm.lo[2], sm.lo[3]));
     const int32_t kv_hi = max(max(sm.hi[0], sm.hi[1]), max(sm.hi[2], sm.hi[3]));
-    const int32_t full_lo = max(max(sm.flo[0], sm.flo[1]), max(sm.flo[2], sm.flo[3]));
-    const int32_t full_hi = min(min(sm.fhi[0], sm.fhi[1]), min(sm.fhi[2], sm.fhi[3]));
+    const int32_t span = hi - lo;  // visible iff (j - lo) < span, unsigned
 
-    Frag8 qf[KSTEPS], gf[KSTEPS];
+    // Q (P waves) or dO (dS waves) of this lane's query as the B operand: col = query, k = d
+    Frag8 bf[KSTEPS];
     {
+        const uint16_t *src = pwave ? q : d_o;
         const int64_t off = ((b * Tq + qi) * Hq + h) * D + half * 8;
 #pragma unroll
-        for (int s = 0; s < KSTEPS; s++) {
-            qf[s].u = qvalid ? *(const uint4 *)(q + off + s * 16) : make_uint4(0, 0, 0, 0);
-            gf[s].u = qvalid ? *(const uint4 *)(d_o + off + s * 16) : make_uint4(0, 0, 0, 0);
-        }
+        for (int s = 0; s < KSTEPS; s++)
+            bf[s].u = qvalid ? *(const uint4 *)(src + off + s * 16) : make_uint4(0, 0, 0, 0);
     }
     f32x16_t acc[DT32];
 #pragma unroll
@@ -657,104 +672,172 @@ __global__ __launch_bounds__(256, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + (b * Tk * Hkv + kh) * D, kvbytes);
     const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
 
-    constexpr int CPR = D / 8, NCH = kDqN * CPR / 256, RSTEP = 256 / CPR;
-    const int crow = tid / CPR, ccol = tid % CPR;
-    const uint32_t goff = (uint32_t)(crow * kvstride + ccol * 8) * 2;
-    uint4 kreg[NCH], vreg[NCH];
-    auto load_tile = [&](int32_t j0) {
-        const uint32_t base = (uint32_t)j0 * (uint32_t)kvstride * 2 + goff;
+    // staging: a tile's K and V rows in 16-byte chunks over the 512 threads, two register
+    // sets, every call the same loads (tiles past the range re-read the first)
+    constexpr int CPR = D / 8, NCH = (kDqStep * CPR + 511) / 512, RSTEP = 512 / CPR;
+    const int crow = tid / CPR, ccol = tid % CPR;  // crow >= kDqStep: no chunk (D = 64)
+    struct KvStage {
+        uint4 k[NCH], v[NCH];
+    };
+    KvStage st0, st1;
+    const int nsteps = kv_lo < kv_hi ? (kv_hi - kv_lo + kDqStep - 1) / kDqStep : 0;
+    auto load = [&](KvStage &x, int n) __attribute__((always_inline)) {
+        const int32_t j0 = kv_lo + (n < nsteps ? n : 0) * kDqStep;
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            const uint32_t off = base + (uint32_t)(u * RSTEP * kvstride * 2);
-            kreg[u] = buf_load16(krs, off);
-            vreg[u] = buf_load16(vrs, off);
+            const int r = (crow + u * RSTEP) & (kDqStep - 1);
+            const uint32_t off = (uint32_t)((j0 + r) * kvstride + ccol * 8) * 2;
+            x.k[u] = buf_load16(krs, off);
+            x.v[u] = buf_load16(vrs, off);
         }
     };
-    auto store_tile = [&]() {
+    auto store = [&](const KvStage &x, DqSlot<D> &sl) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
             const int r = crow + u * RSTEP;
-            sm.k[r * (RS / 8) + ccol] = kreg[u];
-            sm.kt[r * (TS / 8) + ccol] = kreg[u];
-            sm.v[r * (RS / 8) + ccol] = vreg[u];
+            if (r >= kDqStep) break;
+            sl.k[r * (RS / 8) + ccol] = x.k[u];
+            sl.kt[r * (TS / 8) + ccol] = x.k[u];
+            sl.v[r * (RS / 8) + ccol] = x.v[u];
         }
     };
-    const uint16_t *sk = (const uint16_t *)sm.k, *sv = (const uint16_t *)sm.v;
-    const uint16_t *skt = (const uint16_t *)sm.kt;
 
-    if (kv_lo < kv_hi) load_tile(kv_lo);
-    for (int32_t j0 = kv_lo; j0 < kv_hi; j0 += kDqN) {
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (j0 + kDqN < kv_hi) load_tile(j0 + kDqN);
-        const bool masked = PAD || j0 < full_lo || j0 + kDqN > full_hi;
-        Frag8 df[2][2];
-        // straight-line bodies for unmasked tiles and for tiles with the visibility test
-        auto sweep = [&](auto masked_c) {
-            constexpr bool MASKED = decltype(masked_c)::value;
+    // P waves, step n (keys j0 = kv_lo + 32 n): S^T = K Q^T, P into LDS
+    auto pstep = [&](const int n, const int cslot) __attribute__((always_inline)) {
+        const int32_t j0 = kv_lo + n * kDqStep;
+        const uint16_t *ka = (const uint16_t *)sm.slot[cslot].k + col * RS + half * 8;
+        f32x16_t s;
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                f32x16_t s, dp;
+        for (int i = 0; i < 16; i++) s[i] = 0.f;
 #pragma unroll
-                for (int i = 0; i < 16; i++) s[i] = dp[i] = 0.f;
-                const uint16_t *ka = sk + (t * 32 + col) * RS + half * 8;
-                const uint16_t *va = sv + (t * 32 + col) * RS + half * 8;
-#pragma unroll
-                for (int st = 0; st < KSTEPS; st++) {
-                    Frag8 a;
-                    a.u = *(const uint4 *)(ka + st * 16);
-                    s = mfma32<DT>(a, qf[st], s);
-                    a.u = *(const uint4 *)(va + st * 16);
-                    dp = mfma32<DT>(a, gf[st], dp);
-                }
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    float ds[8];
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const int i = 8 * u + e;
-                        float p = fast_exp2(fmaf(s[i], c2, nlse));
-                        if constexpr (MASKED) {
-                            const int32_t j = j0 + t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                            bool vis = (j >= lo) & (j < hi);
-                            if constexpr (PAD) vis = vis & (pad[j < Tk ? j : Tk - 1] == 0);
-                            p = vis ? p : 0.f;
-                        }
-                        ds[e] = p * (dp[i] - dl);
-                    }
-                    df[t][u].u = make_uint4(pack2<DT>(ds[0], ds[1]), pack2<DT>(ds[2], ds[3]),
-                                            pack2<DT>(ds[4], ds[5]), pack2<DT>(ds[6], ds[7]));
-                }
-            }
-        };
-        if (masked)
-            sweep(std::true_type{});
-        else
-            sweep(std::false_type{});
-        // dQ^T += K^T dS^T: A = K^T by transposed reads of the row-major K tile
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int dt = 0; dt < DT32; dt++) {
-                    const Frag8 a = lds_tr_frag(skt, TS, t * 32 + u * 16, dt * 32, lane);
-                    acc[dt] = mfma32<DT>(a, df[t][u], acc[dt]);
-                }
-    }
-    if (!qvalid) return;
-    uint16_t *op = dq + ((b * Tq + qi) * Hq + h) * D;
-#pragma unroll
-    for (int dt = 0; dt < DT32; dt++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            const int d = dt * 32 + g4 * 8 + half * 4;
-            uint2 wv;
-            wv.x = pack2<DT>(acc[dt][g4 * 4 + 0] * scale, acc[dt][g4 * 4 + 1] * scale);
-            wv.y = pack2<DT>(acc[dt][g4 * 4 + 2] * scale, acc[dt][g4 * 4 + 3] * scale);
-            *(uint2 *)(op + d) = wv;
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(ka + st * 16);
+            s = mfma32<DT>(a, bf[st], s);
         }
+        // element i is key j0 + 8 (i / 4) + 4 h + i % 4
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            float p4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * jj + e;
+                const int32_t j = j0 + jj * 8 + half * 4 + e;
+                float x = fast_exp2(fmaf(s[i], c2, nlse));
+                bool vis = (uint32_t)(j - lo) < (uint32_t)span;
+                if constexpr (PAD) vis = vis & (pad[j < Tk ? j : Tk - 1] == 0);
+                p4[e] = vis ? x : 0.f;
+            }
+            sm.p[n & 1][qw][jj][lane] = make_float4(p4[0], p4[1], p4[2], p4[3]);
+        }
+    };
+    // dS waves, step m: dP^T = V dO^T, dS = P (dP - delta), dQ^T += K^T dS^T
+    auto dsstep = [&](const int m, const int mslot) __attribute__((always_inline)) {
+        const DqSlot<D> &sl = sm.slot[mslot];
+        const uint16_t *va = (const uint16_t *)sl.v + col * RS + half * 8;
+        const uint16_t *skt = (const uint16_t *)sl.kt;
+        f32x16_t dp;
+#pragma unroll
+        for (int i = 0; i < 16; i++) dp[i] = 0.f;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(va + st * 16);
+            dp = mfma32<DT>(a, bf[st], dp);
+        }
+        float ds[16];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const float4 p4 = sm.p[m & 1][qw][jj][lane];
+            ds[4 * jj + 0] = p4.x * (dp[4 * jj + 0] - dl);
+            ds[4 * jj + 1] = p4.y * (dp[4 * jj + 1] - dl);
+            ds[4 * jj + 2] = p4.z * (dp[4 * jj + 2] - dl);
+            ds[4 * jj + 3] = p4.w * (dp[4 * jj + 3] - dl);
+        }
+        Frag8 df[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            df[u].u = make_uint4(pack2<DT>(ds[8 * u], ds[8 * u + 1]),
+                                 pack2<DT>(ds[8 * u + 2], ds[8 * u + 3]),
+                                 pack2<DT>(ds[8 * u + 4], ds[8 * u + 5]),
+                                 pack2<DT>(ds[8 * u + 6], ds[8 * u + 7]));
+        // A = K^T by transposed reads of the row-major K tile
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int dt = 0; dt < DT32; dt++) {
+                const Frag8 a = lds_tr_frag(skt, TS, u * 16, dt * 32, lane);
+                acc[dt] = mfma32<DT>(a, df[u], acc[dt]);
+            }
+    };
+
+    // prologue: step 0 into slot 0, steps 1 and 2 loading into the two register sets
+    load(st0, 0);
+    if (nsteps > 0) store(st0, sm.slot[0]);
+    load(st0, 1);
+    load(st1, 2);
+    __syncthreads();
+    // iterations n = 0 .. nsteps: the P waves compute step n (n < nsteps), the dS waves step
+    // n - 1 (n >= 1); each iteration stores step n + 1 from its set and loads step n + 3
+    int cs = 0, ns = 1, ps = 2;
+    auto rotate = [&]() __attribute__((always_inline)) {
+        const int t = ps;
+        ps = cs;
+        cs = ns;
+        ns = t;
+    };
+    auto restage = [&](const int n, KvStage &x) __attribute__((always_inline)) {
+        if (n + 1 < nsteps) store(x, sm.slot[ns]);
+        load(x, n + 3);
+    };
+    if (pwave) {
+        int n = 0;
+        auto one = [&](KvStage &x) __attribute__((always_inline)) {
+            restage(n, x);
+            pstep(n, cs);
+            __syncthreads();
+            n++;
+            rotate();
+        };
+        for (;;) {
+            if (n >= nsteps) break;
+            one(st0);
+            if (n >= nsteps) break;
+            one(st1);
+        }
+        __syncthreads();  // iteration nsteps
+    } else {
+        restage(0, st0);
+        __syncthreads();
+        int n = 1;
+        rotate();
+        auto one = [&](KvStage &x) __attribute__((always_inline)) {
+            restage(n, x);
+            dsstep(n - 1, ps);
+            __syncthreads();
+            n++;
+            rotate();
+        };
+        for (;;) {
+            if (n > nsteps) break;
+            one(st1);
+            if (n > nsteps) break;
+            one(st0);
+        }
+        if (qvalid) {
+            uint16_t *op = dq + ((b * Tq + qi) * Hq + h) * D;
+#pragma unroll
+            for (int dt = 0; dt < DT32; dt++)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int d = dt * 32 + g4 * 8 + half * 4;
+                    uint2 wv;
+                    wv.x = pack2<DT>(acc[dt][g4 * 4 + 0] * scale, acc[dt][g4 * 4 + 1] * scale);
+                    wv.y = pack2<DT>(acc[dt][g4 * 4 + 2] * scale, acc[dt][g4 * 4 + 3] * scale);
+                    *(uint2 *)(op + d) = wv;
+                }
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -802,7 +885,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
                                                                 qq, kk, vv, gg, delta, w,      \
                                                                 (uint16_t *)dk, (uint16_t *)dv); } \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
-        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq,  \
+        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq,  \
                                                              kk, vv, gg, delta, w,             \
                                                              (uint16_t *)dq); }                \
     } else {                                                                                   \
@@ -811,7 +894,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
                                                                  qq, kk, vv, gg, delta, w,     \
                                                                  (uint16_t *)dk, (uint16_t *)dv); } \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
-        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 256, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
+        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
                                                               kk, vv, gg, delta, w,            \
                                                               (uint16_t *)dq); }               \
     }
