@@ -171,12 +171,15 @@ def main():
     del c2
     if want("attn4096"):
         c = syn.config2_single(dev)
-        ms, mf, mb, _, _ = bench_attention(torch, dm, ops, lib, c, args.steps, args.warmup)
+        ms, mf, mb, _, kms4 = bench_attention(torch, dm, ops, lib, c, args.steps, args.warmup)
         P = syn.visible_pairs([4096])
         secondary["attention_fwd_bwd_T4096"] = dict(
             unit="TFLOP/s", value=14 * P * 128 * 32 / ms / 1e9, ms_per_step=ms,
             fwd_tflops=4 * P * 128 * 32 / mf / 1e9, bwd_tflops=10 * P * 128 * 32 / mb / 1e9,
-            frac_of_bf16_peak=14 * P * 128 * 32 / ms / 1e9 / BF16_PEAK_TFLOPS)
+            frac_of_bf16_peak=14 * P * 128 * 32 / ms / 1e9 / BF16_PEAK_TFLOPS,
+            kernel_us={k: round(v[0] * 1e3, 2) for k, v in kms4.items()})
+        print("attention T=4096 kernels: " + ", ".join(
+            f"{k} {v[0] * 1e3:.1f} us" for k, v in kms4.items()), file=sys.stderr, flush=True)
         print(f"attention T=4096: {ms:.3f} ms/step, "
               f"{secondary['attention_fwd_bwd_T4096']['value']:.1f} TFLOP/s", file=sys.stderr,
               flush=True)

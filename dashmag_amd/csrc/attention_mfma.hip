@@ -64,14 +64,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     const int64_t Tq = m.tq, Tk = m.tk;
     const int64_t ntiles = (Tq + kFwdM - 1) / kFwdM;
     const int64_t nwork = ntiles * Hq * B;
-    const int64_t work = xcd_remap(blockIdx.x, gridDim.x);
+    const int64_t work = blockIdx.x;
     if (work >= nwork) return;
     // heads fastest (a key-value group's query heads share K/V in one L2), then tiles from the
     // longest (last) down, then batch
-    const int64_t h = work % Hq;
+    // the key-value head is the fastest index: consecutive blocks go to consecutive XCDs, so
+    // an XCD (with Hkv = 8) holds one key-value head, whose keys and values stay in its L2,
+    // and every XCD gets query tiles of every length (the longest first)
+    const int64_t kh = work % Hkv;
+    const int64_t h = kh * (Hq / Hkv) + (work / Hkv) % (Hq / Hkv);
     const int64_t tile = ntiles - 1 - (work / Hq) % ntiles;
     const int64_t b = work / (Hq * ntiles);
-    const int64_t kh = h / (Hq / Hkv);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
     const int64_t qi = tile * kFwdM + wave * 32 + col;  // this lane's query row

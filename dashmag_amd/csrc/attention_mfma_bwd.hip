@@ -30,7 +30,33 @@ struct BwdWs {
     int32_t *rlo;     // [B, Tq]
     int32_t *rhi;     // [B, Tq]
     int32_t *trange;  // [B, ntiles, 4]: union lo, union hi, full lo, full hi
+    int hsplit;       // dK/dV workgroups per (key block, key-value head): query heads split
+    float *kvpart;    // hsplit > 1: [hsplit][2][B, Tk, Hkv, D] f32 partial dK (scaled), dV
+    int32_t *kbsteps; // [B, nkb + 1]: query tiles that see each key block
+    int32_t *order;   // [nwork]: dK/dV work items, the most steps first
 };
+
+// When there are few key blocks (a single long sequence), the dK/dV grid is too small to keep
+// the chip busy and its causal work is uneven: the query heads of a group are then split over
+// up to 4 workgroups per key block (at least two workgroups per compute unit), which write f32
+// partials that a small kernel sums in a fixed order.
+static int dkdv_hsplit(const dm_attention_desc *d) {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    const int64_t group = d->hq / d->hkv;
+    const int64_t nwork = (d->tk + kKvBlock - 1) / kKvBlock * d->hkv * d->b;
+    int split = 1;
+    while (split < 4 && group % (2 * split) == 0 && nwork * split < 2 * cus) split *= 2;
+    return split;
+}
 
 static size_t bwd_layout(const dm_attention_desc *d, char *base, BwdWs *w) {
     const int64_t rows = d->b * d->tq * d->hq, qrows = d->b * d->tq;
@@ -46,6 +72,12 @@ static size_t bwd_layout(const dm_attention_desc *d, char *base, BwdWs *w) {
     x.rlo = (int32_t *)take(qrows * 4);
     x.rhi = (int32_t *)take(qrows * 4);
     x.trange = (int32_t *)take(d->b * ntiles * 4 * 4);
+    x.hsplit = dkdv_hsplit(d);
+    x.kvpart = x.hsplit > 1 ? (float *)take((size_t)x.hsplit * 2 * d->b * d->tk * d->hkv * d->d * 4)
+                            : nullptr;
+    const int64_t nkb = (d->tk + kKvBlock - 1) / kKvBlock;
+    x.kbsteps = (int32_t *)take(d->b * (nkb + 1) * 4);
+    x.order = (int32_t *)take(nkb * d->hkv * d->b * x.hsplit * 4);
     if (w) *w = x;
     return off;
 }
@@ -129,6 +161,66 @@ __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) 
     }
 }
 
+// The dK/dV work list, longest first (a workgroup's time is its number of steps; running the
+// longest first keeps the compute units evenly loaded to the end). One workgroup: per batch
+// row, a difference array over the key blocks counts the tiles whose union interval reaches
+// each block; the items are then placed by a counting sort on their step counts, descending.
+// (Items with equal counts land in any order: the order only schedules, it does not change
+// what a workgroup computes.)
+constexpr int kOrderBuckets = 1024;
+
+__global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t Tk, int64_t Hkv,
+                                                  int64_t group, BwdWs w) {
+    __shared__ int32_t hist[kOrderBuckets];
+    const int tid = threadIdx.x;
+    const int64_t ntiles = (Tq + kRowTile - 1) / kRowTile;
+    const int64_t nkb = (Tk + kKvBlock - 1) / kKvBlock;
+    const int hs = w.hsplit;
+    const int64_t per = group / hs;  // query heads per work item
+    // difference array per batch row, then its prefix sum (one thread per row)
+    for (int64_t x = tid; x < B * (nkb + 1); x += 1024) w.kbsteps[x] = 0;
+    __syncthreads();
+    for (int64_t x = tid; x < B * ntiles; x += 1024) {
+        const int64_t b = x / ntiles;
+        const int32_t *r = w.trange + x * 4;
+        if (r[0] < r[1]) {
+            atomicAdd(&w.kbsteps[b * (nkb + 1) + r[0] / kKvBlock], 1);
+            atomicAdd(&w.kbsteps[b * (nkb + 1) + (r[1] - 1) / kKvBlock + 1], -1);
+        }
+    }
+    __syncthreads();
+    for (int64_t b = tid; b < B; b += 1024) {
+        int32_t run = 0;
+        for (int64_t kb = 0; kb <= nkb; kb++) {
+            run += w.kbsteps[b * (nkb + 1) + kb];
+            w.kbsteps[b * (nkb + 1) + kb] = run;
+        }
+    }
+    __syncthreads();
+    // bucket = min(steps, kOrderBuckets - 1), steps = tiles x heads per item
+    for (int x = tid; x < kOrderBuckets; x += 1024) hist[x] = 0;
+    __syncthreads();
+    const int64_t nwork = nkb * Hkv * B * hs;
+    auto bucket = [&](int64_t item) {
+        const int64_t kb = (item / (Hkv * hs)) % nkb, b = item / (Hkv * hs * nkb);
+        const int64_t steps = (int64_t)w.kbsteps[b * (nkb + 1) + kb] * per;
+        return (int)(steps < kOrderBuckets - 1 ? steps : kOrderBuckets - 1);
+    };
+    for (int64_t x = tid; x < nwork; x += 1024) atomicAdd(&hist[bucket(x)], 1);
+    __syncthreads();
+    if (tid == 0) {  // exclusive offsets, the largest bucket first
+        int32_t run = 0;
+        for (int x = kOrderBuckets - 1; x >= 0; x--) {
+            const int32_t c = hist[x];
+            hist[x] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int64_t x = tid; x < nwork; x += 1024) w.order[atomicAdd(&hist[bucket(x)], 1)] = (int32_t)x;
+
+}
+
 // ------------------------------------------------------------------------------------------
 // dK, dV
 // ------------------------------------------------------------------------------------------
@@ -198,11 +290,16 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     constexpr int KSTEPS = D / 16, DT32 = D / 32;
     const int64_t Tq = m.tq, Tk = m.tk;
     const int64_t nkb = (Tk + kKvBlock - 1) / kKvBlock;
-    const int64_t nwork = nkb * Hkv * B;
-    const int64_t work = xcd_remap(blockIdx.x, gridDim.x);
-    if (work >= nwork) return;
-    const int64_t kh = work % Hkv, kb = (work / Hkv) % nkb, b = work / (Hkv * nkb);
+    const int hs = w.hsplit;
+    const int64_t nwork = nkb * Hkv * B * hs;
+    // the key-value head is the fastest index (an XCD holds one, with Hkv = 8), then the part of
+    // the query heads, then the key block (the longest first under a causal mask)
+    if ((int64_t)blockIdx.x >= nwork) return;
+    const int64_t work = w.order[blockIdx.x];
+    const int64_t kh = work % Hkv, part = (work / Hkv) % hs;
+    const int64_t kb = (work / (Hkv * hs)) % nkb, b = work / (Hkv * hs * nkb);
     const int64_t group = Hq / Hkv;
+    const int64_t h_first = kh * group + part * (group / hs);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool pwave = wave < 4;  // computes P and dV; the other half dS and dK
@@ -238,7 +335,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     // A wavefront walks them 64 tiles at a time: one vector load of the tiles' ranges and two
     // ballots give the seeing tiles and the ones needing the per-element mask as bit masks, so
     // a step costs no memory round trip.
-    const int32_t hend = (int32_t)((kh + 1) * group);
+    const int32_t hend = (int32_t)(h_first + group / hs);
     struct TileIter {
         int32_t h, t;       // current step (h == hend: done)
         int32_t c0;         // first tile of the current 64-tile chunk
@@ -275,7 +372,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
         }
     };
     auto start = [&](TileIter &it) {
-        it.h = (int32_t)(kh * group);
+        it.h = (int32_t)h_first;
         it.c0 = 0;
         it.t = -1;
         if (j0 >= Tk) {
@@ -374,10 +471,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     // prologue: step 0 into slot 0, steps 1 and 2 loading into the two register sets
     {
         const Entry e0 = entry(0), e1 = entry(1), e2 = entry(2);
-        load(stg0, e0.valid ? e0.h : kh * group, e0.valid ? e0.t : 0);
+        load(stg0, e0.valid ? e0.h : h_first, e0.valid ? e0.t : 0);
         if (e0.valid) store(stg0, sm.slot[0]);
-        load(stg0, e1.valid ? e1.h : kh * group, e1.valid ? e1.t : 0);
-        load(stg1, e2.valid ? e2.h : kh * group, e2.valid ? e2.t : 0);
+        load(stg0, e1.valid ? e1.h : h_first, e1.valid ? e1.t : 0);
+        load(stg1, e2.valid ? e2.h : h_first, e2.valid ? e2.t : 0);
     }
     __syncthreads();
 
@@ -387,7 +484,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
         if (entry(n + 1).valid) store(x, sm.slot[nslot]);
         const Entry e = entry(n + 3);
         // a step past the last loads the group's first tile again (the same loads every call)
-        load(x, e.valid ? e.h : kh * group, e.valid ? e.t : 0);
+        load(x, e.valid ? e.h : h_first, e.valid ? e.t : 0);
     };
     // P waves, step n: S = Q K^T, P (handed over in LDS), dV += P^T dO
     auto pstep = [&](const int n, const int cslot, auto masked_c) __attribute__((always_inline)) {
@@ -550,18 +647,53 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     }
     // write dV (P waves) or dK (scaled, dS waves): lane holds column d = 32 dt + col, rows =
     // keys 32 kw + 8 (i / 4) + 4 h + i % 4
-    uint16_t *out = pwave ? dv : dk;
     const float f = pwave ? 1.f : scale;
+    if (hs == 1) {
+        uint16_t *out = pwave ? dv : dk;
 #pragma unroll
-    for (int dt = 0; dt < DT32; dt++)
+        for (int dt = 0; dt < DT32; dt++)
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            const int64_t ja = j0 + kw * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-            const uint32_t x2 = pack2<DT>(acc[dt][i] * f, acc[dt][i + 1] * f);
-            const int64_t off = ((b * Tk + ja) * Hkv + kh) * D + dt * 32 + col;
-            if (ja < Tk) out[off] = (uint16_t)(x2 & 0xffffu);
-            if (ja + 1 < Tk) out[off + Hkv * D] = (uint16_t)(x2 >> 16);
+            for (int i = 0; i < 16; i += 2) {
+                const int64_t ja = j0 + kw * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                const uint32_t x2 = pack2<DT>(acc[dt][i] * f, acc[dt][i + 1] * f);
+                const int64_t off = ((b * Tk + ja) * Hkv + kh) * D + dt * 32 + col;
+                if (ja < Tk) out[off] = (uint16_t)(x2 & 0xffffu);
+                if (ja + 1 < Tk) out[off + Hkv * D] = (uint16_t)(x2 >> 16);
+            }
+    } else {
+        // f32 partial of this part: [part][dK = 0, dV = 1][B, Tk, Hkv, D]
+        const int64_t n = B * Tk * Hkv * D;
+        float *out = w.kvpart + (part * 2 + (pwave ? 1 : 0)) * n;
+#pragma unroll
+        for (int dt = 0; dt < DT32; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int64_t ja = j0 + kw * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                if (ja < Tk) out[((b * Tk + ja) * Hkv + kh) * D + dt * 32 + col] = acc[dt][i] * f;
+            }
+    }
+}
+
+// dK, dV = the sum of the parts' f32 partials, in part order, in the dtype.
+template <int DT>
+__global__ __launch_bounds__(256) void bwd_kv_reduce(int64_t n, int hs, const float *__restrict__ part,
+                                                     uint16_t *__restrict__ dk,
+                                                     uint16_t *__restrict__ dv) {
+    const int64_t i4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // 4 elements per thread
+    if (i4 >= n) return;
+#pragma unroll
+    for (int which = 0; which < 2; which++) {
+        float4 s = *(const float4 *)(part + which * n + i4);
+        for (int p = 1; p < hs; p++) {
+            const float4 x = *(const float4 *)(part + (p * 2 + which) * n + i4);
+            s.x += x.x;
+            s.y += x.y;
+            s.z += x.z;
+            s.w += x.w;
         }
+        uint16_t *out = which ? dv : dk;
+        *(uint2 *)(out + i4) = make_uint2(pack2<DT>(s.x, s.y), pack2<DT>(s.z, s.w));
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -605,12 +737,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     const int64_t Tq = m.tq, Tk = m.tk;
     const int64_t ntiles = (Tq + kDqM - 1) / kDqM;
     const int64_t nwork = ntiles * Hq * B;
-    const int64_t work = xcd_remap(blockIdx.x, gridDim.x);
+    const int64_t work = blockIdx.x;
     if (work >= nwork) return;
-    const int64_t h = work % Hq;
+    // the key-value head is the fastest index: consecutive blocks go to consecutive XCDs, so
+    // an XCD (with Hkv = 8) holds one key-value head, whose keys and values stay in its L2,
+    // and every XCD gets query tiles of every length (the longest first)
+    const int64_t kh = work % Hkv;
+    const int64_t h = kh * (Hq / Hkv) + (work / Hkv) % (Hq / Hkv);
     const int64_t tile = ntiles - 1 - (work / Hq) % ntiles;
     const int64_t b = work / (Hq * ntiles);
-    const int64_t kh = h / (Hq / Hkv);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool pwave = wave < 4;  // computes P; the other half dS and dQ
@@ -870,8 +1005,8 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     const int64_t ntiles_r = (d->tq + kRowTile - 1) / kRowTile;
     const int64_t nkb = (d->tk + kKvBlock - 1) / kKvBlock;
     const int64_t nq = (d->tq + kDqM - 1) / kDqM;
-    const int64_t nb_kv = (nkb * d->hkv * d->b + 7) / 8 * 8;
-    const int64_t nb_q = (nq * d->hq * d->b + 7) / 8 * 8;
+    const int64_t nb_kv = nkb * d->hkv * d->b * w.hsplit;
+    const int64_t nb_q = nq * d->hq * d->b;
     if (nb_kv >= (1ll << 31) || nb_q >= (1ll << 31)) return refuse("attention_backward: too large");
     const uint16_t *qq = (const uint16_t *)q, *kk = (const uint16_t *)k, *vv = (const uint16_t *)v;
     const uint16_t *oo = (const uint16_t *)o, *gg = (const uint16_t *)d_o;
@@ -879,6 +1014,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, oo, gg, lse, \
                                                                    delta, w);                  \
     bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
+    bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, w);              \
     if (m.pad) {                                                                               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
@@ -904,6 +1040,16 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
         if (d->d == 64) { BWD(DM_F16, 64); } else { BWD(DM_F16, 128); }
     }
 #undef BWD
+    if (w.hsplit > 1) {
+        const int64_t n = d->b * d->tk * d->hkv * d->d;  // a multiple of 4 (D is 64 or 128)
+        const unsigned blocks = (unsigned)((n / 4 + 255) / 256);
+        if (d->dtype == DM_BF16)
+            bwd_kv_reduce<DM_BF16><<<blocks, 256, 0, st>>>(n, w.hsplit, w.kvpart, (uint16_t *)dk,
+                                                         (uint16_t *)dv);
+        else
+            bwd_kv_reduce<DM_F16><<<blocks, 256, 0, st>>>(n, w.hsplit, w.kvpart, (uint16_t *)dk,
+                                                        (uint16_t *)dv);
+    }
     probe_add(DM_PROBE_ATTN_BWD_MFMA, 4);
     DM_LAUNCH_CHECK("attention_backward: MFMA launch");
     return DM_OK;

@@ -154,11 +154,4 @@ __device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_
     return make_uint4(x[0], x[1], x[2], x[3]);
 }
 
-// Linear block index remapped so that consecutive logical work items land on one XCD (block
-// b runs on XCD b % 8): XCD x takes logical items [x * per, (x + 1) * per).
-__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nblocks) {
-    const int64_t per = (nblocks + 7) / 8;
-    return (b % 8) * per + b / 8;
-}
-
 }  // namespace dm
