@@ -487,8 +487,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
         load(x, e.valid ? e.h : h_first, e.valid ? e.t : 0);
     };
     // P waves, step n: S = Q K^T, P (handed over in LDS), dV += P^T dO
-    auto pstep = [&](const int n, const int cslot, auto masked_c) __attribute__((always_inline)) {
-        constexpr bool MASKED = decltype(masked_c)::value;
+    auto pstep = [&](const int n, const int cslot, const bool masked_flag)
+                     __attribute__((always_inline)) {
         const DkdvSlot<D> &sl = sm.slot[cslot];
         const uint16_t *sq = (const uint16_t *)sl.q, *sgt = (const uint16_t *)sl.gt;
         f32x16_t s;
@@ -501,33 +501,44 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
             a.u = *(const uint4 *)(qa + st * 16);
             s = mfma32<DT>(a, bf[st], s);
         }
-        // P = exp2(S c - lse2); element i is query 8 (i / 4) + 4 h + i % 4
+        // P = exp2(S c - lse2); element i is query 8 (i / 4) + 4 h + i % 4. The per-element
+        // visibility test runs only on tiles the intervals cut (a branch around this VALU work
+        // only; the products stay on one path)
         float p[16];
+        auto probs = [&](auto cut_c) __attribute__((always_inline)) {
+            constexpr bool CUT = decltype(cut_c)::value;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int r0 = j * 8 + half * 4;
-            const float4 l4 = *(const float4 *)(sl.lse2 + r0);
-            const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-            int lo4[4] = {0, 0, 0, 0}, hi4[4] = {0, 0, 0, 0};
-            if constexpr (MASKED) {
-                // rows hold lo and hi - lo: key visible iff (key - lo) < (hi - lo) unsigned
-                const int4 a4 = *(const int4 *)(sl.rlo + r0);
-                const int4 b4 = *(const int4 *)(sl.rhi + r0);
-                lo4[0] = a4.x; lo4[1] = a4.y; lo4[2] = a4.z; lo4[3] = a4.w;
-                hi4[0] = b4.x; hi4[1] = b4.y; hi4[2] = b4.z; hi4[3] = b4.w;
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float x = fast_exp2(fmaf(s[4 * j + e], c2, -lv[e]));
-                if constexpr (MASKED) {
-                    const bool vis = (uint32_t)(mkey - lo4[e]) < (uint32_t)hi4[e];
-                    x = vis ? x : 0.f;
+            for (int j = 0; j < 4; j++) {
+                const int r0 = j * 8 + half * 4;
+                const float4 l4 = *(const float4 *)(sl.lse2 + r0);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                int lo4[4] = {0, 0, 0, 0}, hi4[4] = {0, 0, 0, 0};
+                if constexpr (CUT) {
+                    // rows hold lo and hi - lo: key visible iff (key - lo) < (hi - lo) unsigned
+                    const int4 a4 = *(const int4 *)(sl.rlo + r0);
+                    const int4 b4 = *(const int4 *)(sl.rhi + r0);
+                    lo4[0] = a4.x; lo4[1] = a4.y; lo4[2] = a4.z; lo4[3] = a4.w;
+                    hi4[0] = b4.x; hi4[1] = b4.y; hi4[2] = b4.z; hi4[3] = b4.w;
                 }
-                p[4 * j + e] = x;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x = fast_exp2(fmaf(s[4 * j + e], c2, -lv[e]));
+                    if constexpr (CUT) {
+                        const bool vis = (uint32_t)(mkey - lo4[e]) < (uint32_t)hi4[e];
+                        x = vis ? x : 0.f;
+                    }
+                    p[4 * j + e] = x;
+                }
             }
+        };
+        if (masked_flag)
+            probs(std::true_type{});
+        else
+            probs(std::false_type{});
+#pragma unroll
+        for (int j = 0; j < 4; j++)
             sm.p[n & 1][kw][j][lane] =
                 make_float4(p[4 * j], p[4 * j + 1], p[4 * j + 2], p[4 * j + 3]);
-        }
         DM_STAMP(0, n, 2);
         Frag8 pf[2];
 #pragma unroll
@@ -607,9 +618,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
             DM_STAMP(0, n, 0);
             restage(n, ns, x);
             DM_STAMP(0, n, 1);
-            // one code path for every tile (a branch here would split the accumulators'
-            // registers); the per-element test costs three VALU operations per score
-            pstep(n, cs, std::true_type{});
+            pstep(n, cs, entry(n).masked);
             DM_STAMP(0, n, 3);
             if (wave == 0) publish(n + 5);
             __syncthreads();
