@@ -698,6 +698,7 @@ GdrArgs gdr_args(const dm_gdr_desc *d, const void *q, const void *k, const void 
                  const void *g, const void *beta) {
     GdrArgs a;
     a.H = d->h;
+    a.rows = d->b * d->t;
     a.Dk = d->dk;
     a.Dv = d->dv;
     a.g_dt = d->g_dtype;

@@ -10,8 +10,9 @@
 //   gdr_mfma_state   per (sequence, head), serial over the sequence's chunks: the state S lives
 //                    in registers in the 32x32 products' output layout, which is also the
 //                    operand layout of the next product, so it never leaves the wavefronts;
-//                    V' = U - W S; S <- exp(G_last) S + K^T (lam V'); S and V' are stored as
-//                    ready-made operand fragments for the output kernel.
+//                    V' = U - W S; S <- exp(G_last) S + (lam K)^T V'; its operands come from
+//                    the prep kernel as ready-made fragments (no LDS, no barriers); S and V'
+//                    are stored as operand fragments for the output kernel.
 //   gdr_mfma_output  per (chunk, head), parallel: O^T = scale gamma (S^T Q^T) + V'^T Aqk^T.
 // Notation as chunk/reference.rs:11-18 (Q scaled, G_last the chunk's last cumulative gate).
 #include <string>
@@ -32,11 +33,13 @@ constexpr int kTrS = kD + 32;   // row stride read by ds_read_b64_tr_b16
 struct MfmaWs {
     int32_t *seq_chunk0, *chunk_seq, *chunk_tok0, *chunk_len;
     float *G;          // [ch][64]
-    uint16_t *W, *U;   // [ch][64][128] row-major
+    uint16_t *Wf;      // [ch][2 token tiles][8 dk steps][64 lanes][8]: W as A fragments of V' = W S
+    uint16_t *Uc;      // [ch][4 dv tiles][2 token tiles][2][64 lanes][8]: U in the product layout
+    uint16_t *Kf;      // [ch][4 dk tiles][4 token steps][64 lanes][8]: (lam K)^T as A fragments
     uint16_t *Aqk;     // [ch][64][64] row-major, scale included
     uint16_t *Sf;      // [ch][4 dv tiles][8 dk steps][64 lanes][8]: S entering the chunk
     uint16_t *Vf;      // [ch][4 dv tiles][4 token steps][64 lanes][8]: V'
-    uint16_t *Qn, *Kn; // [ch][64][128] normalised queries and keys (with the l2 normalisation)
+    uint16_t *Qn;      // [ch][64][128] normalised queries (with the l2 normalisation)
 };
 
 static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w) {
@@ -53,15 +56,13 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w) {
     x.chunk_tok0 = (int32_t *)take(nc * 4);
     x.chunk_len = (int32_t *)take(nc * 4);
     x.G = (float *)take(ch * kC * 4);
-    x.W = (uint16_t *)take(ch * kC * kD * 2);
-    x.U = (uint16_t *)take(ch * kC * kD * 2);
+    x.Wf = (uint16_t *)take(ch * kC * kD * 2);
+    x.Uc = (uint16_t *)take(ch * kC * kD * 2);
+    x.Kf = (uint16_t *)take(ch * kC * kD * 2);
     x.Aqk = (uint16_t *)take(ch * kC * kC * 2);
     x.Sf = (uint16_t *)take(ch * kD * kD * 2);
     x.Vf = (uint16_t *)take(ch * kC * kD * 2);
-    if (d->qk_l2norm) {
-        x.Qn = (uint16_t *)take(ch * kC * kD * 2);
-        x.Kn = (uint16_t *)take(ch * kC * kD * 2);
-    }
+    if (d->qk_l2norm) x.Qn = (uint16_t *)take(ch * kC * kD * 2);
     if (w) *w = x;
     return off;
 }
@@ -148,7 +149,6 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             kv = make_uint4(pack2<DT>(kf[0] * ki, kf[1] * ki), pack2<DT>(kf[2] * ki, kf[3] * ki),
                             pack2<DT>(kf[4] * ki, kf[5] * ki), pack2<DT>(kf[6] * ki, kf[7] * ki));
             *(uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8) = qv;
-            *(uint4 *)(w.Kn + (ch * kC + r) * kD + c * 8) = kv;
         }
         sm.q[r * (kRowS / 8) + c] = qv;
         sm.k[r * (kRowS / 8) + c] = kv;
@@ -178,6 +178,31 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         for (int e = 0; e < 4; e++)
             ko[e] = pack2<DT>(unpack_lo<DT>(kw[e]) * fk, unpack_hi<DT>(kw[e]) * fk);
         sm.x[r * (kTrS / 8) + c] = make_uint4(ko[0], ko[1], ko[2], ko[3]);
+    }
+    // (lam K)^T as the state pass's A fragments: fragment (dk tile r, token step st), lane l
+    // holds dk = 32 r + l % 32 at tokens 16 st + 8 j + 4 (l / 32) + e in slot 4 j + e (the k
+    // order of the V' fragments it meets); lam = exp(G_last - G)
+    {
+        uint16_t *kf_out = w.Kf + ch * kC * kD;
+        const float glast = sm.g[kC - 1];
+        for (int xx = tid; xx < 16 * 64; xx += 256) {
+            const int f = xx / 64, l = xx % 64, r = f / 4, st = f % 4;
+            const int dkx = r * 32 + (l & 31), hh = l >> 5;
+            float v8[8];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int tok = st * 16 + 8 * j + 4 * hh + e;
+                    const uint16_t kb = ks[tok * kRowS + dkx];
+                    const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
+                                                     : (float)__builtin_bit_cast(_Float16, kb);
+                    v8[4 * j + e] = kv * __expf(glast - sm.g[tok]);
+                }
+            *(uint4 *)(kf_out + (size_t)xx * 8) =
+                make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
+                           pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
+        }
     }
 
     // K K^T and Q K^T on the lower tiles (0,0), (1,0), (1,1) (waves 0-2); A = beta (K K^T) o
@@ -336,25 +361,40 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     __syncthreads();
     product(ut);
     __syncthreads();
-    // stage W and U as rows (element i: row 32 ti + 8 (i / 4) + 4 h + i % 4, column
-    // 32 wave + col), then store whole rows
+    // U in the state pass's layout: that of the products' output, the lane's 16 values of
+    // token tile ti as two 16-byte pieces
     {
-        uint16_t *wrows = (uint16_t *)sm.k, *urows = (uint16_t *)sm.q;
+        uint16_t *uc = w.Uc + ch * kC * kD + (size_t)wave * 2 * 2 * 64 * 8;
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                *(uint4 *)(uc + ((ti * 2 + qq) * 64 + lane) * 8) =
+                    make_uint4(pack2<DT>(ut[ti][8 * qq + 0], ut[ti][8 * qq + 1]),
+                               pack2<DT>(ut[ti][8 * qq + 2], ut[ti][8 * qq + 3]),
+                               pack2<DT>(ut[ti][8 * qq + 4], ut[ti][8 * qq + 5]),
+                               pack2<DT>(ut[ti][8 * qq + 6], ut[ti][8 * qq + 7]));
+            }
+    }
+    // W as the state pass's A fragments: stage the rows (element i: row 32 ti + 8 (i / 4) +
+    // 4 h + i % 4, column 32 wave + col), then fragment (token tile t, dk step st), lane l:
+    // row 32 t + l % 32, columns 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
+    {
+        uint16_t *wrows = (uint16_t *)sm.k;
 #pragma unroll
         for (int ti = 0; ti < 2; ti++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                const uint32_t p2 = pack2<DT>(wt[ti][i], ut[ti][i]);
-                wrows[r * kRowS + wave * 32 + col] = (uint16_t)(p2 & 0xffffu);
-                urows[r * kRowS + wave * 32 + col] = (uint16_t)(p2 >> 16);
+                wrows[r * kRowS + wave * 32 + col] = (uint16_t)(pack2<DT>(wt[ti][i], 0.f) & 0xffffu);
             }
         __syncthreads();
-        uint16_t *Wout = w.W + ch * kC * kD, *Uout = w.U + ch * kC * kD;
-        for (int xx = tid; xx < kC * 16; xx += 256) {
-            const int r = xx / 16, c = xx % 16;
-            *(uint4 *)(Wout + r * kD + c * 8) = sm.k[r * (kRowS / 8) + c];
-            *(uint4 *)(Uout + r * kD + c * 8) = sm.q[r * (kRowS / 8) + c];
+        uint16_t *wf = w.Wf + ch * kC * kD;
+        for (int xx = tid; xx < 16 * 64; xx += 256) {
+            const int f = xx / 64, l = xx % 64, t = f / 8, st = f % 8;
+            const uint16_t *row = wrows + (t * 32 + (l & 31)) * kRowS + st * 16 + (l >> 5) * 4;
+            const uint2 lo4 = *(const uint2 *)row, hi4 = *(const uint2 *)(row + 8);
+            *(uint4 *)(wf + (size_t)xx * 8) = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
         }
     }
 }
@@ -363,27 +403,26 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 // State pass
 // ------------------------------------------------------------------------------------------
 
-struct StateSmem {
-    uint4 w[kC * kRowB / 8 + 1];  // W rows (8-byte reads), +1: kRowB is not a multiple of 8
-    uint4 k[kC * kTrS / 8];       // K rows read transposed
-    uint4 u[kC * kTrS / 8];       // U rows read transposed
-    float g[kC];
+// Each wavefront owns 32 state columns and reads its operands -- W and (lam K)^T as ready-made
+// A fragments, U in the products' layout -- straight from HBM into registers two chunks ahead:
+// no LDS, no barriers; the chain per chunk is S -> (pack) -> 16 products -> (U - .) -> 16
+// products -> S.
+struct ChunkOps {
+    Frag8 wf[2][8];  // W: token tile t, dk step st
+    uint4 uc[2][2];  // U: token tile t, two 8-value halves of the lane's 16
+    Frag8 kf[4][4];  // (lam K)^T: dk tile r, token step st
+    float glast;     // G at the chunk's last token
 };
 
-// One workgroup of 4 wavefronts per (sequence, head); wavefront w owns state columns
-// [32 w, 32 w + 32) over all 128 rows: 4 output tiles of 32 x 32 in f32.
 template <int DT>
 __global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, const float *h0,
                                                          float *final_state) {
-    __shared__ StateSmem sm;
     const int64_t sh = blockIdx.x, s = sh / a.H, h = sh % a.H;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
     const int dv = wave * 32 + col;  // this lane's state column
-    uint16_t *ws_ = (uint16_t *)sm.w, *kss = (uint16_t *)sm.k, *uss = (uint16_t *)sm.u;
-    const int64_t seq_t0 = c0 < c1 ? w.chunk_tok0[c0] : 0;
-    const int64_t seq_end = c0 < c1 ? (int64_t)w.chunk_tok0[c1 - 1] + w.chunk_len[c1 - 1] : 0;
 
     // S: tile r holds rows 32 r + 8 (i / 4) + 4 h + i % 4 of column dv
     f32x16_t S[4];
@@ -397,48 +436,32 @@ __global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, co
                 S[r][i] = src ? src[row * kD + dv] : 0.f;
             }
     }
-    // staging of a chunk's W, U and K (rows of 16 16-byte chunks), two chunks ahead: set A for
-    // even steps, set B for odd ones
-    auto load = [&](int c, uint4 *r_, float &g_) {
+    // a chunk's operands (a chunk past the sequence's last loads the last again: every call
+    // issues the same loads)
+    auto load = [&](int c, ChunkOps &x) __attribute__((always_inline)) {
+        c = c < c1 ? c : c1 - 1;
         const int64_t ch = (int64_t)c * a.H + h;
-        const uint16_t *W = w.W + ch * kC * kD, *U = w.U + ch * kC * kD;
-        if (tid < kC) g_ = w.G[ch * kC + tid];
-        // a sequence's chunks are consecutive, kC tokens apart
-        const int64_t tok0 = seq_t0 + (int64_t)(c - c0) * kC;
-        const int len = (int)min((int64_t)kC, seq_end - tok0);
+        const uint16_t *wf = w.Wf + ch * kC * kD, *kf = w.Kf + ch * kC * kD;
+        const uint16_t *uc = w.Uc + ch * kC * kD + (size_t)wave * 2 * 2 * 64 * 8;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int x = tid + 256 * u, r = x / 16, cc = x % 16;
-            r_[u] = *(const uint4 *)(W + r * kD + cc * 8);
-            r_[4 + u] = *(const uint4 *)(U + r * kD + cc * 8);
-            // keys: the normalised chunk-major copy, or the inputs' rows
-            if (a.l2norm)
-                r_[8 + u] = *(const uint4 *)(w.Kn + (ch * kC + r) * kD + cc * 8);
-            else
-                r_[8 + u] = r < len ? *(const uint4 *)((const uint16_t *)a.k +
-                                                       ((tok0 + r) * a.H + h) * kD + cc * 8)
-                                    : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store = [&](const uint4 *r_, float g_) {
-        if (tid < kC) sm.g[tid] = g_;
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int x = tid + 256 * u, r = x / 16, cc = x % 16;
-            uint2 *wp = (uint2 *)(ws_ + r * kRowB + cc * 8);
-            wp[0] = make_uint2(r_[u].x, r_[u].y);
-            wp[1] = make_uint2(r_[u].z, r_[u].w);
-            sm.u[r * (kTrS / 8) + cc] = r_[4 + u];
-            sm.k[r * (kTrS / 8) + cc] = r_[8 + u];
-        }
+            for (int st = 0; st < 8; st++)
+                x.wf[t][st].u = *(const uint4 *)(wf + ((t * 8 + st) * 64 + lane) * 8);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++)
+                x.uc[t][qq] = *(const uint4 *)(uc + ((t * 2 + qq) * 64 + lane) * 8);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                x.kf[r][st].u = *(const uint4 *)(kf + ((r * 4 + st) * 64 + lane) * 8);
+        x.glast = w.G[ch * kC + kC - 1];
     };
-    auto step = [&](int c, uint4 *r_, float &g_) {
+    auto step = [&](int c, ChunkOps &x) __attribute__((always_inline)) {
         const int64_t ch = (int64_t)c * a.H + h;
-        __syncthreads();
-        store(r_, g_);
-        __syncthreads();
-        if (c + 2 < c1) load(c + 2, r_, g_);
-
         // S as operand fragments (k = state row, col = dv), in the dtype; also stored for the
         // output kernel in fragment order [dv tile][k step][lane]
         Frag8 sf[8];
@@ -452,8 +475,7 @@ __global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, co
                                   pack2<DT>(S[r][8 * u + 6], S[r][8 * u + 7]));
             *(uint4 *)(sfo + (st * 64 + lane) * 8) = sf[st].u;
         }
-        // V' = U - W S: 2 token tiles; A = W rows (k slots in the fragments' state-row order:
-        // 16 st + 8 j + 4 h + e), B = S fragments
+        // W S for the 2 token tiles (k slots in the fragments' state-row order)
         f32x16_t vp[2];
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -462,41 +484,29 @@ __global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, co
 #pragma unroll
         for (int st = 0; st < 8; st++)
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const uint16_t *wrow = ws_ + (t * 32 + col) * kRowB + st * 16 + half * 4;
-                const uint2 lo4 = *(const uint2 *)(wrow), hi4 = *(const uint2 *)(wrow + 8);
-                Frag8 aw;
-                aw.u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
-                vp[t] = mfma32<DT>(aw, sf[st], vp[t]);
-            }
-        // U in the same layout by transposed reads of the U rows (token t 32 + 16 u + ...)
-        const float glast = sm.g[kC - 1];
+            for (int t = 0; t < 2; t++) vp[t] = mfma32<DT>(x.wf[t][st], sf[st], vp[t]);
+        // V' = U - W S, as B fragments of the state update (token order 32 t + 16 u + ...) and
+        // stored for the output kernel
         Frag8 vlf[4];
         uint16_t *vfo = w.Vf + ch * kC * kD + (size_t)wave * 4 * 64 * 8;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const Frag8 uf = lds_tr_frag(uss, kTrS, t * 32 + u * 16, wave * 32, lane);
-                const uint32_t uw[4] = {uf.u.x, uf.u.y, uf.u.z, uf.u.w};
-                float v8[8], l8[8];
+                const uint32_t uw[4] = {x.uc[t][u].x, x.uc[t][u].y, x.uc[t][u].z, x.uc[t][u].w};
+                float v8[8];
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    const int i = 8 * u + e;
                     const float uu = (e & 1) ? unpack_hi<DT>(uw[e / 2]) : unpack_lo<DT>(uw[e / 2]);
-                    v8[e] = uu - vp[t][i];
-                    const int tok = t * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                    l8[e] = v8[e] * __expf(glast - sm.g[tok]);
+                    v8[e] = uu - vp[t][8 * u + e];
                 }
                 const int st = t * 2 + u;
-                const uint4 vf = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
-                                            pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
-                vlf[st].u = make_uint4(pack2<DT>(l8[0], l8[1]), pack2<DT>(l8[2], l8[3]),
-                                       pack2<DT>(l8[4], l8[5]), pack2<DT>(l8[6], l8[7]));
-                *(uint4 *)(vfo + (st * 64 + lane) * 8) = vf;
+                vlf[st].u = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
+                                       pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
+                *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
             }
-        // S <- exp(G_last) S + K^T (lam V'): A = K^T by transposed reads of the K rows
-        const float gl = __expf(glast);
+        // S <- exp(G_last) S + (lam K)^T V'
+        const float gl = __expf(x.glast);
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
@@ -504,18 +514,20 @@ __global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, co
 #pragma unroll
         for (int st = 0; st < 4; st++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const Frag8 ak = lds_tr_frag(kss, kTrS, st * 16, r * 32, lane);
-                S[r] = mfma32<DT>(ak, vlf[st], S[r]);
-            }
+            for (int r = 0; r < 4; r++) S[r] = mfma32<DT>(x.kf[r][st], vlf[st], S[r]);
     };
-    uint4 ra[12], rb[12];
-    float ga = 0.f, gb = 0.f;
-    if (c0 < c1) load(c0, ra, ga);
-    if (c0 + 1 < c1) load(c0 + 1, rb, gb);
+    // two operand sets in turn (named statically), each loaded two chunks ahead of its use
+    ChunkOps oa, ob;
+    if (c0 < c1) {
+        load(c0, oa);
+        load(c0 + 1, ob);
+    }
     for (int c = c0; c < c1; c += 2) {
-        step(c, ra, ga);
-        if (c + 1 < c1) step(c + 1, rb, gb);
+        step(c, oa);
+        load(c + 2, oa);
+        if (c + 1 >= c1) break;
+        step(c + 1, ob);
+        load(c + 3, ob);
     }
     if (final_state) {
         float *dst = final_state + sh * kD * kD;
@@ -626,7 +638,9 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
 // ------------------------------------------------------------------------------------------
 
 bool gdr_mfma_takes(const dm_gdr_desc *d) {
-    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk == kD && d->dv == kD;
+    // (the state pass addresses the keys through a 32-bit buffer range)
+    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk == kD && d->dv == kD &&
+           d->b * d->t * d->h * kD * 2 < (1ll << 32);
 }
 
 size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { return mfma_layout(d, nullptr, nullptr); }
@@ -638,6 +652,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
     mfma_layout(d, (char *)workspace, &w);
     GdrArgs a;
     a.H = d->h;
+    a.rows = d->b * d->t;
     a.Dk = d->dk;
     a.Dv = d->dv;
     a.g_dt = d->g_dtype;

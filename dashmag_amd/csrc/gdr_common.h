@@ -9,6 +9,7 @@ constexpr int kChunk = 64;  // tokens per chunk (chunk/reference.rs:26)
 
 struct GdrArgs {
     int64_t H, Dk, Dv;
+    int64_t rows;  // B * T token rows of the inputs
     int g_dt, beta_dt, l2norm;
     float scale;
     const void *q, *k, *v, *g, *beta;
