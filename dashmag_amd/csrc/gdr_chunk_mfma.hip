@@ -415,11 +415,13 @@ struct ChunkOps {
 };
 
 template <int DT>
-__global__ __launch_bounds__(256, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, const float *h0,
-                                                         float *final_state) {
-    const int64_t sh = blockIdx.x, s = sh / a.H, h = sh % a.H;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+__global__ __launch_bounds__(64, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, const float *h0,
+                                                        float *final_state) {
+    // one wavefront per workgroup: the four of a (sequence, head) on different compute units,
+    // each streaming its operands through its own L1
+    const int64_t sh = blockIdx.x / 4, s = sh / a.H, h = sh % a.H;
+    const int lane = threadIdx.x;
+    const int wave = blockIdx.x % 4;
     const int col = lane & 31, half = lane >> 5;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
     const int dv = wave * 32 + col;  // this lane's state column
@@ -675,7 +677,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state<DM_BF16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state<DM_BF16><<<seqs * 4, 64, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -688,7 +690,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state<DM_F16><<<seqs, 256, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state<DM_F16><<<seqs * 4, 64, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
