@@ -79,7 +79,7 @@ struct PrepSmem {
     uint4 q[kC * kRowS / 8];  // queries, rows; later T (f32); later U rows
     uint4 x[kC * kTrS / 8];   // beta gamma K, then beta V: rows read transposed
     float a[kC][kC + 4];      // A (strictly lower), f32, 16-byte aligned rows
-    float g[kC], gam[kC], bet[kC];
+    float g[kC], gam[kC], bet[kC], lam[kC];
 };
 static_assert(sizeof(float) * kC * (kC + 4) <= sizeof(uint4) * kC * kRowS / 8, "T in q");
 static_assert(sizeof(float) * 3 * 16 * 20 <= sizeof(uint4) * kC * kRowS / 8, "M in k");
@@ -103,25 +103,32 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         sm.g[tid] = ok ? ld_any(a.g_dt, a.g, (tok0 + tid) * a.H + h) : 0.f;
         sm.bet[tid] = ok ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
     }
-    uint4 vreg[4];
+    // every row's loads issued before any is used (rows past the chunk's tokens read the last
+    // valid row and are zeroed after)
+    uint4 vreg[4], qraw[4], kraw[4];
     {
-        const uint16_t *vin = (const uint16_t *)a.v;
+        const uint16_t *vin = (const uint16_t *)a.v, *qin = (const uint16_t *)a.q,
+                       *kin = (const uint16_t *)a.k;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
-            vreg[u] = r < len ? *(const uint4 *)(vin + ((tok0 + r) * a.H + h) * kD + c * 8)
-                              : make_uint4(0, 0, 0, 0);
+            const int64_t off = ((tok0 + (r < len ? r : len - 1)) * a.H + h) * kD + c * 8;
+            vreg[u] = *(const uint4 *)(vin + off);
+            qraw[u] = *(const uint4 *)(qin + off);
+            kraw[u] = *(const uint4 *)(kin + off);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int r = (tid + 256 * u) / 16;
+            if (r >= len) vreg[u] = qraw[u] = kraw[u] = make_uint4(0, 0, 0, 0);
         }
     }
     // queries and keys: 16 lanes per row, zero past the chunk's tokens; normalised in f32 and
     // rounded back to the dtype when asked
-    const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k;
-    for (int r = tid / 16; r < kC; r += 16) {
-        const int c = tid % 16;
-        const bool ok = r < len;
-        const int64_t off = ((tok0 + r) * a.H + h) * kD + c * 8;
-        uint4 qv = ok ? *(const uint4 *)(qin + off) : make_uint4(0, 0, 0, 0);
-        uint4 kv = ok ? *(const uint4 *)(kin + off) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
+        uint4 qv = qraw[u], kv = kraw[u];
         if (a.l2norm) {
             float qf[8], kf[8];
             const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, kw[4] = {kv.x, kv.y, kv.z, kv.w};
@@ -164,6 +171,7 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         }
         sm.g[lane] = x;
         sm.gam[lane] = __expf(x);
+        sm.lam[lane] = __expf(__shfl(x, kC - 1, 64) - x);
         w.G[ch * kC + lane] = x;
     }
     __syncthreads();
@@ -181,27 +189,23 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     }
     // (lam K)^T as the state pass's A fragments: fragment (dk tile r, token step st), lane l
     // holds dk = 32 r + l % 32 at tokens 16 st + 8 j + 4 (l / 32) + e in slot 4 j + e (the k
-    // order of the V' fragments it meets); lam = exp(G_last - G)
+    // order of the V' fragments it meets): transposed reads of the key rows, then lam per token
     {
         uint16_t *kf_out = w.Kf + ch * kC * kD;
-        const float glast = sm.g[kC - 1];
-        for (int xx = tid; xx < 16 * 64; xx += 256) {
-            const int f = xx / 64, l = xx % 64, r = f / 4, st = f % 4;
-            const int dkx = r * 32 + (l & 31), hh = l >> 5;
-            float v8[8];
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+        for (int st = 0; st < 4; st++) {
+            const Frag8 kt = lds_tr_frag(ks, kRowS, st * 16, wave * 32, lane);
+            const uint32_t kw[4] = {kt.u.x, kt.u.y, kt.u.z, kt.u.w};
+            uint32_t o[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int tok = st * 16 + 8 * j + 4 * hh + e;
-                    const uint16_t kb = ks[tok * kRowS + dkx];
-                    const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
-                                                     : (float)__builtin_bit_cast(_Float16, kb);
-                    v8[4 * j + e] = kv * __expf(glast - sm.g[tok]);
-                }
-            *(uint4 *)(kf_out + (size_t)xx * 8) =
-                make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
-                           pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
+            for (int e2 = 0; e2 < 4; e2++) {
+                // slots 2 e2, 2 e2 + 1: j = e2 / 2, e = 2 (e2 % 2) + {0, 1}
+                const int tok = st * 16 + 8 * (e2 / 2) + 4 * half + 2 * (e2 % 2);
+                o[e2] = pack2<DT>(unpack_lo<DT>(kw[e2]) * sm.lam[tok],
+                                  unpack_hi<DT>(kw[e2]) * sm.lam[tok + 1]);
+            }
+            *(uint4 *)(kf_out + (size_t)((wave * 4 + st) * 64 + lane) * 8) =
+                make_uint4(o[0], o[1], o[2], o[3]);
         }
     }
 
