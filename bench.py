@@ -250,10 +250,14 @@ def main():
               args_t + [c["h0"], c["do"], fin, dq, dk_, dv_, dg, db, dh0, wsb]]
         fnb = lambda: check(lib.dm_gdr_chunk_bwd(ctypes.byref(desc), *pb[:14], pb[14], nbb, st),  # noqa
                             lib)
-        msb = Timed(torch, fnb).run(2, 1)
+        tmb = Timed(torch, fnb)
+        msb = tmb.run(max(3, args.steps // 4), 1)
         secondary["gdr_chunk_bwd"] = dict(unit="tokens/s", value=t / msb * 1e3, ms_per_call=msb,
-                                          tflops=32.5e6 * nch / msb / 1e9)
-        print(f"gdr chunk bwd: {msb:.3f} ms", file=sys.stderr, flush=True)
+                                          tflops=32.5e6 * nch / msb / 1e9,
+                                          kernel_us={k: round(v[0] * 1e3, 2)
+                                                     for k, v in tmb.kernel_ms.items()})
+        print(f"gdr chunk bwd: {msb:.3f} ms, kernels (us) "
+              f"{secondary['gdr_chunk_bwd']['kernel_us']}", file=sys.stderr, flush=True)
         del c, ws, wsb
 
     # ---- gated delta step, config 5 ----

@@ -108,7 +108,7 @@ def probe_reset() -> None:
 
 
 KERNELS = ["attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "decode_split", "gdr_prep", "gdr_state",
-           "gdr_output", "gdr_step"]
+           "gdr_output", "gdr_step", "gdr_bwd_pre", "gdr_bwd_state", "gdr_bwd_grads"]
 
 
 def kernel_timing(enable: bool) -> None:

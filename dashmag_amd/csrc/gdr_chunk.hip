@@ -775,6 +775,7 @@ int dm_gdr_chunk_fwd(const dm_gdr_desc *d, const void *q, const void *k, const v
 
 size_t dm_gdr_chunk_bwd_workspace(const dm_gdr_desc *d) {
     if (!d) return 0;
+    if (gdr_mfma_takes(d)) return gdr_mfma_bwd_workspace(d);
     return gdr_ws_layout(d, true, nullptr, nullptr);
 }
 
@@ -790,6 +791,9 @@ int dm_gdr_chunk_bwd(const dm_gdr_desc *d, const void *q, const void *k, const v
     hipStream_t st = (hipStream_t)stream;
     const int64_t S = gdr_nseq(d), nc = gdr_chunk_bound(d);
     if (S * d->h == 0) return DM_OK;
+    if (gdr_mfma_takes(d))
+        return launch_gdr_mfma_bwd(d, q, k, v, g, beta, h0, d_out, d_final, dq, dk, dv, dg,
+                                   dbeta, dh0, workspace, st);
     GdrWs w;
     gdr_ws_layout(d, true, (char *)workspace, &w);
     GdrArgs a = gdr_args(d, q, k, v, g, beta);

@@ -40,9 +40,15 @@ struct MfmaWs {
     uint16_t *Sf;      // [ch][4 dv tiles][8 dk steps][64 lanes][8]: S entering the chunk
     uint16_t *Vf;      // [ch][4 dv tiles][4 token steps][64 lanes][8]: V'
     uint16_t *Qn;      // [ch][64][128] normalised queries (with the l2 normalisation)
+    // the backward's, besides
+    uint16_t *Tm;      // [ch][64][64] T = (I + A)^-1, row-major
+    uint16_t *Krf;     // [ch][2 token tiles][8 dk steps][64][8]: lam K as A fragments (rows tokens)
+    uint16_t *WTf;     // [ch][4 dk tiles][4 token steps][64][8]: W^T as A fragments
+    uint16_t *F;       // [ch][4 dv tiles][4 dk tiles][64][16]: (gamma Q)^T dO - W^T (Aqk^T dO)
+    uint16_t *dSf;     // [ch][4 dv tiles][8 dk steps][64][8]: dS after the chunk, as S in Sf
 };
 
-static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w) {
+static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd = false) {
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d), ch = nc * d->h;
     size_t off = 0;
     auto take = [&](size_t bytes) -> char * {
@@ -63,6 +69,13 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w) {
     x.Sf = (uint16_t *)take(ch * kD * kD * 2);
     x.Vf = (uint16_t *)take(ch * kC * kD * 2);
     if (d->qk_l2norm) x.Qn = (uint16_t *)take(ch * kC * kD * 2);
+    if (bwd) {
+        x.Tm = (uint16_t *)take(ch * kC * kC * 2);
+        x.Krf = (uint16_t *)take(ch * kC * kD * 2);
+        x.WTf = (uint16_t *)take(ch * kC * kD * 2);
+        x.F = (uint16_t *)take(ch * kD * kD * 2);
+        x.dSf = (uint16_t *)take(ch * kD * kD * 2);
+    }
     if (w) *w = x;
     return off;
 }
@@ -206,6 +219,25 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             }
             *(uint4 *)(kf_out + (size_t)((wave * 4 + st) * 64 + lane) * 8) =
                 make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        // for the backward, lam K also as A fragments with rows = tokens (the layout of W's):
+        // fragment (token tile t, dk step st), lane l: row 32 t + l % 32, columns
+        // 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
+        if (w.Krf) {
+            uint16_t *kr_out = w.Krf + ch * kC * kD;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int f = wave * 4 + j, t = f / 8, st = f % 8, row = t * 32 + col;
+                const uint16_t *rp = ks + row * kRowS + st * 16 + half * 4;
+                const uint2 lo4 = *(const uint2 *)rp, hi4 = *(const uint2 *)(rp + 8);
+                const uint32_t kw[4] = {lo4.x, lo4.y, hi4.x, hi4.y};
+                const float lm = sm.lam[row];
+                uint32_t o[4];
+#pragma unroll
+                for (int e2 = 0; e2 < 4; e2++)
+                    o[e2] = pack2<DT>(unpack_lo<DT>(kw[e2]) * lm, unpack_hi<DT>(kw[e2]) * lm);
+                *(uint4 *)(kr_out + (size_t)(f * 64 + lane) * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
         }
     }
 
@@ -365,6 +397,14 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     __syncthreads();
     product(ut);
     __syncthreads();
+    // for the backward: T, row-major in the dtype
+    if (w.Tm) {
+        uint16_t *tout = w.Tm + ch * kC * kC;
+        for (int xx = tid; xx < kC * kC / 2; xx += 256) {
+            const int r = xx / (kC / 2), c2 = (xx % (kC / 2)) * 2;
+            *(uint32_t *)(tout + r * kC + c2) = pack2<DT>(tt[r][c2], tt[r][c2 + 1]);
+        }
+    }
     // U in the state pass's layout: that of the products' output, the lane's 16 values of
     // token tile ti as two 16-byte pieces
     {
@@ -399,6 +439,15 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             const uint16_t *row = wrows + (t * 32 + (l & 31)) * kRowS + st * 16 + (l >> 5) * 4;
             const uint2 lo4 = *(const uint2 *)row, hi4 = *(const uint2 *)(row + 8);
             *(uint4 *)(wf + (size_t)xx * 8) = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+        }
+        // for the backward, W^T as A fragments (rows dk, k = tokens), as (lam K)^T in Kf
+        if (w.WTf) {
+            uint16_t *wt_out = w.WTf + ch * kC * kD;
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const Frag8 x = lds_tr_frag(wrows, kRowS, st * 16, wave * 32, lane);
+                *(uint4 *)(wt_out + (size_t)((wave * 4 + st) * 64 + lane) * 8) = x.u;
+            }
         }
     }
 }
@@ -640,6 +689,780 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
 }
 
 // ------------------------------------------------------------------------------------------
+// Backward (chunk/reference.rs:519-695 restated for the products; notation as the forward's)
+// ------------------------------------------------------------------------------------------
+//
+//   gdr_bwd_pre    per (chunk, head): F = (gamma scale Q)^T dO - W^T (Aqk^T dO), the part of
+//                  the state gradient's chunk step that does not depend on the state
+//   gdr_bwd_state  per (sequence, head, 32 state columns), serial over the chunks in reverse:
+//                  dS_c = exp(G_last) dS_{c+1} - W^T ((lam K) dS_{c+1}) + F; stores dS_{c+1}
+//                  per chunk and dh0
+//   gdr_bwd_grads  per (chunk, head): dV' = (lam K) dS_{c+1} + Aqk^T dO, then every gradient
+//                  the chunk gives (dq, dk, dv, dg, dbeta)
+
+// An A or B fragment from a row-major 16-bit tile whose rows are the fragment's rows (A) or
+// columns (B) and whose columns are k: rows r0 + lane % 32, k slots 16 st + 8 j + 4 h + e at
+// columns k0 + 4 h + [0, 4) and k0 + 8 + 4 h + [0, 4) (the order lds_tr_frag's slots have).
+__device__ __forceinline__ Frag8 row_frag(const uint16_t *t, int stride, int r0, int k0,
+                                          int lane) {
+    const uint16_t *p = t + (r0 + (lane & 31)) * stride + k0 + (lane >> 5) * 4;
+    const uint2 lo = *(const uint2 *)p, hi = *(const uint2 *)(p + 8);
+    Frag8 f;
+    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    return f;
+}
+
+// The 32x32 product output's element i of a lane: row 8 (i / 4) + 4 (lane / 32) + i % 4 of the
+// tile, column lane % 32.
+__device__ __forceinline__ int crow(int i, int lane) { return (i / 4) * 8 + (lane >> 5) * 4 + (i % 4); }
+
+// Its 16 values stored transposed into a row-major 16-bit tile X^T: row (the tile's column)
+// c0 + lane % 32, columns r0 + crow(i): runs of 4, 8-byte stores.
+template <int DT>
+__device__ __forceinline__ void store_ct(uint16_t *t, int stride, int r0, int c0,
+                                         const f32x16_t &v, int lane, float f = 1.f) {
+    uint16_t *row = t + (c0 + (lane & 31)) * stride + r0 + (lane >> 5) * 4;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        *(uint2 *)(row + g * 8) = make_uint2(pack2<DT>(v[4 * g] * f, v[4 * g + 1] * f),
+                                             pack2<DT>(v[4 * g + 2] * f, v[4 * g + 3] * f));
+}
+
+// Sum over the 32 lanes that share lane / 32 (the columns of a product tile).
+__device__ __forceinline__ float sum32(float x) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// A product tile's output fragment as the B (or A) operand of a next product whose k is the
+// tile's rows: k step u takes elements 8 u .. 8 u + 7.
+template <int DT>
+__device__ __forceinline__ Frag8 c_frag(const f32x16_t &v, int u, float f = 1.f) {
+    Frag8 x;
+    x.u = make_uint4(pack2<DT>(v[8 * u] * f, v[8 * u + 1] * f), pack2<DT>(v[8 * u + 2] * f, v[8 * u + 3] * f),
+                     pack2<DT>(v[8 * u + 4] * f, v[8 * u + 5] * f), pack2<DT>(v[8 * u + 6] * f, v[8 * u + 7] * f));
+    return x;
+}
+
+// x rounded to the dtype and back
+template <int DT>
+__device__ __forceinline__ float round_to(float x) {
+    return unpack_lo<DT>(pack2<DT>(x, 0.f));
+}
+
+__device__ __forceinline__ f32x16_t zero16() {
+    f32x16_t z;
+#pragma unroll
+    for (int i = 0; i < 16; i++) z[i] = 0.f;
+    return z;
+}
+
+constexpr int kR = kD + 8;  // 128-column tiles (row and transposed reads)
+constexpr int kT = kC + 8;  // 64-column tiles
+
+// F per (chunk, head): wave w takes state columns 32 w + [0, 32).
+struct BwdPreSmem {
+    uint16_t dO[kC * kR];   // dO rows
+    uint16_t qg[kC * kR];   // gamma scale Q rows
+    uint16_t aq[kC * kT];   // Aqk rows
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const void *d_out) {
+    __shared__ BwdPreSmem sm;
+    const int64_t ch = blockIdx.x, n = ch / a.H, h = ch % a.H;
+    const int len = w.chunk_len[n];
+    if (len == 0) return;
+    const int64_t tok0 = w.chunk_tok0[n];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint16_t *dob = (const uint16_t *)d_out, *qin = (const uint16_t *)a.q;
+    uint4 dv[4], qv[4], av[2];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
+        dv[u] = *(const uint4 *)(dob + row * kD + c * 8);
+        qv[u] = a.l2norm ? *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8)
+                         : *(const uint4 *)(qin + row * kD + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int x = tid + 256 * u, r = x / 8, c = x % 8;
+        av[u] = *(const uint4 *)(w.Aqk + ch * kC * kC + r * kC + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        const bool ok = r < len;
+        const float f = ok ? a.scale * __expf(w.G[ch * kC + r]) : 0.f;
+        const uint32_t qw[4] = {qv[u].x, qv[u].y, qv[u].z, qv[u].w};
+        uint32_t qo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) qo[e] = pack2<DT>(unpack_lo<DT>(qw[e]) * f, unpack_hi<DT>(qw[e]) * f);
+        *(uint4 *)(sm.qg + r * kR + c * 8) = make_uint4(qo[0], qo[1], qo[2], qo[3]);
+        *(uint4 *)(sm.dO + r * kR + c * 8) = ok ? dv[u] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int x = tid + 256 * u, r = x / 8, c = x % 8;
+        *(uint4 *)(sm.aq + r * kT + c * 8) = av[u];
+    }
+    __syncthreads();
+    // dO as B fragments (k = token, col = state column)
+    Frag8 bo[4];
+#pragma unroll
+    for (int st = 0; st < 4; st++) bo[st] = lds_tr_frag(sm.dO, kR, st * 16, wave * 32, lane);
+    // Aqk^T dO (rows = tokens j), then as B fragments of W^T (.), negated
+    Frag8 nd[4];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        f32x16_t x = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+            x = mfma32<DT>(lds_tr_frag(sm.aq, kT, st * 16, t * 32, lane), bo[st], x);
+        nd[2 * t] = c_frag<DT>(x, 0, -1.f);
+        nd[2 * t + 1] = c_frag<DT>(x, 1, -1.f);
+    }
+    // F = (gamma scale Q)^T dO - W^T (Aqk^T dO): rows dk (4 tiles), stored in the product
+    // layout in the dtype: [dv tile][dk tile][lane][16]
+    const uint16_t *wtf = w.WTf + ch * kC * kD;
+    uint16_t *fo = w.F + ch * kD * kD + (size_t)wave * 4 * 64 * 16;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        f32x16_t x = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            x = mfma32<DT>(lds_tr_frag(sm.qg, kR, st * 16, r * 32, lane), bo[st], x);
+            Frag8 wa;
+            wa.u = *(const uint4 *)(wtf + ((r * 4 + st) * 64 + lane) * 8);
+            x = mfma32<DT>(wa, nd[st], x);
+        }
+        uint4 *o = (uint4 *)(fo + ((size_t)r * 64 + lane) * 16);
+        o[0] = c_frag<DT>(x, 0).u;
+        o[1] = c_frag<DT>(x, 1).u;
+    }
+}
+
+// The state gradient, backwards over a sequence's chunks; one wavefront per 32 state columns
+// (as the forward's state pass). Operands two chunks ahead, straight into registers.
+struct BwdOps {
+    Frag8 kr[2][8];  // lam K: token tile t, dk step st (rows = tokens)
+    Frag8 wt[4][4];  // W^T: dk tile r, token step st
+    uint4 f[4][2];   // F: dk tile r, the lane's 16 values as two 16-byte halves
+    float glast;
+};
+
+template <int DT>
+__global__ __launch_bounds__(64, 1) void gdr_bwd_state(GdrArgs a, MfmaWs w, const float *d_final,
+                                                       float *dh0) {
+    const int64_t sh = blockIdx.x / 4, s = sh / a.H, h = sh % a.H;
+    const int lane = threadIdx.x;
+    const int wave = blockIdx.x % 4;
+    const int col = lane & 31, half = lane >> 5;
+    const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
+    const int dv = wave * 32 + col;
+    // dS: tile r holds rows 32 r + 8 (i / 4) + 4 h + i % 4 of column dv
+    f32x16_t D[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+            D[r][i] = d_final ? d_final[sh * kD * kD + row * kD + dv] : 0.f;
+        }
+    // a chunk before the sequence's first loads the first again (every call the same loads)
+    auto load = [&](int c, BwdOps &x) __attribute__((always_inline)) {
+        c = c >= c0 ? c : c0;
+        const int64_t ch = (int64_t)c * a.H + h;
+        const uint16_t *kr = w.Krf + ch * kC * kD, *wt = w.WTf + ch * kC * kD;
+        const uint16_t *f = w.F + ch * kD * kD + (size_t)wave * 4 * 64 * 16;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int st = 0; st < 8; st++)
+                x.kr[t][st].u = *(const uint4 *)(kr + ((t * 8 + st) * 64 + lane) * 8);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                x.wt[r][st].u = *(const uint4 *)(wt + ((r * 4 + st) * 64 + lane) * 8);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            x.f[r][0] = *(const uint4 *)(f + ((size_t)r * 64 + lane) * 16);
+            x.f[r][1] = *(const uint4 *)(f + ((size_t)r * 64 + lane) * 16 + 8);
+        }
+        x.glast = w.G[ch * kC + kC - 1];
+    };
+    auto step = [&](int c, BwdOps &x) __attribute__((always_inline)) {
+        const int64_t ch = (int64_t)c * a.H + h;
+        // dS after the chunk (dS_{c+1}), kept for the gradients as S is in Sf
+        Frag8 df[8];
+        uint16_t *dso = w.dSf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            df[st] = c_frag<DT>(D[st / 2], st % 2);
+            *(uint4 *)(dso + (st * 64 + lane) * 8) = df[st].u;
+        }
+        // X = (lam K) dS_{c+1}: 2 token tiles
+        f32x16_t X[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) X[t] = zero16();
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) X[t] = mfma32<DT>(x.kr[t][st], df[st], X[t]);
+        Frag8 nx[4];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            nx[2 * t] = c_frag<DT>(X[t], 0, -1.f);
+            nx[2 * t + 1] = c_frag<DT>(X[t], 1, -1.f);
+        }
+        // dS_c = exp(G_last) dS_{c+1} + F - W^T X
+        const float gl = __expf(x.glast);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t fw[8] = {x.f[r][0].x, x.f[r][0].y, x.f[r][0].z, x.f[r][0].w,
+                                    x.f[r][1].x, x.f[r][1].y, x.f[r][1].z, x.f[r][1].w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float fv = (i & 1) ? unpack_hi<DT>(fw[i / 2]) : unpack_lo<DT>(fw[i / 2]);
+                D[r][i] = D[r][i] * gl + fv;
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) D[r] = mfma32<DT>(x.wt[r][st], nx[st], D[r]);
+    };
+    BwdOps oa, ob;
+    if (c0 < c1) {
+        load(c1 - 1, oa);
+        load(c1 - 2, ob);
+    }
+    for (int c = c1 - 1; c >= c0; c -= 2) {
+        step(c, oa);
+        load(c - 2, oa);
+        if (c - 1 < c0) break;
+        step(c - 1, ob);
+        load(c - 3, ob);
+    }
+    if (dh0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                dh0[sh * kD * kD + row * kD + dv] = D[r][i];
+            }
+    }
+}
+
+// The gradients of one (chunk, head). Wave w owns columns 32 w + [0, 32) of dq, dk, dv (all 64
+// tokens) and the 32x32 tile (w / 2, w % 2) of the 64x64 intermediates. LDS in two phases:
+// first S^T, dS^T, V'^T and dO (the products over the state columns), then Q, K, V, T and the
+// token-by-token intermediates; dV'^T and Aqk live through both.
+namespace bl {
+constexpr int ST = 0, DST = 34816, VPT = 69632, DOB = 88064, DVPT = 105472, AQ = 123904;
+constexpr int QB = 0, KB = 17408, VB = 34816, DWT = 52224, TB = 70656, M1T = 79872, DTT = 89088;
+constexpr int M2T = 133120, M3BT = 142336;      // m2^T, later m3^T; m3b^T
+constexpr int DVLO = M2T;                       // dV'^T's rounding residual, until m2^T
+constexpr int TOKF = 151552;                    // G, gamma, lam, beta, qi, ki [64] f32
+constexpr int RED = TOKF + 6 * 256;             // 4 floats
+constexpr int PART = RED + 16;                  // 8 x [4][64] f32 partial sums
+constexpr int BYTES = PART + 8 * 1024;
+}  // namespace bl
+static_assert(bl::DTT + kC * kT * 2 <= bl::DVPT && bl::AQ + kC * kT * 2 <= bl::M2T, "phases");
+static_assert(bl::BYTES <= 160 * 1024, "LDS");
+
+template <int DT>
+__global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
+                                                        void *dq, void *dk, void *dv, void *dg,
+                                                        void *dbeta) {
+    __shared__ __align__(16) char smem[bl::BYTES];
+    const int64_t ch = blockIdx.x, n = ch / a.H, h = ch % a.H;
+    const int len = w.chunk_len[n];
+    if (len == 0) return;
+    const int64_t tok0 = w.chunk_tok0[n];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const int ti = wave >> 1, tj = wave & 1;  // this wave's 64x64 tile
+    auto U16 = [&](int off) { return (uint16_t *)(smem + off); };
+    auto F32 = [&](int off) { return (float *)(smem + off); };
+    uint16_t *sST = U16(bl::ST), *sDST = U16(bl::DST), *sVPT = U16(bl::VPT), *sDOB = U16(bl::DOB);
+    uint16_t *sDVPT = U16(bl::DVPT), *sAQ = U16(bl::AQ), *sDVLO = U16(bl::DVLO);
+    float *tG = F32(bl::TOKF), *tGam = tG + 64, *tLam = tG + 128, *tBet = tG + 192,
+          *tQi = tG + 256, *tKi = tG + 320;
+    float *pGam = F32(bl::PART), *pU = pGam + 256, *pS = pGam + 512, *pBet = pGam + 768,
+          *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
+
+    // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
+    if (tid < kC) {
+        const float gv = w.G[ch * kC + tid];
+        tG[tid] = gv;
+        tGam[tid] = __expf(gv);
+        tLam[tid] = __expf(w.G[ch * kC + kC - 1] - gv);
+        tBet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
+    }
+    {
+        const uint16_t *sf = w.Sf + ch * kD * kD, *dsf = w.dSf + ch * kD * kD;
+        // fragment (dv tile p, dk step st), lane l: column dv = 32 p + l % 32 (a row of X^T),
+        // dk runs 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
+        for (int x = tid; x < 32 * 64; x += 256) {
+            const int f = x / 64, l = x % 64, p = f / 8, st = f % 8;
+            const uint4 v1 = *(const uint4 *)(sf + (size_t)x * 8);
+            const uint4 v2 = *(const uint4 *)(dsf + (size_t)x * 8);
+            const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
+            *(uint2 *)(sST + r * kR + c) = make_uint2(v1.x, v1.y);
+            *(uint2 *)(sST + r * kR + c + 8) = make_uint2(v1.z, v1.w);
+            *(uint2 *)(sDST + r * kR + c) = make_uint2(v2.x, v2.y);
+            *(uint2 *)(sDST + r * kR + c + 8) = make_uint2(v2.z, v2.w);
+        }
+        const uint16_t *vf = w.Vf + ch * kC * kD;
+        for (int x = tid; x < 16 * 64; x += 256) {
+            const int f = x / 64, l = x % 64, p = f / 4, st = f % 4;
+            const uint4 v1 = *(const uint4 *)(vf + (size_t)x * 8);
+            const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
+            *(uint2 *)(sVPT + r * kT + c) = make_uint2(v1.x, v1.y);
+            *(uint2 *)(sVPT + r * kT + c + 8) = make_uint2(v1.z, v1.w);
+        }
+        const uint16_t *dob = (const uint16_t *)d_out;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
+            const uint4 v1 = *(const uint4 *)(dob + row * kD + c * 8);
+            *(uint4 *)(sDOB + r * kR + c * 8) = r < len ? v1 : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 256 * u, r = x / 8, c = x % 8;
+            *(uint4 *)(sAQ + r * kT + c * 8) = *(const uint4 *)(w.Aqk + ch * kC * kC + r * kC + c * 8);
+        }
+        for (int x = tid; x < 8 * 256; x += 256) pGam[x] = 0.f;
+    }
+    __syncthreads();
+    // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns, stored as dV'^T
+    {
+        const uint16_t *kr = w.Krf + ch * kC * kD;
+        const uint16_t *dsf = w.dSf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            f32x16_t x = zero16();
+#pragma unroll
+            for (int st = 0; st < 8; st++) {
+                Frag8 ka, db;
+                ka.u = *(const uint4 *)(kr + ((t * 8 + st) * 64 + lane) * 8);
+                db.u = *(const uint4 *)(dsf + (st * 64 + lane) * 8);
+                x = mfma32<DT>(ka, db, x);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                x = mfma32<DT>(lds_tr_frag(sAQ, kT, st * 16, t * 32, lane),
+                               lds_tr_frag(sDOB, kR, st * 16, wave * 32, lane), x);
+            store_ct<DT>(sDVPT, kT, t * 32, wave * 32, x, lane);
+            // and what the rounding left, for T^T dV' (d beta's largest term)
+#pragma unroll
+            for (int i = 0; i < 16; i++) x[i] -= round_to<DT>(x[i]);
+            store_ct<DT>(sDVLO, kT, t * 32, wave * 32, x, lane);
+        }
+    }
+    __syncthreads();
+    // (a) d(gamma q) = dO S^T, (e) dkt = V' dS_{c+1}^T, (f) dw = -dV' S^T: 2 token tiles of the
+    // wave's 32 dk columns; (b) d attn = dO V'^T on the wave's tile, zero above the diagonal
+    f32x16_t dqg[2], dkt[2], dw[2], datt = zero16();
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        dqg[t] = dkt[t] = dw[t] = zero16();
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const Frag8 bs = lds_tr_frag(sST, kR, st * 16, wave * 32, lane);
+            dqg[t] = mfma32<DT>(row_frag(sDOB, kR, t * 32, st * 16, lane), bs, dqg[t]);
+            dw[t] = mfma32<DT>(lds_tr_frag(sDVPT, kT, st * 16, t * 32, lane), bs, dw[t]);
+            dkt[t] = mfma32<DT>(lds_tr_frag(sVPT, kT, st * 16, t * 32, lane),
+                                lds_tr_frag(sDST, kR, st * 16, wave * 32, lane), dkt[t]);
+        }
+    }
+    if (!(ti == 0 && tj == 1)) {
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+            datt = mfma32<DT>(row_frag(sDOB, kR, ti * 32, st * 16, lane),
+                              lds_tr_frag(sVPT, kT, st * 16, tj * 32, lane), datt);
+    }
+    // <S, dS_{c+1}> over the chunk
+    {
+        float acc = 0.f;
+        for (int x = tid; x < kD * 16; x += 256) {
+            const int r = x / 16, c = (x % 16) * 8;
+            const uint4 s1 = *(const uint4 *)(sST + r * kR + c), s2 = *(const uint4 *)(sDST + r * kR + c);
+            const uint32_t a1[4] = {s1.x, s1.y, s1.z, s1.w}, a2[4] = {s2.x, s2.y, s2.z, s2.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                acc += unpack_lo<DT>(a1[e]) * unpack_lo<DT>(a2[e]) + unpack_hi<DT>(a1[e]) * unpack_hi<DT>(a2[e]);
+        }
+        acc = sum32(acc);
+        acc += __shfl_xor(acc, 32, 64);
+        if (lane == 0) F32(bl::RED)[wave] = acc;
+    }
+    __syncthreads();  // phase 1 done: S^T, dS^T, V'^T and dO are dead
+
+    // ---- phase 2: Q, K (normalised as the forward did, with the inverse norms), V, T ----
+    {
+        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
+                       *vin = (const uint16_t *)a.v;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+            const bool ok = r < len;
+            const int64_t row = (tok0 + (ok ? r : len - 1)) * a.H + h;
+            uint4 qv = *(const uint4 *)(qin + row * kD + c * 8);
+            uint4 kv = *(const uint4 *)(kin + row * kD + c * 8);
+            const uint4 vv = *(const uint4 *)(vin + row * kD + c * 8);
+            float qi = 1.f, ki = 1.f;
+            if (a.l2norm) {
+                const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, kw[4] = {kv.x, kv.y, kv.z, kv.w};
+                float sq = 0.f, sk = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float q0 = unpack_lo<DT>(qw[e]), q1 = unpack_hi<DT>(qw[e]);
+                    const float k0 = unpack_lo<DT>(kw[e]), k1 = unpack_hi<DT>(kw[e]);
+                    sq += q0 * q0 + q1 * q1;
+                    sk += k0 * k0 + k1 * k1;
+                }
+#pragma unroll
+                for (int o = 8; o >= 1; o >>= 1) {
+                    sq += __shfl_xor(sq, o, 64);
+                    sk += __shfl_xor(sk, o, 64);
+                }
+                qi = 1.f / sqrtf(sq + 1e-6f);
+                ki = 1.f / sqrtf(sk + 1e-6f);
+                uint32_t qo[4], ko[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    qo[e] = pack2<DT>(unpack_lo<DT>(qw[e]) * qi, unpack_hi<DT>(qw[e]) * qi);
+                    ko[e] = pack2<DT>(unpack_lo<DT>(kw[e]) * ki, unpack_hi<DT>(kw[e]) * ki);
+                }
+                qv = make_uint4(qo[0], qo[1], qo[2], qo[3]);
+                kv = make_uint4(ko[0], ko[1], ko[2], ko[3]);
+            }
+            const uint4 z = make_uint4(0, 0, 0, 0);
+            *(uint4 *)(U16(bl::QB) + r * kR + c * 8) = ok ? qv : z;
+            *(uint4 *)(U16(bl::KB) + r * kR + c * 8) = ok ? kv : z;
+            *(uint4 *)(U16(bl::VB) + r * kR + c * 8) = ok ? vv : z;
+            if (c == 0) {
+                tQi[r] = qi;
+                tKi[r] = ki;
+            }
+        }
+        for (int x = tid; x < kC * kC / 8; x += 256) {
+            const int r = x / 8, c = x % 8;
+            *(uint4 *)(U16(bl::TB) + r * kT + c * 8) = *(const uint4 *)(w.Tm + ch * kC * kC + r * kC + c * 8);
+        }
+    }
+    uint16_t *sQB = U16(bl::QB), *sKB = U16(bl::KB), *sVB = U16(bl::VB), *sDWT = U16(bl::DWT);
+    uint16_t *sTB = U16(bl::TB), *sM1T = U16(bl::M1T), *sDTT = U16(bl::DTT);
+    uint16_t *sM2T = U16(bl::M2T), *sM3BT = U16(bl::M3BT);
+    // dw^T (negated: dw = -dV' S^T) and m1^T = (d attn o decay)^T
+#pragma unroll
+    for (int t = 0; t < 2; t++) store_ct<DT>(sDWT, kT, t * 32, wave * 32, dw[t], lane, -1.f);
+    {
+        f32x16_t m = zero16();
+        if (!(ti == 0 && tj == 1)) {
+            const int j = tj * 32 + col;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = ti * 32 + crow(i, lane);
+                if (j > r) datt[i] = 0.f;
+                m[i] = datt[i] * (r >= j ? __expf(tG[r] - tG[j]) : 0.f);
+            }
+        }
+        store_ct<DT>(sM1T, kT, ti * 32, tj * 32, m, lane);
+    }
+    __syncthreads();  // Q, K, V, T, dw^T, m1^T in place
+    const float scale = a.scale;
+    // (d) d attn o attn: + row sums, - column sums into dG
+    if (!(ti == 0 && tj == 1)) {
+        const int j = tj * 32 + col;
+        float cs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = ti * 32 + crow(i, lane);
+            const uint16_t ab = sAQ[r * kT + j];
+            const float av = (DT == DM_BF16) ? __uint_as_float((uint32_t)ab << 16)
+                                             : (float)__builtin_bit_cast(_Float16, ab);
+            const float p = datt[i] * av;
+            cs += p;
+            const float rs = sum32(p);
+            if (col == 0) pGr[wave * 64 + r] += rs;
+        }
+        cs += __shfl_xor(cs, 32, 64);
+        if (half == 0) pGc[wave * 64 + j] += cs;
+    }
+    // dq = gamma d(gamma q) + m1 K; dk = lam dkt + scale m1^T Q; d gamma, s partial sums
+    f32x16_t dqa[2], dka[2], dva[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        float gsum[16], ssum[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+            const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
+            const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
+                                             : (float)__builtin_bit_cast(_Float16, qb);
+            const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
+                                             : (float)__builtin_bit_cast(_Float16, kb);
+            gsum[i] = dqg[t][i] * qv * scale;
+            ssum[i] = dkt[t][i] * kv;
+            dqa[t][i] = tGam[r] * dqg[t][i];
+            dka[t][i] = tLam[r] * dkt[t][i];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float g1 = sum32(gsum[i]), s1 = sum32(ssum[i]);
+            if (col == 0) {
+                const int r = t * 32 + crow(i, lane);
+                pGam[wave * 64 + r] += g1;
+                pS[wave * 64 + r] += s1;
+            }
+        }
+        f32x16_t x = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            dqa[t] = mfma32<DT>(lds_tr_frag(sM1T, kT, st * 16, t * 32, lane),
+                                lds_tr_frag(sKB, kR, st * 16, wave * 32, lane), dqa[t]);
+            x = mfma32<DT>(row_frag(sM1T, kT, t * 32, st * 16, lane),
+                           lds_tr_frag(sQB, kR, st * 16, wave * 32, lane), x);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) dka[t][i] += scale * x[i];
+    }
+    // (g) dT = dV' (beta V)^T + dw (beta gamma K)^T on the wave's tile, stored as dT^T
+    {
+        f32x16_t c1 = zero16(), c2 = zero16();
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            c1 = mfma32<DT>(lds_tr_frag(sDVPT, kT, st * 16, ti * 32, lane),
+                            row_frag(sVB, kR, tj * 32, st * 16, lane), c1);
+            c2 = mfma32<DT>(lds_tr_frag(sDWT, kT, st * 16, ti * 32, lane),
+                            row_frag(sKB, kR, tj * 32, st * 16, lane), c2);
+        }
+        const int j = tj * 32 + col;
+        const float bj = tBet[j], bgj = tBet[j] * tGam[j];
+#pragma unroll
+        for (int i = 0; i < 16; i++) c1[i] = c1[i] * bj + c2[i] * bgj;
+        store_ct<DT>(sDTT, kT, ti * 32, tj * 32, c1, lane);
+    }
+    // (h) dvb = T^T dV', dkbg = T^T dw: dv = beta dvb; dk += beta gamma dkbg; sums for d beta,
+    // d gamma
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        f32x16_t xb = zero16(), xk = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const Frag8 ta = lds_tr_frag(sTB, kT, st * 16, t * 32, lane);
+            xb = mfma32<DT>(ta, row_frag(sDVPT, kT, wave * 32, st * 16, lane), xb);
+            xb = mfma32<DT>(ta, row_frag(sDVLO, kT, wave * 32, st * 16, lane), xb);
+            xk = mfma32<DT>(ta, row_frag(sDWT, kT, wave * 32, st * 16, lane), xk);
+        }
+        float bs[16], us[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+            const uint16_t vb = sVB[r * kR + c], kb = sKB[r * kR + c];
+            const float vv = (DT == DM_BF16) ? __uint_as_float((uint32_t)vb << 16)
+                                             : (float)__builtin_bit_cast(_Float16, vb);
+            const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
+                                             : (float)__builtin_bit_cast(_Float16, kb);
+            dva[t][i] = tBet[r] * xb[i];
+            dka[t][i] += tBet[r] * tGam[r] * xk[i];
+            bs[i] = xb[i] * vv;
+            us[i] = xk[i] * kv;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float b1 = sum32(bs[i]), u1 = sum32(us[i]);
+            if (col == 0) {
+                const int r = t * 32 + crow(i, lane);
+                pBet[wave * 64 + r] += b1;
+                pU[wave * 64 + r] += u1;
+            }
+        }
+    }
+    __syncthreads();  // dT^T complete
+    // (i) m2 = T^T dT on the wave's tile (a, b) = (ti, tj), stored as m2^T
+    {
+        f32x16_t m2 = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+            m2 = mfma32<DT>(lds_tr_frag(sTB, kT, st * 16, ti * 32, lane),
+                            row_frag(sDTT, kT, tj * 32, st * 16, lane), m2);
+        store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m2, lane);
+    }
+    __syncthreads();
+    // dA = -(m2 T^T) strictly below the diagonal on tile (a, c) = (ti, tj); the recomputed
+    // A = beta (K K^T) o decay for the gate's sums; m3 = dA o decay
+    f32x16_t m3 = zero16(), m3b = zero16();
+    if (!(ti == 0 && tj == 1)) {
+        f32x16_t da = zero16(), kk = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+            da = mfma32<DT>(lds_tr_frag(sM2T, kT, st * 16, ti * 32, lane),
+                            row_frag(sTB, kT, tj * 32, st * 16, lane), da);
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+            kk = mfma32<DT>(row_frag(sKB, kR, ti * 32, st * 16, lane),
+                            row_frag(sKB, kR, tj * 32, st * 16, lane), kk);
+        const int j = tj * 32 + col;
+        float cs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = ti * 32 + crow(i, lane);
+            const bool lower = r > j;
+            const float d = lower ? -da[i] : 0.f;
+            const float dec = lower ? __expf(tG[r] - tG[j]) : 0.f;
+            const float am = tBet[r] * kk[i] * dec;
+            const float p = d * am;
+            cs += p;
+            const float rs = sum32(p);
+            if (col == 0) pGr[wave * 64 + r] += rs;
+            m3[i] = d * dec;
+            m3b[i] = m3[i] * tBet[r];
+        }
+        cs += __shfl_xor(cs, 32, 64);
+        if (half == 0) pGc[wave * 64 + j] += cs;
+    }
+    __syncthreads();  // m2^T dead: m3^T takes its place
+    store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m3, lane);
+    store_ct<DT>(sM3BT, kT, ti * 32, tj * 32, m3b, lane);
+    __syncthreads();
+    // (j) dkbeta = m3 K: dk += beta dkbeta; d beta sums; dk += m3^T (beta K)
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        f32x16_t xb = zero16(), xt = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const Frag8 kb = lds_tr_frag(sKB, kR, st * 16, wave * 32, lane);
+            xb = mfma32<DT>(lds_tr_frag(sM2T, kT, st * 16, t * 32, lane), kb, xb);
+            xt = mfma32<DT>(row_frag(sM3BT, kT, t * 32, st * 16, lane), kb, xt);
+        }
+        float bs[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+            const uint16_t kb = sKB[r * kR + c];
+            const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
+                                             : (float)__builtin_bit_cast(_Float16, kb);
+            dka[t][i] += tBet[r] * xb[i] + xt[i];
+            bs[i] = xb[i] * kv;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float b1 = sum32(bs[i]);
+            if (col == 0) pBet[wave * 64 + crow(i, lane) + t * 32] += b1;
+        }
+    }
+    // (m) the l2 normalisation's sums: <qn, scale dq>, <kn, dk> per token
+    if (a.l2norm) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            float qs[16], ks[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+                const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
+                const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
+                                                 : (float)__builtin_bit_cast(_Float16, qb);
+                const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
+                                                 : (float)__builtin_bit_cast(_Float16, kb);
+                qs[i] = qv * dqa[t][i] * scale;
+                ks[i] = kv * dka[t][i];
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float q1 = sum32(qs[i]), k1 = sum32(ks[i]);
+                if (col == 0) {
+                    const int r = t * 32 + crow(i, lane);
+                    pSq[wave * 64 + r] = q1;
+                    pSk[wave * 64 + r] = k1;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // per token: dG, then dg = its reverse cumulative sum; d beta
+    if (wave == 0) {
+        const int i = lane;
+        float gam = 0.f, u = 0.f, s = 0.f, bet = 0.f, gr = 0.f;
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+            gam += pGam[x * 64 + i];
+            u += pU[x * 64 + i];
+            s += pS[x * 64 + i];
+            bet += pBet[x * 64 + i];
+            gr += pGr[x * 64 + i] - pGc[x * 64 + i];
+        }
+        gam += tBet[i] * u;
+        bet += tGam[i] * u;
+        const float ls = tLam[i] * s;
+        float dG = gr - ls + gam * tGam[i];
+        float lam_sum = ls;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) lam_sum += __shfl_xor(lam_sum, o, 64);
+        const float* red = F32(bl::RED);
+        const float sds = red[0] + red[1] + red[2] + red[3];
+        if (i == kC - 1) dG += lam_sum + sds * __expf(tG[kC - 1]);
+        // reverse inclusive scan
+        float x = dG;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float y = __shfl_down(x, o, 64);
+            if (i + o < 64) x += y;
+        }
+        if (i < len) {
+            const int64_t tk = (tok0 + i) * a.H + h;
+            st_any(a.g_dt, dg, tk, x);
+            st_any(a.beta_dt, dbeta, tk, bet);
+        }
+        if (a.l2norm) {
+            float sq = 0.f, sk = 0.f;
+#pragma unroll
+            for (int x2 = 0; x2 < 4; x2++) {
+                sq += pSq[x2 * 64 + i];
+                sk += pSk[x2 * 64 + i];
+            }
+            pSq[i] = sq;
+            pSk[i] = sk;
+        }
+    }
+    __syncthreads();
+    // dq, dk (the scale and the l2 normalisation undone), dv
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = t * 32 + crow(i, lane);
+            if (r >= len) continue;
+            const int c = wave * 32 + col;
+            const int64_t o = ((tok0 + r) * a.H + h) * kD + c;
+            float qo = dqa[t][i] * scale, ko = dka[t][i];
+            if (a.l2norm) {
+                const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
+                const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
+                                                 : (float)__builtin_bit_cast(_Float16, qb);
+                const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
+                                                 : (float)__builtin_bit_cast(_Float16, kb);
+                qo = tQi[r] * (qo - qv * pSq[r]);
+                ko = tKi[r] * (ko - kv * pSk[r]);
+            }
+            st<DT>(dq, o, qo);
+            st<DT>(dk, o, ko);
+            st<DT>(dv, o, dva[t][i]);
+        }
+}
+
+// ------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------
 
@@ -703,6 +1526,62 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
     }
     probe_add(DM_PROBE_GDR_CHUNK_FWD, 4);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule: MFMA launch");
+    return DM_OK;
+}
+
+size_t gdr_mfma_bwd_workspace(const dm_gdr_desc *d) {
+    return mfma_layout(d, nullptr, nullptr, true);
+}
+
+// plan -> prep (with T, lam K and W^T for the backward) -> the forward's state pass (S and V'
+// per chunk) -> F per chunk -> the state gradient's pass (dS per chunk, dh0) -> the gradients
+template <int DT>
+static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chunks,
+                                 unsigned seqs, const float *h0, const void *d_out,
+                                 const float *d_final, void *dq, void *dk, void *dv, void *dg,
+                                 void *dbeta, float *dh0, hipStream_t st) {
+    {
+        KernelTimer t(DM_KERNEL_GDR_PREP, st);
+        if (chunks) gdr_mfma_prep<DT><<<chunks, 256, 0, st>>>(a, w);
+    }
+    {
+        KernelTimer t(DM_KERNEL_GDR_STATE, st);
+        gdr_mfma_state<DT><<<seqs * 4, 64, 0, st>>>(a, w, h0, nullptr);
+    }
+    {
+        KernelTimer t(DM_KERNEL_GDR_BWD_PRE, st);
+        if (chunks) gdr_bwd_pre<DT><<<chunks, 256, 0, st>>>(a, w, d_out);
+    }
+    {
+        KernelTimer t(DM_KERNEL_GDR_BWD_STATE, st);
+        gdr_bwd_state<DT><<<seqs * 4, 64, 0, st>>>(a, w, d_final, dh0);
+    }
+    {
+        KernelTimer t(DM_KERNEL_GDR_BWD_GRADS, st);
+        if (chunks)
+            gdr_bwd_grads<DT><<<chunks, 256, 0, st>>>(a, w, d_out, dq, dk, dv, dg, dbeta);
+    }
+}
+
+int launch_gdr_mfma_bwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
+                        const void *g, const void *beta, const float *h0, const void *d_out,
+                        const float *d_final, void *dq, void *dk, void *dv, void *dg,
+                        void *dbeta, float *dh0, void *workspace, hipStream_t st) {
+    MfmaWs w;
+    mfma_layout(d, (char *)workspace, &w, true);
+    const GdrArgs a = gdr_args(d, q, k, v, g, beta);
+    const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
+    int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st);
+    if (rc) return rc;
+    const unsigned chunks = (unsigned)(nc * d->h), seqs = (unsigned)(S * d->h);
+    if (d->dtype == DM_BF16)
+        gdr_mfma_bwd_kernels<DM_BF16>(a, w, chunks, seqs, h0, d_out, d_final, dq, dk, dv, dg,
+                                      dbeta, dh0, st);
+    else
+        gdr_mfma_bwd_kernels<DM_F16>(a, w, chunks, seqs, h0, d_out, d_final, dq, dk, dv, dg,
+                                     dbeta, dh0, st);
+    probe_add(DM_PROBE_GDR_CHUNK_BWD, 6);
+    DM_LAUNCH_CHECK("chunk_gated_delta_rule_backward: MFMA launch");
     return DM_OK;
 }
 

@@ -35,5 +35,12 @@ size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d);
 int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
                         const void *g, const void *beta, const float *h0, void *out,
                         float *final_state, void *workspace, hipStream_t st);
+size_t gdr_mfma_bwd_workspace(const dm_gdr_desc *d);
+int launch_gdr_mfma_bwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
+                        const void *g, const void *beta, const float *h0, const void *d_out,
+                        const float *d_final, void *dq, void *dk, void *dv, void *dg,
+                        void *dbeta, float *dh0, void *workspace, hipStream_t st);
+GdrArgs gdr_args(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
+                 const void *g, const void *beta);
 
 }  // namespace dm

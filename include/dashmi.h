@@ -123,6 +123,9 @@ typedef enum {
     DM_KERNEL_GDR_STATE,      /* chunked gated delta rule: the state pass */
     DM_KERNEL_GDR_OUTPUT,     /* chunked gated delta rule: the output */
     DM_KERNEL_GDR_STEP,       /* gated delta rule step */
+    DM_KERNEL_GDR_BWD_PRE,    /* chunked gated delta rule backward: per-chunk state-gradient terms */
+    DM_KERNEL_GDR_BWD_STATE,  /* chunked gated delta rule backward: the state-gradient pass */
+    DM_KERNEL_GDR_BWD_GRADS,  /* chunked gated delta rule backward: per-chunk gradients */
     DM_KERNEL_COUNT
 } dm_kernel;
 int dm_kernel_timing(int enable);

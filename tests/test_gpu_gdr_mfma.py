@@ -73,3 +73,45 @@ def test_mfma_packed_equals_per_sequence():
         o1, f1 = dm.chunk_gated_delta_rule(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b],
                                            beta[:, a:b], h0[s:s + 1], None, opts)
         assert torch.equal(o1, out[:, a:b]) and torch.equal(f1, fin[s:s + 1])
+
+
+# The backward's bounds are the reference's for its tensor-core kernels in bf16 at these head
+# shapes (crates/dash-ops/tests/gated_delta_chunk.rs:510-531): 7.5e-3 with the l2 normalisation
+# at [1, 200, 2, 128, 128], 1.2e-2 without it (the gate's gradient, a difference of sums within
+# each chunk, is the largest error, as the reference measured). f16 carries more mantissa.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("lens,h,l2norm,tol", [
+    ([200], 2, True, 7.5e-3),
+    ([200], 2, False, 1.2e-2),
+    ([37, 64, 0, 100, 5, 1], 3, True, 7.5e-3),
+    ([130, 300], 2, False, 1.2e-2),
+])
+def test_mfma_backward_matches_oracle(dtype, lens, h, l2norm, tol):
+    T, D = sum(lens), 128
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    seed = 300 + sum(lens) + 7 * l2norm
+    q = syn.normal(seed, (1, T, h, D), "cuda")
+    k = syn.normal(seed + 1, (1, T, h, D), "cuda")
+    if not l2norm:
+        q, k = syn.l2norm(q), syn.l2norm(k)
+    v = syn.normal(seed + 2, (1, T, h, D), "cuda")
+    g = -torch.nn.functional.softplus(syn.normal(seed + 3, (1, T, h), "cuda"))
+    beta = torch.sigmoid(syn.normal(seed + 4, (1, T, h), "cuda"))
+    h0 = syn.normal(seed + 5, (len(lens), h, D, D), "cuda", std=0.1)
+    do = syn.normal(seed + 6, (1, T, h, D), "cuda").to(dtype)
+    dfin = syn.normal(seed + 7, (len(lens), h, D, D), "cuda", std=0.1)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    print(f"backward case lens {lens} h {h} l2norm {l2norm} {dtype}", flush=True)
+    _lib.probe_reset()
+    opts = dm.ChunkGatedDeltaOptions(qk_l2norm=l2norm, output_final_state=True)
+    r = dm.chunk_gated_delta_rule_backward(q, k, v, g, beta, h0, cu.cuda(), do, dfin, opts)
+    torch.cuda.synchronize()
+    assert _lib.probe_counts()["gdr_chunk_bwd"] > 0
+    e = oracle.gdr_chunk_bwd(host(q), host(k), host(v), host(g), host(beta), host(h0), host(do),
+                             host(dfin), cu.numpy(), l2norm, precision="f64")
+    worst = 0.0
+    for name, a_, e_ in zip(["dq", "dk", "dv", "dg", "dbeta", "dh0"], r, e):
+        rr = errors(host(a_), e_)[1]
+        worst = max(worst, rr)
+        print(f"  {name}: rel {rr:.2e}")
+    assert worst <= tol
