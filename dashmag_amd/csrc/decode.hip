@@ -4,7 +4,8 @@
 // all the query heads of a key-value head's group (the GQA reuse), and writes a normalised
 // partial output and its log-sum-exp in f32. Pass 2 merges the spans by their log-sum-exp.
 //
-// Bandwidth-bound, no MFMA: each K/V row (D * 2 bytes) is read by D / 8 lanes with 16-byte
+// Bandwidth-bound. D = 128 runs its products on MFMA (decode_split_mfma); D = 64 and 256 on the
+// vector units (decode_split): each K/V row (D * 2 bytes) is read by D / 8 lanes with 16-byte
 // loads, one wavefront covering 64 * 8 / D rows per load, the dot products reduced across the
 // row's lanes with xor shuffles; f32 online softmax per lane group.
 #include <string>
@@ -18,6 +19,7 @@ namespace dm {
 constexpr int kDecodeRows = 4;        // K/V rows each lane group loads per step
 constexpr int kDecodeMinSpan = 512;    // fewest keys a workgroup takes
 constexpr int kDecodeWorkgroups = 1024;  // the split count aims at about this many workgroups
+constexpr int kDecodeWorkgroupsMfma = 4096;  // the same for the MFMA kernel (shorter per key)
 
 struct Bf16x8 {
     uint4 raw;
@@ -255,6 +257,170 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
     }
 }
 
+// The split pass for D = 128 on MFMA. Each wavefront sweeps its quarter of the split in blocks
+// of 32 keys: the block's K and V rows arrive by coalesced 16-byte loads (4 rows per load), go to
+// the wavefront's own LDS tiles, and the next block's loads are in flight while this block is
+// used. Per block, S^T = K q^T (32 keys x the group's heads, padded to 32 columns) and
+// O^T += V^T P^T (4 tiles of 32 columns x the heads) run as 32x32x16 products: the scores'
+// output layout (lane = head, rows = keys) is the B operand of the second product as it stands,
+// and V^T comes from transposed LDS reads. Each lane keeps the online softmax of its head in f32.
+template <int DT, int G>
+__global__ __launch_bounds__(256, 2) void decode_split_mfma(
+    int64_t S, int64_t Hq, int64_t Hkv, int64_t left, float scale, int nsplit, int span,
+    const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
+    const int32_t *__restrict__ lengths, float *__restrict__ part_o, float *__restrict__ part_lse) {
+    constexpr int D = 128, NW = 4, BK = 32;
+    constexpr int KS = D + 8, VS = D + 32;  // row strides (elements) of the row and transposed reads
+    struct Tiles {
+        uint16_t k[BK * KS];
+        uint16_t v[BK * VS];
+    };
+    static_assert(sizeof(float) * NW * (G * D + 2 * G) <= sizeof(Tiles) * NW, "combine in tiles");
+    __shared__ __align__(16) Tiles tiles[NW];
+    const int kh = blockIdx.x, split = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31, half = lane >> 5;
+
+    int64_t len = lengths ? (int64_t)lengths[b] : S;
+    if (len > S) len = S;
+    if (len < 0) len = 0;
+    int64_t lo = left >= 0 ? len - 1 - left : 0;
+    if (lo < 0) lo = 0;
+    const int64_t start = lo + (int64_t)split * span;
+    int64_t end = start + span;
+    if (end > len) end = len;
+
+    // the queries as B operands: column = head col (zero past the group), k slots
+    // d = 16 st + 4 h + e and 16 st + 8 + 4 h + e (the order of the key rows' A fragments)
+    Frag8 qf[8];
+#pragma unroll
+    for (int st = 0; st < 8; st++) {
+        if (col < G) {
+            const uint16_t *qp =
+                (const uint16_t *)q + (b * Hq + kh * G + col) * D + st * 16 + half * 4;
+            const uint2 a = *(const uint2 *)qp, c = *(const uint2 *)(qp + 8);
+            qf[st].u = make_uint4(a.x, a.y, c.x, c.y);
+        } else {
+            qf[st].u = make_uint4(0, 0, 0, 0);
+        }
+    }
+    const float qscale = scale * 1.4426950408889634f;
+
+    const int64_t row_stride = Hkv * D * 2;
+    const char *kb = (const char *)k + (b * S * Hkv + kh) * D * 2;
+    const char *vb = (const char *)v + (b * S * Hkv + kh) * D * 2;
+    // each wavefront sweeps a contiguous quarter of the split
+    const int64_t per_wave = span / NW;
+    const int64_t w0 = start + wave * per_wave;
+    const int64_t w1 = min(w0 + per_wave, end);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb + w0 * row_stride, 0xffffffffu);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb + w0 * row_stride, 0xffffffffu);
+    Tiles &t = tiles[wave];
+    uint4 kr[8], vr[8];
+    // block rows past the wavefront's range load row w1 - 1 again (their scores are -inf)
+    auto load = [&](int64_t j0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int64_t key = min(j0 + 4 * u + (lane >> 4), w1 - 1);
+            const uint32_t off = (uint32_t)((key - w0) * row_stride) + (lane & 15) * 16;
+            kr[u] = buf_load16_nt(krs, off);
+            vr[u] = buf_load16_nt(vrs, off);
+        }
+    };
+    auto stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int r = 4 * u + (lane >> 4), c = (lane & 15) * 8;
+            *(uint4 *)(t.k + r * KS + c) = kr[u];
+            *(uint4 *)(t.v + r * VS + c) = vr[u];
+        }
+    };
+    float m = -INFINITY, l = 0.f;
+    f32x16_t acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) acc[dt] = zero16();
+    auto block = [&](int64_t j0) __attribute__((always_inline)) {
+        f32x16_t sc = zero16();
+#pragma unroll
+        for (int st = 0; st < 8; st++) sc = mfma32<DT>(row_frag(t.k, KS, 0, st * 16, lane), qf[st], sc);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            sc[i] = j0 + crow(i, lane) < w1 ? sc[i] * qscale : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);
+        // with nothing visible yet (mn = -inf) every factor below is exp2(-inf) = 0
+        const float ref = mn == -INFINITY ? 0.f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - ref);
+        m = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            sc[i] = __builtin_amdgcn_exp2f(sc[i] - ref);
+            ps += sc[i];
+        }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[dt][i] *= alpha;
+        const Frag8 p0 = c_frag<DT>(sc, 0), p1 = c_frag<DT>(sc, 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            acc[dt] = mfma32<DT>(lds_tr_frag(t.v, VS, 0, dt * 32, lane), p0, acc[dt]);
+            acc[dt] = mfma32<DT>(lds_tr_frag(t.v, VS, 16, dt * 32, lane), p1, acc[dt]);
+        }
+    };
+    if (w0 < w1) {
+        load(w0);
+        int64_t j0 = w0;
+        for (; j0 + BK < w1; j0 += BK) {
+            stage();
+            load(j0 + BK);
+            block(j0);
+        }
+        stage();
+        block(j0);
+    }
+    l += __shfl_xor(l, 32, 64);
+
+    // the wavefronts' partial results through LDS (the tiles' space): [NW][G] m and l,
+    // [NW][G][D] acc
+    __syncthreads();
+    float *sm_acc = (float *)tiles, *sm_m = sm_acc + NW * G * D, *sm_l = sm_m + NW * G;
+    if (col < G) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) sm_acc[(wave * G + col) * D + dt * 32 + crow(i, lane)] = acc[dt][i];
+        if (half == 0) {
+            sm_m[wave * G + col] = m;
+            sm_l[wave * G + col] = l;
+        }
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < G * D; x += 256) {
+        const int g = x / D, d = x % D;
+        float M = -INFINITY;
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_m[w * G + g]);
+        float L = 0.f, A = 0.f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < NW; w++) {
+                const float f = __builtin_amdgcn_exp2f(sm_m[w * G + g] - M);
+                L += sm_l[w * G + g] * f;
+                A += sm_acc[(w * G + g) * D + d] * f;
+            }
+        }
+        const int64_t pr = (b * Hq + kh * G + g) * nsplit + split;
+        part_o[pr * D + d] = L > 0.f ? A / L : 0.f;
+        if (d == 0) part_lse[pr] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
+    }
+}
+
 // Pass 2: merges the splits of one (sequence, query head) by their log-sum-exp.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge(int64_t rows, int64_t D, int nsplit,
@@ -343,7 +509,8 @@ static bool split_takes(const dm_attention_desc *d) {
 static int span_of(const dm_attention_desc *d) {
     int64_t span = kDecodeMinSpan;
     const int64_t heads = d->b * d->hkv;
-    while (span < d->tk && heads * ((d->tk + span - 1) / span) > kDecodeWorkgroups) span *= 2;
+    const int64_t target = d->d == 128 ? kDecodeWorkgroupsMfma : kDecodeWorkgroups;
+    while (span < d->tk && heads * ((d->tk + span - 1) / span) > target) span *= 2;
     return (int)span;
 }
 
@@ -418,6 +585,9 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
     float *part_o = (float *)workspace;
     float *part_lse = (float *)((char *)workspace + align_up(parts * d->d * sizeof(float)));
     dim3 grid(nsplit, (unsigned)d->hkv, (unsigned)d->b);
+    // the MFMA kernel's grid: key-value heads fastest (the heads of a split read neighbouring
+    // bytes of the same cache rows at about the same time)
+    dim3 grid_hf((unsigned)d->hkv, nsplit, (unsigned)d->b);
     const int g = (int)(d->hq / d->hkv);
 #define DEC_SPLIT(DT, DD, GG)                                                               \
     decode_split<DT, DD, GG><<<grid, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, span, \
@@ -429,10 +599,20 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         case 4: DEC_SPLIT(DT, DD, 4); break;         \
         default: DEC_SPLIT(DT, DD, 8); break;        \
     }
+#define DEC_MFMA(DT, GG)                                                                    \
+    decode_split_mfma<DT, GG><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, \
+                                                    span, q, k, v, lengths, part_o, part_lse)
+#define DEC_G128(DT)                                 \
+    switch (g) {                                     \
+        case 1: DEC_MFMA(DT, 1); break;              \
+        case 2: DEC_MFMA(DT, 2); break;              \
+        case 4: DEC_MFMA(DT, 4); break;              \
+        default: DEC_MFMA(DT, 8); break;             \
+    }
 #define DEC_D(DT)                                    \
     switch (d->d) {                                  \
         case 64: DEC_G(DT, 64); break;               \
-        case 128: DEC_G(DT, 128); break;             \
+        case 128: DEC_G128(DT); break;               \
         default: DEC_G(DT, 256); break;              \
     }
     {
@@ -445,6 +625,8 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         decode_merge<DM_F16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
     }
 #undef DEC_D
+#undef DEC_G128
+#undef DEC_MFMA
 #undef DEC_G
 #undef DEC_SPLIT
     probe_add(DM_PROBE_DECODE_SPLIT);

@@ -700,22 +700,6 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
 //   gdr_bwd_grads  per (chunk, head): dV' = (lam K) dS_{c+1} + Aqk^T dO, then every gradient
 //                  the chunk gives (dq, dk, dv, dg, dbeta)
 
-// An A or B fragment from a row-major 16-bit tile whose rows are the fragment's rows (A) or
-// columns (B) and whose columns are k: rows r0 + lane % 32, k slots 16 st + 8 j + 4 h + e at
-// columns k0 + 4 h + [0, 4) and k0 + 8 + 4 h + [0, 4) (the order lds_tr_frag's slots have).
-__device__ __forceinline__ Frag8 row_frag(const uint16_t *t, int stride, int r0, int k0,
-                                          int lane) {
-    const uint16_t *p = t + (r0 + (lane & 31)) * stride + k0 + (lane >> 5) * 4;
-    const uint2 lo = *(const uint2 *)p, hi = *(const uint2 *)(p + 8);
-    Frag8 f;
-    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    return f;
-}
-
-// The 32x32 product output's element i of a lane: row 8 (i / 4) + 4 (lane / 32) + i % 4 of the
-// tile, column lane % 32.
-__device__ __forceinline__ int crow(int i, int lane) { return (i / 4) * 8 + (lane >> 5) * 4 + (i % 4); }
-
 // Its 16 values stored transposed into a row-major 16-bit tile X^T: row (the tile's column)
 // c0 + lane % 32, columns r0 + crow(i): runs of 4, 8-byte stores.
 template <int DT>
@@ -733,29 +717,6 @@ __device__ __forceinline__ float sum32(float x) {
 #pragma unroll
     for (int o = 16; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
     return x;
-}
-
-// A product tile's output fragment as the B (or A) operand of a next product whose k is the
-// tile's rows: k step u takes elements 8 u .. 8 u + 7.
-template <int DT>
-__device__ __forceinline__ Frag8 c_frag(const f32x16_t &v, int u, float f = 1.f) {
-    Frag8 x;
-    x.u = make_uint4(pack2<DT>(v[8 * u] * f, v[8 * u + 1] * f), pack2<DT>(v[8 * u + 2] * f, v[8 * u + 3] * f),
-                     pack2<DT>(v[8 * u + 4] * f, v[8 * u + 5] * f), pack2<DT>(v[8 * u + 6] * f, v[8 * u + 7] * f));
-    return x;
-}
-
-// x rounded to the dtype and back
-template <int DT>
-__device__ __forceinline__ float round_to(float x) {
-    return unpack_lo<DT>(pack2<DT>(x, 0.f));
-}
-
-__device__ __forceinline__ f32x16_t zero16() {
-    f32x16_t z;
-#pragma unroll
-    for (int i = 0; i < 16; i++) z[i] = 0.f;
-    return z;
 }
 
 constexpr int kR = kD + 8;  // 128-column tiles (row and transposed reads)
