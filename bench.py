@@ -76,7 +76,7 @@ class Timed:
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary (a line ``traffic_bytes_per_launch <kernel>: N``), or None when it has none."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic_attention_decode_step.md")
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_per_kernel.md")
     try:
         for line in open(path):
             if line.startswith(f"traffic_bytes_per_launch {kernel}:"):

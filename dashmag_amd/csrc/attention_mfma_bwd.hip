@@ -168,6 +168,7 @@ __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) 
 // (Items with equal counts land in any order: the order only schedules, it does not change
 // what a workgroup computes.)
 constexpr int kOrderBuckets = 1024;
+constexpr int kOrderLds = 8192;  // per-block counts held in LDS up to this many
 
 __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t Tk, int64_t Hkv,
                                                   int64_t group, BwdWs w) {
@@ -177,23 +178,37 @@ __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t
     const int64_t nkb = (Tk + kKvBlock - 1) / kKvBlock;
     const int hs = w.hsplit;
     const int64_t per = group / hs;  // query heads per work item
-    // difference array per batch row, then its prefix sum (one thread per row)
-    for (int64_t x = tid; x < B * (nkb + 1); x += 1024) w.kbsteps[x] = 0;
+    // difference array per batch row (in LDS when it fits), then its prefix sum, one wavefront
+    // per batch row, 64 blocks at a time
+    __shared__ int32_t cnt_lds[kOrderLds];
+    const int64_t ncnt = B * (nkb + 1);
+    int32_t *cnt = ncnt <= kOrderLds ? cnt_lds : w.kbsteps;
+    for (int64_t x = tid; x < ncnt; x += 1024) cnt[x] = 0;
     __syncthreads();
     for (int64_t x = tid; x < B * ntiles; x += 1024) {
         const int64_t b = x / ntiles;
         const int32_t *r = w.trange + x * 4;
         if (r[0] < r[1]) {
-            atomicAdd(&w.kbsteps[b * (nkb + 1) + r[0] / kKvBlock], 1);
-            atomicAdd(&w.kbsteps[b * (nkb + 1) + (r[1] - 1) / kKvBlock + 1], -1);
+            atomicAdd(&cnt[b * (nkb + 1) + r[0] / kKvBlock], 1);
+            atomicAdd(&cnt[b * (nkb + 1) + (r[1] - 1) / kKvBlock + 1], -1);
         }
     }
     __syncthreads();
-    for (int64_t b = tid; b < B; b += 1024) {
-        int32_t run = 0;
-        for (int64_t kb = 0; kb <= nkb; kb++) {
-            run += w.kbsteps[b * (nkb + 1) + kb];
-            w.kbsteps[b * (nkb + 1) + kb] = run;
+    {
+        const int lane = tid & 63;
+        for (int64_t b = tid >> 6; b < B; b += 16) {
+            int32_t carry = 0;
+            for (int64_t base = 0; base <= nkb; base += 64) {
+                const int64_t kb = base + lane;
+                int32_t x = kb <= nkb ? cnt[b * (nkb + 1) + kb] : 0;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int32_t y = __shfl_up(x, o, 64);
+                    if (lane >= o) x += y;
+                }
+                if (kb <= nkb) cnt[b * (nkb + 1) + kb] = x + carry;
+                carry += __shfl(x, 63, 64);
+            }
         }
     }
     __syncthreads();
@@ -203,7 +218,7 @@ __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t
     const int64_t nwork = nkb * Hkv * B * hs;
     auto bucket = [&](int64_t item) {
         const int64_t kb = (item / (Hkv * hs)) % nkb, b = item / (Hkv * hs * nkb);
-        const int64_t steps = (int64_t)w.kbsteps[b * (nkb + 1) + kb] * per;
+        const int64_t steps = (int64_t)cnt[b * (nkb + 1) + kb] * per;
         return (int)(steps < kOrderBuckets - 1 ? steps : kOrderBuckets - 1);
     };
     for (int64_t x = tid; x < nwork; x += 1024) atomicAdd(&hist[bucket(x)], 1);
