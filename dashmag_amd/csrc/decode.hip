@@ -70,22 +70,6 @@ __device__ __forceinline__ float dot8(const uint4 &a, const uint4 &b) {
     return t;
 }
 
-// Sum over aligned groups of N lanes (N = 8, 16 or 32) by DPP moves within 16-lane rows: quad
-// swaps, then the half-row mirror (lane i with 7 - i) and the row mirror (lane i with 15 - i)
-// pair lanes from the other half each time, so every lane ends with its group's sum.
-template <int N>
-__device__ __forceinline__ float group_sum(float t) {
-#define DM_DPP(x, ctrl) \
-    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xf, 0xf, false))
-    t += DM_DPP(t, 0xB1);   // quad_perm [1, 0, 3, 2]
-    t += DM_DPP(t, 0x4E);   // quad_perm [2, 3, 0, 1]
-    t += DM_DPP(t, 0x141);  // row_half_mirror
-    if constexpr (N >= 16) t += DM_DPP(t, 0x140);  // row_mirror
-#undef DM_DPP
-    if constexpr (N >= 32) t += __shfl_xor(t, 16, 64);
-    return t;
-}
-
 // One split of one (sequence, key-value head): keys [base + split * span, ...) of the keys the
 // sequence's query sees, [lo, hi). Writes part_o [B, Hq, nsplit, D] (normalised) and part_lse
 // [B, Hq, nsplit] (-inf for a split that sees nothing).

@@ -31,6 +31,7 @@ constexpr int kRowB = kD + 4;   // row stride read by ds_read_b64 rows (32 rows 
 constexpr int kTrS = kD + 32;   // row stride read by ds_read_b64_tr_b16
 
 struct MfmaWs {
+    int64_t nsh;       // sequences x heads
     int32_t *seq_chunk0, *chunk_seq, *chunk_tok0, *chunk_len;
     float *G;          // [ch][64]
     uint16_t *Wf;      // [ch][2 token tiles][8 dk steps][64 lanes][8]: W as A fragments of V' = W S
@@ -57,6 +58,7 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd 
         return p;
     };
     MfmaWs x{};
+    x.nsh = S * d->h;
     x.seq_chunk0 = (int32_t *)take((S + 1) * 4);
     x.chunk_seq = (int32_t *)take(nc * 4);
     x.chunk_tok0 = (int32_t *)take(nc * 4);
@@ -456,6 +458,18 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 // State pass
 // ------------------------------------------------------------------------------------------
 
+// The state passes' workgroup -> (sequence x head, column block): workgroup x goes to XCD x % 8,
+// and the four column blocks of a (sequence, head) take workgroups 8 apart, so they share one
+// XCD's L2 (the operands are read from HBM once). Grid: state_grid(nsh) workgroups.
+__host__ __device__ inline int64_t state_grid(int64_t nsh) { return (nsh + 7) / 8 * 32; }
+__device__ __forceinline__ bool state_item(int64_t x, int64_t grid, int64_t nsh, int64_t *sh,
+                                           int *wave) {
+    const int64_t xcd = x % 8, y = x / 8;
+    *wave = (int)(y % 4);
+    *sh = (y / 4) * 8 + xcd;
+    return *sh < nsh;
+}
+
 // Each wavefront owns 32 state columns and reads its operands -- W and (lam K)^T as ready-made
 // A fragments, U in the products' layout -- straight from HBM into registers two chunks ahead:
 // no LDS, no barriers; the chain per chunk is S -> (pack) -> 16 products -> (U - .) -> 16
@@ -470,11 +484,14 @@ struct ChunkOps {
 template <int DT>
 __global__ __launch_bounds__(64, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, const float *h0,
                                                         float *final_state) {
-    // one wavefront per workgroup: the four of a (sequence, head) on different compute units,
-    // each streaming its operands through its own L1
-    const int64_t sh = blockIdx.x / 4, s = sh / a.H, h = sh % a.H;
+    // one wavefront per workgroup: the four of a (sequence, head) on different compute units of
+    // one XCD (workgroups go to the XCDs in turn), each streaming its operands through its own
+    // L1 from the shared L2
+    int64_t sh;
+    int wave;
+    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &wave)) return;
+    const int64_t s = sh / a.H, h = sh % a.H;
     const int lane = threadIdx.x;
-    const int wave = blockIdx.x % 4;
     const int col = lane & 31, half = lane >> 5;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
     const int dv = wave * 32 + col;  // this lane's state column
@@ -713,11 +730,7 @@ __device__ __forceinline__ void store_ct(uint16_t *t, int stride, int r0, int c0
 }
 
 // Sum over the 32 lanes that share lane / 32 (the columns of a product tile).
-__device__ __forceinline__ float sum32(float x) {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
+__device__ __forceinline__ float sum32(float x) { return group_sum<32>(x); }
 
 constexpr int kR = kD + 8;  // 128-column tiles (row and transposed reads)
 constexpr int kT = kC + 8;  // 64-column tiles
@@ -818,9 +831,11 @@ struct BwdOps {
 template <int DT>
 __global__ __launch_bounds__(64, 1) void gdr_bwd_state(GdrArgs a, MfmaWs w, const float *d_final,
                                                        float *dh0) {
-    const int64_t sh = blockIdx.x / 4, s = sh / a.H, h = sh % a.H;
+    int64_t sh;
+    int wave;
+    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &wave)) return;
+    const int64_t s = sh / a.H, h = sh % a.H;
     const int lane = threadIdx.x;
-    const int wave = blockIdx.x % 4;
     const int col = lane & 31, half = lane >> 5;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
     const int dv = wave * 32 + col;
@@ -1465,7 +1480,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state<DM_BF16><<<seqs * 4, 64, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state<DM_BF16><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1478,7 +1493,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state<DM_F16><<<seqs * 4, 64, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state<DM_F16><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1507,7 +1522,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_STATE, st);
-        gdr_mfma_state<DT><<<seqs * 4, 64, 0, st>>>(a, w, h0, nullptr);
+        gdr_mfma_state<DT><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, h0, nullptr);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_PRE, st);
@@ -1515,7 +1530,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_STATE, st);
-        gdr_bwd_state<DT><<<seqs * 4, 64, 0, st>>>(a, w, d_final, dh0);
+        gdr_bwd_state<DT><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, d_final, dh0);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_GRADS, st);

@@ -193,4 +193,20 @@ __device__ __forceinline__ f32x16_t zero16() {
     return z;
 }
 
+// Sum over aligned groups of N lanes (N = 8, 16 or 32) by DPP moves within 16-lane rows: quad
+// swaps, then the half-row mirror (lane i with 7 - i) and the row mirror (lane i with 15 - i)
+// pair lanes from the other half each time, so every lane ends with its group's sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float t) {
+#define DM_DPP(x, ctrl) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xf, 0xf, false))
+    t += DM_DPP(t, 0xB1);   // quad_perm [1, 0, 3, 2]
+    t += DM_DPP(t, 0x4E);   // quad_perm [2, 3, 0, 1]
+    t += DM_DPP(t, 0x141);  // row_half_mirror
+    if constexpr (N >= 16) t += DM_DPP(t, 0x140);  // row_mirror
+#undef DM_DPP
+    if constexpr (N >= 32) t += __shfl_xor(t, 16, 64);
+    return t;
+}
+
 }  // namespace dm
