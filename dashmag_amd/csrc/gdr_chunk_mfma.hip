@@ -951,6 +951,9 @@ constexpr int BYTES = PART + 8 * 1024;
 }  // namespace bl
 static_assert(bl::DTT + kC * kT * 2 <= bl::DVPT && bl::AQ + kC * kT * 2 <= bl::M2T, "phases");
 static_assert(bl::BYTES <= 160 * 1024, "LDS");
+static_assert(kC * kR * 2 <= bl::TOKF - bl::M2T && kC * kR * 2 <= bl::DTT + kC * kT * 2 - bl::TB &&
+                  kC * kR * 2 <= bl::TB - bl::DWT,
+              "output rows in dead regions");
 
 template <int DT>
 __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
@@ -974,6 +977,25 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     float *pGam = F32(bl::PART), *pU = pGam + 256, *pS = pGam + 512, *pBet = pGam + 768,
           *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
 
+    // phase 2's rows (Q, K, V, T) are loaded first and held in registers through phase 1
+    uint4 q2[4], k2[4], v2[4], t2[2];
+    {
+        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
+                       *vin = (const uint16_t *)a.v;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
+            q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
+            k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
+            v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 256 * u, r = x / 8, c = x % 8;
+            t2[u] = *(const uint4 *)(w.Tm + ch * kC * kC + r * kC + c * 8);
+        }
+    }
     // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
     if (tid < kC) {
         const float gv = w.G[ch * kC + tid];
@@ -984,38 +1006,54 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     }
     {
         const uint16_t *sf = w.Sf + ch * kD * kD, *dsf = w.dSf + ch * kD * kD;
-        // fragment (dv tile p, dk step st), lane l: column dv = 32 p + l % 32 (a row of X^T),
-        // dk runs 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
-        for (int x = tid; x < 32 * 64; x += 256) {
-            const int f = x / 64, l = x % 64, p = f / 8, st = f % 8;
-            const uint4 v1 = *(const uint4 *)(sf + (size_t)x * 8);
-            const uint4 v2 = *(const uint4 *)(dsf + (size_t)x * 8);
-            const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
-            *(uint2 *)(sST + r * kR + c) = make_uint2(v1.x, v1.y);
-            *(uint2 *)(sST + r * kR + c + 8) = make_uint2(v1.z, v1.w);
-            *(uint2 *)(sDST + r * kR + c) = make_uint2(v2.x, v2.y);
-            *(uint2 *)(sDST + r * kR + c + 8) = make_uint2(v2.z, v2.w);
+        const uint16_t *vf = w.Vf + ch * kC * kD, *dob = (const uint16_t *)d_out;
+        // every load issued before the first store
+        uint4 s1[8], s2[8], s3[4], s4[4], s5[2];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s1[i] = *(const uint4 *)(sf + (size_t)(tid + 256 * i) * 8);
+            s2[i] = *(const uint4 *)(dsf + (size_t)(tid + 256 * i) * 8);
         }
-        const uint16_t *vf = w.Vf + ch * kC * kD;
-        for (int x = tid; x < 16 * 64; x += 256) {
-            const int f = x / 64, l = x % 64, p = f / 4, st = f % 4;
-            const uint4 v1 = *(const uint4 *)(vf + (size_t)x * 8);
-            const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
-            *(uint2 *)(sVPT + r * kT + c) = make_uint2(v1.x, v1.y);
-            *(uint2 *)(sVPT + r * kT + c + 8) = make_uint2(v1.z, v1.w);
-        }
-        const uint16_t *dob = (const uint16_t *)d_out;
+#pragma unroll
+        for (int i = 0; i < 4; i++) s3[i] = *(const uint4 *)(vf + (size_t)(tid + 256 * i) * 8);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int x = tid + 256 * u, r = x / 16, c = x % 16;
             const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
-            const uint4 v1 = *(const uint4 *)(dob + row * kD + c * 8);
-            *(uint4 *)(sDOB + r * kR + c * 8) = r < len ? v1 : make_uint4(0, 0, 0, 0);
+            s4[u] = *(const uint4 *)(dob + row * kD + c * 8);
         }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int x = tid + 256 * u, r = x / 8, c = x % 8;
-            *(uint4 *)(sAQ + r * kT + c * 8) = *(const uint4 *)(w.Aqk + ch * kC * kC + r * kC + c * 8);
+            s5[u] = *(const uint4 *)(w.Aqk + ch * kC * kC + r * kC + c * 8);
+        }
+        // fragment (dv tile p, dk step st), lane l: column dv = 32 p + l % 32 (a row of X^T),
+        // dk runs 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int x = tid + 256 * i, f = x / 64, l = x % 64, p = f / 8, st = f % 8;
+            const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
+            *(uint2 *)(sST + r * kR + c) = make_uint2(s1[i].x, s1[i].y);
+            *(uint2 *)(sST + r * kR + c + 8) = make_uint2(s1[i].z, s1[i].w);
+            *(uint2 *)(sDST + r * kR + c) = make_uint2(s2[i].x, s2[i].y);
+            *(uint2 *)(sDST + r * kR + c + 8) = make_uint2(s2[i].z, s2[i].w);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int x = tid + 256 * i, f = x / 64, l = x % 64, p = f / 4, st = f % 4;
+            const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
+            *(uint2 *)(sVPT + r * kT + c) = make_uint2(s3[i].x, s3[i].y);
+            *(uint2 *)(sVPT + r * kT + c + 8) = make_uint2(s3[i].z, s3[i].w);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+            *(uint4 *)(sDOB + r * kR + c * 8) = r < len ? s4[u] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 256 * u, r = x / 8, c = x % 8;
+            *(uint4 *)(sAQ + r * kT + c * 8) = s5[u];
         }
         for (int x = tid; x < 8 * 256; x += 256) pGam[x] = 0.f;
     }
@@ -1086,16 +1124,12 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 
     // ---- phase 2: Q, K (normalised as the forward did, with the inverse norms), V, T ----
     {
-        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
-                       *vin = (const uint16_t *)a.v;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int x = tid + 256 * u, r = x / 16, c = x % 16;
             const bool ok = r < len;
-            const int64_t row = (tok0 + (ok ? r : len - 1)) * a.H + h;
-            uint4 qv = *(const uint4 *)(qin + row * kD + c * 8);
-            uint4 kv = *(const uint4 *)(kin + row * kD + c * 8);
-            const uint4 vv = *(const uint4 *)(vin + row * kD + c * 8);
+            uint4 qv = q2[u], kv = k2[u];
+            const uint4 vv = v2[u];
             float qi = 1.f, ki = 1.f;
             if (a.l2norm) {
                 const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, kw[4] = {kv.x, kv.y, kv.z, kv.w};
@@ -1132,9 +1166,10 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
                 tKi[r] = ki;
             }
         }
-        for (int x = tid; x < kC * kC / 8; x += 256) {
-            const int r = x / 8, c = x % 8;
-            *(uint4 *)(U16(bl::TB) + r * kT + c * 8) = *(const uint4 *)(w.Tm + ch * kC * kC + r * kC + c * 8);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 256 * u, r = x / 8, c = x % 8;
+            *(uint4 *)(U16(bl::TB) + r * kT + c * 8) = t2[u];
         }
     }
     uint16_t *sQB = U16(bl::QB), *sKB = U16(bl::KB), *sVB = U16(bl::VB), *sDWT = U16(bl::DWT);
@@ -1413,15 +1448,15 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
     }
     __syncthreads();
-    // dq, dk (the scale and the l2 normalisation undone), dv
+    // dq, dk (the scale and the l2 normalisation undone), dv: staged as rows in LDS (regions
+    // dead by now), then stored 16 bytes per lane
+    uint16_t *oq = U16(bl::DWT), *ok_ = U16(bl::M2T), *ov = U16(bl::TB);
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = t * 32 + crow(i, lane);
-            if (r >= len) continue;
             const int c = wave * 32 + col;
-            const int64_t o = ((tok0 + r) * a.H + h) * kD + c;
             float qo = dqa[t][i] * scale, ko = dka[t][i];
             if (a.l2norm) {
                 const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
@@ -1432,10 +1467,21 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
                 qo = tQi[r] * (qo - qv * pSq[r]);
                 ko = tKi[r] * (ko - kv * pSk[r]);
             }
-            st<DT>(dq, o, qo);
-            st<DT>(dk, o, ko);
-            st<DT>(dv, o, dva[t][i]);
+            oq[r * kR + c] = (uint16_t)(pack2<DT>(qo, 0.f) & 0xffffu);
+            ok_[r * kR + c] = (uint16_t)(pack2<DT>(ko, 0.f) & 0xffffu);
+            ov[r * kR + c] = (uint16_t)(pack2<DT>(dva[t][i], 0.f) & 0xffffu);
         }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        if (r < len) {
+            const int64_t o = ((tok0 + r) * a.H + h) * kD + c * 8;
+            *(uint4 *)((uint16_t *)dq + o) = *(const uint4 *)(oq + r * kR + c * 8);
+            *(uint4 *)((uint16_t *)dk + o) = *(const uint4 *)(ok_ + r * kR + c * 8);
+            *(uint4 *)((uint16_t *)dv + o) = *(const uint4 *)(ov + r * kR + c * 8);
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------
