@@ -18,14 +18,17 @@ namespace dm {
 //   S <- S + k delta^T;  out <- S^T q.
 template <int DT, int MAXR>
 __global__ __launch_bounds__(256) void gdr_step_kernel(
-    int64_t nseq, int64_t H, int64_t Dk, int64_t Dv, const int32_t *__restrict__ cu, int g_dt,
+    int64_t nseq, int64_t H, int64_t Dk, int64_t Dv, int ncs, const int32_t *__restrict__ cu, int g_dt,
     int beta_dt, int l2norm, float scale, const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g, const void *__restrict__ beta,
     const float *state_in, float *state_out, void *__restrict__ out) {
-    const int64_t sh = blockIdx.x;
+    // the state's columns are independent: ncs workgroups share a (sequence, head), each
+    // taking Dv / ncs columns (every one recomputes the token's normalisation)
+    const int64_t sh = blockIdx.x / ncs;
     const int64_t s = sh / H, h = sh % H;
+    const int64_t Dw = Dv / ncs, c0 = (blockIdx.x % ncs) * Dw;
     const int tid = threadIdx.x;
-    const int NQ = (int)(Dv / 4);       // column quads
+    const int NQ = (int)(Dw / 4);       // column quads
     const int NKG = 256 / NQ;           // row groups
     const int quad = tid % NQ, kg = tid / NQ;
     const bool active = kg < NKG;
@@ -35,7 +38,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     extern __shared__ float sm[];
     float *qs = sm;            // [Dk]
     float *ks = qs + Dk;       // [Dk]
-    float *red = ks + Dk;      // [NKG][Dv] partial sums
+    float *red = ks + Dk;      // [NKG][Dw] partial sums
     __shared__ float norm2[2];
 
     int64_t t0, t1;
@@ -53,7 +56,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     for (int rr = 0; rr < MAXR; rr++) {
         const int64_t row = r0 + rr;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (active && rr < rows_per && row < Dk) x = *(const float4 *)(sin + row * Dv + quad * 4);
+        if (active && rr < rows_per && row < Dk) x = *(const float4 *)(sin + row * Dv + c0 + quad * 4);
         st_[rr][0] = x.x;
         st_[rr][1] = x.y;
         st_[rr][2] = x.z;
@@ -105,14 +108,14 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
         }
         if (active)
 #pragma unroll
-            for (int c = 0; c < 4; c++) red[kg * Dv + quad * 4 + c] = part[c];
+            for (int c = 0; c < 4; c++) red[kg * Dw + quad * 4 + c] = part[c];
         __syncthreads();
         float delta[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             float kv = 0.f;
-            for (int x = 0; x < NKG; x++) kv += red[x * Dv + quad * 4 + c];
-            delta[c] = (ld<DT>(v, (t * H + h) * Dv + quad * 4 + c) - kv) * bt;
+            for (int x = 0; x < NKG; x++) kv += red[x * Dw + quad * 4 + c];
+            delta[c] = (ld<DT>(v, (t * H + h) * Dv + c0 + quad * 4 + c) - kv) * bt;
         }
         __syncthreads();
         // S <- S + k delta^T ; partial S^T q
@@ -132,14 +135,14 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
         }
         if (active)
 #pragma unroll
-            for (int c = 0; c < 4; c++) red[kg * Dv + quad * 4 + c] = part[c];
+            for (int c = 0; c < 4; c++) red[kg * Dw + quad * 4 + c] = part[c];
         __syncthreads();
         if (kg == 0) {
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 float o = 0.f;
-                for (int x = 0; x < NKG; x++) o += red[x * Dv + quad * 4 + c];
-                st<DT>(out, (t * H + h) * Dv + quad * 4 + c, o);
+                for (int x = 0; x < NKG; x++) o += red[x * Dw + quad * 4 + c];
+                st<DT>(out, (t * H + h) * Dv + c0 + quad * 4 + c, o);
             }
         }
         __syncthreads();
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     for (int rr = 0; rr < MAXR; rr++) {
         const int64_t row = r0 + rr;
         if (active && rr < rows_per && row < Dk)
-            *(float4 *)(sout + row * Dv + quad * 4) =
+            *(float4 *)(sout + row * Dv + c0 + quad * 4) =
                 make_float4(st_[rr][0], st_[rr][1], st_[rr][2], st_[rr][3]);
     }
 }
@@ -190,18 +193,22 @@ extern "C" int dm_gdr_step(const dm_gdr_desc *d, const void *q, const void *k, c
                       ")");
     hipStream_t st = (hipStream_t)stream;
     const int64_t nseq = d->cu_seqlens ? d->nseq : d->b;
-    const int64_t blocks = nseq * d->h;
+    // columns per workgroup: 64 where Dv allows it (more, shorter workgroups let the state's
+    // reads and writes of different workgroups overlap)
+    const int ncs = (d->dv >= 128 && d->dv % 64 == 0) ? (int)(d->dv / 64) : 1;
+    const int64_t blocks = nseq * d->h * ncs;
     if (blocks == 0 || d->dk * d->dv == 0) return DM_OK;
-    const int nq = (int)(d->dv / 4);
+    const int64_t dw = d->dv / ncs;
+    const int nq = (int)(dw / 4);
     const int nkg = 256 / nq;
     const int rows = (int)((d->dk + nkg - 1) / nkg);
-    const size_t smem = (size_t)(2 * d->dk + nkg * d->dv) * sizeof(float);
+    const size_t smem = (size_t)(2 * d->dk + nkg * dw) * sizeof(float);
     const float scale =
         d->has_scale ? d->scale : (float)(1.0 / std::sqrt((double)d->dk));
     const int l2 = d->qk_l2norm ? 1 : 0;
 #define STEP(DT, R)                                                                          \
     gdr_step_kernel<DT, R><<<(unsigned)blocks, 256, smem, st>>>(                             \
-        nseq, d->h, d->dk, d->dv, d->cu_seqlens, d->g_dtype, d->beta_dtype, l2, scale, q, k, v, \
+        nseq, d->h, d->dk, d->dv, ncs, d->cu_seqlens, d->g_dtype, d->beta_dtype, l2, scale, q, k, v, \
         g, beta, state_in, state_out, out)
 #define STEP_R(DT)                                  \
     if (rows <= 4) STEP(DT, 4);                     \
