@@ -86,18 +86,19 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd 
 // Prep
 // ------------------------------------------------------------------------------------------
 
-// 73.6 KB: two workgroups per CU. The query tile's space later holds T, and the key tile's the
-// block products; both then stage the W and U rows for coalesced stores. One buffer holds
-// beta gamma K for W, then beta V for U.
+// 77 KB: two workgroups per CU. The query tile's space later holds T (f32), and the key tile's
+// beta V (for U's product, staged while T is computed); the key tile's space then stages the W
+// rows for the fragment stores.
 struct PrepSmem {
-    uint4 k[kC * kRowS / 8];  // keys, rows; later block products; later W rows
+    uint4 k[kC * kRowS / 8];  // keys, rows; later beta V rows; later W rows
     uint4 q[kC * kRowS / 8];  // queries, rows; later T (f32); later U rows
-    uint4 x[kC * kTrS / 8];   // beta gamma K, then beta V: rows read transposed
+    uint4 x[kC * kTrS / 8];   // beta gamma K: rows read transposed
     float a[kC][kC + 4];      // A (strictly lower), f32, 16-byte aligned rows
+    float mm[3][16][20];      // T's off-diagonal block products
     float g[kC], gam[kC], bet[kC], lam[kC];
 };
 static_assert(sizeof(float) * kC * (kC + 4) <= sizeof(uint4) * kC * kRowS / 8, "T in q");
-static_assert(sizeof(float) * 3 * 16 * 20 <= sizeof(uint4) * kC * kRowS / 8, "M in k");
+static_assert(sizeof(PrepSmem) <= 80 * 1024, "two workgroups per compute unit");
 
 template <int DT>
 __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     const int col = lane & 31, half = lane >> 5;
     uint16_t *ks = (uint16_t *)sm.k, *qs = (uint16_t *)sm.q, *xs = (uint16_t *)sm.x;
     float(*tt)[kC + 4] = (float(*)[kC + 4])sm.q;  // T, in the query tile's space
-    float(*mm)[16][20] = (float(*)[16][20])sm.k;  // block products, in the key tile's
+    float(*mm)[16][20] = sm.mm;
 
     // gates; the values, in registers until U (16 lanes per row, 4 rows per thread)
     if (tid < kC) {
@@ -279,6 +280,19 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         }
     }
     __syncthreads();  // the query and key tiles are dead from here
+    // beta V rows for U's product, in the key tile's space
+    uint16_t *vs = ks;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
+        const float fv = sm.bet[r];
+        const uint32_t vw[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+        uint32_t vo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            vo[e] = pack2<DT>(unpack_lo<DT>(vw[e]) * fv, unpack_hi<DT>(vw[e]) * fv);
+        *(uint4 *)(vs + r * kRowS + c * 8) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+    }
 
     // T = (I + A)^-1 by 16 x 16 blocks. Diagonal block b (wave b), row by row, lane c holding
     // column c in registers: T[i][c] = [i == c] - sum_{x < i} A[i][x] T[x][c] (rows of A read
@@ -362,42 +376,24 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         level(std::integral_constant<int, 3>{});
     }
 
-    // W = T (beta gamma K), then U = T (beta V): 8 output tiles each (2 token rows x 4 columns
-    // of 32), wave w taking column tile w. A = T rows (f32 -> dtype) with k slots
+    // W = T (beta gamma K) and U = T (beta V) in one pass: 8 output tiles each (2 token rows x 4
+    // columns of 32), wave w taking column tile w. A = T rows (f32 -> dtype) with k slots
     // 16 st + 8 j + 4 h + e, B = the scaled rows read transposed (k = token, col = column).
-    auto product = [&](f32x16_t *res) {
-#pragma unroll
-        for (int ti = 0; ti < 2; ti++) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) res[ti][i] = 0.f;
-#pragma unroll
-            for (int st = 0; st < kC / 16; st++) {
-                Frag8 at;
-                const float *tr = &tt[ti * 32 + col][st * 16 + half * 4];
-                at.u = make_uint4(pack2<DT>(tr[0], tr[1]), pack2<DT>(tr[2], tr[3]),
-                                  pack2<DT>(tr[8], tr[9]), pack2<DT>(tr[10], tr[11]));
-                const Frag8 bx = lds_tr_frag(xs, kTrS, st * 16, wave * 32, lane);
-                res[ti] = mfma32<DT>(at, bx, res[ti]);
-            }
-        }
-    };
     f32x16_t wt[2], ut[2];
-    product(wt);
-    __syncthreads();
-    // beta V rows in the same buffer
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
-        const float fv = sm.bet[r];
-        const uint32_t vw[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
-        uint32_t vo[4];
+    for (int ti = 0; ti < 2; ti++) {
+        wt[ti] = zero16();
+        ut[ti] = zero16();
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            vo[e] = pack2<DT>(unpack_lo<DT>(vw[e]) * fv, unpack_hi<DT>(vw[e]) * fv);
-        sm.x[r * (kTrS / 8) + c] = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+        for (int st = 0; st < kC / 16; st++) {
+            Frag8 at;
+            const float *tr = &tt[ti * 32 + col][st * 16 + half * 4];
+            at.u = make_uint4(pack2<DT>(tr[0], tr[1]), pack2<DT>(tr[2], tr[3]),
+                              pack2<DT>(tr[8], tr[9]), pack2<DT>(tr[10], tr[11]));
+            wt[ti] = mfma32<DT>(at, lds_tr_frag(xs, kTrS, st * 16, wave * 32, lane), wt[ti]);
+            ut[ti] = mfma32<DT>(at, lds_tr_frag(vs, kRowS, st * 16, wave * 32, lane), ut[ti]);
+        }
     }
-    __syncthreads();
-    product(ut);
     __syncthreads();
     // for the backward: T, row-major in the dtype
     if (w.Tm) {
