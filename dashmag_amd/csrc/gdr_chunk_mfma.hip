@@ -609,6 +609,147 @@ __global__ __launch_bounds__(64, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, con
     }
 }
 
+// The state pass with the rows of S split over a pair of wavefronts (one workgroup per column
+// block): wavefront p holds rows 64 p + [0, 64) of the block's 32 columns. Per chunk each
+// computes its part of W S (8 products over its 64 state rows), the pair swaps the parts through
+// LDS (two buffers by chunk parity: one barrier per chunk), both form V' = U - W S, and each
+// updates its own rows: S_p <- e^{G_last} S_p + (lam K)_p^T V' (8 products). Per wavefront
+// that is half the products, half the operands and half the state of a single wavefront per
+// block, on the chain every chunk waits for.
+struct HalfOps {
+    Frag8 wf[2][4];  // W: token tile t, dk step 4 p + st
+    uint4 uc[2][2];  // U: token tile t, two 8-value halves of the lane's 16
+    Frag8 kf[2][4];  // (lam K)^T: dk tile 2 p + r, token step st
+    float glast;
+};
+
+template <int DT>
+__global__ __launch_bounds__(128, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, const float *h0,
+                                                         float *final_state) {
+    __shared__ __align__(16) float xch[2][2][2][16][64];  // [parity][wavefront][token tile][i][lane]
+    int64_t sh;
+    int blk;
+    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
+    const int64_t s = sh / a.H, h = sh % a.H;
+    const int lane = threadIdx.x & 63;
+    const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row half
+    const int col = lane & 31;
+    const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
+    const int dv = blk * 32 + col;
+
+    // S_p: tile r holds rows 64 p + 32 r + crow(i) of column dv
+    f32x16_t S[2];
+    {
+        const float *src = h0 ? h0 + sh * kD * kD : nullptr;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                S[r][i] = src ? src[(p * 64 + r * 32 + crow(i, lane)) * kD + dv] : 0.f;
+    }
+    auto load = [&](int c, HalfOps &x) __attribute__((always_inline)) {
+        c = c < c1 ? c : c1 - 1;
+        const int64_t ch = (int64_t)c * a.H + h;
+        const uint16_t *wf = w.Wf + ch * kC * kD, *kf = w.Kf + ch * kC * kD;
+        const uint16_t *uc = w.Uc + ch * kC * kD + (size_t)blk * 2 * 2 * 64 * 8;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                x.wf[t][st].u = *(const uint4 *)(wf + ((t * 8 + p * 4 + st) * 64 + lane) * 8);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++)
+                x.uc[t][qq] = *(const uint4 *)(uc + ((t * 2 + qq) * 64 + lane) * 8);
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                x.kf[r][st].u = *(const uint4 *)(kf + (((p * 2 + r) * 4 + st) * 64 + lane) * 8);
+        x.glast = w.G[ch * kC + kC - 1];
+    };
+    auto step = [&](int c, const HalfOps &x) __attribute__((always_inline)) {
+        const int64_t ch = (int64_t)c * a.H + h;
+        // this half of S as operand fragments (dk steps 4 p + st), also stored for the output
+        Frag8 sf[4];
+        uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)blk * 8 * 64 * 8;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            sf[st] = c_frag<DT>(S[st / 2], st % 2);
+            *(uint4 *)(sfo + ((p * 4 + st) * 64 + lane) * 8) = sf[st].u;
+        }
+        // this half's part of W S
+        f32x16_t vp[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) vp[t] = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) vp[t] = mfma32<DT>(x.wf[t][st], sf[st], vp[t]);
+        // swap the parts
+        float(*mine)[16][64] = xch[c & 1][p];
+        float(*other)[16][64] = xch[c & 1][p ^ 1];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) mine[t][i][lane] = vp[t][i];
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) vp[t][i] += other[t][i][lane];
+        // V' = U - W S (the same in both wavefronts; wavefront p stores token tile p)
+        Frag8 vlf[4];
+        uint16_t *vfo = w.Vf ? w.Vf + ch * kC * kD + (size_t)blk * 4 * 64 * 8 : nullptr;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t uw[4] = {x.uc[t][u].x, x.uc[t][u].y, x.uc[t][u].z, x.uc[t][u].w};
+                float v8[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float uu = (e & 1) ? unpack_hi<DT>(uw[e / 2]) : unpack_lo<DT>(uw[e / 2]);
+                    v8[e] = uu - vp[t][8 * u + e];
+                }
+                const int st = t * 2 + u;
+                vlf[st].u = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
+                                       pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
+                if (vfo && t == p) *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
+            }
+        // S_p <- exp(G_last) S_p + (lam K)_p^T V'
+        const float gl = __expf(x.glast);
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) S[r][i] *= gl;
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) S[r] = mfma32<DT>(x.kf[r][st], vlf[st], S[r]);
+    };
+    HalfOps oa, ob;
+    if (c0 < c1) {
+        load(c0, oa);
+        load(c0 + 1, ob);
+    }
+    for (int c = c0; c < c1; c += 2) {
+        step(c, oa);
+        load(c + 2, oa);
+        if (c + 1 >= c1) break;
+        step(c + 1, ob);
+        load(c + 3, ob);
+    }
+    if (final_state) {
+        float *dst = final_state + sh * kD * kD;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) dst[(p * 64 + r * 32 + crow(i, lane)) * kD + dv] = S[r][i];
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // Output
 // ------------------------------------------------------------------------------------------
@@ -1522,7 +1663,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state<DM_BF16><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state2<DM_BF16><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1535,7 +1676,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state<DM_F16><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state2<DM_F16><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1564,7 +1705,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_STATE, st);
-        gdr_mfma_state<DT><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, h0, nullptr);
+        gdr_mfma_state2<DT><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, h0, nullptr);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_PRE, st);
