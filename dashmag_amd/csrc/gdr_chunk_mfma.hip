@@ -7,12 +7,12 @@
 //                    T = (I + A)^-1 in f32 by 16 x 16 blocks (each diagonal block by column
 //                    forward substitution, the rest by block forward substitution); W = T (beta
 //                    gamma K), U = T (beta V) (MFMA); Aqk = scale (Q K^T o decay).
-//   gdr_mfma_state   per (sequence, head), serial over the sequence's chunks: the state S lives
-//                    in registers in the 32x32 products' output layout, which is also the
-//                    operand layout of the next product, so it never leaves the wavefronts;
-//                    V' = U - W S; S <- exp(G_last) S + (lam K)^T V'; its operands come from
-//                    the prep kernel as ready-made fragments (no LDS, no barriers); S and V'
-//                    are stored as operand fragments for the output kernel.
+//   gdr_mfma_state2  per (sequence, head, 32 state columns), serial over the sequence's chunks:
+//                    the state S lives in registers in the 32x32 products' output layout, which
+//                    is also the operand layout of the next product, its rows split over a
+//                    pair of wavefronts; V' = U - W S; S <- exp(G_last) S + (lam K)^T V'; the
+//                    operands come from the prep kernel as ready-made fragments straight into
+//                    registers; S and V' are stored as operand fragments for the output kernel.
 //   gdr_mfma_output  per (chunk, head), parallel: O^T = scale gamma (S^T Q^T) + V'^T Aqk^T.
 // Notation as chunk/reference.rs:11-18 (Q scaled, G_last the chunk's last cumulative gate).
 #include <string>
@@ -466,149 +466,6 @@ __device__ __forceinline__ bool state_item(int64_t x, int64_t grid, int64_t nsh,
     return *sh < nsh;
 }
 
-// Each wavefront owns 32 state columns and reads its operands -- W and (lam K)^T as ready-made
-// A fragments, U in the products' layout -- straight from HBM into registers two chunks ahead:
-// no LDS, no barriers; the chain per chunk is S -> (pack) -> 16 products -> (U - .) -> 16
-// products -> S.
-struct ChunkOps {
-    Frag8 wf[2][8];  // W: token tile t, dk step st
-    uint4 uc[2][2];  // U: token tile t, two 8-value halves of the lane's 16
-    Frag8 kf[4][4];  // (lam K)^T: dk tile r, token step st
-    float glast;     // G at the chunk's last token
-};
-
-template <int DT>
-__global__ __launch_bounds__(64, 1) void gdr_mfma_state(GdrArgs a, MfmaWs w, const float *h0,
-                                                        float *final_state) {
-    // one wavefront per workgroup: the four of a (sequence, head) on different compute units of
-    // one XCD (workgroups go to the XCDs in turn), each streaming its operands through its own
-    // L1 from the shared L2
-    int64_t sh;
-    int wave;
-    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &wave)) return;
-    const int64_t s = sh / a.H, h = sh % a.H;
-    const int lane = threadIdx.x;
-    const int col = lane & 31, half = lane >> 5;
-    const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
-    const int dv = wave * 32 + col;  // this lane's state column
-
-    // S: tile r holds rows 32 r + 8 (i / 4) + 4 h + i % 4 of column dv
-    f32x16_t S[4];
-    {
-        const float *src = h0 ? h0 + sh * kD * kD : nullptr;
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                S[r][i] = src ? src[row * kD + dv] : 0.f;
-            }
-    }
-    // a chunk's operands (a chunk past the sequence's last loads the last again: every call
-    // issues the same loads)
-    auto load = [&](int c, ChunkOps &x) __attribute__((always_inline)) {
-        c = c < c1 ? c : c1 - 1;
-        const int64_t ch = (int64_t)c * a.H + h;
-        const uint16_t *wf = w.Wf + ch * kC * kD, *kf = w.Kf + ch * kC * kD;
-        const uint16_t *uc = w.Uc + ch * kC * kD + (size_t)wave * 2 * 2 * 64 * 8;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int st = 0; st < 8; st++)
-                x.wf[t][st].u = *(const uint4 *)(wf + ((t * 8 + st) * 64 + lane) * 8);
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++)
-                x.uc[t][qq] = *(const uint4 *)(uc + ((t * 2 + qq) * 64 + lane) * 8);
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int st = 0; st < 4; st++)
-                x.kf[r][st].u = *(const uint4 *)(kf + ((r * 4 + st) * 64 + lane) * 8);
-        x.glast = w.G[ch * kC + kC - 1];
-    };
-    auto step = [&](int c, ChunkOps &x) __attribute__((always_inline)) {
-        const int64_t ch = (int64_t)c * a.H + h;
-        // S as operand fragments (k = state row, col = dv), in the dtype; also stored for the
-        // output kernel in fragment order [dv tile][k step][lane]
-        Frag8 sf[8];
-        uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
-#pragma unroll
-        for (int st = 0; st < 8; st++) {
-            const int r = st / 2, u = st % 2;
-            sf[st].u = make_uint4(pack2<DT>(S[r][8 * u + 0], S[r][8 * u + 1]),
-                                  pack2<DT>(S[r][8 * u + 2], S[r][8 * u + 3]),
-                                  pack2<DT>(S[r][8 * u + 4], S[r][8 * u + 5]),
-                                  pack2<DT>(S[r][8 * u + 6], S[r][8 * u + 7]));
-            *(uint4 *)(sfo + (st * 64 + lane) * 8) = sf[st].u;
-        }
-        // W S for the 2 token tiles (k slots in the fragments' state-row order)
-        f32x16_t vp[2];
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) vp[t][i] = 0.f;
-#pragma unroll
-        for (int st = 0; st < 8; st++)
-#pragma unroll
-            for (int t = 0; t < 2; t++) vp[t] = mfma32<DT>(x.wf[t][st], sf[st], vp[t]);
-        // V' = U - W S, as B fragments of the state update (token order 32 t + 16 u + ...) and
-        // stored for the output kernel
-        Frag8 vlf[4];
-        uint16_t *vfo = w.Vf + ch * kC * kD + (size_t)wave * 4 * 64 * 8;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t uw[4] = {x.uc[t][u].x, x.uc[t][u].y, x.uc[t][u].z, x.uc[t][u].w};
-                float v8[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float uu = (e & 1) ? unpack_hi<DT>(uw[e / 2]) : unpack_lo<DT>(uw[e / 2]);
-                    v8[e] = uu - vp[t][8 * u + e];
-                }
-                const int st = t * 2 + u;
-                vlf[st].u = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
-                                       pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
-                *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
-            }
-        // S <- exp(G_last) S + (lam K)^T V'
-        const float gl = __expf(x.glast);
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) S[r][i] *= gl;
-#pragma unroll
-        for (int st = 0; st < 4; st++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) S[r] = mfma32<DT>(x.kf[r][st], vlf[st], S[r]);
-    };
-    // two operand sets in turn (named statically), each loaded two chunks ahead of its use
-    ChunkOps oa, ob;
-    if (c0 < c1) {
-        load(c0, oa);
-        load(c0 + 1, ob);
-    }
-    for (int c = c0; c < c1; c += 2) {
-        step(c, oa);
-        load(c + 2, oa);
-        if (c + 1 >= c1) break;
-        step(c + 1, ob);
-        load(c + 3, ob);
-    }
-    if (final_state) {
-        float *dst = final_state + sh * kD * kD;
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                dst[row * kD + dv] = S[r][i];
-            }
-    }
-}
-
 // The state pass with the rows of S split over a pair of wavefronts (one workgroup per column
 // block): wavefront p holds rows 64 p + [0, 64) of the block's 32 columns. Per chunk each
 // computes its part of W S (8 products over its 64 state rows), the pair swaps the parts through
@@ -848,7 +705,7 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
 //
 //   gdr_bwd_pre    per (chunk, head): F = (gamma scale Q)^T dO - W^T (Aqk^T dO), the part of
 //                  the state gradient's chunk step that does not depend on the state
-//   gdr_bwd_state  per (sequence, head, 32 state columns), serial over the chunks in reverse:
+//   gdr_bwd_state2 per (sequence, head, 32 state columns), serial over the chunks in reverse:
 //                  dS_c = exp(G_last) dS_{c+1} - W^T ((lam K) dS_{c+1}) + F; stores dS_{c+1}
 //                  per chunk and dh0
 //   gdr_bwd_grads  per (chunk, head): dV' = (lam K) dS_{c+1} + Aqk^T dO, then every gradient
@@ -956,86 +813,98 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
     }
 }
 
-// The state gradient, backwards over a sequence's chunks; one wavefront per 32 state columns
-// (as the forward's state pass). Operands two chunks ahead, straight into registers.
-struct BwdOps {
-    Frag8 kr[2][8];  // lam K: token tile t, dk step st (rows = tokens)
-    Frag8 wt[4][4];  // W^T: dk tile r, token step st
-    uint4 f[4][2];   // F: dk tile r, the lane's 16 values as two 16-byte halves
+// The state gradient, backwards over a sequence's chunks, with the rows of dS split over a pair
+// of wavefronts per column block (as the forward's state pass): each forms its part of X = (lam K) dS_{c+1} over its 64 rows, the pair
+// swaps the parts through LDS, and each updates its own rows.
+struct BwdHalfOps {
+    Frag8 kr[2][4];  // lam K: token tile t, dk step 4 p + st
+    Frag8 wt[2][4];  // W^T: dk tile 2 p + r, token step st
+    uint4 f[2][2];   // F: dk tile 2 p + r, the lane's 16 values as two 16-byte halves
     float glast;
 };
 
 template <int DT>
-__global__ __launch_bounds__(64, 1) void gdr_bwd_state(GdrArgs a, MfmaWs w, const float *d_final,
-                                                       float *dh0) {
+__global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, const float *d_final,
+                                                        float *dh0) {
+    __shared__ __align__(16) float xch[2][2][2][16][64];  // [parity][wavefront][token tile][i][lane]
     int64_t sh;
-    int wave;
-    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &wave)) return;
+    int blk;
+    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
     const int64_t s = sh / a.H, h = sh % a.H;
-    const int lane = threadIdx.x;
-    const int col = lane & 31, half = lane >> 5;
+    const int lane = threadIdx.x & 63;
+    const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row half
+    const int col = lane & 31;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
-    const int dv = wave * 32 + col;
-    // dS: tile r holds rows 32 r + 8 (i / 4) + 4 h + i % 4 of column dv
-    f32x16_t D[4];
+    const int dv = blk * 32 + col;
+    // dS_p: tile r holds rows 64 p + 32 r + crow(i) of column dv
+    f32x16_t D[2];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int r = 0; r < 2; r++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-            D[r][i] = d_final ? d_final[sh * kD * kD + row * kD + dv] : 0.f;
-        }
+        for (int i = 0; i < 16; i++)
+            D[r][i] = d_final ? d_final[sh * kD * kD + (p * 64 + r * 32 + crow(i, lane)) * kD + dv] : 0.f;
     // a chunk before the sequence's first loads the first again (every call the same loads)
-    auto load = [&](int c, BwdOps &x) __attribute__((always_inline)) {
+    auto load = [&](int c, BwdHalfOps &x) __attribute__((always_inline)) {
         c = c >= c0 ? c : c0;
         const int64_t ch = (int64_t)c * a.H + h;
         const uint16_t *kr = w.Krf + ch * kC * kD, *wt = w.WTf + ch * kC * kD;
-        const uint16_t *f = w.F + ch * kD * kD + (size_t)wave * 4 * 64 * 16;
+        const uint16_t *f = w.F + ch * kD * kD + (size_t)blk * 4 * 64 * 16;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int st = 0; st < 8; st++)
-                x.kr[t][st].u = *(const uint4 *)(kr + ((t * 8 + st) * 64 + lane) * 8);
+            for (int st = 0; st < 4; st++)
+                x.kr[t][st].u = *(const uint4 *)(kr + ((t * 8 + p * 4 + st) * 64 + lane) * 8);
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int r = 0; r < 2; r++)
 #pragma unroll
             for (int st = 0; st < 4; st++)
-                x.wt[r][st].u = *(const uint4 *)(wt + ((r * 4 + st) * 64 + lane) * 8);
+                x.wt[r][st].u = *(const uint4 *)(wt + (((p * 2 + r) * 4 + st) * 64 + lane) * 8);
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            x.f[r][0] = *(const uint4 *)(f + ((size_t)r * 64 + lane) * 16);
-            x.f[r][1] = *(const uint4 *)(f + ((size_t)r * 64 + lane) * 16 + 8);
+        for (int r = 0; r < 2; r++) {
+            x.f[r][0] = *(const uint4 *)(f + ((size_t)(p * 2 + r) * 64 + lane) * 16);
+            x.f[r][1] = *(const uint4 *)(f + ((size_t)(p * 2 + r) * 64 + lane) * 16 + 8);
         }
         x.glast = w.G[ch * kC + kC - 1];
     };
-    auto step = [&](int c, BwdOps &x) __attribute__((always_inline)) {
+    auto step = [&](int c, const BwdHalfOps &x) __attribute__((always_inline)) {
         const int64_t ch = (int64_t)c * a.H + h;
-        // dS after the chunk (dS_{c+1}), kept for the gradients as S is in Sf
-        Frag8 df[8];
-        uint16_t *dso = w.dSf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
+        // this half of dS after the chunk, kept for the gradients as S is in Sf
+        Frag8 df[4];
+        uint16_t *dso = w.dSf + ch * kD * kD + (size_t)blk * 8 * 64 * 8;
 #pragma unroll
-        for (int st = 0; st < 8; st++) {
+        for (int st = 0; st < 4; st++) {
             df[st] = c_frag<DT>(D[st / 2], st % 2);
-            *(uint4 *)(dso + (st * 64 + lane) * 8) = df[st].u;
+            *(uint4 *)(dso + ((p * 4 + st) * 64 + lane) * 8) = df[st].u;
         }
-        // X = (lam K) dS_{c+1}: 2 token tiles
+        // this half's part of X = (lam K) dS_{c+1}
         f32x16_t X[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) X[t] = zero16();
 #pragma unroll
-        for (int st = 0; st < 8; st++)
+        for (int st = 0; st < 4; st++)
 #pragma unroll
             for (int t = 0; t < 2; t++) X[t] = mfma32<DT>(x.kr[t][st], df[st], X[t]);
+        float(*mine)[16][64] = xch[c & 1][p];
+        float(*other)[16][64] = xch[c & 1][p ^ 1];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) mine[t][i][lane] = X[t][i];
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) X[t][i] += other[t][i][lane];
         Frag8 nx[4];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             nx[2 * t] = c_frag<DT>(X[t], 0, -1.f);
             nx[2 * t + 1] = c_frag<DT>(X[t], 1, -1.f);
         }
-        // dS_c = exp(G_last) dS_{c+1} + F - W^T X
+        // dS_c = exp(G_last) dS_{c+1} + F - W^T X on this half's rows
         const float gl = __expf(x.glast);
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
+        for (int r = 0; r < 2; r++) {
             const uint32_t fw[8] = {x.f[r][0].x, x.f[r][0].y, x.f[r][0].z, x.f[r][0].w,
                                     x.f[r][1].x, x.f[r][1].y, x.f[r][1].z, x.f[r][1].w};
 #pragma unroll
@@ -1047,9 +916,9 @@ __global__ __launch_bounds__(64, 1) void gdr_bwd_state(GdrArgs a, MfmaWs w, cons
 #pragma unroll
         for (int st = 0; st < 4; st++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) D[r] = mfma32<DT>(x.wt[r][st], nx[st], D[r]);
+            for (int r = 0; r < 2; r++) D[r] = mfma32<DT>(x.wt[r][st], nx[st], D[r]);
     };
-    BwdOps oa, ob;
+    BwdHalfOps oa, ob;
     if (c0 < c1) {
         load(c1 - 1, oa);
         load(c1 - 2, ob);
@@ -1063,12 +932,10 @@ __global__ __launch_bounds__(64, 1) void gdr_bwd_state(GdrArgs a, MfmaWs w, cons
     }
     if (dh0) {
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int r = 0; r < 2; r++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int row = r * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                dh0[sh * kD * kD + row * kD + dv] = D[r][i];
-            }
+            for (int i = 0; i < 16; i++)
+                dh0[sh * kD * kD + (p * 64 + r * 32 + crow(i, lane)) * kD + dv] = D[r][i];
     }
 }
 
@@ -1713,7 +1580,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_STATE, st);
-        gdr_bwd_state<DT><<<(unsigned)state_grid(seqs), 64, 0, st>>>(a, w, d_final, dh0);
+        gdr_bwd_state2<DT><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, d_final, dh0);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_GRADS, st);
