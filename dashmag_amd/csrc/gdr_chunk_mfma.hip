@@ -473,36 +473,42 @@ __device__ __forceinline__ bool state_item(int64_t x, int64_t grid, int64_t nsh,
 // updates its own rows: S_p <- e^{G_last} S_p + (lam K)_p^T V' (8 products). Per wavefront
 // that is half the products, half the operands and half the state of a single wavefront per
 // block, on the chain every chunk waits for.
-struct HalfOps {
-    Frag8 wf[2][4];  // W: token tile t, dk step 4 p + st
-    uint4 uc[2][2];  // U: token tile t, two 8-value halves of the lane's 16
-    Frag8 kf[2][4];  // (lam K)^T: dk tile 2 p + r, token step st
+constexpr int kStateParts = 2;  // wavefronts sharing a column block's state rows (4 measured slower)
+
+template <int NP>
+struct PartOps {
+    static constexpr int RT = 4 / NP, KS = 8 / NP;  // state tiles and dk steps per wavefront
+    Frag8 wf[2][KS];  // W: token tile t, dk step KS p + st
+    uint4 uc[2][2];   // U: token tile t, two 8-value halves of the lane's 16
+    Frag8 kf[RT][4];  // (lam K)^T: dk tile RT p + r, token step st
     float glast;
 };
 
-template <int DT>
-__global__ __launch_bounds__(128, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, const float *h0,
-                                                         float *final_state) {
-    __shared__ __align__(16) float xch[2][2][2][16][64];  // [parity][wavefront][token tile][i][lane]
+template <int DT, int NP>
+__global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, const float *h0,
+                                                             float *final_state) {
+    constexpr int RT = 4 / NP, KS = 8 / NP;
+    using HalfOps = PartOps<NP>;
+    __shared__ __align__(16) float xch[2][NP][2][16][64];  // [parity][wavefront][token tile][i][lane]
     int64_t sh;
     int blk;
     if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
     const int64_t s = sh / a.H, h = sh % a.H;
     const int lane = threadIdx.x & 63;
-    const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row half
+    const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row part
     const int col = lane & 31;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
     const int dv = blk * 32 + col;
 
-    // S_p: tile r holds rows 64 p + 32 r + crow(i) of column dv
-    f32x16_t S[2];
+    // S_p: tile r holds rows 32 (RT p + r) + crow(i) of column dv
+    f32x16_t S[RT];
     {
         const float *src = h0 ? h0 + sh * kD * kD : nullptr;
 #pragma unroll
-        for (int r = 0; r < 2; r++)
+        for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                S[r][i] = src ? src[(p * 64 + r * 32 + crow(i, lane)) * kD + dv] : 0.f;
+                S[r][i] = src ? src[((RT * p + r) * 32 + crow(i, lane)) * kD + dv] : 0.f;
     }
     auto load = [&](int c, HalfOps &x) __attribute__((always_inline)) {
         c = c < c1 ? c : c1 - 1;
@@ -512,51 +518,54 @@ __global__ __launch_bounds__(128, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, c
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int st = 0; st < 4; st++)
-                x.wf[t][st].u = *(const uint4 *)(wf + ((t * 8 + p * 4 + st) * 64 + lane) * 8);
+            for (int st = 0; st < KS; st++)
+                x.wf[t][st].u = *(const uint4 *)(wf + ((t * 8 + p * KS + st) * 64 + lane) * 8);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int qq = 0; qq < 2; qq++)
                 x.uc[t][qq] = *(const uint4 *)(uc + ((t * 2 + qq) * 64 + lane) * 8);
 #pragma unroll
-        for (int r = 0; r < 2; r++)
+        for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int st = 0; st < 4; st++)
-                x.kf[r][st].u = *(const uint4 *)(kf + (((p * 2 + r) * 4 + st) * 64 + lane) * 8);
+                x.kf[r][st].u = *(const uint4 *)(kf + (((p * RT + r) * 4 + st) * 64 + lane) * 8);
         x.glast = w.G[ch * kC + kC - 1];
     };
     auto step = [&](int c, const HalfOps &x) __attribute__((always_inline)) {
         const int64_t ch = (int64_t)c * a.H + h;
-        // this half of S as operand fragments (dk steps 4 p + st), also stored for the output
-        Frag8 sf[4];
+        // this part of S as operand fragments (dk steps KS p + st), also stored for the output
+        Frag8 sf[KS];
         uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)blk * 8 * 64 * 8;
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
+        for (int st = 0; st < KS; st++) {
             sf[st] = c_frag<DT>(S[st / 2], st % 2);
-            *(uint4 *)(sfo + ((p * 4 + st) * 64 + lane) * 8) = sf[st].u;
+            *(uint4 *)(sfo + ((p * KS + st) * 64 + lane) * 8) = sf[st].u;
         }
-        // this half's part of W S
+        // this part's share of W S
         f32x16_t vp[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) vp[t] = zero16();
 #pragma unroll
-        for (int st = 0; st < 4; st++)
+        for (int st = 0; st < KS; st++)
 #pragma unroll
             for (int t = 0; t < 2; t++) vp[t] = mfma32<DT>(x.wf[t][st], sf[st], vp[t]);
-        // swap the parts
-        float(*mine)[16][64] = xch[c & 1][p];
-        float(*other)[16][64] = xch[c & 1][p ^ 1];
+        // swap the shares (summed in the same order in every wavefront)
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) mine[t][i][lane] = vp[t][i];
+            for (int i = 0; i < 16; i++) xch[c & 1][p][t][i][lane] = vp[t][i];
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) vp[t][i] += other[t][i][lane];
-        // V' = U - W S (the same in both wavefronts; wavefront p stores token tile p)
+            for (int i = 0; i < 16; i++) {
+                float acc = xch[c & 1][0][t][i][lane];
+#pragma unroll
+                for (int q = 1; q < NP; q++) acc += xch[c & 1][q][t][i][lane];
+                vp[t][i] = acc;
+            }
+        // V' = U - W S (the same in every wavefront; wavefront p stores the steps st = p mod NP)
         Frag8 vlf[4];
         uint16_t *vfo = w.Vf ? w.Vf + ch * kC * kD + (size_t)blk * 4 * 64 * 8 : nullptr;
 #pragma unroll
@@ -573,18 +582,18 @@ __global__ __launch_bounds__(128, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, c
                 const int st = t * 2 + u;
                 vlf[st].u = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
                                        pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
-                if (vfo && t == p) *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
+                if (vfo && st % NP == p) *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
             }
         // S_p <- exp(G_last) S_p + (lam K)_p^T V'
         const float gl = __expf(x.glast);
 #pragma unroll
-        for (int r = 0; r < 2; r++)
+        for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int i = 0; i < 16; i++) S[r][i] *= gl;
 #pragma unroll
         for (int st = 0; st < 4; st++)
 #pragma unroll
-            for (int r = 0; r < 2; r++) S[r] = mfma32<DT>(x.kf[r][st], vlf[st], S[r]);
+            for (int r = 0; r < RT; r++) S[r] = mfma32<DT>(x.kf[r][st], vlf[st], S[r]);
     };
     HalfOps oa, ob;
     if (c0 < c1) {
@@ -601,9 +610,9 @@ __global__ __launch_bounds__(128, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, c
     if (final_state) {
         float *dst = final_state + sh * kD * kD;
 #pragma unroll
-        for (int r = 0; r < 2; r++)
+        for (int r = 0; r < RT; r++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) dst[(p * 64 + r * 32 + crow(i, lane)) * kD + dv] = S[r][i];
+            for (int i = 0; i < 16; i++) dst[((RT * p + r) * 32 + crow(i, lane)) * kD + dv] = S[r][i];
     }
 }
 
@@ -1530,7 +1539,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state2<DM_BF16><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state2<DM_BF16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1543,7 +1552,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state2<DM_F16><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, h0, final_state);
+            gdr_mfma_state2<DM_F16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, 0, st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1572,7 +1581,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_STATE, st);
-        gdr_mfma_state2<DT><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, h0, nullptr);
+        gdr_mfma_state2<DT, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, 0, st>>>(a, w, h0, nullptr);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_PRE, st);
