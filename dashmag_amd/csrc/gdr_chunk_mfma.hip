@@ -674,6 +674,7 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
 #pragma unroll
     for (int st = 0; st < 4; st++) vf[st].u = *(const uint4 *)(vfo + (st * 64 + lane) * 8);
     __syncthreads();
+    uint2 res[2][4];  // O, packed: token tile tt, the lane's 4 groups of 4 columns
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) {
         const int tok = tt * 32 + col;  // this lane's token (column of O^T)
@@ -695,15 +696,29 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
                 intra = mfma32<DT>(vf[st], ba, intra);
             }
         }
-        if (tok >= len) continue;
         const float f = a.scale * __expf(sm.g[tok]);
-        uint16_t *op = (uint16_t *)out + ((tok0 + tok) * a.H + h) * kD + wave * 32;
 #pragma unroll
         for (int g4 = 0; g4 < 4; g4++) {
-            uint2 v2;
-            v2.x = pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]);
-            v2.y = pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]);
-            *(uint2 *)(op + g4 * 8 + half * 4) = v2;
+            res[tt][g4].x = pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]);
+            res[tt][g4].y = pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]);
+        }
+    }
+    // O as rows through LDS (the queries' space, dead now), then 16-byte stores along the rows
+    __syncthreads();
+    uint16_t *orow = qs;
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++)
+            *(uint2 *)(orow + (tt * 32 + col) * kRowB + wave * 32 + g4 * 8 + half * 4) = res[tt][g4];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        if (r < len) {
+            const uint2 *src = (const uint2 *)(orow + r * kRowB + c * 8);
+            *(uint4 *)((uint16_t *)out + ((tok0 + r) * a.H + h) * kD + c * 8) =
+                make_uint4(src[0].x, src[0].y, src[1].x, src[1].y);
         }
     }
 }
