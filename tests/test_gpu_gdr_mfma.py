@@ -80,13 +80,15 @@ def test_mfma_packed_equals_per_sequence():
 # at [1, 200, 2, 128, 128], 1.2e-2 without it (the gate's gradient, a difference of sums within
 # each chunk, is the largest error, as the reference measured). f16 carries more mantissa.
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("lens,h,l2norm,tol", [
-    ([200], 2, True, 7.5e-3),
-    ([200], 2, False, 1.2e-2),
-    ([37, 64, 0, 100, 5, 1], 3, True, 7.5e-3),
-    ([130, 300], 2, False, 1.2e-2),
+@pytest.mark.parametrize("lens,h,l2norm,tol,states", [
+    ([200], 2, True, 7.5e-3, True),
+    ([200], 2, False, 1.2e-2, True),
+    ([37, 64, 0, 100, 5, 1], 3, True, 7.5e-3, True),
+    ([130, 300], 2, False, 1.2e-2, True),
+    ([64, 1, 300], 2, True, 7.5e-3, False),
 ])
-def test_mfma_backward_matches_oracle(dtype, lens, h, l2norm, tol):
+def test_mfma_backward_matches_oracle(dtype, lens, h, l2norm, tol, states):
+    """`states` False: no initial state and no final state's gradient (zero in the oracle)."""
     T, D = sum(lens), 128
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
     seed = 300 + sum(lens) + 7 * l2norm
@@ -97,9 +99,9 @@ def test_mfma_backward_matches_oracle(dtype, lens, h, l2norm, tol):
     v = syn.normal(seed + 2, (1, T, h, D), "cuda")
     g = -torch.nn.functional.softplus(syn.normal(seed + 3, (1, T, h), "cuda"))
     beta = torch.sigmoid(syn.normal(seed + 4, (1, T, h), "cuda"))
-    h0 = syn.normal(seed + 5, (len(lens), h, D, D), "cuda", std=0.1)
+    h0 = syn.normal(seed + 5, (len(lens), h, D, D), "cuda", std=0.1) if states else None
     do = syn.normal(seed + 6, (1, T, h, D), "cuda").to(dtype)
-    dfin = syn.normal(seed + 7, (len(lens), h, D, D), "cuda", std=0.1)
+    dfin = syn.normal(seed + 7, (len(lens), h, D, D), "cuda", std=0.1) if states else None
     q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     print(f"backward case lens {lens} h {h} l2norm {l2norm} {dtype}", flush=True)
     _lib.probe_reset()
@@ -107,10 +109,16 @@ def test_mfma_backward_matches_oracle(dtype, lens, h, l2norm, tol):
     r = dm.chunk_gated_delta_rule_backward(q, k, v, g, beta, h0, cu.cuda(), do, dfin, opts)
     torch.cuda.synchronize()
     assert _lib.probe_counts()["gdr_chunk_bwd"] > 0
-    e = oracle.gdr_chunk_bwd(host(q), host(k), host(v), host(g), host(beta), host(h0), host(do),
-                             host(dfin), cu.numpy(), l2norm, precision="f64")
+    e = oracle.gdr_chunk_bwd(host(q), host(k), host(v), host(g), host(beta),
+                             None if h0 is None else host(h0), host(do),
+                             None if dfin is None else host(dfin), cu.numpy(), l2norm,
+                             precision="f64")
+    names = ["dq", "dk", "dv", "dg", "dbeta", "dh0"]
+    if h0 is None:
+        assert r[5] is None
+        names, r, e = names[:5], r[:5], e[:5]
     worst = 0.0
-    for name, a_, e_ in zip(["dq", "dk", "dv", "dg", "dbeta", "dh0"], r, e):
+    for name, a_, e_ in zip(names, r, e):
         rr = errors(host(a_), e_)[1]
         worst = max(worst, rr)
         print(f"  {name}: rel {rr:.2e}")
