@@ -973,8 +973,8 @@ constexpr int QB = 0, KB = 17408, VB = 34816, DWT = 52224, TB = 70656, M1T = 798
 constexpr int M2T = 133120, M3BT = 142336;      // m2^T, later m3^T; m3b^T
 constexpr int DVLO = M2T;                       // dV'^T's rounding residual, until m2^T
 constexpr int TOKF = 151552;                    // G, gamma, lam, beta, qi, ki [64] f32
-constexpr int RED = TOKF + 6 * 256;             // 4 floats
-constexpr int PART = RED + 16;                  // 8 x [4][64] f32 partial sums
+constexpr int RED = TOKF + 6 * 256;             // 8 floats
+constexpr int PART = RED + 32;                  // 8 x [4][64] f32 partial sums
 constexpr int BYTES = PART + 8 * 1024;
 }  // namespace bl
 static_assert(bl::DTT + kC * kT * 2 <= bl::DVPT && bl::AQ + kC * kT * 2 <= bl::M2T, "phases");
@@ -984,7 +984,7 @@ static_assert(kC * kR * 2 <= bl::TOKF - bl::M2T && kC * kR * 2 <= bl::DTT + kC *
               "output rows in dead regions");
 
 template <int DT>
-__global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
+__global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
                                                         void *dq, void *dk, void *dv, void *dg,
                                                         void *dbeta) {
     __shared__ __align__(16) char smem[bl::BYTES];
@@ -995,7 +995,11 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
-    const int ti = wave >> 1, tj = wave & 1;  // this wave's 64x64 tile
+    // wavefront w: columns 32 (w % 4) + [0, 32) of dq, dk, dv at tokens 32 (w / 4) + [0, 32);
+    // wavefronts 0-3 also the 32x32 tile (w / 2, w % 2) of the 64x64 intermediates
+    const int cw = wave & 3, tw = wave >> 2;
+    const bool tilew = wave < 4;
+    const int ti = (wave >> 1) & 1, tj = wave & 1;
     auto U16 = [&](int off) { return (uint16_t *)(smem + off); };
     auto F32 = [&](int off) { return (float *)(smem + off); };
     uint16_t *sST = U16(bl::ST), *sDST = U16(bl::DST), *sVPT = U16(bl::VPT), *sDOB = U16(bl::DOB);
@@ -1006,23 +1010,19 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
           *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
 
     // phase 2's rows (Q, K, V, T) are loaded first and held in registers through phase 1
-    uint4 q2[4], k2[4], v2[4], t2[2];
+    uint4 q2[2], k2[2], v2[2], t2;
     {
         const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
                        *vin = (const uint16_t *)a.v;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 512 * u, r = x / 16, c = x % 16;
             const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
             q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
             k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
             v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int x = tid + 256 * u, r = x / 8, c = x % 8;
-            t2[u] = *(const uint4 *)(w.Tm + ch * kC * kC + r * kC + c * 8);
-        }
+        t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
     }
     // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
     if (tid < kC) {
@@ -1036,30 +1036,26 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         const uint16_t *sf = w.Sf + ch * kD * kD, *dsf = w.dSf + ch * kD * kD;
         const uint16_t *vf = w.Vf + ch * kC * kD, *dob = (const uint16_t *)d_out;
         // every load issued before the first store
-        uint4 s1[8], s2[8], s3[4], s4[4], s5[2];
+        uint4 s1[4], s2[4], s3[2], s4[2], s5;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            s1[i] = *(const uint4 *)(sf + (size_t)(tid + 256 * i) * 8);
-            s2[i] = *(const uint4 *)(dsf + (size_t)(tid + 256 * i) * 8);
+        for (int i = 0; i < 4; i++) {
+            s1[i] = *(const uint4 *)(sf + (size_t)(tid + 512 * i) * 8);
+            s2[i] = *(const uint4 *)(dsf + (size_t)(tid + 512 * i) * 8);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) s3[i] = *(const uint4 *)(vf + (size_t)(tid + 256 * i) * 8);
+        for (int i = 0; i < 2; i++) s3[i] = *(const uint4 *)(vf + (size_t)(tid + 512 * i) * 8);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 512 * u, r = x / 16, c = x % 16;
             const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
             s4[u] = *(const uint4 *)(dob + row * kD + c * 8);
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int x = tid + 256 * u, r = x / 8, c = x % 8;
-            s5[u] = *(const uint4 *)(w.Aqk + ch * kC * kC + r * kC + c * 8);
-        }
+        s5 = *(const uint4 *)(w.Aqk + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
         // fragment (dv tile p, dk step st), lane l: column dv = 32 p + l % 32 (a row of X^T),
         // dk runs 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int x = tid + 256 * i, f = x / 64, l = x % 64, p = f / 8, st = f % 8;
+        for (int i = 0; i < 4; i++) {
+            const int x = tid + 512 * i, f = x / 64, l = x % 64, p = f / 8, st = f % 8;
             const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
             *(uint2 *)(sST + r * kR + c) = make_uint2(s1[i].x, s1[i].y);
             *(uint2 *)(sST + r * kR + c + 8) = make_uint2(s1[i].z, s1[i].w);
@@ -1067,31 +1063,27 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             *(uint2 *)(sDST + r * kR + c + 8) = make_uint2(s2[i].z, s2[i].w);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int x = tid + 256 * i, f = x / 64, l = x % 64, p = f / 4, st = f % 4;
+        for (int i = 0; i < 2; i++) {
+            const int x = tid + 512 * i, f = x / 64, l = x % 64, p = f / 4, st = f % 4;
             const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
             *(uint2 *)(sVPT + r * kT + c) = make_uint2(s3[i].x, s3[i].y);
             *(uint2 *)(sVPT + r * kT + c + 8) = make_uint2(s3[i].z, s3[i].w);
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 512 * u, r = x / 16, c = x % 16;
             *(uint4 *)(sDOB + r * kR + c * 8) = r < len ? s4[u] : make_uint4(0, 0, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int x = tid + 256 * u, r = x / 8, c = x % 8;
-            *(uint4 *)(sAQ + r * kT + c * 8) = s5[u];
-        }
-        for (int x = tid; x < 8 * 256; x += 256) pGam[x] = 0.f;
+        *(uint4 *)(sAQ + (tid / 8) * kT + (tid % 8) * 8) = s5;
+        for (int x = tid; x < 8 * 256; x += 512) pGam[x] = 0.f;
     }
     __syncthreads();
-    // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns, stored as dV'^T
+    // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns and 32 tokens, stored as dV'^T
     {
         const uint16_t *kr = w.Krf + ch * kC * kD;
-        const uint16_t *dsf = w.dSf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
+        const uint16_t *dsf = w.dSf + ch * kD * kD + (size_t)cw * 8 * 64 * 8;
+        const int t = tw;
+        {
             f32x16_t x = zero16();
 #pragma unroll
             for (int st = 0; st < 8; st++) {
@@ -1103,31 +1095,31 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 #pragma unroll
             for (int st = 0; st < 4; st++)
                 x = mfma32<DT>(lds_tr_frag(sAQ, kT, st * 16, t * 32, lane),
-                               lds_tr_frag(sDOB, kR, st * 16, wave * 32, lane), x);
-            store_ct<DT>(sDVPT, kT, t * 32, wave * 32, x, lane);
+                               lds_tr_frag(sDOB, kR, st * 16, cw * 32, lane), x);
+            store_ct<DT>(sDVPT, kT, t * 32, cw * 32, x, lane);
             // and what the rounding left, for T^T dV' (d beta's largest term)
 #pragma unroll
             for (int i = 0; i < 16; i++) x[i] -= round_to<DT>(x[i]);
-            store_ct<DT>(sDVLO, kT, t * 32, wave * 32, x, lane);
+            store_ct<DT>(sDVLO, kT, t * 32, cw * 32, x, lane);
         }
     }
     __syncthreads();
-    // (a) d(gamma q) = dO S^T, (e) dkt = V' dS_{c+1}^T, (f) dw = -dV' S^T: 2 token tiles of the
-    // wave's 32 dk columns; (b) d attn = dO V'^T on the wave's tile, zero above the diagonal
-    f32x16_t dqg[2], dkt[2], dw[2], datt = zero16();
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        dqg[t] = dkt[t] = dw[t] = zero16();
+    // (a) d(gamma q) = dO S^T, (e) dkt = V' dS_{c+1}^T, (f) dw = -dV' S^T: the wave's token tile
+    // of its 32 dk columns; (b) d attn = dO V'^T on the wave's tile, zero above the diagonal
+    f32x16_t dqg, dkt, dw, datt = zero16();
+    {
+        const int t = tw;
+        dqg = dkt = dw = zero16();
 #pragma unroll
         for (int st = 0; st < 8; st++) {
-            const Frag8 bs = lds_tr_frag(sST, kR, st * 16, wave * 32, lane);
-            dqg[t] = mfma32<DT>(row_frag(sDOB, kR, t * 32, st * 16, lane), bs, dqg[t]);
-            dw[t] = mfma32<DT>(lds_tr_frag(sDVPT, kT, st * 16, t * 32, lane), bs, dw[t]);
-            dkt[t] = mfma32<DT>(lds_tr_frag(sVPT, kT, st * 16, t * 32, lane),
-                                lds_tr_frag(sDST, kR, st * 16, wave * 32, lane), dkt[t]);
+            const Frag8 bs = lds_tr_frag(sST, kR, st * 16, cw * 32, lane);
+            dqg = mfma32<DT>(row_frag(sDOB, kR, t * 32, st * 16, lane), bs, dqg);
+            dw = mfma32<DT>(lds_tr_frag(sDVPT, kT, st * 16, t * 32, lane), bs, dw);
+            dkt = mfma32<DT>(lds_tr_frag(sVPT, kT, st * 16, t * 32, lane),
+                             lds_tr_frag(sDST, kR, st * 16, cw * 32, lane), dkt);
         }
     }
-    if (!(ti == 0 && tj == 1)) {
+    if (tilew && !(ti == 0 && tj == 1)) {
 #pragma unroll
         for (int st = 0; st < 8; st++)
             datt = mfma32<DT>(row_frag(sDOB, kR, ti * 32, st * 16, lane),
@@ -1136,7 +1128,7 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     // <S, dS_{c+1}> over the chunk
     {
         float acc = 0.f;
-        for (int x = tid; x < kD * 16; x += 256) {
+        for (int x = tid; x < kD * 16; x += 512) {
             const int r = x / 16, c = (x % 16) * 8;
             const uint4 s1 = *(const uint4 *)(sST + r * kR + c), s2 = *(const uint4 *)(sDST + r * kR + c);
             const uint32_t a1[4] = {s1.x, s1.y, s1.z, s1.w}, a2[4] = {s2.x, s2.y, s2.z, s2.w};
@@ -1153,8 +1145,8 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     // ---- phase 2: Q, K (normalised as the forward did, with the inverse norms), V, T ----
     {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int x = tid + 256 * u, r = x / 16, c = x % 16;
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 512 * u, r = x / 16, c = x % 16;
             const bool ok = r < len;
             uint4 qv = q2[u], kv = k2[u];
             const uint4 vv = v2[u];
@@ -1194,19 +1186,14 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
                 tKi[r] = ki;
             }
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int x = tid + 256 * u, r = x / 8, c = x % 8;
-            *(uint4 *)(U16(bl::TB) + r * kT + c * 8) = t2[u];
-        }
+        *(uint4 *)(U16(bl::TB) + (tid / 8) * kT + (tid % 8) * 8) = t2;
     }
     uint16_t *sQB = U16(bl::QB), *sKB = U16(bl::KB), *sVB = U16(bl::VB), *sDWT = U16(bl::DWT);
     uint16_t *sTB = U16(bl::TB), *sM1T = U16(bl::M1T), *sDTT = U16(bl::DTT);
     uint16_t *sM2T = U16(bl::M2T), *sM3BT = U16(bl::M3BT);
     // dw^T (negated: dw = -dV' S^T) and m1^T = (d attn o decay)^T
-#pragma unroll
-    for (int t = 0; t < 2; t++) store_ct<DT>(sDWT, kT, t * 32, wave * 32, dw[t], lane, -1.f);
-    {
+    store_ct<DT>(sDWT, kT, tw * 32, cw * 32, dw, lane, -1.f);
+    if (tilew) {
         f32x16_t m = zero16();
         if (!(ti == 0 && tj == 1)) {
             const int j = tj * 32 + col;
@@ -1222,7 +1209,7 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     __syncthreads();  // Q, K, V, T, dw^T, m1^T in place
     const float scale = a.scale;
     // (d) d attn o attn: + row sums, - column sums into dG
-    if (!(ti == 0 && tj == 1)) {
+    if (tilew && !(ti == 0 && tj == 1)) {
         const int j = tj * 32 + col;
         float cs = 0.f;
 #pragma unroll
@@ -1240,45 +1227,45 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         if (half == 0) pGc[wave * 64 + j] += cs;
     }
     // dq = gamma d(gamma q) + m1 K; dk = lam dkt + scale m1^T Q; d gamma, s partial sums
-    f32x16_t dqa[2], dka[2], dva[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
+    f32x16_t dqa, dka, dva;
+    {
+        const int t = tw;
         float gsum[16], ssum[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+            const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
             const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
             const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
                                              : (float)__builtin_bit_cast(_Float16, qb);
             const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
                                              : (float)__builtin_bit_cast(_Float16, kb);
-            gsum[i] = dqg[t][i] * qv * scale;
-            ssum[i] = dkt[t][i] * kv;
-            dqa[t][i] = tGam[r] * dqg[t][i];
-            dka[t][i] = tLam[r] * dkt[t][i];
+            gsum[i] = dqg[i] * qv * scale;
+            ssum[i] = dkt[i] * kv;
+            dqa[i] = tGam[r] * dqg[i];
+            dka[i] = tLam[r] * dkt[i];
         }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float g1 = sum32(gsum[i]), s1 = sum32(ssum[i]);
             if (col == 0) {
                 const int r = t * 32 + crow(i, lane);
-                pGam[wave * 64 + r] += g1;
-                pS[wave * 64 + r] += s1;
+                pGam[cw * 64 + r] += g1;
+                pS[cw * 64 + r] += s1;
             }
         }
         f32x16_t x = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            dqa[t] = mfma32<DT>(lds_tr_frag(sM1T, kT, st * 16, t * 32, lane),
-                                lds_tr_frag(sKB, kR, st * 16, wave * 32, lane), dqa[t]);
+            dqa = mfma32<DT>(lds_tr_frag(sM1T, kT, st * 16, t * 32, lane),
+                             lds_tr_frag(sKB, kR, st * 16, cw * 32, lane), dqa);
             x = mfma32<DT>(row_frag(sM1T, kT, t * 32, st * 16, lane),
-                           lds_tr_frag(sQB, kR, st * 16, wave * 32, lane), x);
+                           lds_tr_frag(sQB, kR, st * 16, cw * 32, lane), x);
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) dka[t][i] += scale * x[i];
+        for (int i = 0; i < 16; i++) dka[i] += scale * x[i];
     }
     // (g) dT = dV' (beta V)^T + dw (beta gamma K)^T on the wave's tile, stored as dT^T
-    {
+    if (tilew) {
         f32x16_t c1 = zero16(), c2 = zero16();
 #pragma unroll
         for (int st = 0; st < 8; st++) {
@@ -1295,27 +1282,27 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     }
     // (h) dvb = T^T dV', dkbg = T^T dw: dv = beta dvb; dk += beta gamma dkbg; sums for d beta,
     // d gamma
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
+    {
+        const int t = tw;
         f32x16_t xb = zero16(), xk = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             const Frag8 ta = lds_tr_frag(sTB, kT, st * 16, t * 32, lane);
-            xb = mfma32<DT>(ta, row_frag(sDVPT, kT, wave * 32, st * 16, lane), xb);
-            xb = mfma32<DT>(ta, row_frag(sDVLO, kT, wave * 32, st * 16, lane), xb);
-            xk = mfma32<DT>(ta, row_frag(sDWT, kT, wave * 32, st * 16, lane), xk);
+            xb = mfma32<DT>(ta, row_frag(sDVPT, kT, cw * 32, st * 16, lane), xb);
+            xb = mfma32<DT>(ta, row_frag(sDVLO, kT, cw * 32, st * 16, lane), xb);
+            xk = mfma32<DT>(ta, row_frag(sDWT, kT, cw * 32, st * 16, lane), xk);
         }
         float bs[16], us[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+            const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
             const uint16_t vb = sVB[r * kR + c], kb = sKB[r * kR + c];
             const float vv = (DT == DM_BF16) ? __uint_as_float((uint32_t)vb << 16)
                                              : (float)__builtin_bit_cast(_Float16, vb);
             const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
                                              : (float)__builtin_bit_cast(_Float16, kb);
-            dva[t][i] = tBet[r] * xb[i];
-            dka[t][i] += tBet[r] * tGam[r] * xk[i];
+            dva[i] = tBet[r] * xb[i];
+            dka[i] += tBet[r] * tGam[r] * xk[i];
             bs[i] = xb[i] * vv;
             us[i] = xk[i] * kv;
         }
@@ -1324,14 +1311,14 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             const float b1 = sum32(bs[i]), u1 = sum32(us[i]);
             if (col == 0) {
                 const int r = t * 32 + crow(i, lane);
-                pBet[wave * 64 + r] += b1;
-                pU[wave * 64 + r] += u1;
+                pBet[cw * 64 + r] += b1;
+                pU[cw * 64 + r] += u1;
             }
         }
     }
     __syncthreads();  // dT^T complete
     // (i) m2 = T^T dT on the wave's tile (a, b) = (ti, tj), stored as m2^T
-    {
+    if (tilew) {
         f32x16_t m2 = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++)
@@ -1343,7 +1330,7 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     // dA = -(m2 T^T) strictly below the diagonal on tile (a, c) = (ti, tj); the recomputed
     // A = beta (K K^T) o decay for the gate's sums; m3 = dA o decay
     f32x16_t m3 = zero16(), m3b = zero16();
-    if (!(ti == 0 && tj == 1)) {
+    if (tilew && !(ti == 0 && tj == 1)) {
         f32x16_t da = zero16(), kk = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++)
@@ -1373,58 +1360,60 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         if (half == 0) pGc[wave * 64 + j] += cs;
     }
     __syncthreads();  // m2^T dead: m3^T takes its place
-    store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m3, lane);
-    store_ct<DT>(sM3BT, kT, ti * 32, tj * 32, m3b, lane);
+    if (tilew) {
+        store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m3, lane);
+        store_ct<DT>(sM3BT, kT, ti * 32, tj * 32, m3b, lane);
+    }
     __syncthreads();
     // (j) dkbeta = m3 K: dk += beta dkbeta; d beta sums; dk += m3^T (beta K)
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
+    {
+        const int t = tw;
         f32x16_t xb = zero16(), xt = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            const Frag8 kb = lds_tr_frag(sKB, kR, st * 16, wave * 32, lane);
+            const Frag8 kb = lds_tr_frag(sKB, kR, st * 16, cw * 32, lane);
             xb = mfma32<DT>(lds_tr_frag(sM2T, kT, st * 16, t * 32, lane), kb, xb);
             xt = mfma32<DT>(row_frag(sM3BT, kT, t * 32, st * 16, lane), kb, xt);
         }
         float bs[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+            const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
             const uint16_t kb = sKB[r * kR + c];
             const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
                                              : (float)__builtin_bit_cast(_Float16, kb);
-            dka[t][i] += tBet[r] * xb[i] + xt[i];
+            dka[i] += tBet[r] * xb[i] + xt[i];
             bs[i] = xb[i] * kv;
         }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float b1 = sum32(bs[i]);
-            if (col == 0) pBet[wave * 64 + crow(i, lane) + t * 32] += b1;
+            if (col == 0) pBet[cw * 64 + crow(i, lane) + t * 32] += b1;
         }
     }
     // (m) the l2 normalisation's sums: <qn, scale dq>, <kn, dk> per token
     if (a.l2norm) {
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
+        {
+            const int t = tw;
             float qs[16], ks[16];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const int r = t * 32 + crow(i, lane), c = wave * 32 + col;
+                const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
                 const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
                 const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
                                                  : (float)__builtin_bit_cast(_Float16, qb);
                 const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
                                                  : (float)__builtin_bit_cast(_Float16, kb);
-                qs[i] = qv * dqa[t][i] * scale;
-                ks[i] = kv * dka[t][i];
+                qs[i] = qv * dqa[i] * scale;
+                ks[i] = kv * dka[i];
             }
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float q1 = sum32(qs[i]), k1 = sum32(ks[i]);
                 if (col == 0) {
                     const int r = t * 32 + crow(i, lane);
-                    pSq[wave * 64 + r] = q1;
-                    pSk[wave * 64 + r] = k1;
+                    pSq[cw * 64 + r] = q1;
+                    pSk[cw * 64 + r] = k1;
                 }
             }
         }
@@ -1450,7 +1439,7 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) lam_sum += __shfl_xor(lam_sum, o, 64);
         const float* red = F32(bl::RED);
-        const float sds = red[0] + red[1] + red[2] + red[3];
+        const float sds = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
         if (i == kC - 1) dG += lam_sum + sds * __expf(tG[kC - 1]);
         // reverse inclusive scan
         float x = dG;
@@ -1479,13 +1468,13 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     // dq, dk (the scale and the l2 normalisation undone), dv: staged as rows in LDS (regions
     // dead by now), then stored 16 bytes per lane
     uint16_t *oq = U16(bl::DWT), *ok_ = U16(bl::M2T), *ov = U16(bl::TB);
-#pragma unroll
-    for (int t = 0; t < 2; t++)
+    {
+        const int t = tw;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = t * 32 + crow(i, lane);
-            const int c = wave * 32 + col;
-            float qo = dqa[t][i] * scale, ko = dka[t][i];
+            const int c = cw * 32 + col;
+            float qo = dqa[i] * scale, ko = dka[i];
             if (a.l2norm) {
                 const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
                 const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
@@ -1497,12 +1486,13 @@ __global__ __launch_bounds__(256, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             }
             oq[r * kR + c] = (uint16_t)(pack2<DT>(qo, 0.f) & 0xffffu);
             ok_[r * kR + c] = (uint16_t)(pack2<DT>(ko, 0.f) & 0xffffu);
-            ov[r * kR + c] = (uint16_t)(pack2<DT>(dva[t][i], 0.f) & 0xffffu);
+            ov[r * kR + c] = (uint16_t)(pack2<DT>(dva[i], 0.f) & 0xffffu);
         }
+    }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int x = tid + 256 * u, r = x / 16, c = x % 16;
+    for (int u = 0; u < 2; u++) {
+        const int x = tid + 512 * u, r = x / 16, c = x % 16;
         if (r < len) {
             const int64_t o = ((tok0 + r) * a.H + h) * kD + c * 8;
             *(uint4 *)((uint16_t *)dq + o) = *(const uint4 *)(oq + r * kR + c * 8);
@@ -1609,7 +1599,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_GRADS, st);
         if (chunks)
-            gdr_bwd_grads<DT><<<chunks, 256, 0, st>>>(a, w, d_out, dq, dk, dv, dg, dbeta);
+            gdr_bwd_grads<DT><<<chunks, 512, 0, st>>>(a, w, d_out, dq, dk, dv, dg, dbeta);
     }
 }
 
