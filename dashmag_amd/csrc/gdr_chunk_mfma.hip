@@ -996,7 +996,8 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
     // wavefront w: columns 32 (w % 4) + [0, 32) of dq, dk, dv at tokens 32 (w / 4) + [0, 32);
-    // wavefronts 0-3 also the 32x32 tile (w / 2, w % 2) of the 64x64 intermediates
+    // and the 32x32 tile ((w / 2) % 2, w % 2) of the 64x64 intermediates: dT on wavefronts 4-7,
+    // the others on wavefronts 0-3
     const int cw = wave & 3, tw = wave >> 2;
     const bool tilew = wave < 4;
     const int ti = (wave >> 1) & 1, tj = wave & 1;
@@ -1009,21 +1010,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     float *pGam = F32(bl::PART), *pU = pGam + 256, *pS = pGam + 512, *pBet = pGam + 768,
           *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
 
-    // phase 2's rows (Q, K, V, T) are loaded first and held in registers through phase 1
-    uint4 q2[2], k2[2], v2[2], t2;
-    {
-        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
-                       *vin = (const uint16_t *)a.v;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int x = tid + 512 * u, r = x / 16, c = x % 16;
-            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
-            q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
-            k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
-            v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
-        }
-        t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
-    }
+    uint4 q2[2], k2[2], v2[2], t2;  // phase 2's rows, loaded during phase 1's products
     // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
     if (tid < kC) {
         const float gv = w.G[ch * kC + tid];
@@ -1076,6 +1063,20 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
         *(uint4 *)(sAQ + (tid / 8) * kT + (tid % 8) * 8) = s5;
         for (int x = tid; x < 8 * 256; x += 512) pGam[x] = 0.f;
+    }
+    // phase 2's rows (Q, K, V, T), in flight during phase 1's products
+    {
+        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
+                       *vin = (const uint16_t *)a.v;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 512 * u, r = x / 16, c = x % 16;
+            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
+            q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
+            k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
+            v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
+        }
+        t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
     }
     __syncthreads();
     // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns and 32 tokens, stored as dV'^T
@@ -1264,8 +1265,9 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 #pragma unroll
         for (int i = 0; i < 16; i++) dka[i] += scale * x[i];
     }
-    // (g) dT = dV' (beta V)^T + dw (beta gamma K)^T on the wave's tile, stored as dT^T
-    if (tilew) {
+    // (g) dT = dV' (beta V)^T + dw (beta gamma K)^T on tile (ti, tj), stored as dT^T: wavefronts
+    // 4-7 (0-3 have the d attn sums above)
+    if (!tilew) {
         f32x16_t c1 = zero16(), c2 = zero16();
 #pragma unroll
         for (int st = 0; st < 8; st++) {
