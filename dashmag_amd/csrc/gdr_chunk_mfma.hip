@@ -489,7 +489,7 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
                                                              float *final_state) {
     constexpr int RT = 4 / NP, KS = 8 / NP;
     using HalfOps = PartOps<NP>;
-    __shared__ __align__(16) float xch[2][NP][2][16][64];  // [parity][wavefront][token tile][i][lane]
+    __shared__ __align__(16) float4 xch[2][NP][2][4][64];  // [parity][wavefront][token tile][i / 4][lane]
     int64_t sh;
     int blk;
     if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
@@ -554,16 +554,27 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) xch[c & 1][p][t][i][lane] = vp[t][i];
+            for (int g = 0; g < 4; g++)
+                xch[c & 1][p][t][g][lane] =
+                    make_float4(vp[t][4 * g], vp[t][4 * g + 1], vp[t][4 * g + 2], vp[t][4 * g + 3]);
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float acc = xch[c & 1][0][t][i][lane];
+            for (int g = 0; g < 4; g++) {
+                float4 acc = xch[c & 1][0][t][g][lane];
 #pragma unroll
-                for (int q = 1; q < NP; q++) acc += xch[c & 1][q][t][i][lane];
-                vp[t][i] = acc;
+                for (int q = 1; q < NP; q++) {
+                    const float4 y = xch[c & 1][q][t][g][lane];
+                    acc.x += y.x;
+                    acc.y += y.y;
+                    acc.z += y.z;
+                    acc.w += y.w;
+                }
+                vp[t][4 * g] = acc.x;
+                vp[t][4 * g + 1] = acc.y;
+                vp[t][4 * g + 2] = acc.z;
+                vp[t][4 * g + 3] = acc.w;
             }
         // V' = U - W S (the same in every wavefront; wavefront p stores the steps st = p mod NP)
         Frag8 vlf[4];
@@ -850,7 +861,7 @@ struct BwdHalfOps {
 template <int DT>
 __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, const float *d_final,
                                                         float *dh0) {
-    __shared__ __align__(16) float xch[2][2][2][16][64];  // [parity][wavefront][token tile][i][lane]
+    __shared__ __align__(16) float4 xch[2][2][2][4][64];  // [parity][wavefront][token tile][i / 4][lane]
     int64_t sh;
     int blk;
     if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
@@ -908,17 +919,24 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
         for (int st = 0; st < 4; st++)
 #pragma unroll
             for (int t = 0; t < 2; t++) X[t] = mfma32<DT>(x.kr[t][st], df[st], X[t]);
-        float(*mine)[16][64] = xch[c & 1][p];
-        float(*other)[16][64] = xch[c & 1][p ^ 1];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) mine[t][i][lane] = X[t][i];
+            for (int g = 0; g < 4; g++)
+                xch[c & 1][p][t][g][lane] =
+                    make_float4(X[t][4 * g], X[t][4 * g + 1], X[t][4 * g + 2], X[t][4 * g + 3]);
         __syncthreads();
+        // the two shares summed in the same order in both wavefronts
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) X[t][i] += other[t][i][lane];
+            for (int g = 0; g < 4; g++) {
+                const float4 x0 = xch[c & 1][0][t][g][lane], x1 = xch[c & 1][1][t][g][lane];
+                X[t][4 * g] = x0.x + x1.x;
+                X[t][4 * g + 1] = x0.y + x1.y;
+                X[t][4 * g + 2] = x0.z + x1.z;
+                X[t][4 * g + 3] = x0.w + x1.w;
+            }
         Frag8 nx[4];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
