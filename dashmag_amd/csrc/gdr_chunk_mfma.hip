@@ -1028,7 +1028,6 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     float *pGam = F32(bl::PART), *pU = pGam + 256, *pS = pGam + 512, *pBet = pGam + 768,
           *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
 
-    uint4 q2[2], k2[2], v2[2], t2;  // phase 2's rows, loaded during phase 1's products
     // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
     if (tid < kC) {
         const float gv = w.G[ch * kC + tid];
@@ -1081,20 +1080,6 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
         *(uint4 *)(sAQ + (tid / 8) * kT + (tid % 8) * 8) = s5;
         for (int x = tid; x < 8 * 256; x += 512) pGam[x] = 0.f;
-    }
-    // phase 2's rows (Q, K, V, T), in flight during phase 1's products
-    {
-        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
-                       *vin = (const uint16_t *)a.v;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int x = tid + 512 * u, r = x / 16, c = x % 16;
-            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
-            q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
-            k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
-            v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
-        }
-        t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
     }
     __syncthreads();
     // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns and 32 tokens, stored as dV'^T
@@ -1162,6 +1147,20 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     __syncthreads();  // phase 1 done: S^T, dS^T, V'^T and dO are dead
 
     // ---- phase 2: Q, K (normalised as the forward did, with the inverse norms), V, T ----
+    uint4 q2[2], k2[2], v2[2], t2;
+    {
+        const uint16_t *qin = (const uint16_t *)a.q, *kin = (const uint16_t *)a.k,
+                       *vin = (const uint16_t *)a.v;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int x = tid + 512 * u, r = x / 16, c = x % 16;
+            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
+            q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
+            k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
+            v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
+        }
+        t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
+    }
     {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
@@ -1196,10 +1195,15 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
                 qv = make_uint4(qo[0], qo[1], qo[2], qo[3]);
                 kv = make_uint4(ko[0], ko[1], ko[2], ko[3]);
             }
-            const uint4 z = make_uint4(0, 0, 0, 0);
-            *(uint4 *)(U16(bl::QB) + r * kR + c * 8) = ok ? qv : z;
-            *(uint4 *)(U16(bl::KB) + r * kR + c * 8) = ok ? kv : z;
-            *(uint4 *)(U16(bl::VB) + r * kR + c * 8) = ok ? vv : z;
+            // rows past the chunk's tokens are zero (component-wise selects: a select of whole
+            // vectors goes through private memory)
+            const uint32_t keep = ok ? 0xffffffffu : 0u;
+            *(uint4 *)(U16(bl::QB) + r * kR + c * 8) =
+                make_uint4(qv.x & keep, qv.y & keep, qv.z & keep, qv.w & keep);
+            *(uint4 *)(U16(bl::KB) + r * kR + c * 8) =
+                make_uint4(kv.x & keep, kv.y & keep, kv.z & keep, kv.w & keep);
+            *(uint4 *)(U16(bl::VB) + r * kR + c * 8) =
+                make_uint4(vv.x & keep, vv.y & keep, vv.z & keep, vv.w & keep);
             if (c == 0) {
                 tQi[r] = qi;
                 tKi[r] = ki;
