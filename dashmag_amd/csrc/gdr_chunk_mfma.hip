@@ -781,7 +781,20 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint16_t *dob = (const uint16_t *)d_out, *qin = (const uint16_t *)a.q;
+    // every load issued first: the rows, Aqk, the gates, and W^T's fragments
     uint4 dv[4], qv[4], av[2];
+    float gv[4];
+    Frag8 wa[4][4];
+    {
+        const uint16_t *wtf = w.WTf + ch * kC * kD;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                wa[r][st].u = *(const uint4 *)(wtf + ((r * 4 + st) * 64 + lane) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) gv[u] = w.G[ch * kC + (tid + 256 * u) / 16];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int x = tid + 256 * u, r = x / 16, c = x % 16;
@@ -799,7 +812,7 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
     for (int u = 0; u < 4; u++) {
         const int x = tid + 256 * u, r = x / 16, c = x % 16;
         const bool ok = r < len;
-        const float f = ok ? a.scale * __expf(w.G[ch * kC + r]) : 0.f;
+        const float f = ok ? a.scale * __expf(gv[u]) : 0.f;
         const uint32_t qw[4] = {qv[u].x, qv[u].y, qv[u].z, qv[u].w};
         uint32_t qo[4];
 #pragma unroll
@@ -830,7 +843,6 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
     }
     // F = (gamma scale Q)^T dO - W^T (Aqk^T dO): rows dk (4 tiles), stored in the product
     // layout in the dtype: [dv tile][dk tile][lane][16]
-    const uint16_t *wtf = w.WTf + ch * kC * kD;
     uint16_t *fo = w.F + ch * kD * kD + (size_t)wave * 4 * 64 * 16;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -838,9 +850,7 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             x = mfma32<DT>(lds_tr_frag(sm.qg, kR, st * 16, r * 32, lane), bo[st], x);
-            Frag8 wa;
-            wa.u = *(const uint4 *)(wtf + ((r * 4 + st) * 64 + lane) * 8);
-            x = mfma32<DT>(wa, nd[st], x);
+            x = mfma32<DT>(wa[r][st], nd[st], x);
         }
         uint4 *o = (uint4 *)(fo + ((size_t)r * 64 + lane) * 16);
         o[0] = c_frag<DT>(x, 0).u;
