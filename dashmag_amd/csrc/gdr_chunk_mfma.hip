@@ -113,14 +113,8 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     float(*tt)[kC + 4] = (float(*)[kC + 4])sm.q;  // T, in the query tile's space
     float(*mm)[16][20] = sm.mm;
 
-    // gates; the values, in registers until U (16 lanes per row, 4 rows per thread)
-    if (tid < kC) {
-        const bool ok = tid < len;
-        sm.g[tid] = ok ? ld_any(a.g_dt, a.g, (tok0 + tid) * a.H + h) : 0.f;
-        sm.bet[tid] = ok ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
-    }
     // every row's loads issued before any is used (rows past the chunk's tokens read the last
-    // valid row and are zeroed after)
+    // valid row and are zeroed after); the values stay in registers until U
     uint4 vreg[4], qraw[4], kraw[4];
     {
         const uint16_t *vin = (const uint16_t *)a.v, *qin = (const uint16_t *)a.q,
@@ -138,6 +132,12 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             const int r = (tid + 256 * u) / 16;
             if (r >= len) vreg[u] = qraw[u] = kraw[u] = make_uint4(0, 0, 0, 0);
         }
+    }
+    // the gates (after the rows' loads: their reads wait on the memory counter)
+    if (tid < kC) {
+        const bool ok = tid < len;
+        sm.g[tid] = ok ? ld_any(a.g_dt, a.g, (tok0 + tid) * a.H + h) : 0.f;
+        sm.bet[tid] = ok ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
     }
     // queries and keys: 16 lanes per row, zero past the chunk's tokens; normalised in f32 and
     // rounded back to the dtype when asked
@@ -1039,13 +1039,6 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
           *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
 
     // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
-    if (tid < kC) {
-        const float gv = w.G[ch * kC + tid];
-        tG[tid] = gv;
-        tGam[tid] = __expf(gv);
-        tLam[tid] = __expf(w.G[ch * kC + kC - 1] - gv);
-        tBet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
-    }
     {
         const uint16_t *sf = w.Sf + ch * kD * kD, *dsf = w.dSf + ch * kD * kD;
         const uint16_t *vf = w.Vf + ch * kC * kD, *dob = (const uint16_t *)d_out;
@@ -1065,6 +1058,14 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             s4[u] = *(const uint4 *)(dob + row * kD + c * 8);
         }
         s5 = *(const uint4 *)(w.Aqk + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
+        // per-token values (after the rows' loads: these reads wait on the memory counter)
+        if (tid < kC) {
+            const float gv = w.G[ch * kC + tid];
+            tG[tid] = gv;
+            tGam[tid] = __expf(gv);
+            tLam[tid] = __expf(w.G[ch * kC + kC - 1] - gv);
+            tBet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
+        }
         // fragment (dv tile p, dk step st), lane l: column dv = 32 p + l % 32 (a row of X^T),
         // dk runs 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
 #pragma unroll
