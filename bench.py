@@ -164,6 +164,8 @@ def main():
         ms, mf, mb, probes, kms = bench_attention(torch, dm, ops, lib, c2, args.steps, args.warmup,
                                              c2["cu_seqlens"])
         head = dict(ms=ms, ms_fwd=mf, ms_bwd=mb, probes=probes, kernel_ms=kms)
+        secondary["attention_config2_kernel_us"] = {k: round(v[0] * 1e3, 2)
+                                                    for k, v in kms.items()}
         print("attention config 2 kernels: " + ", ".join(
             f"{k} {v[0] * 1e3:.1f} us" for k, v in kms.items()), file=sys.stderr, flush=True)
         print(f"attention config 2: {ms:.3f} ms/step (fwd {mf:.3f}, bwd {mb:.3f}), "

@@ -1,7 +1,7 @@
 // Attention forward and backward: the entry points, their contract checks, and the generic
 // kernels (any dtype, any head width up to 256, f32 arithmetic, one wavefront per row). The
-// MFMA kernels for bf16/f16 with D in {64, 128} live in attention_mfma.hip and are chosen
-// here when they take the call.
+// MFMA kernels for bf16/f16 with D in {64, 128} live in attention_fwd.hip and
+// attention_mfma_bwd.hip and are chosen here when they take the call.
 #include <algorithm>
 #include <string>
 

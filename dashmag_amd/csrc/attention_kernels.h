@@ -16,7 +16,7 @@ int launch_attn_fwd_generic(const MaskInfo &m, const dm_attention_desc *d, float
                             const void *q, const void *k, const void *v, void *o, float *lse,
                             hipStream_t st);
 
-// MFMA paths (attention_mfma.hip): bf16/f16, D in {64, 128}.
+// MFMA paths (attention_fwd.hip, attention_mfma_bwd.hip): bf16/f16, D in {64, 128}.
 bool mfma_fwd_takes(const dm_attention_desc *d);
 int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float scale,
                          const void *q, const void *k, const void *v, void *o, float *lse,
