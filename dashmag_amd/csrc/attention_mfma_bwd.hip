@@ -951,20 +951,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     };
     if (pwave) {
         int n = 0;
+        // (both halves run on every pass, the second computing nothing past the last step: on
+        // every path through the loop the second register set's loads are then the most recent,
+        // and the compiler's wait counts keep them in flight across a step)
         auto one = [&](KvStage &x) __attribute__((always_inline)) {
             restage(n, x);
-            pstep(n, cs);
+            if (n < nsteps) pstep(n, cs);
             __syncthreads();
             n++;
             rotate();
         };
-        for (;;) {
-            if (n >= nsteps) break;
+        while (n < nsteps) {
             one(st0);
-            if (n >= nsteps) break;
             one(st1);
         }
-        __syncthreads();  // iteration nsteps
+        __syncthreads();  // the dS waves' last iteration
     } else {
         restage(0, st0);
         __syncthreads();
@@ -972,15 +973,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         rotate();
         auto one = [&](KvStage &x) __attribute__((always_inline)) {
             restage(n, x);
-            dsstep(n - 1, ps);
+            if (n <= nsteps) dsstep(n - 1, ps);
             __syncthreads();
             n++;
             rotate();
         };
-        for (;;) {
-            if (n > nsteps) break;
+        while (n <= nsteps) {
             one(st1);
-            if (n > nsteps) break;
             one(st0);
         }
         if (qvalid) {
