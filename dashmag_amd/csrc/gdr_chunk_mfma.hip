@@ -611,11 +611,13 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
         load(c0, oa);
         load(c0 + 1, ob);
     }
+    // (both halves issue their loads on every pass, the second step's products conditional: on
+    // every path through the loop the second set's loads are then the most recent, and the
+    // compiler's wait counts keep them in flight across a step)
     for (int c = c0; c < c1; c += 2) {
         step(c, oa);
         load(c + 2, oa);
-        if (c + 1 >= c1) break;
-        step(c + 1, ob);
+        if (c + 1 < c1) step(c + 1, ob);
         load(c + 3, ob);
     }
     if (final_state) {
