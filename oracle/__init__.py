@@ -3,7 +3,7 @@
 A ctypes front end over ``oracle/liboracle.so``, the plain-C restatement of dash-ops' reference
 implementations (``crates/dash-ops/src/attention/reference.rs``,
 ``crates/dash-ops/src/gated_delta/chunk/reference.rs``,
-``crates/dash-ops/src/gated_delta/recurrent.rs:309-404``). Only ``tests/``,
+``crates/dash-ops/src/gated_delta/recurrent.rs:309-404``, ``crates/dash-ops/src/conv1d/reference.rs``). Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this module: as the
 checker of the HIP path, and as the timed CPU baseline. The product package ``dashmag_amd`` never
 imports it.
@@ -218,3 +218,79 @@ def gdr_step(q, k, v, g, beta, state, cu=None, l2norm=False, scale=None, precisi
         ctypes.byref(s), _p(q), _p(k), _p(v), _p(g), _p(beta), _p(st), _p(out))
     assert rc == 0
     return out, st
+
+
+class _Conv1d(ctypes.Structure):
+    _fields_ = [
+        ("b", ctypes.c_int64), ("t", ctypes.c_int64), ("c", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("cu", ctypes.c_void_p), ("nseq", ctypes.c_int64),
+        ("has_bias", ctypes.c_int32), ("silu", ctypes.c_int32),
+        ("has_h0", ctypes.c_int32), ("w", ctypes.c_int64),
+        ("has_final", ctypes.c_int32), ("w_out", ctypes.c_int64),
+    ]
+
+
+def _conv1d(x, weight, bias, h0, cu, silu, w_out):
+    b, t, c = x.shape
+    k = weight.shape[1]
+    cu = None if cu is None else _i64(cu)
+    s = _Conv1d(b=b, t=t, c=c, k=k, cu=None if cu is None else cu.ctypes.data,
+                nseq=0 if cu is None else len(cu) - 1, has_bias=int(bias is not None),
+                silu=int(bool(silu)), has_h0=int(h0 is not None),
+                w=0 if h0 is None else h0.shape[1], has_final=int(w_out is not None),
+                w_out=0 if w_out is None else int(w_out))
+    return s, cu, (len(cu) - 1 if cu is not None else b)
+
+
+def conv1d_fwd(x, weight, bias=None, h0=None, cu=None, silu=False, w_out=None,
+               precision="f32"):
+    """The causal depthwise conv1d (conv1d/reference.rs:223-268): ``x`` ``[B, T, C]``,
+    ``weight`` ``[C, K]``, ``bias`` ``[C]``, initial states ``h0`` ``[S, W, C]``; returns the
+    output ``[B, T, C]`` and, with ``w_out``, the final states ``[S, w_out, C]``."""
+    x, weight = _f32(x), _f32(weight)
+    bias = None if bias is None else _f32(bias)
+    h0 = None if h0 is None else _f32(h0)
+    s, cu, nseq = _conv1d(x, weight, bias, h0, cu, silu, w_out)
+    out = np.zeros_like(x)
+    fin = np.zeros((nseq, s.w_out, s.c), np.float32) if w_out is not None else None
+    rc = getattr(lib(), f"dmo_conv1d_fwd_{precision}")(
+        ctypes.byref(s), _p(x), _p(weight), _p(bias), _p(h0), _p(out), _p(fin))
+    assert rc == 0
+    return out, fin
+
+
+def conv1d_bwd(x, weight, bias, h0, grad_out, grad_final=None, cu=None, silu=False,
+               precision="f32"):
+    """The conv1d's gradients (conv1d/reference.rs:270-482): ``(grad_x, grad_weight, grad_bias,
+    grad_h0)``, ``grad_bias`` None without a bias, ``grad_h0`` None without initial states; the
+    final states' gradient ``grad_final`` ``[S, W', C]`` is optional."""
+    x, weight, grad_out = _f32(x), _f32(weight), _f32(grad_out)
+    bias = None if bias is None else _f32(bias)
+    h0 = None if h0 is None else _f32(h0)
+    grad_final = None if grad_final is None else _f32(grad_final)
+    s, cu, nseq = _conv1d(x, weight, bias, h0, cu, silu,
+                          None if grad_final is None else grad_final.shape[1])
+    gx, gw = np.zeros_like(x), np.zeros_like(weight)
+    gb = np.zeros(x.shape[2], np.float32) if bias is not None else None
+    gh = np.zeros_like(h0) if h0 is not None else None
+    rc = getattr(lib(), f"dmo_conv1d_bwd_{precision}")(
+        ctypes.byref(s), _p(x), _p(weight), _p(bias), _p(h0), _p(grad_out), _p(grad_final),
+        _p(gx), _p(gw), _p(gb), _p(gh))
+    assert rc == 0
+    return gx, gw, gb, gh
+
+
+def conv1d_update(x, weight, bias, state, silu=False, precision="f32"):
+    """One decoding step (conv1d/reference.rs:484-520): ``x`` ``[B, C]``, ``state`` ``[B, W, C]``;
+    returns ``(out [B, C], next_state [B, W, C])``."""
+    x, weight, state = _f32(x), _f32(weight), _f32(state)
+    bias = None if bias is None else _f32(bias)
+    b, c = x.shape
+    k, w = weight.shape[1], state.shape[1]
+    out, nxt = np.zeros_like(x), np.zeros_like(state)
+    f = getattr(lib(), f"dmo_conv1d_update_{precision}")
+    f.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int32] * 2 + [ctypes.c_void_p] * 6
+    rc = f(b, c, k, w, int(bias is not None), int(bool(silu)), _p(x), _p(weight), _p(bias),
+           _p(state), _p(out), _p(nxt))
+    assert rc == 0
+    return out, nxt

@@ -2,7 +2,8 @@
  *
  * TEST INFRASTRUCTURE ONLY: a plain-C restatement of dash-ops' reference implementations
  * (crates/dash-ops/src/attention/reference.rs, crates/dash-ops/src/gated_delta/chunk/reference.rs,
- * crates/dash-ops/src/gated_delta/recurrent.rs:309-404), compiled in f32 (the reference's own
+ * crates/dash-ops/src/gated_delta/recurrent.rs:309-404, crates/dash-ops/src/conv1d/reference.rs),
+ * compiled in f32 (the reference's own
  * precision, suffix _f32) and in f64 (suffix _f64). Only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg load it, as the checker and as the timed CPU baseline; the product
  * library never links it.
@@ -43,6 +44,19 @@ typedef struct {
     int32_t qk_l2norm;
     float scale;
 } dmo_gdr;
+
+/* One causal conv1d call (crates/dash-contract/src/conv1d.rs): x [B, T, C], weight [C, K],
+ * bias [C], states [S, W, C]; packed sequences over a batch of one when cu is not NULL. */
+typedef struct {
+    int64_t b, t, c, k;
+    const int64_t *cu; /* [nseq + 1] or NULL */
+    int64_t nseq;
+    int32_t has_bias, silu;
+    int32_t has_h0;    /* initial states of w steps */
+    int64_t w;
+    int32_t has_final; /* final states of w_out steps */
+    int64_t w_out;
+} dmo_conv1d;
 
 /* The sequence of `n` positions cut by `cu` [s + 1] that holds position `at`: the number of
  * ends at or before it, clamped into 0..s (reference.rs:118-159 `sequences`), and whether any
@@ -92,6 +106,7 @@ int dmo_attention_visible(const dmo_attention *a, int64_t b, int64_t i, int64_t 
 #define LOG logf
 #define SQRT sqrtf
 #include "oracle_body.h"
+#include "oracle_conv1d.h"
 #undef R
 #undef FN
 #undef EXP
@@ -104,6 +119,7 @@ int dmo_attention_visible(const dmo_attention *a, int64_t b, int64_t i, int64_t 
 #define LOG log
 #define SQRT sqrt
 #include "oracle_body.h"
+#include "oracle_conv1d.h"
 #undef R
 #undef FN
 #undef EXP
