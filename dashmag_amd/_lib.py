@@ -15,7 +15,9 @@ DM_MASK_NONE, DM_MASK_KEY_PADDING, DM_MASK_PACKED = 0, 1, 2
 DM_UNBOUNDED = (1 << 64) - 1
 
 PROBES = ["attn_fwd_mfma", "attn_fwd_generic", "attn_bwd_mfma", "attn_bwd_generic",
-          "decode_split", "decode_merge", "gdr_chunk_fwd", "gdr_chunk_bwd", "gdr_step"]
+          "decode_split", "decode_merge", "gdr_chunk_fwd", "gdr_chunk_bwd", "gdr_step",
+          "conv1d_fwd", "conv1d_bwd", "conv1d_update"]
+DM_ACT_NONE, DM_ACT_SILU = 0, 1
 
 
 class AttentionOptionsC(ctypes.Structure):
@@ -43,9 +45,19 @@ class GdrDesc(ctypes.Structure):
                 ("scale", ctypes.c_float)]
 
 
+class Conv1dDesc(ctypes.Structure):
+    _fields_ = [("b", ctypes.c_int64), ("t", ctypes.c_int64), ("c", ctypes.c_int64),
+                ("k", ctypes.c_int64), ("dtype", ctypes.c_int32),
+                ("cu_seqlens", ctypes.c_void_p), ("nseq", ctypes.c_int64),
+                ("has_bias", ctypes.c_int32), ("activation", ctypes.c_int32),
+                ("has_initial", ctypes.c_int32), ("w", ctypes.c_int64),
+                ("has_final", ctypes.c_int32), ("w_out", ctypes.c_int64)]
+
+
 #: Every symbol include/dashmi.h declares, with (restype, argtypes).
 _VP, _SZ, _I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64
 _AD, _GD = ctypes.POINTER(AttentionDesc), ctypes.POINTER(GdrDesc)
+_CD = ctypes.POINTER(Conv1dDesc)
 SIGNATURES = {
     "dm_last_error": (ctypes.c_char_p, []),
     "dm_describe": (ctypes.c_int, [ctypes.c_char_p, _SZ]),
@@ -69,6 +81,11 @@ SIGNATURES = {
     "dm_gdr_chunk_bwd_workspace": (_SZ, [_GD]),
     "dm_gdr_chunk_bwd": (ctypes.c_int, [_GD] + [_VP] * 15 + [_SZ, _VP]),
     "dm_gdr_step": (ctypes.c_int, [_GD] + [_VP] * 9),
+    "dm_causal_conv1d_fwd": (ctypes.c_int, [_CD] + [_VP] * 7),
+    "dm_causal_conv1d_bwd_workspace": (_SZ, [_CD]),
+    "dm_causal_conv1d_bwd": (ctypes.c_int, [_CD] + [_VP] * 5 + [ctypes.c_int] + [_VP] * 6
+                             + [_SZ, _VP]),
+    "dm_causal_conv1d_update": (ctypes.c_int, [_CD] + [_VP] * 7),
 }
 
 _lib = None
@@ -108,7 +125,8 @@ def probe_reset() -> None:
 
 
 KERNELS = ["attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "decode_split", "gdr_prep", "gdr_state",
-           "gdr_output", "gdr_step", "gdr_bwd_pre", "gdr_bwd_state", "gdr_bwd_grads"]
+           "gdr_output", "gdr_step", "gdr_bwd_pre", "gdr_bwd_state", "gdr_bwd_grads",
+           "conv1d_fwd", "conv1d_bwd", "conv1d_update"]
 
 
 def kernel_timing(enable: bool) -> None:

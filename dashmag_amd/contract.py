@@ -142,6 +142,43 @@ class GatedDeltaStepOptions:
         return GatedDeltaStepOptions(options.qk_l2norm, options.scale)
 
 
+class Activation(enum.Enum):
+    """crates/dash-contract/src/conv1d.rs:81-90: the conv1d's activation after the bias."""
+
+    NONE = 0
+    SILU = 1
+
+
+@dataclasses.dataclass(frozen=True)
+class CausalConv1dOptions:
+    """crates/dash-contract/src/conv1d.rs:92-126: no activation, no final state; the final
+    states' length ``None`` for the initial states' (``K - 1`` without them)."""
+
+    activation: Activation = Activation.NONE
+    output_final_state: bool = False
+    final_state_len: Optional[int] = None
+
+    def with_activation(self, activation: Activation):
+        return dataclasses.replace(self, activation=activation)
+
+    def with_final_state(self, v: bool):
+        return dataclasses.replace(self, output_final_state=v)
+
+    def with_final_state_len(self, n: int):
+        return dataclasses.replace(self, output_final_state=True, final_state_len=int(n))
+
+
+@dataclasses.dataclass(frozen=True)
+class CausalConv1dStepOptions:
+    """crates/dash-contract/src/conv1d.rs:128-140."""
+
+    activation: Activation = Activation.NONE
+
+    @staticmethod
+    def from_sequence(options: CausalConv1dOptions) -> "CausalConv1dStepOptions":
+        return CausalConv1dStepOptions(options.activation)
+
+
 def query_scale(scale: Optional[float], dk: int) -> float:
     """The gated delta rule's query scale: ``1/sqrt(Dk)`` unless given
     (crates/dash-ops/src/gated_delta.rs:17)."""

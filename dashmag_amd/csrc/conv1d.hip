@@ -1,0 +1,774 @@
+// The causal depthwise conv1d (crates/dash-contract/src/conv1d.rs; dash-ops' CausalConv1dBackend,
+// crates/dash-ops/src/conv1d.rs:198-360, kernels in conv1d/cube.rs) on gfx950: forward,
+// backward and the decoding step, bandwidth-bound elementwise work without MFMA.
+//
+// Per sequence and channel c, with h the history (the initial state's W steps, then the inputs,
+// zeros before those) and K the kernel width:
+//   y[t, c] = sum_{j < K} weight[c, j] h[t - (K - 1) + j, c] (+ bias[c]);  out = y or SiLU(y).
+//
+// Layout: x, out, gradients [B, T, C] (C fastest), weight [C, K], bias [C], states [S, W, C] f32.
+// A thread owns one 16-byte vector of channels (8 of a 16-bit dtype, 4 of f32; one channel when
+// C is not a multiple of that) over a segment of consecutive steps, holding the taps and a
+// sliding window of the last K - 1 inputs in registers, so x is read from HBM once (plus K - 1
+// steps per segment) and the output written once; consecutive threads read consecutive 16-byte
+// pieces of a row. Segments may cross sequence boundaries (packed sequences): the window is
+// refilled from the initial state, or zeros, at each sequence's first step.
+//
+// The backward sweeps each sequence's part of a segment from its last step to its first, with a
+// window of the next K - 1 steps' pre-activation gradients: the input gradient of step t is
+// sum_j weight[j] dy[t + K - 1 - j]. The weight and bias gradients are summed per thread over
+// its segment, written as per-segment partials, and summed over the segments in a fixed order by
+// a second kernel (deterministic). Kernel widths 1..8 are template parameters; wider ones (up to
+// 16) run one channel per thread with the taps right-aligned in a window of 16.
+#include <string>
+
+#include "attention_kernels.h"
+#include "mfma.h"
+
+namespace dm {
+
+constexpr int kCv1Threads = 256;
+constexpr int kCv1MaxK = 16;
+
+struct Cv1Args {
+    int64_t rows;       // B * T (a sequence per batch row) or T (packed)
+    int64_t t;          // steps per batch row
+    int64_t c, k;       // channels, kernel width
+    int64_t nseq;       // sequences S
+    const int32_t *cu;  // packed boundaries [S + 1], or null
+    int64_t w;          // initial states' steps (with has_h0)
+    int64_t w_out;      // final states' steps (with the final states)
+    int32_t has_h0, has_bias, silu;
+    int64_t seg_len;    // steps per segment
+    int64_t cv;         // channel vectors per row
+};
+
+// The sequence holding row r: s and its rows [s0, s1) (packed: the last sequence whose start is
+// at or before r with a nonempty span; empty sequences are stepped over).
+__device__ __forceinline__ void cv1_seq(const Cv1Args &a, int64_t r, int64_t *s, int64_t *s0,
+                                        int64_t *s1) {
+    if (!a.cu) {
+        *s = r / a.t;
+        *s0 = *s * a.t;
+        *s1 = *s0 + a.t;
+        return;
+    }
+    int64_t lo = 0, hi = a.nseq - 1;  // the first s with cu[s + 1] > r
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)a.cu[mid + 1] > r)
+            hi = mid;
+        else
+            lo = mid + 1;
+    }
+    *s = lo;
+    *s0 = a.cu[lo];
+    *s1 = a.cu[lo + 1];
+}
+
+__device__ __forceinline__ void cv1_next(const Cv1Args &a, int64_t *s, int64_t *s0, int64_t *s1) {
+    ++*s;
+    *s0 = *s1;
+    *s1 = a.cu ? (int64_t)a.cu[*s + 1] : *s0 + a.t;
+}
+
+// VEC consecutive elements of dtype DT at element i, as f32 (16-byte loads when VEC > 1)
+template <int DT, int VEC>
+__device__ __forceinline__ void cv1_ld(const void *p, int64_t i, float *v) {
+    if constexpr (VEC == 1) {
+        v[0] = ld<DT>(p, i);
+    } else if constexpr (DT == DM_F32) {
+#pragma unroll
+        for (int q = 0; q < VEC / 4; q++) {
+            const float4 a = *(const float4 *)((const float *)p + i + 4 * q);
+            v[4 * q] = a.x;
+            v[4 * q + 1] = a.y;
+            v[4 * q + 2] = a.z;
+            v[4 * q + 3] = a.w;
+        }
+    } else {
+        const uint4 a = *(const uint4 *)((const uint16_t *)p + i);
+        const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[2 * e] = unpack_lo<DT>(u[e]);
+            v[2 * e + 1] = unpack_hi<DT>(u[e]);
+        }
+    }
+}
+
+// the same for f32 states, VEC elements (VEC = 8 of a 16-bit dtype: two 16-byte loads)
+template <int VEC>
+__device__ __forceinline__ void cv1_ld_state(const float *p, int64_t i, float *v) {
+    if constexpr (VEC == 1)
+        v[0] = p[i];
+    else
+        cv1_ld<DM_F32, VEC>(p, i, v);
+}
+
+// VEC f32 values stored at element i in dtype DT, rounded to nearest even
+template <int DT, int VEC>
+__device__ __forceinline__ void cv1_st(void *p, int64_t i, const float *v) {
+    if constexpr (VEC == 1) {
+        st<DT>(p, i, v[0]);
+    } else if constexpr (DT == DM_F32) {
+#pragma unroll
+        for (int q = 0; q < VEC / 4; q++)
+            *(float4 *)((float *)p + i + 4 * q) =
+                make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+        *(uint4 *)((uint16_t *)p + i) =
+            make_uint4(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]), pack2<DT>(v[4], v[5]),
+                       pack2<DT>(v[6], v[7]));
+    }
+}
+
+// h[tau] of sequence s (rows [s0, ...)), channels c0 .. c0 + VEC: the inputs at tau >= 0, the
+// initial state's step W + tau for -W <= tau < 0, zeros before
+template <int DT, int VEC>
+__device__ __forceinline__ void cv1_hist(const Cv1Args &a, const void *x, const float *h0, int64_t s,
+                                         int64_t s0, int64_t tau, int64_t c0, float *v) {
+    if (tau >= 0) {
+        cv1_ld<DT, VEC>(x, (s0 + tau) * a.c + c0, v);
+    } else if (a.has_h0 && tau >= -a.w) {
+        cv1_ld_state<VEC>(h0, (s * a.w + a.w + tau) * a.c + c0, v);
+    } else {
+#pragma unroll
+        for (int e = 0; e < VEC; e++) v[e] = 0.f;
+    }
+}
+
+__device__ __forceinline__ float cv1_sigmoid(float y) { return 1.f / (1.f + expf(-y)); }
+
+// SiLU(y) = y sigmoid(y). For f32 inputs in f64, rounded once: the device's expf is about an
+// ulp off, which the f32 conformance bounds (about 1.3 ulp of the largest output) do not leave
+// room for; for 16-bit inputs the output's rounding to the dtype dominates and f32 suffices.
+template <int DT>
+__device__ __forceinline__ float cv1_silu(float y) {
+    if constexpr (DT == DM_F32) {
+        const double yd = y;
+        return (float)(yd / (1.0 + exp(-yd)));
+    } else {
+        return __fmul_rn(y, cv1_sigmoid(y));
+    }
+}
+
+// acc + a b with the product and the sum rounded separately, as the reference's tensor
+// operations round them (no fused multiply-add: the conformance bounds are about an ulp)
+__device__ __forceinline__ float cv1_madd(float acc, float a, float b) {
+    return __fadd_rn(acc, __fmul_rn(a, b));
+}
+
+// The taps as KT registers per channel: tap j of a kernel of width k < KT sits at KT - k + j, the
+// others are zero (so a window of KT steps ending at the current step applies the kernel).
+template <int DT, int VEC, int KT>
+__device__ __forceinline__ void cv1_taps(const Cv1Args &a, const void *wt, int64_t c0,
+                                         float (&wv)[KT][VEC]) {
+    const int off = KT - (int)a.k;
+#pragma unroll
+    for (int j = 0; j < KT; j++)
+#pragma unroll
+        for (int e = 0; e < VEC; e++)
+            wv[j][e] = j >= off ? ld<DT>(wt, (c0 + e) * a.k + (j - off)) : 0.f;
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward (conv1d/reference.rs:183-268)
+// ------------------------------------------------------------------------------------------
+
+template <int DT, int VEC, int KT>
+__global__ __launch_bounds__(kCv1Threads) void conv1d_fwd_kernel(Cv1Args a, const void *__restrict__ x,
+                                                                 const void *__restrict__ wt,
+                                                                 const void *__restrict__ bias,
+                                                                 const float *__restrict__ h0,
+                                                                 void *__restrict__ out) {
+    const int64_t cvi = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
+    if (cvi >= a.cv) return;
+    const int64_t c0 = cvi * VEC;
+    const int64_t r0 = (int64_t)blockIdx.y * a.seg_len;
+    const int64_t r1 = min(r0 + a.seg_len, a.rows);
+    if (r0 >= r1) return;
+    float wv[KT][VEC], bv[VEC];
+    cv1_taps<DT, VEC, KT>(a, wt, c0, wv);
+#pragma unroll
+    for (int e = 0; e < VEC; e++) bv[e] = a.has_bias ? ld<DT>(bias, c0 + e) : 0.f;
+    int64_t s, s0, s1;
+    cv1_seq(a, r0, &s, &s0, &s1);
+    for (int64_t r = r0; r < r1;) {
+        while (r >= s1) cv1_next(a, &s, &s0, &s1);
+        const int64_t pend = min(r1, s1);
+        // the KT - 1 steps before r
+        float win[KT][VEC];
+#pragma unroll
+        for (int j = 0; j < KT - 1; j++) cv1_hist<DT, VEC>(a, x, h0, s, s0, r - s0 - (KT - 1) + j, c0, win[j]);
+#pragma unroll 4
+        for (; r < pend; r++) {
+            cv1_ld<DT, VEC>(x, r * a.c + c0, win[KT - 1]);
+            float o[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; e++) {
+                // the taps in order, then the bias (reference.rs:94-105)
+                float y = 0.f;
+#pragma unroll
+                for (int j = 0; j < KT; j++) y = cv1_madd(y, wv[j][e], win[j][e]);
+                if (a.has_bias) y = __fadd_rn(y, bv[e]);
+                if (a.silu) y = cv1_silu<DT>(y);
+                o[e] = y;
+            }
+            cv1_st<DT, VEC>(out, r * a.c + c0, o);
+#pragma unroll
+            for (int j = 0; j < KT - 1; j++)
+#pragma unroll
+                for (int e = 0; e < VEC; e++) win[j][e] = win[j + 1][e];
+        }
+    }
+}
+
+// The final states: the last W' steps of each sequence's history, zeros in front where it is
+// shorter (reference.rs:183-197). One thread per (sequence, step, channel).
+template <int DT>
+__global__ __launch_bounds__(kCv1Threads) void conv1d_final_kernel(Cv1Args a, const void *__restrict__ x,
+                                                                   const float *__restrict__ h0,
+                                                                   float *__restrict__ fin) {
+    const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
+    const int64_t item = blockIdx.x / cb;
+    const int64_t c = (blockIdx.x % cb) * kCv1Threads + threadIdx.x;
+    if (c >= a.c) return;
+    const int64_t s = item / a.w_out, i = item % a.w_out;
+    int64_t s0, len;
+    if (a.cu) {
+        s0 = a.cu[s];
+        len = a.cu[s + 1] - s0;
+    } else {
+        s0 = s * a.t;
+        len = a.t;
+    }
+    const int64_t wh = a.has_h0 ? a.w : 0;
+    const int64_t hstep = wh + len - a.w_out + i;  // step of the history, from its first
+    float v = 0.f;
+    if (hstep >= wh)
+        v = ld<DT>(x, (s0 + hstep - wh) * a.c + c);
+    else if (hstep >= 0)
+        v = h0[(s * a.w + hstep) * a.c + c];
+    fin[(s * a.w_out + i) * a.c + c] = v;
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward (conv1d/reference.rs:270-482)
+// ------------------------------------------------------------------------------------------
+
+// dy = go SiLU'(y), SiLU'(y) = s (y (1 - s) + 1) with s = sigmoid(y) (reference.rs:117-134);
+// in f64 for f32 inputs, as the forward's SiLU
+template <int DT>
+__device__ __forceinline__ float cv1_dy(float g, float y, int silu) {
+    if (!silu) return g;
+    if constexpr (DT == DM_F32) {
+        const double yd = y, sg = 1.0 / (1.0 + exp(-yd));
+        return (float)((double)g * (sg * (yd * (1.0 - sg) + 1.0)));
+    } else {
+        const float sg = cv1_sigmoid(y);
+        return __fmul_rn(g, __fmul_rn(sg, __fadd_rn(__fmul_rn(y, __fsub_rn(1.f, sg)), 1.f)));
+    }
+}
+
+template <int DT, int GT, int VEC, int KT>
+__global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
+    Cv1Args a, const void *__restrict__ x, const void *__restrict__ wt, const void *__restrict__ bias,
+    const float *__restrict__ h0, const void *__restrict__ go, const float *__restrict__ gfin,
+    void *__restrict__ gx, float *__restrict__ part) {
+    const int64_t cvi = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
+    if (cvi >= a.cv) return;
+    const int64_t c0 = cvi * VEC;
+    const int64_t seg = blockIdx.y;
+    const int64_t r0 = seg * a.seg_len;
+    const int64_t r1 = min(r0 + a.seg_len, a.rows);
+    float wv[KT][VEC], bv[VEC];
+    cv1_taps<DT, VEC, KT>(a, wt, c0, wv);
+#pragma unroll
+    for (int e = 0; e < VEC; e++) bv[e] = a.has_bias ? ld<DT>(bias, c0 + e) : 0.f;
+    float aw[KT][VEC], ab[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; e++) {
+        ab[e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < KT; j++) aw[j][e] = 0.f;
+    }
+    const int64_t wh = a.has_h0 ? a.w : 0;
+    // the pre-activation gradient of step tau of sequence s from its window
+    auto dy_at = [&](int64_t s, int64_t s0, int64_t tau, const float (&xw)[KT][VEC], float *d) {
+        float g[VEC];
+        cv1_ld<GT, VEC>(go, (s0 + tau) * a.c + c0, g);
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            float y = 0.f;
+#pragma unroll
+            for (int j = 0; j < KT; j++) y = cv1_madd(y, wv[j][e], xw[j][e]);
+            if (a.has_bias) y = __fadd_rn(y, bv[e]);
+            d[e] = cv1_dy<DT>(g[e], y, a.silu);
+        }
+    };
+    if (r0 < r1) {
+        int64_t s, s0, s1;
+        cv1_seq(a, r0, &s, &s0, &s1);
+        for (int64_t r = r0; r < r1;) {
+            while (r >= s1) cv1_next(a, &s, &s0, &s1);
+            const int64_t p0 = r, p1 = min(r1, s1), len = s1 - s0;
+            // the pre-activation gradients of the KT - 1 steps after the piece (zero past the
+            // sequence): gwin[i] holds step p1 + i
+            float gwin[KT][VEC];
+#pragma unroll
+            for (int i = 0; i < KT - 1; i++) {
+                const int64_t tau = p1 - s0 + i;
+                if (tau < len) {
+                    float xw[KT][VEC];
+#pragma unroll
+                    for (int j = 0; j < KT; j++) cv1_hist<DT, VEC>(a, x, h0, s, s0, tau - (KT - 1) + j, c0, xw[j]);
+                    dy_at(s, s0, tau, xw, gwin[i]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VEC; e++) gwin[i][e] = 0.f;
+                }
+            }
+            // the inputs' window of the piece's last step: xw[j] = h[t - (KT - 1) + j]
+            float xw[KT][VEC];
+#pragma unroll
+            for (int j = 0; j < KT; j++) cv1_hist<DT, VEC>(a, x, h0, s, s0, p1 - 1 - s0 - (KT - 1) + j, c0, xw[j]);
+            const int64_t P = wh + len;
+            for (int64_t t = p1 - 1; t >= p0; t--) {
+                float d[VEC];
+                dy_at(s, s0, t - s0, xw, d);
+                // dx[t] = sum_j weight[j] dy[t + K - 1 - j], the taps in order (:296-316): with
+                // the taps right-aligned at KT, tap slot j reads dy[t + KT - 1 - j], which is d
+                // for j = KT - 1 and gwin[KT - 2 - j] before
+                float o[VEC];
+#pragma unroll
+                for (int e = 0; e < VEC; e++) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int j = 0; j < KT; j++) {
+                        if (j < KT - (int)a.k) continue;  // (zero taps)
+                        const float dj = j == KT - 1 ? d[e] : gwin[KT - 2 - j][e];
+                        acc = cv1_madd(acc, wv[j][e], dj);
+                    }
+                    o[e] = acc;
+                }
+                // the final states' gradient onto the inputs among the history's last W' steps
+                if (gfin) {
+                    const int64_t idx = wh + (t - s0) - (P - a.w_out);
+                    if (idx >= 0) {
+                        float f[VEC];
+                        cv1_ld_state<VEC>(gfin, (s * a.w_out + idx) * a.c + c0, f);
+#pragma unroll
+                        for (int e = 0; e < VEC; e++) o[e] = __fadd_rn(o[e], f[e]);
+                    }
+                }
+                cv1_st<DT, VEC>(gx, t * a.c + c0, o);
+#pragma unroll
+                for (int e = 0; e < VEC; e++) {
+                    ab[e] = __fadd_rn(ab[e], d[e]);
+#pragma unroll
+                    for (int j = 0; j < KT; j++) aw[j][e] = cv1_madd(aw[j][e], d[e], xw[j][e]);
+                }
+                // slide both windows one step back
+#pragma unroll
+                for (int i = KT - 2; i > 0; i--)
+#pragma unroll
+                    for (int e = 0; e < VEC; e++) gwin[i][e] = gwin[i - 1][e];
+#pragma unroll
+                for (int e = 0; e < VEC; e++) gwin[0][e] = d[e];
+#pragma unroll
+                for (int j = KT - 1; j > 0; j--)
+#pragma unroll
+                    for (int e = 0; e < VEC; e++) xw[j][e] = xw[j - 1][e];
+                if (t > p0) cv1_hist<DT, VEC>(a, x, h0, s, s0, t - 1 - s0 - (KT - 1), c0, xw[0]);
+            }
+            r = p1;
+        }
+    }
+    // this segment's partial sums of the weight's and the bias's gradients: [seg][C][K + 1]
+    const int off = KT - (int)a.k;
+#pragma unroll
+    for (int e = 0; e < VEC; e++) {
+        float *pp = part + (seg * a.c + c0 + e) * (a.k + 1);
+#pragma unroll
+        for (int j = 0; j < KT; j++)
+            if (j >= off) pp[j - off] = aw[j][e];
+        pp[a.k] = ab[e];
+    }
+}
+
+// The weight's and the bias's gradients: the segments' partials summed in segment order.
+template <int DT>
+__global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_reduce(int64_t nseg, int64_t C, int64_t K,
+                                                                 const float *__restrict__ part,
+                                                                 void *__restrict__ gw,
+                                                                 void *__restrict__ gb) {
+    const int64_t i = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
+    if (i >= C * (K + 1)) return;
+    float acc = 0.f;
+    for (int64_t g = 0; g < nseg; g++) acc = __fadd_rn(acc, part[g * C * (K + 1) + i]);
+    const int64_t c = i / (K + 1), j = i % (K + 1);
+    if (j < K)
+        st<DT>(gw, c * K + j, acc);
+    else if (gb)
+        st<DT>(gb, c, acc);
+}
+
+// The initial states' gradient: per (sequence, channel), the padded steps before the first step
+// take sum_j weight[j] dy[q - j] (reference.rs:318-325), the state's earlier steps zero, then the
+// final states' gradient where the history is short enough to keep state steps (:342-373). A few
+// steps per sequence: computed in f64 and rounded once (f32 leaves it about an ulp off, the width
+// of its conformance bound).
+template <int DT, int GT>
+__global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_h0_kernel(
+    Cv1Args a, const void *__restrict__ x, const void *__restrict__ wt, const void *__restrict__ bias,
+    const float *__restrict__ h0, const void *__restrict__ go, const float *__restrict__ gfin,
+    float *__restrict__ gh0) {
+    const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
+    const int64_t s = blockIdx.x / cb;
+    const int64_t c = (blockIdx.x % cb) * kCv1Threads + threadIdx.x;
+    if (c >= a.c) return;
+    int64_t s0, len;
+    if (a.cu) {
+        s0 = a.cu[s];
+        len = a.cu[s + 1] - s0;
+    } else {
+        s0 = s * a.t;
+        len = a.t;
+    }
+    const int64_t K = a.k, W = a.w;
+    const double b = a.has_bias ? (double)ld<DT>(bias, c) : 0.0;
+    auto hist = [&](int64_t tau) -> double {
+        if (tau >= 0) return ld<DT>(x, (s0 + tau) * a.c + c);
+        if (tau >= -W) return h0[(s * W + W + tau) * a.c + c];
+        return 0.0;
+    };
+    auto dy = [&](int64_t t) -> double {
+        double y = 0.0;
+        for (int64_t j = 0; j < K; j++) y += (double)ld<DT>(wt, c * K + j) * hist(t - (K - 1) + j);
+        y += b;
+        const double g = ld<GT>(go, (s0 + t) * a.c + c);
+        if (!a.silu) return g;
+        const double sg = 1.0 / (1.0 + exp(-y));
+        return g * (sg * (y * (1.0 - sg) + 1.0));
+    };
+    const int64_t P = W + len;
+    for (int64_t i = 0; i < W; i++) {
+        double g = 0.0;
+        const int64_t q = i - (W - (K - 1));  // padded step before the first
+        if (q >= 0)
+            for (int64_t j = 0; j < K; j++) {
+                const int64_t t = q - j;
+                if (t >= 0 && t < len) g += (double)ld<DT>(wt, c * K + j) * dy(t);
+            }
+        if (gfin) {
+            const int64_t idx = i - (P - a.w_out);
+            if (idx >= 0) g += gfin[(s * a.w_out + idx) * a.c + c];
+        }
+        gh0[(s * W + i) * a.c + c] = (float)g;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// The decoding step (conv1d/reference.rs:484-520)
+// ------------------------------------------------------------------------------------------
+
+// One thread per (row, channel): the state's last K - 1 steps and the token through the taps;
+// the next state is the state without its oldest step, then the token (written in ascending
+// step order after every read, so it may overwrite the state in place).
+template <int DT>
+__global__ __launch_bounds__(kCv1Threads) void conv1d_update_kernel(
+    int64_t B, int64_t C, int64_t K, int64_t W, int has_bias, int silu, const void *__restrict__ x,
+    const void *__restrict__ wt, const void *__restrict__ bias, const float *state, void *__restrict__ out,
+    float *next) {
+    const int64_t i = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
+    if (i >= B * C) return;
+    const int64_t b = i / C, c = i % C;
+    const float xv = ld<DT>(x, i);
+    float y = 0.f;
+    for (int64_t j = 0; j < K; j++) {
+        const float v = j < K - 1 ? state[(b * W + W - (K - 1) + j) * C + c] : xv;
+        y = cv1_madd(y, v, ld<DT>(wt, c * K + j));
+    }
+    if (has_bias) y = __fadd_rn(y, ld<DT>(bias, c));
+    if (silu) y = cv1_silu<DT>(y);
+    st<DT>(out, i, y);
+    for (int64_t s = 0; s < W; s++)
+        next[(b * W + s) * C + c] = s + 1 < W ? state[(b * W + s + 1) * C + c] : xv;
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------
+
+static int cv1_check(const dm_conv1d_desc *d, const char *op, bool step) {
+    const std::string o(op);
+    if (!d) return refuse(o + ": null descriptor");
+    if (d->dtype != DM_F32 && d->dtype != DM_BF16 && d->dtype != DM_F16)
+        return refuse(o + ": the dtype must be f32, bf16 or f16");
+    if (d->k < 1) return refuse(o + ": the kernel width must be at least 1");
+    if (d->k > kCv1MaxK)
+        return refuse(o + ": kernel widths above " + std::to_string(kCv1MaxK) +
+                      " are not implemented, got " + std::to_string(d->k));
+    if (d->b < 0 || d->t < 0 || d->c < 0) return refuse(o + ": negative dimensions");
+    if (d->activation != DM_ACT_NONE && d->activation != DM_ACT_SILU)
+        return refuse(o + ": activation " + std::to_string(d->activation) + " is not implemented");
+    if (step) {
+        if (d->w + 1 < d->k)
+            return refuse(o + ": a state of " + std::to_string(d->w) +
+                          " steps cannot feed a kernel of width " + std::to_string(d->k) +
+                          "; it needs at least " + std::to_string(d->k - 1));
+        return DM_OK;
+    }
+    if (d->cu_seqlens) {
+        if (d->b != 1)
+            return refuse(o + ": packed sequences lie along T of a batch of one, got B = " +
+                          std::to_string(d->b));
+        if (d->nseq < 1) return refuse(o + ": cu_seqlens must hold N + 1 >= 2 offsets");
+    }
+    if (d->has_initial && d->w + 1 < d->k)
+        return refuse(o + ": a initial state of " + std::to_string(d->w) +
+                      " steps cannot feed a kernel of width " + std::to_string(d->k) +
+                      "; it needs at least " + std::to_string(d->k - 1));
+    if (d->has_final && d->w_out < 0) return refuse(o + ": negative final state length");
+    return DM_OK;
+}
+
+static int64_t cv1_nseq(const dm_conv1d_desc *d) { return d->cu_seqlens ? d->nseq : d->b; }
+
+// the vector width (channels per thread) a call takes: 16 bytes of channels when C divides
+static int cv1_vec(const dm_conv1d_desc *d) {
+    const int v = d->dtype == DM_F32 ? 4 : 8;
+    // (widths above 8 run one channel per thread)
+    return d->c % v == 0 && d->k <= 8 ? v : 1;
+}
+
+static Cv1Args cv1_args(const dm_conv1d_desc *d) {
+    Cv1Args a{};
+    a.rows = d->cu_seqlens ? d->t : d->b * d->t;
+    a.t = d->t;
+    a.c = d->c;
+    a.k = d->k;
+    a.nseq = cv1_nseq(d);
+    a.cu = d->cu_seqlens;
+    a.w = d->has_initial ? d->w : 0;
+    a.w_out = d->has_final ? d->w_out : 0;
+    a.has_h0 = d->has_initial ? 1 : 0;
+    a.has_bias = d->has_bias ? 1 : 0;
+    a.silu = d->activation == DM_ACT_SILU ? 1 : 0;
+    const int vec = cv1_vec(d);
+    a.cv = (d->c + vec - 1) / vec;
+    // segments: about 256K threads in all, each segment at least 16 steps, at most 256 segments
+    int64_t nseg = (256 * 1024 + a.cv - 1) / std::max<int64_t>(a.cv, 1);
+    nseg = std::min<int64_t>(nseg, 256);
+    nseg = std::min<int64_t>(nseg, (a.rows + 15) / 16);
+    nseg = std::max<int64_t>(nseg, 1);
+    a.seg_len = (a.rows + nseg - 1) / nseg;
+    return a;
+}
+
+static int64_t cv1_nseg(const Cv1Args &a) { return a.rows ? (a.rows + a.seg_len - 1) / a.seg_len : 0; }
+
+// kernel width -> template instance: 1..8 exactly, wider ones in a window of 16
+#define CV1_K_SWITCH(K, MACRO, ...)        \
+    switch (K) {                           \
+        case 1: MACRO(1, __VA_ARGS__); break; \
+        case 2: MACRO(2, __VA_ARGS__); break; \
+        case 3: MACRO(3, __VA_ARGS__); break; \
+        case 4: MACRO(4, __VA_ARGS__); break; \
+        case 5: MACRO(5, __VA_ARGS__); break; \
+        case 6: MACRO(6, __VA_ARGS__); break; \
+        case 7: MACRO(7, __VA_ARGS__); break; \
+        case 8: MACRO(8, __VA_ARGS__); break; \
+        default: MACRO(16, __VA_ARGS__); break; \
+    }
+
+template <int DT>
+static void cv1_fwd_launch(const Cv1Args &a, int vec, const void *x, const void *w, const void *bias,
+                           const float *h0, void *out, hipStream_t st) {
+    const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)cv1_nseg(a));
+    constexpr int V = DT == DM_F32 ? 4 : 8;
+#define CV1_FWD(KT, VV) conv1d_fwd_kernel<DT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, out)
+    if (vec == V && a.k <= 8) {
+        CV1_K_SWITCH(a.k, CV1_FWD, V)
+    } else {
+        CV1_K_SWITCH(a.k, CV1_FWD, 1)
+    }
+#undef CV1_FWD
+}
+
+template <int DT, int GT>
+static void cv1_bwd_launch(const Cv1Args &a, int vec, const void *x, const void *w, const void *bias,
+                           const float *h0, const void *go, const float *gfin, void *gx, float *part,
+                           hipStream_t st) {
+    const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)cv1_nseg(a));
+    constexpr int V = DT == DM_F32 ? 4 : 8;
+#define CV1_BWD(KT, VV) \
+    conv1d_bwd_kernel<DT, GT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, go, gfin, gx, part)
+    if (vec == V && a.k <= 8) {
+        CV1_K_SWITCH(a.k, CV1_BWD, V)
+    } else {
+        CV1_K_SWITCH(a.k, CV1_BWD, 1)
+    }
+#undef CV1_BWD
+}
+
+}  // namespace dm
+
+using namespace dm;
+
+extern "C" {
+
+int dm_causal_conv1d_fwd(const dm_conv1d_desc *d, const void *x, const void *weight,
+                         const void *bias, const float *initial_state, void *out,
+                         float *final_state, void *stream) {
+    const char *op = "causal_conv1d";
+    if (int rc = cv1_check(d, op, false)) return rc;
+    if (d->has_bias && !bias) return refuse(std::string(op) + ": has_bias without a bias");
+    if (d->has_initial && !initial_state)
+        return refuse(std::string(op) + ": has_initial without initial states");
+    if (d->has_final && !final_state)
+        return refuse(std::string(op) + ": has_final without a final state buffer");
+    hipStream_t st = (hipStream_t)stream;
+    const Cv1Args a = cv1_args(d);
+    const int vec = cv1_vec(d);
+    {
+        KernelTimer timer(DM_KERNEL_CONV1D_FWD, st);
+        if (a.rows > 0 && a.c > 0) {
+            if (d->dtype == DM_F32)
+                cv1_fwd_launch<DM_F32>(a, vec, x, weight, bias, initial_state, out, st);
+            else if (d->dtype == DM_BF16)
+                cv1_fwd_launch<DM_BF16>(a, vec, x, weight, bias, initial_state, out, st);
+            else
+                cv1_fwd_launch<DM_F16>(a, vec, x, weight, bias, initial_state, out, st);
+        }
+    }
+    if (d->has_final && a.w_out > 0 && a.nseq > 0 && a.c > 0) {
+        const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
+        const unsigned blocks = (unsigned)(a.nseq * a.w_out * cb);
+        if (d->dtype == DM_F32)
+            conv1d_final_kernel<DM_F32><<<blocks, kCv1Threads, 0, st>>>(a, x, initial_state, final_state);
+        else if (d->dtype == DM_BF16)
+            conv1d_final_kernel<DM_BF16><<<blocks, kCv1Threads, 0, st>>>(a, x, initial_state, final_state);
+        else
+            conv1d_final_kernel<DM_F16><<<blocks, kCv1Threads, 0, st>>>(a, x, initial_state, final_state);
+    }
+    probe_add(DM_PROBE_CONV1D_FWD);
+    DM_LAUNCH_CHECK("causal_conv1d: launch");
+    return DM_OK;
+}
+
+size_t dm_causal_conv1d_bwd_workspace(const dm_conv1d_desc *d) {
+    if (!d || d->k < 1 || d->c < 0) return 0;
+    const Cv1Args a = cv1_args(d);
+    return align_up((size_t)std::max<int64_t>(cv1_nseg(a), 1) * (size_t)d->c * (size_t)(d->k + 1) *
+                    sizeof(float));
+}
+
+int dm_causal_conv1d_bwd(const dm_conv1d_desc *d, const void *x, const void *weight,
+                         const void *bias, const float *initial_state, const void *grad_out,
+                         int grad_out_dtype, const float *grad_final_state, void *grad_x,
+                         void *grad_weight, void *grad_bias, float *grad_initial_state,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    const char *op = "causal_conv1d_backward";
+    if (int rc = cv1_check(d, op, false)) return rc;
+    if (grad_out_dtype != DM_F32 && grad_out_dtype != d->dtype)
+        return refuse(std::string(op) + ": the output's gradient is f32 or the inputs' dtype");
+    if (d->has_bias && (!bias || !grad_bias))
+        return refuse(std::string(op) + ": has_bias without the bias or its gradient");
+    if (d->has_initial && (!initial_state || !grad_initial_state))
+        return refuse(std::string(op) + ": has_initial without the states or their gradient");
+    if (workspace_bytes < dm_causal_conv1d_bwd_workspace(d))
+        return refuse(std::string(op) +
+                      ": the workspace is smaller than dm_causal_conv1d_bwd_workspace");
+    hipStream_t st = (hipStream_t)stream;
+    const Cv1Args a = cv1_args(d);
+    const int vec = cv1_vec(d);
+    const float *gfin = d->has_final && a.w_out > 0 ? grad_final_state : nullptr;
+    float *part = (float *)workspace;
+    const int64_t nseg = cv1_nseg(a);
+    {
+        KernelTimer timer(DM_KERNEL_CONV1D_BWD, st);
+        if (a.c > 0 && nseg > 0) {
+#define CV1_BWD_DT(DT)                                                                               \
+    if (grad_out_dtype == DM_F32)                                                                    \
+        cv1_bwd_launch<DT, DM_F32>(a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, st); \
+    else                                                                                             \
+        cv1_bwd_launch<DT, DT>(a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, st)
+            if (d->dtype == DM_F32) {
+                cv1_bwd_launch<DM_F32, DM_F32>(a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, st);
+            } else if (d->dtype == DM_BF16) {
+                CV1_BWD_DT(DM_BF16);
+            } else {
+                CV1_BWD_DT(DM_F16);
+            }
+#undef CV1_BWD_DT
+        }
+    }
+    if (a.c > 0) {
+        const int64_t n = a.c * (a.k + 1);
+        const unsigned blocks = (unsigned)((n + kCv1Threads - 1) / kCv1Threads);
+        void *gb = d->has_bias ? grad_bias : nullptr;
+        if (nseg == 0) {
+            // no steps at all: the weight's and the bias's gradients are zero
+            fill_zero(grad_weight, (size_t)(a.c * a.k) * dtype_bytes(d->dtype), st);
+            if (gb) fill_zero(gb, (size_t)a.c * dtype_bytes(d->dtype), st);
+        } else if (d->dtype == DM_F32) {
+            conv1d_bwd_reduce<DM_F32><<<blocks, kCv1Threads, 0, st>>>(nseg, a.c, a.k, part, grad_weight, gb);
+        } else if (d->dtype == DM_BF16) {
+            conv1d_bwd_reduce<DM_BF16><<<blocks, kCv1Threads, 0, st>>>(nseg, a.c, a.k, part, grad_weight, gb);
+        } else {
+            conv1d_bwd_reduce<DM_F16><<<blocks, kCv1Threads, 0, st>>>(nseg, a.c, a.k, part, grad_weight, gb);
+        }
+    }
+    if (d->has_initial && a.w > 0 && a.nseq > 0 && a.c > 0) {
+        const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
+        const unsigned blocks = (unsigned)(a.nseq * cb);
+#define CV1_H0(DT, GT)                                                                             \
+    conv1d_bwd_h0_kernel<DT, GT><<<blocks, kCv1Threads, 0, st>>>(a, x, weight, bias, initial_state, \
+                                                                 grad_out, gfin, grad_initial_state)
+        if (d->dtype == DM_F32) {
+            CV1_H0(DM_F32, DM_F32);
+        } else if (d->dtype == DM_BF16) {
+            if (grad_out_dtype == DM_F32) { CV1_H0(DM_BF16, DM_F32); } else { CV1_H0(DM_BF16, DM_BF16); }
+        } else {
+            if (grad_out_dtype == DM_F32) { CV1_H0(DM_F16, DM_F32); } else { CV1_H0(DM_F16, DM_F16); }
+        }
+#undef CV1_H0
+    }
+    probe_add(DM_PROBE_CONV1D_BWD);
+    DM_LAUNCH_CHECK("causal_conv1d_backward: launch");
+    return DM_OK;
+}
+
+int dm_causal_conv1d_update(const dm_conv1d_desc *d, const void *x, const void *weight,
+                            const void *bias, const float *state, void *out, float *next_state,
+                            void *stream) {
+    const char *op = "causal_conv1d_update";
+    if (int rc = cv1_check(d, op, true)) return rc;
+    if (d->has_bias && !bias) return refuse(std::string(op) + ": has_bias without a bias");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t n = d->b * d->c;
+    if (n > 0) {
+        KernelTimer timer(DM_KERNEL_CONV1D_UPDATE, st);
+        const unsigned blocks = (unsigned)((n + kCv1Threads - 1) / kCv1Threads);
+        const int silu = d->activation == DM_ACT_SILU;
+#define CV1_UPD(DT)                                                                                \
+    conv1d_update_kernel<DT><<<blocks, kCv1Threads, 0, st>>>(d->b, d->c, d->k, d->w, d->has_bias, \
+                                                             silu, x, weight, bias, state, out,   \
+                                                             next_state)
+        if (d->dtype == DM_F32) {
+            CV1_UPD(DM_F32);
+        } else if (d->dtype == DM_BF16) {
+            CV1_UPD(DM_BF16);
+        } else {
+            CV1_UPD(DM_F16);
+        }
+#undef CV1_UPD
+    }
+    probe_add(DM_PROBE_CONV1D_UPDATE);
+    DM_LAUNCH_CHECK("causal_conv1d_update: launch");
+    return DM_OK;
+}
+
+}  // extern "C"

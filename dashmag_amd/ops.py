@@ -17,8 +17,9 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .contract import (AttentionMask, AttentionOptions, ChunkGatedDeltaOptions,
-                       GatedDeltaStepOptions, UNBOUNDED, Unsupported)
+from .contract import (Activation, AttentionMask, AttentionOptions, CausalConv1dOptions,
+                       CausalConv1dStepOptions, ChunkGatedDeltaOptions, GatedDeltaStepOptions,
+                       UNBOUNDED, Unsupported)
 
 _DT = {torch.float32: _lib.DM_F32, torch.bfloat16: _lib.DM_BF16, torch.float16: _lib.DM_F16}
 
@@ -345,4 +346,164 @@ def gated_delta_step(q, k, v, g, beta, state, cu_seqlens=None,
     _check(op, _lib.lib().dm_gdr_step(ctypes.byref(desc), _ptr(qc), _ptr(kc), _ptr(vc),
                                       _ptr(gc), _ptr(bc), _ptr(st_in), _ptr(st_out), _ptr(out),
                                       _stream()))
+    return out, st_out
+
+
+# ------------------------------------------------------------------------------------------
+# Causal conv1d
+# ------------------------------------------------------------------------------------------
+
+def _conv1d_desc(op, x, weight, bias, states, cu_seqlens, activation, keep):
+    """The descriptor of a call, after dash-ops' checks (conv1d.rs:774-820): ``x`` ``[B, T, C]``
+    (or ``[B, C]`` for the step), ``weight`` ``[C, K]``, ``bias`` ``[C]``, states ``[S, W, C]``
+    f32; the refusals raise :class:`Unsupported` with dash-ops' messages."""
+    if x.dim() not in (2, 3):
+        raise Unsupported(f"{op}: x must be [B, T, C] (or [B, C] for a step)")
+    c = x.shape[-1]
+    if weight.dim() != 2:
+        raise Unsupported(f"{op}: weight must be [C, K]")
+    wc, k = weight.shape
+    if k < 1:
+        raise Unsupported(f"{op}: the kernel width must be at least 1")
+    if wc != c:
+        raise Unsupported(f"{op}: x has {c} channels, weight [C, K] has {wc}")
+    if weight.dtype != x.dtype:
+        raise Unsupported(f"{op}: x and weight must share one dtype")
+    if bias is not None:
+        if tuple(bias.shape) != (c,):
+            raise Unsupported(f"{op}: x has {c} channels, bias [C] has {tuple(bias.shape)}")
+        if bias.dtype != x.dtype:
+            raise Unsupported(f"{op}: x and bias must share one dtype")
+    if activation not in (Activation.NONE, Activation.SILU):
+        raise Unsupported(f"{op}: activation {activation} is not implemented")
+    desc = _lib.Conv1dDesc()
+    desc.dtype = _dtype(op, x)
+    desc.c, desc.k = c, k
+    desc.has_bias = int(bias is not None)
+    desc.activation = _lib.DM_ACT_SILU if activation == Activation.SILU else _lib.DM_ACT_NONE
+    if x.dim() == 3:
+        desc.b, desc.t = x.shape[0], x.shape[1]
+    else:
+        desc.b, desc.t = x.shape[0], 1
+    nseq = desc.b
+    if cu_seqlens is not None:
+        if x.shape[0] != 1:
+            raise Unsupported(f"{op}: packed sequences lie along T of a batch of one, "
+                              f"got B = {x.shape[0]}")
+        cu = _offsets(cu_seqlens, x.device)
+        if cu.numel() < 2:
+            raise Unsupported(f"{op}: cu_seqlens must hold N + 1 >= 2 offsets, got {cu.numel()}")
+        keep.append(cu)
+        desc.cu_seqlens = cu.data_ptr()
+        desc.nseq = nseq = cu.numel() - 1
+    for what, st in states:
+        if st is None:
+            continue
+        if st.dim() != 3 or st.shape[0] != nseq or st.shape[2] != c:
+            raise Unsupported(f"{op}: the {what} {list(st.shape)} must be [S, W, C] with "
+                              f"S = {nseq} sequences and C = {c} channels")
+        if st.shape[1] + 1 < k:
+            raise Unsupported(f"{op}: a {what} of {st.shape[1]} steps cannot feed a kernel of "
+                              f"width {k}; it needs at least {k - 1}")
+        if st.dtype != torch.float32:
+            raise Unsupported(f"{op}: the {what} is f32")
+    return desc, nseq
+
+
+def causal_conv1d(x, weight, bias=None, initial_state=None, cu_seqlens=None,
+                  options: Optional[CausalConv1dOptions] = None):
+    """The causal depthwise conv1d (dash-ops conv1d.rs:690, contract conv1d.rs:1-79): ``x``
+    ``[B, T, C]``, ``weight`` ``[C, K]``, ``bias`` ``[C]``, ``initial_state`` ``[S, W, C]`` f32;
+    returns ``(out [B, T, C] in x's dtype, final states [S, W', C] f32 or None)``."""
+    op = "causal_conv1d"
+    options = options or CausalConv1dOptions()
+    _device(op, x, weight, bias, initial_state)
+    keep = []
+    desc, nseq = _conv1d_desc(op, x, weight, bias, [("initial state", initial_state)],
+                              cu_seqlens, options.activation, keep)
+    if initial_state is not None:
+        desc.has_initial, desc.w = 1, initial_state.shape[1]
+    fin = None
+    if options.output_final_state:
+        if options.final_state_len is not None:
+            w_out = options.final_state_len
+        else:
+            w_out = initial_state.shape[1] if initial_state is not None else desc.k - 1
+        desc.has_final, desc.w_out = 1, int(w_out)
+        fin = torch.empty((nseq, int(w_out), desc.c), dtype=torch.float32, device=x.device)
+    xc, wc = x.contiguous(), weight.contiguous()
+    bc = None if bias is None else bias.contiguous()
+    h0 = None if initial_state is None else initial_state.contiguous()
+    out = torch.empty_like(xc)
+    _check(op, _lib.lib().dm_causal_conv1d_fwd(ctypes.byref(desc), _ptr(xc), _ptr(wc), _ptr(bc),
+                                               _ptr(h0), _ptr(out), _ptr(fin), _stream()))
+    return out, fin
+
+
+def causal_conv1d_backward(x, weight, bias, initial_state, cu_seqlens, grad_out,
+                           grad_final_state=None, options: Optional[CausalConv1dOptions] = None):
+    """The conv1d's gradients (CausalConv1dBackend::causal_conv1d_backward, conv1d.rs:300-329),
+    from the output's (``grad_out``, f32 or x's dtype) and the final states' (``[S, W', C]`` f32,
+    or None): ``(grad_x, grad_weight, grad_bias or None, grad_initial_state or None)``."""
+    op = "causal_conv1d_backward"
+    options = options or CausalConv1dOptions()
+    _device(op, x, weight, bias, initial_state, grad_out, grad_final_state)
+    keep = []
+    desc, nseq = _conv1d_desc(op, x, weight, bias, [("initial state", initial_state)],
+                              cu_seqlens, options.activation, keep)
+    if tuple(grad_out.shape) != tuple(x.shape):
+        raise Unsupported(f"{op}: the output's gradient must be shaped as x")
+    if grad_out.dtype not in (torch.float32, x.dtype):
+        raise Unsupported(f"{op}: the output's gradient is f32 or x's dtype")
+    if initial_state is not None:
+        desc.has_initial, desc.w = 1, initial_state.shape[1]
+    if grad_final_state is not None:
+        if (grad_final_state.dim() != 3 or grad_final_state.shape[0] != nseq
+                or grad_final_state.shape[2] != desc.c
+                or grad_final_state.dtype != torch.float32):
+            raise Unsupported(f"{op}: the final states' gradient must be [S, W', C] f32")
+        desc.has_final, desc.w_out = 1, grad_final_state.shape[1]
+    xc, wc, gc = x.contiguous(), weight.contiguous(), grad_out.contiguous()
+    bc = None if bias is None else bias.contiguous()
+    h0 = None if initial_state is None else initial_state.contiguous()
+    gf = None if grad_final_state is None else grad_final_state.contiguous()
+    gx, gw = torch.empty_like(xc), torch.empty_like(wc)
+    gb = None if bias is None else torch.empty_like(bc)
+    gh = None if initial_state is None else torch.empty_like(h0)
+    ws = _workspace(_lib.lib().dm_causal_conv1d_bwd_workspace(ctypes.byref(desc)), x.device)
+    _check(op, _lib.lib().dm_causal_conv1d_bwd(
+        ctypes.byref(desc), _ptr(xc), _ptr(wc), _ptr(bc), _ptr(h0), _ptr(gc),
+        _DT[grad_out.dtype], _ptr(gf), _ptr(gx), _ptr(gw), _ptr(gb), _ptr(gh), _ptr(ws),
+        ws.numel(), _stream()))
+    return gx, gw, gb, gh
+
+
+def causal_conv1d_update(x, weight, bias, state,
+                         options: Optional[CausalConv1dStepOptions] = None,
+                         in_place: bool = False):
+    """One decoding step (conv1d.rs:750): ``x`` ``[B, C]``, ``state`` ``[B, W, C]`` f32 to
+    ``(out [B, C] in x's dtype, next state [B, W, C] f32)``; with ``in_place`` the next state is
+    written over ``state`` (which must be contiguous)."""
+    op = "causal_conv1d_update"
+    options = options or CausalConv1dStepOptions()
+    _device(op, x, weight, bias, state)
+    keep = []
+    if x.dim() != 2:
+        raise Unsupported(f"{op}: x must be [B, C]")
+    desc, _ = _conv1d_desc(op, x, weight, bias, [("state", state)], None, options.activation,
+                           keep)
+    desc.w = state.shape[1]
+    xc, wc = x.contiguous(), weight.contiguous()
+    bc = None if bias is None else bias.contiguous()
+    if in_place:
+        if not state.is_contiguous():
+            raise Unsupported(f"{op}: an in-place state must be contiguous")
+        st_in = st_out = state
+    else:
+        st_in = state.contiguous()
+        st_out = torch.empty_like(st_in)
+    out = torch.empty_like(xc)
+    _check(op, _lib.lib().dm_causal_conv1d_update(ctypes.byref(desc), _ptr(xc), _ptr(wc),
+                                                  _ptr(bc), _ptr(st_in), _ptr(out), _ptr(st_out),
+                                                  _stream()))
     return out, st_out

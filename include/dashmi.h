@@ -12,6 +12,11 @@
  *   dm_gdr_chunk_bwd     ChunkGatedDeltaBackend::chunk_gated_delta_backward (the Autodiff node's
  *                        backward, chunk.rs:542-767, as an explicit entry point)
  *   dm_gdr_step          GatedDeltaStepBackend::gated_delta_step crates/dash-ops/src/gated_delta/recurrent.rs:52-81, :158
+ *   dm_causal_conv1d_fwd     CausalConv1dBackend::causal_conv1d  crates/dash-ops/src/conv1d.rs:198-300, :690
+ *   dm_causal_conv1d_bwd     CausalConv1dBackend::causal_conv1d_backward
+ *                                                               crates/dash-ops/src/conv1d.rs:300-329
+ *   dm_causal_conv1d_update  CausalConv1dBackend::causal_conv1d_update
+ *                                                               crates/dash-ops/src/conv1d.rs:331-360, :750
  *
  * Conventions (crates/dash-contract/src/lib.rs:38-91):
  *   - Every tensor is a device pointer to a contiguous array in the contract's layout:
@@ -85,6 +90,24 @@ typedef struct {
     float scale;
 } dm_gdr_desc;
 
+/* The causal conv1d's activation (crates/dash-contract/src/conv1d.rs:81-90). */
+typedef enum { DM_ACT_NONE = 0, DM_ACT_SILU = 1 } dm_activation;
+/* One causal conv1d call's shapes and options (conv1d.rs:774-820 check_parameters/check_state;
+ * the contract's CausalConv1dOptions, crates/dash-contract/src/conv1d.rs:92-140): x [B, T, C],
+ * weight [C, K], bias [C], states [S, W, C] f32. The step: x [B, C], state [B, w, C]. */
+typedef struct {
+    int64_t b, t, c, k;
+    int32_t dtype;             /* x, weight, bias, the output and their gradients */
+    const int32_t *cu_seqlens; /* packed: [nseq + 1] over a batch of one; NULL: a sequence per row */
+    int64_t nseq;
+    int32_t has_bias;
+    int32_t activation;        /* dm_activation */
+    int32_t has_initial;       /* initial states of w steps (w >= K - 1); the step's state length */
+    int64_t w;
+    int32_t has_final;         /* final states of w_out steps */
+    int64_t w_out;
+} dm_conv1d_desc;
+
 /* The message of this thread's last refusal or error. */
 const char *dm_last_error(void);
 
@@ -105,6 +128,9 @@ typedef enum {
     DM_PROBE_GDR_CHUNK_FWD,
     DM_PROBE_GDR_CHUNK_BWD,
     DM_PROBE_GDR_STEP,
+    DM_PROBE_CONV1D_FWD,
+    DM_PROBE_CONV1D_BWD,
+    DM_PROBE_CONV1D_UPDATE,
     DM_PROBE_COUNT
 } dm_probe;
 uint64_t dm_probe_count(int probe);
@@ -126,6 +152,9 @@ typedef enum {
     DM_KERNEL_GDR_BWD_PRE,    /* chunked gated delta rule backward: per-chunk state-gradient terms */
     DM_KERNEL_GDR_BWD_STATE,  /* chunked gated delta rule backward: the state-gradient pass */
     DM_KERNEL_GDR_BWD_GRADS,  /* chunked gated delta rule backward: per-chunk gradients */
+    DM_KERNEL_CONV1D_FWD,     /* causal conv1d forward */
+    DM_KERNEL_CONV1D_BWD,     /* causal conv1d backward: the input gradient and the partial sums */
+    DM_KERNEL_CONV1D_UPDATE,  /* causal conv1d decoding step */
     DM_KERNEL_COUNT
 } dm_kernel;
 int dm_kernel_timing(int enable);
@@ -186,6 +215,33 @@ int dm_gdr_chunk_bwd(const dm_gdr_desc *desc, const void *q, const void *k, cons
 int dm_gdr_step(const dm_gdr_desc *desc, const void *q, const void *k, const void *v,
                 const void *g, const void *beta, const float *state_in, float *state_out,
                 void *out, void *stream);
+
+/* The causal depthwise conv1d over sequences: out [B, T, C] in dtype and, with has_final, each
+ * sequence's final state (the last w_out steps of its history) [S, w_out, C] f32; with
+ * has_initial, each sequence continues from initial_state [S, w, C] f32. Replaces
+ * conv1d.rs:690 / CausalConv1dBackend::causal_conv1d. Kernel widths up to 16. */
+int dm_causal_conv1d_fwd(const dm_conv1d_desc *desc, const void *x, const void *weight,
+                         const void *bias, const float *initial_state, void *out,
+                         float *final_state, void *stream);
+/* Its gradients from the output's (grad_out [B, T, C], grad_out_dtype f32 or dtype) and, with
+ * has_final, the final states' (grad_final_state [S, w_out, C] f32, or NULL for zeros): grad_x
+ * [B, T, C] and grad_weight [C, K] in dtype, grad_bias [C] in dtype with has_bias,
+ * grad_initial_state [S, w, C] f32 with has_initial. The weight's and the bias's gradients are
+ * summed in a fixed order (deterministic). Replaces CausalConv1dBackend::causal_conv1d_backward
+ * (conv1d.rs:300-329), the Autodiff node's backward as an explicit entry point. */
+size_t dm_causal_conv1d_bwd_workspace(const dm_conv1d_desc *desc);
+int dm_causal_conv1d_bwd(const dm_conv1d_desc *desc, const void *x, const void *weight,
+                         const void *bias, const float *initial_state, const void *grad_out,
+                         int grad_out_dtype, const float *grad_final_state, void *grad_x,
+                         void *grad_weight, void *grad_bias, float *grad_initial_state,
+                         void *workspace, size_t workspace_bytes, void *stream);
+/* One decoding step: x [B, C] (desc->b = B, desc->w = the state's steps W >= K - 1) and state
+ * [B, W, C] f32 to out [B, C] in dtype and next_state [B, W, C] f32 (the state without its oldest
+ * step, then x; next_state may be state itself). Replaces conv1d.rs:750 /
+ * CausalConv1dBackend::causal_conv1d_update. */
+int dm_causal_conv1d_update(const dm_conv1d_desc *desc, const void *x, const void *weight,
+                            const void *bias, const float *state, void *out, float *next_state,
+                            void *stream);
 
 #ifdef __cplusplus
 }
