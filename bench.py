@@ -37,7 +37,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step")
+    p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step,conv1d")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (torch copy_), 5 times: the known-size "
                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
@@ -285,6 +285,60 @@ def main():
         print(f"gdr step: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
               flush=True)
         del c
+
+    # ---- causal conv1d, config 6 (beside config 4: a Gated DeltaNet layer's conv) ----
+    if want("conv1d"):
+        c = syn.conv1d_config(dev)
+        x, wt, go, h0, cu = c["x"], c["weight"], c["go"], c["h0"], c["cu_seqlens"]
+        _, t, ch = x.shape
+        kw, nseq, w = wt.shape[1], h0.shape[0], h0.shape[1]
+        desc = _lib.Conv1dDesc(b=1, t=t, c=ch, k=kw, dtype=_lib.DM_BF16,
+                               cu_seqlens=cu.data_ptr(), nseq=nseq, has_bias=0,
+                               activation=_lib.DM_ACT_SILU, has_initial=1, w=w, has_final=1,
+                               w_out=w)
+        out, gx, gw = torch.empty_like(x), torch.empty_like(x), torch.empty_like(wt)
+        fin, gh = torch.empty_like(h0), torch.empty_like(h0)
+        gfin = torch.ones_like(h0)
+        ws = torch.empty(max(lib.dm_causal_conv1d_bwd_workspace(ctypes.byref(desc)), 1),
+                         dtype=torch.uint8, device=dev)
+        P = lambda tt: None if tt is None else ctypes.c_void_p(tt.data_ptr())  # noqa: E731
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        fwd = lambda: check(lib.dm_causal_conv1d_fwd(  # noqa: E731
+            ctypes.byref(desc), P(x), P(wt), None, P(h0), P(out), P(fin), st), lib)
+        bwd = lambda: check(lib.dm_causal_conv1d_bwd(  # noqa: E731
+            ctypes.byref(desc), P(x), P(wt), None, P(h0), P(go), _lib.DM_BF16, P(gfin), P(gx),
+            P(gw), None, P(gh), P(ws), ws.numel(), st), lib)
+        tf, tb = Timed(torch, fwd), Timed(torch, bwd)
+        ms_f = tf.run(max(args.steps, 50), args.warmup)
+        ms_b = tb.run(max(args.steps, 50), args.warmup)
+        # algorithmic bytes: x read and the output written (forward); x and the output's
+        # gradient read and the input's written (backward); the f32 states in and out
+        sb = nseq * w * ch * 4
+        fwd_bytes = 2 * t * ch * 2 + 2 * sb + ch * kw * 2
+        bwd_bytes = 3 * t * ch * 2 + 3 * sb + ch * kw * 2
+        bs, sx, sst = c["step_x"].shape[0], c["step_x"], c["step_state"]
+        sdesc = _lib.Conv1dDesc(b=bs, t=1, c=ch, k=kw, dtype=_lib.DM_BF16, has_bias=0,
+                                activation=_lib.DM_ACT_SILU, w=w)
+        sout = torch.empty_like(sx)
+        upd = lambda: check(lib.dm_causal_conv1d_update(  # noqa: E731
+            ctypes.byref(sdesc), P(sx), P(wt), None, P(sst), P(sout), P(sst), st), lib)
+        tu = Timed(torch, upd)
+        ms_u = tu.run(max(args.steps, 100), args.warmup)
+        upd_bytes = 2 * bs * ch * 2 + 2 * bs * w * ch * 4
+        kus = {k: round(v[0] * 1e3, 2) for k, v in {**tf.kernel_ms, **tb.kernel_ms,
+                                                    **tu.kernel_ms}.items()}
+        secondary["conv1d"] = dict(
+            unit="GB/s", workload="causal conv1d, bf16, 32768 tokens in config 4's 8 sequences, "
+            "C=6144, K=4, SiLU, initial and final states of 3 steps; step: 128 sequences",
+            fwd_GBps=fwd_bytes / ms_f / 1e6, fwd_us=ms_f * 1e3,
+            fwd_frac_of_hbm_peak=fwd_bytes / ms_f / 1e6 / HBM_PEAK_GBS,
+            bwd_GBps=bwd_bytes / ms_b / 1e6, bwd_us=ms_b * 1e3,
+            bwd_frac_of_hbm_peak=bwd_bytes / ms_b / 1e6 / HBM_PEAK_GBS,
+            step_GBps=upd_bytes / ms_u / 1e6, step_us=ms_u * 1e3, kernel_us=kus)
+        print(f"conv1d: fwd {ms_f * 1e3:.1f} us ({fwd_bytes / ms_f / 1e6:.0f} GB/s), bwd "
+              f"{ms_b * 1e3:.1f} us ({bwd_bytes / ms_b / 1e6:.0f} GB/s), step {ms_u * 1e3:.1f} us",
+              file=sys.stderr, flush=True)
+        del c, x, go, out, gx
 
     # ---- CPU baseline: the oracle on a bounded sample of config 2 ----
     cpu = None

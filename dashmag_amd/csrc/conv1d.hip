@@ -29,6 +29,8 @@ namespace dm {
 
 constexpr int kCv1Threads = 256;
 constexpr int kCv1MaxK = 16;
+constexpr int kCv1Batch = 8;     // forward: steps whose loads are issued together
+constexpr int kCv1BatchBwd = 4;  // backward: the same (its windows and sums take more registers)
 
 struct Cv1Args {
     int64_t rows;       // B * T (a sequence per batch row) or T (packed)
@@ -86,9 +88,18 @@ __device__ __forceinline__ void cv1_ld(const void *p, int64_t i, float *v) {
             v[4 * q + 2] = a.z;
             v[4 * q + 3] = a.w;
         }
+    } else if constexpr (VEC == 4) {
+        const uint2 a = *(const uint2 *)((const uint16_t *)p + i);
+        const uint32_t u[2] = {a.x, a.y};
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            v[2 * e] = unpack_lo<DT>(u[e]);
+            v[2 * e + 1] = unpack_hi<DT>(u[e]);
+        }
     } else {
-        const uint4 a = *(const uint4 *)((const uint16_t *)p + i);
-        const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+        // (non-temporal: the rows stream past once)
+        const u32x4_t a = __builtin_nontemporal_load((const u32x4_t *)((const uint16_t *)p + i));
+        const uint32_t u[4] = {a[0], a[1], a[2], a[3]};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             v[2 * e] = unpack_lo<DT>(u[e]);
@@ -116,10 +127,12 @@ __device__ __forceinline__ void cv1_st(void *p, int64_t i, const float *v) {
         for (int q = 0; q < VEC / 4; q++)
             *(float4 *)((float *)p + i + 4 * q) =
                 make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else if constexpr (VEC == 4) {
+        *(uint2 *)((uint16_t *)p + i) = make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
     } else {
-        *(uint4 *)((uint16_t *)p + i) =
-            make_uint4(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]), pack2<DT>(v[4], v[5]),
-                       pack2<DT>(v[6], v[7]));
+        const u32x4_t o = {pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]), pack2<DT>(v[4], v[5]),
+                           pack2<DT>(v[6], v[7])};
+        __builtin_nontemporal_store(o, (u32x4_t *)((uint16_t *)p + i));
     }
 }
 
@@ -140,6 +153,12 @@ __device__ __forceinline__ void cv1_hist(const Cv1Args &a, const void *x, const 
 
 __device__ __forceinline__ float cv1_sigmoid(float y) { return 1.f / (1.f + expf(-y)); }
 
+// sigmoid(y) for 16-bit inputs: 1 / (1 + 2^(-y log2 e)) on the hardware exponential and
+// reciprocal (about an ulp of f32 each, far below the output's rounding)
+__device__ __forceinline__ float cv1_sigmoid_fast(float y) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * y));
+}
+
 // SiLU(y) = y sigmoid(y). For f32 inputs in f64, rounded once: the device's expf is about an
 // ulp off, which the f32 conformance bounds (about 1.3 ulp of the largest output) do not leave
 // room for; for 16-bit inputs the output's rounding to the dtype dominates and f32 suffices.
@@ -149,15 +168,21 @@ __device__ __forceinline__ float cv1_silu(float y) {
         const double yd = y;
         return (float)(yd / (1.0 + exp(-yd)));
     } else {
-        return __fmul_rn(y, cv1_sigmoid(y));
+        return y * cv1_sigmoid_fast(y);
     }
 }
 
-// acc + a b with the product and the sum rounded separately, as the reference's tensor
-// operations round them (no fused multiply-add: the conformance bounds are about an ulp)
+// acc + a b. For f32 inputs with the product and the sum rounded separately, as the
+// reference's tensor operations round them (its conformance bounds are about an ulp); for 16-bit
+// inputs, whose results are rounded to 8 or 11 bits, one fused multiply-add.
+template <int DT>
 __device__ __forceinline__ float cv1_madd(float acc, float a, float b) {
-    return __fadd_rn(acc, __fmul_rn(a, b));
+    if constexpr (DT == DM_F32)
+        return __fadd_rn(acc, __fmul_rn(a, b));
+    else
+        return fmaf(a, b, acc);
 }
+
 
 // The taps as KT registers per channel: tap j of a kernel of width k < KT sits at KT - k + j, the
 // others are zero (so a window of KT steps ending at the current step applies the kernel).
@@ -201,25 +226,40 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_fwd_kernel(Cv1Args a, cons
         float win[KT][VEC];
 #pragma unroll
         for (int j = 0; j < KT - 1; j++) cv1_hist<DT, VEC>(a, x, h0, s, s0, r - s0 - (KT - 1) + j, c0, win[j]);
-#pragma unroll 4
-        for (; r < pend; r++) {
-            cv1_ld<DT, VEC>(x, r * a.c + c0, win[KT - 1]);
+        // one step from the window (win[KT - 1] the step's input): the taps in order, then the
+        // bias (reference.rs:94-105); then the window slides
+        auto step = [&](int64_t rr) __attribute__((always_inline)) {
             float o[VEC];
 #pragma unroll
             for (int e = 0; e < VEC; e++) {
-                // the taps in order, then the bias (reference.rs:94-105)
                 float y = 0.f;
 #pragma unroll
-                for (int j = 0; j < KT; j++) y = cv1_madd(y, wv[j][e], win[j][e]);
+                for (int j = 0; j < KT; j++) y = cv1_madd<DT>(y, wv[j][e], win[j][e]);
                 if (a.has_bias) y = __fadd_rn(y, bv[e]);
                 if (a.silu) y = cv1_silu<DT>(y);
                 o[e] = y;
             }
-            cv1_st<DT, VEC>(out, r * a.c + c0, o);
+            cv1_st<DT, VEC>(out, rr * a.c + c0, o);
 #pragma unroll
             for (int j = 0; j < KT - 1; j++)
 #pragma unroll
                 for (int e = 0; e < VEC; e++) win[j][e] = win[j + 1][e];
+        };
+        // kCv1Batch steps at a time: their rows' loads all issued before the first is used
+        for (; r + kCv1Batch <= pend; r += kCv1Batch) {
+            float xb[kCv1Batch][VEC];
+#pragma unroll
+            for (int u = 0; u < kCv1Batch; u++) cv1_ld<DT, VEC>(x, (r + u) * a.c + c0, xb[u]);
+#pragma unroll
+            for (int u = 0; u < kCv1Batch; u++) {
+#pragma unroll
+                for (int e = 0; e < VEC; e++) win[KT - 1][e] = xb[u][e];
+                step(r + u);
+            }
+        }
+        for (; r < pend; r++) {
+            cv1_ld<DT, VEC>(x, r * a.c + c0, win[KT - 1]);
+            step(r);
         }
     }
 }
@@ -266,8 +306,8 @@ __device__ __forceinline__ float cv1_dy(float g, float y, int silu) {
         const double yd = y, sg = 1.0 / (1.0 + exp(-yd));
         return (float)((double)g * (sg * (yd * (1.0 - sg) + 1.0)));
     } else {
-        const float sg = cv1_sigmoid(y);
-        return __fmul_rn(g, __fmul_rn(sg, __fadd_rn(__fmul_rn(y, __fsub_rn(1.f, sg)), 1.f)));
+        const float sg = cv1_sigmoid_fast(y);
+        return g * (sg * fmaf(y, 1.f - sg, 1.f));
     }
 }
 
@@ -295,17 +335,21 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
     }
     const int64_t wh = a.has_h0 ? a.w : 0;
     // the pre-activation gradient of step tau of sequence s from its window
-    auto dy_at = [&](int64_t s, int64_t s0, int64_t tau, const float (&xw)[KT][VEC], float *d) {
-        float g[VEC];
-        cv1_ld<GT, VEC>(go, (s0 + tau) * a.c + c0, g);
+    // the pre-activation gradient from the output's gradient g and the inputs' window
+    auto dy_of = [&](const float *g, const float (&xw)[KT][VEC], float *d) {
 #pragma unroll
         for (int e = 0; e < VEC; e++) {
             float y = 0.f;
 #pragma unroll
-            for (int j = 0; j < KT; j++) y = cv1_madd(y, wv[j][e], xw[j][e]);
+            for (int j = 0; j < KT; j++) y = cv1_madd<DT>(y, wv[j][e], xw[j][e]);
             if (a.has_bias) y = __fadd_rn(y, bv[e]);
             d[e] = cv1_dy<DT>(g[e], y, a.silu);
         }
+    };
+    auto dy_at = [&](int64_t s0, int64_t tau, const float (&xw)[KT][VEC], float *d) {
+        float g[VEC];
+        cv1_ld<GT, VEC>(go, (s0 + tau) * a.c + c0, g);
+        dy_of(g, xw, d);
     };
     if (r0 < r1) {
         int64_t s, s0, s1;
@@ -323,7 +367,7 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
                     float xw[KT][VEC];
 #pragma unroll
                     for (int j = 0; j < KT; j++) cv1_hist<DT, VEC>(a, x, h0, s, s0, tau - (KT - 1) + j, c0, xw[j]);
-                    dy_at(s, s0, tau, xw, gwin[i]);
+                    dy_at(s0, tau, xw, gwin[i]);
                 } else {
 #pragma unroll
                     for (int e = 0; e < VEC; e++) gwin[i][e] = 0.f;
@@ -334,9 +378,12 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
 #pragma unroll
             for (int j = 0; j < KT; j++) cv1_hist<DT, VEC>(a, x, h0, s, s0, p1 - 1 - s0 - (KT - 1) + j, c0, xw[j]);
             const int64_t P = wh + len;
-            for (int64_t t = p1 - 1; t >= p0; t--) {
+            // step t from its output gradient g and the windows; then both slide one step back
+            // (xn: the input entering the window, h[t - KT])
+            auto step = [&](int64_t t, const float *g, const float *xn, auto fin_c) __attribute__((always_inline)) {
+                constexpr bool FIN = decltype(fin_c)::value;
                 float d[VEC];
-                dy_at(s, s0, t - s0, xw, d);
+                dy_of(g, xw, d);
                 // dx[t] = sum_j weight[j] dy[t + K - 1 - j], the taps in order (:296-316): with
                 // the taps right-aligned at KT, tap slot j reads dy[t + KT - 1 - j], which is d
                 // for j = KT - 1 and gwin[KT - 2 - j] before
@@ -348,12 +395,12 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
                     for (int j = 0; j < KT; j++) {
                         if (j < KT - (int)a.k) continue;  // (zero taps)
                         const float dj = j == KT - 1 ? d[e] : gwin[KT - 2 - j][e];
-                        acc = cv1_madd(acc, wv[j][e], dj);
+                        acc = cv1_madd<DT>(acc, wv[j][e], dj);
                     }
                     o[e] = acc;
                 }
                 // the final states' gradient onto the inputs among the history's last W' steps
-                if (gfin) {
+                if (FIN) {
                     const int64_t idx = wh + (t - s0) - (P - a.w_out);
                     if (idx >= 0) {
                         float f[VEC];
@@ -367,9 +414,8 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
                 for (int e = 0; e < VEC; e++) {
                     ab[e] = __fadd_rn(ab[e], d[e]);
 #pragma unroll
-                    for (int j = 0; j < KT; j++) aw[j][e] = cv1_madd(aw[j][e], d[e], xw[j][e]);
+                    for (int j = 0; j < KT; j++) aw[j][e] = cv1_madd<DT>(aw[j][e], d[e], xw[j][e]);
                 }
-                // slide both windows one step back
 #pragma unroll
                 for (int i = KT - 2; i > 0; i--)
 #pragma unroll
@@ -380,7 +426,39 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
                 for (int j = KT - 1; j > 0; j--)
 #pragma unroll
                     for (int e = 0; e < VEC; e++) xw[j][e] = xw[j - 1][e];
-                if (t > p0) cv1_hist<DT, VEC>(a, x, h0, s, s0, t - 1 - s0 - (KT - 1), c0, xw[0]);
+#pragma unroll
+                for (int e = 0; e < VEC; e++) xw[0][e] = xn[e];
+            };
+            int64_t t = p1 - 1;
+            // the steps the final states' gradient reaches (the history's last W'), one at a time
+            const int64_t tfin = gfin ? max(p0, s0 + (P - a.w_out) - wh) : p1;
+            for (; t >= tfin; t--) {
+                float g[VEC], xn[VEC];
+                cv1_ld<GT, VEC>(go, t * a.c + c0, g);
+                cv1_hist<DT, VEC>(a, x, h0, s, s0, t - s0 - KT, c0, xn);
+                step(t, g, xn, std::true_type{});
+            }
+            // then kCv1BatchBwd steps at a time, their loads (output gradients and entering
+            // inputs) all issued before the first step; inputs inside the sequence read directly
+            for (; t - (kCv1BatchBwd - 1) >= p0; t -= kCv1BatchBwd) {
+                float gb[kCv1BatchBwd][VEC], xn[kCv1BatchBwd][VEC];
+#pragma unroll
+                for (int u = 0; u < kCv1BatchBwd; u++) cv1_ld<GT, VEC>(go, (t - u) * a.c + c0, gb[u]);
+                if (t - (kCv1BatchBwd - 1) - s0 - KT >= 0) {
+#pragma unroll
+                    for (int u = 0; u < kCv1BatchBwd; u++) cv1_ld<DT, VEC>(x, (t - u - KT) * a.c + c0, xn[u]);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < kCv1BatchBwd; u++) cv1_hist<DT, VEC>(a, x, h0, s, s0, t - u - s0 - KT, c0, xn[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < kCv1BatchBwd; u++) step(t - u, gb[u], xn[u], std::false_type{});
+            }
+            for (; t >= p0; t--) {
+                float g[VEC], xn[VEC];
+                cv1_ld<GT, VEC>(go, t * a.c + c0, g);
+                cv1_hist<DT, VEC>(a, x, h0, s, s0, t - s0 - KT, c0, xn);
+                step(t, g, xn, std::false_type{});
             }
             r = p1;
         }
@@ -406,6 +484,7 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_reduce(int64_t nseg, i
     const int64_t i = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
     if (i >= C * (K + 1)) return;
     float acc = 0.f;
+#pragma unroll 8
     for (int64_t g = 0; g < nseg; g++) acc = __fadd_rn(acc, part[g * C * (K + 1) + i]);
     const int64_t c = i / (K + 1), j = i % (K + 1);
     if (j < K)
@@ -488,7 +567,7 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_update_kernel(
     float y = 0.f;
     for (int64_t j = 0; j < K; j++) {
         const float v = j < K - 1 ? state[(b * W + W - (K - 1) + j) * C + c] : xv;
-        y = cv1_madd(y, v, ld<DT>(wt, c * K + j));
+        y = cv1_madd<DT>(y, v, ld<DT>(wt, c * K + j));
     }
     if (has_bias) y = __fadd_rn(y, ld<DT>(bias, c));
     if (silu) y = cv1_silu<DT>(y);
@@ -537,13 +616,14 @@ static int cv1_check(const dm_conv1d_desc *d, const char *op, bool step) {
 static int64_t cv1_nseq(const dm_conv1d_desc *d) { return d->cu_seqlens ? d->nseq : d->b; }
 
 // the vector width (channels per thread) a call takes: 16 bytes of channels when C divides
-static int cv1_vec(const dm_conv1d_desc *d) {
-    const int v = d->dtype == DM_F32 ? 4 : 8;
-    // (widths above 8 run one channel per thread)
+// (the backward takes 4 channels per thread of any dtype: its windows, taps and sums hold 4 K + 4
+// registers per channel; widths above 8 run one channel per thread)
+static int cv1_vec(const dm_conv1d_desc *d, bool bwd = false) {
+    const int v = bwd || d->dtype == DM_F32 ? 4 : 8;
     return d->c % v == 0 && d->k <= 8 ? v : 1;
 }
 
-static Cv1Args cv1_args(const dm_conv1d_desc *d) {
+static Cv1Args cv1_args(const dm_conv1d_desc *d, bool bwd = false) {
     Cv1Args a{};
     a.rows = d->cu_seqlens ? d->t : d->b * d->t;
     a.t = d->t;
@@ -556,9 +636,9 @@ static Cv1Args cv1_args(const dm_conv1d_desc *d) {
     a.has_h0 = d->has_initial ? 1 : 0;
     a.has_bias = d->has_bias ? 1 : 0;
     a.silu = d->activation == DM_ACT_SILU ? 1 : 0;
-    const int vec = cv1_vec(d);
+    const int vec = cv1_vec(d, bwd);
     a.cv = (d->c + vec - 1) / vec;
-    // segments: about 256K threads in all, each segment at least 16 steps, at most 256 segments
+    // segments: about 256K threads in all, at most 256 segments of at least 16 steps
     int64_t nseg = (256 * 1024 + a.cv - 1) / std::max<int64_t>(a.cv, 1);
     nseg = std::min<int64_t>(nseg, 256);
     nseg = std::min<int64_t>(nseg, (a.rows + 15) / 16);
@@ -602,7 +682,7 @@ static void cv1_bwd_launch(const Cv1Args &a, int vec, const void *x, const void 
                            const float *h0, const void *go, const float *gfin, void *gx, float *part,
                            hipStream_t st) {
     const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)cv1_nseg(a));
-    constexpr int V = DT == DM_F32 ? 4 : 8;
+    constexpr int V = 4;
 #define CV1_BWD(KT, VV) \
     conv1d_bwd_kernel<DT, GT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, go, gfin, gx, part)
     if (vec == V && a.k <= 8) {
@@ -660,7 +740,7 @@ int dm_causal_conv1d_fwd(const dm_conv1d_desc *d, const void *x, const void *wei
 
 size_t dm_causal_conv1d_bwd_workspace(const dm_conv1d_desc *d) {
     if (!d || d->k < 1 || d->c < 0) return 0;
-    const Cv1Args a = cv1_args(d);
+    const Cv1Args a = cv1_args(d, true);
     return align_up((size_t)std::max<int64_t>(cv1_nseg(a), 1) * (size_t)d->c * (size_t)(d->k + 1) *
                     sizeof(float));
 }
@@ -682,8 +762,8 @@ int dm_causal_conv1d_bwd(const dm_conv1d_desc *d, const void *x, const void *wei
         return refuse(std::string(op) +
                       ": the workspace is smaller than dm_causal_conv1d_bwd_workspace");
     hipStream_t st = (hipStream_t)stream;
-    const Cv1Args a = cv1_args(d);
-    const int vec = cv1_vec(d);
+    const Cv1Args a = cv1_args(d, true);
+    const int vec = cv1_vec(d, true);
     const float *gfin = d->has_final && a.w_out > 0 ? grad_final_state : nullptr;
     float *part = (float *)workspace;
     const int64_t nseg = cv1_nseg(a);

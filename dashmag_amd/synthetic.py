@@ -13,7 +13,10 @@ Configs (BASELINE.json ``configs``):
      sequence of 4096 tokens;
   3. decode, bf16, B=64, Hq=32, Hkv=8, D=128, cache lengths uniform in [512, 8192];
   4. chunked gated delta rule, bf16, 32768 tokens in 8 sequences, H=16, Dk=Dv=128;
-  5. gated delta step, 128 sequences, H=16, Dk=Dv=128, f32 state.
+  5. gated delta step, 128 sequences, H=16, Dk=Dv=128, f32 state;
+  6. (beside them, no BASELINE config) the causal conv1d of a Gated DeltaNet layer over config 4's
+     packing: C = 6144 channels (q, k and v of 16 heads of 128), K = 4, SiLU, bf16, initial and
+     final states of 3 steps; and its decoding step over 128 sequences (config 5's batch).
 """
 from __future__ import annotations
 
@@ -158,6 +161,33 @@ def config5(device="cpu", dtype=torch.bfloat16, b=128, h=16, dk=128, dv=128):
     g, beta = gdr_gates(5, (b, h), device)
     state = normal(seed_of(5, STATE), (b, h, dk, dv), device, std=0.1)
     return dict(q=q, k=k, v=v, g=g, beta=as_input(beta, dtype), state=state)
+
+
+def conv1d_config(device="cpu", dtype=torch.bfloat16, c=6144, k=4, w=3, b_step=128):
+    """Config 6: x [1, 32768, C] over config 4's 8 sequences, weight [C, K] (std 1/2), output
+    gradient, initial states [8, W, C] f32; the step's token [b_step, C] and state [b_step, W, C]
+    (tensor indices: x 0, weight 1, output gradient 3, states 6, step token 2)."""
+    cu = _config4_cuts()
+    total, nseq = int(cu[-1]), len(cu) - 1
+    x = as_input(normal(seed_of(6, Q), (1, total, c), device), dtype)
+    weight = as_input(normal(seed_of(6, K), (c, k), device, std=0.5), dtype)
+    go = as_input(normal(seed_of(6, DO), (1, total, c), device), dtype)
+    h0 = normal(seed_of(6, STATE), (nseq, w, c), device)
+    xs = as_input(normal(seed_of(6, V), (b_step, c), device), dtype)
+    state = normal(seed_of(6, STATE), (b_step, w, c), device)
+    return dict(x=x, weight=weight, go=go, h0=h0, cu_seqlens=cu.to(device), step_x=xs,
+                step_state=state)
+
+
+def _config4_cuts(total=32768, nseq=8):
+    """Config 4's sequence boundaries (see config4)."""
+    u = uniform(seed_of(4, LENGTHS), 1024).tolist()
+    cuts = set()
+    for x in u:
+        cuts.add(1 + int(math.floor(x * (total - 1))))
+        if len(cuts) == nseq - 1:
+            break
+    return torch.tensor([0] + sorted(cuts) + [total], dtype=torch.int32)
 
 
 def visible_pairs(lengths) -> int:
