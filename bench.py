@@ -24,6 +24,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -213,7 +215,65 @@ def main():
             secondary["decode"]["split_kernel_GBps"] = nbytes / ks / 1e6
         print(f"decode: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
               flush=True)
-        del c, k, v
+
+        # the same keys in the other cache layouts: packed back to back (offsets cu_seqlens_k)
+        # and in shuffled pages of 16 keys (a block table)
+        bsz, S, hkv, d = k.shape
+        lens_h = lens.to("cpu", torch.int64)
+        starts = torch.arange(bsz, dtype=torch.int64) * S
+        rows = torch.cat([starts[b] + torch.arange(int(lens_h[b])) for b in range(bsz)]).to(dev)
+        kpk, vpk = k.reshape(-1, hkv, d)[rows], v.reshape(-1, hkv, d)[rows]
+        cu = torch.zeros(bsz + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(lens_h, 0).to(torch.int32)
+        cu = cu.to(dev)
+        pdesc = ops._decode_desc("attention_decode", q, kpk, vpk, S, dm.AttentionOptions())
+        pdesc.cu_seqlens_k, pdesc.nseq = cu.data_ptr(), bsz
+        pnb = lib.dm_attention_decode_workspace(ctypes.byref(pdesc))
+        pws = torch.empty(max(pnb, 1), dtype=torch.uint8, device=dev)
+        pp = [ctypes.c_void_p(t.data_ptr()) for t in (q, kpk, vpk, o, pws)]
+        fn = lambda: check(lib.dm_attention_decode(ctypes.byref(pdesc), pp[0], pp[1], pp[2],  # noqa
+                                                   None, pp[3], pp[4], pnb, st), lib)
+        tm = Timed(torch, fn)
+        ms_p = tm.run(max(args.steps, 50), args.warmup)
+        secondary["decode_packed"] = dict(unit="GB/s", value=nbytes / ms_p / 1e6,
+                                          us_per_call=ms_p * 1e3, layout="packed, cu_seqlens_k",
+                                          frac_of_hbm_peak=nbytes / ms_p / 1e6 / HBM_PEAK_GBS)
+        del kpk, vpk
+        ps = 16
+        npg = [-(-int(n) // ps) for n in lens_h]
+        total = sum(npg)
+        perm = torch.from_numpy(np.random.default_rng(3).permutation(total)).to(torch.int64)
+        table = torch.full((bsz, S // ps), -1, dtype=torch.int32)
+        src = []
+        i = 0
+        for b in range(bsz):
+            table[b, :npg[b]] = perm[i:i + npg[b]].to(torch.int32)
+            src.append(starts[b] + torch.arange(npg[b] * ps))
+            i += npg[b]
+        src = torch.cat(src).to(dev)
+        kpg = torch.empty(total, ps, hkv, d, dtype=k.dtype, device=dev)
+        vpg = torch.empty_like(kpg)
+        kpg[perm.to(dev)] = k.reshape(-1, hkv, d)[src].reshape(total, ps, hkv, d)
+        vpg[perm.to(dev)] = v.reshape(-1, hkv, d)[src].reshape(total, ps, hkv, d)
+        table = table.to(dev)
+        gdesc = ops._decode_desc("attention_decode_paged", q, kpg, vpg, S, dm.AttentionOptions())
+        gnb = lib.dm_attention_decode_paged_workspace(ctypes.byref(gdesc), ps)
+        gws = torch.empty(max(gnb, 1), dtype=torch.uint8, device=dev)
+        gp = [ctypes.c_void_p(t.data_ptr()) for t in (q, kpg, vpg, table, lens, o, gws)]
+        fn = lambda: check(lib.dm_attention_decode_paged(  # noqa
+            ctypes.byref(gdesc), gp[0], gp[1], gp[2], total, ps, gp[3], S // ps, gp[4], gp[5],
+            gp[6], gnb, st), lib)
+        tm = Timed(torch, fn)
+        ms_g = tm.run(max(args.steps, 50), args.warmup)
+        secondary["decode_paged"] = dict(unit="GB/s", value=nbytes / ms_g / 1e6,
+                                         us_per_call=ms_g * 1e3,
+                                         layout=f"pages of {ps} keys, shuffled, block table",
+                                         frac_of_hbm_peak=nbytes / ms_g / 1e6 / HBM_PEAK_GBS,
+                                         kernel_us={k: round(v[0] * 1e3, 2)
+                                                    for k, v in tm.kernel_ms.items()})
+        print(f"decode packed: {ms_p * 1e3:.1f} us; paged ({ps}): {ms_g * 1e3:.1f} us, "
+              f"{nbytes / ms_g / 1e6:.0f} GB/s", file=sys.stderr, flush=True)
+        del c, k, v, kpg, vpg
 
     # ---- gated delta rule chunked, config 4 ----
     if want("gdr"):
@@ -343,7 +403,6 @@ def main():
     # ---- CPU baseline: the oracle on a bounded sample of config 2 ----
     cpu = None
     if not args.no_cpu_baseline and want("attn"):
-        import numpy as np
 
         import oracle
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))

@@ -8,7 +8,8 @@ The operations run as hand-written HIP kernels in ``libdashmi.so`` behind the C 
 from .contract import (Activation, AttentionMask, AttentionOptions, CausalConv1dOptions,
                        CausalConv1dStepOptions, ChunkGatedDeltaOptions, DType,
                        GatedDeltaStepOptions, UNBOUNDED, Unsupported, Window)
-from .ops import (attention, attention_backward, attention_decode, attention_with_lse,
+from .ops import (attention, attention_backward, attention_decode, attention_decode_packed,
+                  attention_decode_paged, attention_with_lse,
                   causal_conv1d, causal_conv1d_backward, causal_conv1d_update,
                   chunk_gated_delta_rule, chunk_gated_delta_rule_backward, gated_delta_step)
 
@@ -16,7 +17,8 @@ __all__ = [
     "Activation", "AttentionMask", "AttentionOptions", "CausalConv1dOptions",
     "CausalConv1dStepOptions", "ChunkGatedDeltaOptions", "DType",
     "GatedDeltaStepOptions", "UNBOUNDED", "Unsupported", "Window",
-    "attention", "attention_backward", "attention_decode", "attention_with_lse",
+    "attention", "attention_backward", "attention_decode", "attention_decode_packed",
+    "attention_decode_paged", "attention_with_lse",
     "causal_conv1d", "causal_conv1d_backward", "causal_conv1d_update",
     "chunk_gated_delta_rule", "chunk_gated_delta_rule_backward", "gated_delta_step",
 ]

@@ -75,6 +75,10 @@ SIGNATURES = {
                                         _SZ, _VP]),
     "dm_attention_decode_workspace": (_SZ, [_AD]),
     "dm_attention_decode": (ctypes.c_int, [_AD, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "dm_attention_decode_paged_workspace": (_SZ, [_AD, ctypes.c_int64]),
+    "dm_attention_decode_paged": (ctypes.c_int, [_AD, _VP, _VP, _VP, ctypes.c_int64,
+                                                 ctypes.c_int64, _VP, ctypes.c_int64, _VP, _VP,
+                                                 _VP, _SZ, _VP]),
     "dm_gdr_chunk_fwd_workspace": (_SZ, [_GD]),
     "dm_gdr_chunk_fwd": (ctypes.c_int, [_GD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
                                         _VP]),

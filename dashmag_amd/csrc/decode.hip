@@ -25,6 +25,40 @@ struct Bf16x8 {
     uint4 raw;
 };
 
+// Where the cache keeps sequence b's keys. Dense: rows b * S .. b * S + S - 1 of k, v
+// [B, S, Hkv, D]. Packed: rows offsets[b] .. offsets[b + 1] - 1 of k, v [N, Hkv, D]
+// (offsets = cu_seqlens_k, [B + 1] int32), at most S of them. Paged: key j of sequence b is row
+// j % page_size of page block_table[b * max_pages + j / page_size] of k, v
+// [num_pages, page_size, Hkv, D]; a page index outside [0, num_pages) reads as zeros.
+struct KvMap {
+    const int32_t *offsets;
+    const int32_t *block_table;
+    int64_t page_size, max_pages, num_pages;
+};
+
+// Sequence b's first cache row (dense and packed) and the number of keys it holds: lengths[b]
+// (every key of its span without lengths), clamped to [0, its span].
+__device__ __forceinline__ void kv_extent(const KvMap &m, int64_t b, int64_t S,
+                                          const int32_t *lengths, int64_t &row0, int64_t &len) {
+    int64_t cap = S;
+    row0 = b * S;
+    if (m.offsets) {
+        row0 = m.offsets[b];
+        const int64_t n = (int64_t)m.offsets[b + 1] - row0;
+        cap = n < S ? n : S;
+        if (cap < 0) cap = 0;
+    }
+    len = lengths ? (int64_t)lengths[b] : cap;
+    if (len > cap) len = cap;
+    if (len < 0) len = 0;
+}
+
+// Paged caches: the cache row of key j of sequence b, or -1 when its page index is out of range.
+__device__ __forceinline__ int64_t kv_page_row(const KvMap &m, int64_t b, int64_t j) {
+    const int64_t pg = m.block_table[b * m.max_pages + j / m.page_size];
+    return pg >= 0 && pg < m.num_pages ? pg * m.page_size + j % m.page_size : -1;
+}
+
 template <int DT>
 __device__ __forceinline__ void unpack8(const uint4 &r, float *x) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
@@ -79,7 +113,7 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
                                                     const void *__restrict__ q,
                                                     const void *__restrict__ k,
                                                     const void *__restrict__ v,
-                                                    const int32_t *__restrict__ lengths,
+                                                    const int32_t *__restrict__ lengths, KvMap map,
                                                     float *__restrict__ part_o,
                                                     float *__restrict__ part_lse) {
     constexpr int LPR = D / 8;       // lanes per K/V row
@@ -91,9 +125,8 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane / LPR, seg = lane % LPR;
 
-    int64_t len = lengths ? (int64_t)lengths[b] : S;
-    if (len > S) len = S;
-    if (len < 0) len = 0;
+    int64_t row0, len;
+    kv_extent(map, b, S, lengths, row0, len);
     int64_t lo = left >= 0 ? len - 1 - left : 0;
     if (lo < 0) lo = 0;
     const int64_t start = lo + (int64_t)split * span;
@@ -120,8 +153,8 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
     }
 
     const int64_t row_stride = Hkv * D * 2;  // bytes between consecutive keys
-    const char *kb = (const char *)k + (b * S * Hkv + kh) * D * 2 + seg * 16;
-    const char *vb = (const char *)v + (b * S * Hkv + kh) * D * 2 + seg * 16;
+    const char *kb = (const char *)k + (row0 * Hkv + kh) * D * 2 + seg * 16;
+    const char *vb = (const char *)v + (row0 * Hkv + kh) * D * 2 + seg * 16;
 
     // each wavefront sweeps a contiguous quarter of the split, kDecodeRows rows per lane group
     // per step; the next step's rows are loaded before this step's are used
@@ -248,11 +281,18 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
 // O^T += V^T P^T (4 tiles of 32 columns x the heads) run as 32x32x16 products: the scores'
 // output layout (lane = head, rows = keys) is the B operand of the second product as it stands,
 // and V^T comes from transposed LDS reads. Each lane keeps the online softmax of its head in f32.
-template <int DT, int G>
+//
+// PAGED: the blocks start at keys that are multiples of 16, so each 16-key half of a block lies
+// in one page (page_size is a multiple of 16). Per half, one wavefront-uniform read of the block
+// table gives the page, and the half's buffer resource starts at the half's first visible key
+// and spans only its visible keys: keys before the wavefront's range (negative offsets wrap past
+// the end), past it, or on a page index out of range read as zeros, and their scores are -inf.
+template <int DT, int G, bool PAGED>
 __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     int64_t S, int64_t Hq, int64_t Hkv, int64_t left, float scale, int nsplit, int span,
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
-    const int32_t *__restrict__ lengths, float *__restrict__ part_o, float *__restrict__ part_lse) {
+    const int32_t *__restrict__ lengths, KvMap map, float *__restrict__ part_o,
+    float *__restrict__ part_lse) {
     constexpr int D = 128, NW = 4, BK = 32;
     constexpr int KS = D + 8, VS = D + 32;  // row strides (elements) of the row and transposed reads
     struct Tiles {
@@ -267,9 +307,8 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 31, half = lane >> 5;
 
-    int64_t len = lengths ? (int64_t)lengths[b] : S;
-    if (len > S) len = S;
-    if (len < 0) len = 0;
+    int64_t row0, len;
+    kv_extent(map, b, S, lengths, row0, len);
     int64_t lo = left >= 0 ? len - 1 - left : 0;
     if (lo < 0) lo = 0;
     const int64_t start = lo + (int64_t)split * span;
@@ -293,8 +332,8 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     const float qscale = scale * 1.4426950408889634f;
 
     const int64_t row_stride = Hkv * D * 2;
-    const char *kb = (const char *)k + (b * S * Hkv + kh) * D * 2;
-    const char *vb = (const char *)v + (b * S * Hkv + kh) * D * 2;
+    const char *kb = (const char *)k + ((PAGED ? 0 : row0) * Hkv + kh) * D * 2;
+    const char *vb = (const char *)v + ((PAGED ? 0 : row0) * Hkv + kh) * D * 2;
     // each wavefront sweeps a contiguous quarter of the split
     const int64_t per_wave = span / NW;
     const int64_t w0 = start + wave * per_wave;
@@ -310,12 +349,32 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     Stage sts;
     // block rows past the wavefront's range load row w1 - 1 again (their scores are -inf)
     auto load = [&](Stage &x, int64_t j0) __attribute__((always_inline)) {
+        if constexpr (PAGED) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int64_t key = min(j0 + 4 * u + (lane >> 4), w1 - 1);
-            const uint32_t off = (uint32_t)((key - w0) * row_stride) + (lane & 15) * 16;
-            x.k[u] = buf_load16_nt(krs, off);
-            x.v[u] = buf_load16_nt(vrs, off);
+            for (int h = 0; h < 2; h++) {
+                const int64_t h0 = j0 + 16 * h;
+                const int64_t first = max(h0, w0), last = min(h0 + 16, w1);
+                int64_t row = first < last ? kv_page_row(map, b, first) : -1;
+                const uint32_t bytes = row >= 0 ? (uint32_t)((last - first) * row_stride) : 0u;
+                if (row < 0) row = 0;
+                const __amdgpu_buffer_rsrc_t kh_rs = make_rsrc(kb + row * row_stride, bytes);
+                const __amdgpu_buffer_rsrc_t vh_rs = make_rsrc(vb + row * row_stride, bytes);
+#pragma unroll
+                for (int u = 4 * h; u < 4 * h + 4; u++) {
+                    const int64_t key = j0 + 4 * u + (lane >> 4);
+                    const uint32_t off = (uint32_t)(int32_t)((key - first) * row_stride) + (lane & 15) * 16;
+                    x.k[u] = buf_load16_nt(kh_rs, off);
+                    x.v[u] = buf_load16_nt(vh_rs, off);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int64_t key = min(j0 + 4 * u + (lane >> 4), w1 - 1);
+                const uint32_t off = (uint32_t)((key - w0) * row_stride) + (lane & 15) * 16;
+                x.k[u] = buf_load16_nt(krs, off);
+                x.v[u] = buf_load16_nt(vrs, off);
+            }
         }
     };
     auto stage = [&](const Stage &x) __attribute__((always_inline)) {
@@ -337,7 +396,8 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            sc[i] = j0 + crow(i, lane) < w1 ? sc[i] * qscale : -INFINITY;
+            const int64_t key = j0 + crow(i, lane);
+            sc[i] = key < w1 && (!PAGED || key >= w0) ? sc[i] * qscale : -INFINITY;
             mx = fmaxf(mx, sc[i]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -367,8 +427,9 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     // (the loop is a single block: with the last block peeled off, as a separate copy after the
     // loop, the kernel measured 15% slower)
     if (w0 < w1) {
-        load(sts, w0);
-        for (int64_t j0 = w0;; j0 += BK) {
+        const int64_t a0 = PAGED ? (w0 & ~(int64_t)15) : w0;
+        load(sts, a0);
+        for (int64_t j0 = a0;; j0 += BK) {
             stage(sts);
             load(sts, j0 + BK);
             block(j0);
@@ -435,20 +496,21 @@ __global__ __launch_bounds__(256) void decode_merge(int64_t rows, int64_t D, int
 }
 
 // The generic decode: the generic attention forward's arithmetic, one wavefront per
-// (sequence, query head), for head widths and groups the split kernel does not take.
-template <int DT, int NPL>
+// (sequence, query head), for head widths, groups and dtypes the split kernels do not take, and
+// for paged caches whose pages are not a multiple of 16 keys (a key on a page index out of range
+// counts as zeros).
+template <int DT, int NPL, bool PAGED>
 __global__ __launch_bounds__(256) void decode_generic(int64_t B, int64_t S, int64_t Hq,
                                                       int64_t Hkv, int64_t D, int64_t left,
                                                       float scale, const void *q, const void *k,
                                                       const void *v, const int32_t *lengths,
-                                                      void *o) {
+                                                      KvMap map, void *o) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= B * Hq) return;
     const int64_t b = row / Hq, h = row % Hq, kh = h / (Hq / Hkv);
-    int64_t len = lengths ? (int64_t)lengths[b] : S;
-    if (len > S) len = S;
-    if (len < 0) len = 0;
+    int64_t row0, len;
+    kv_extent(map, b, S, lengths, row0, len);
     int64_t lo = left >= 0 ? len - 1 - left : 0;
     if (lo < 0) lo = 0;
     float qr[NPL], acc[NPL];
@@ -460,12 +522,13 @@ __global__ __launch_bounds__(256) void decode_generic(int64_t B, int64_t S, int6
     }
     float mx = -INFINITY, l = 0.f;
     for (int64_t j = lo; j < len; j++) {
-        const int64_t kr = ((b * S + j) * Hkv + kh) * D;
+        const int64_t cr = PAGED ? kv_page_row(map, b, j) : row0 + j;
+        const int64_t kr = (cr * Hkv + kh) * D;
         float s = 0.f;
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
             int64_t d = lane + 64 * e;
-            if (d < D) s += qr[e] * ld<DT>(k, kr + d);
+            if (d < D && cr >= 0) s += qr[e] * ld<DT>(k, kr + d);
         }
         s = wave_sum(s) * scale;
         const float mn = fmaxf(mx, s);
@@ -474,7 +537,7 @@ __global__ __launch_bounds__(256) void decode_generic(int64_t B, int64_t S, int6
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
             int64_t d = lane + 64 * e;
-            acc[e] = acc[e] * alpha + p * (d < D ? ld<DT>(v, kr + d) : 0.f);
+            acc[e] = acc[e] * alpha + p * (d < D && cr >= 0 ? ld<DT>(v, kr + d) : 0.f);
         }
         mx = mn;
     }
@@ -492,9 +555,12 @@ static bool split_takes(const dm_attention_desc *d) {
            (d->d == 64 || d->d == 128 || d->d == 256) && (g == 1 || g == 2 || g == 4 || g == 8);
 }
 
-// Keys per split: the smallest power of two from kDecodeMinSpan up that keeps the grid within
-// about kDecodeWorkgroups workgroups (long streams per workgroup keep the loads in flight; a
-// small batch still gets enough workgroups to cover the chip).
+// A paged cache runs the split pass on MFMA for D = 128 and pages of a multiple of 16 keys; every
+// other paged call takes the generic kernel.
+static bool paged_split_takes(const dm_attention_desc *d, int64_t page_size) {
+    return split_takes(d) && d->d == 128 && page_size % 16 == 0;
+}
+
 static int span_of(const dm_attention_desc *d) {
     int64_t span = kDecodeMinSpan;
     const int64_t heads = d->b * d->hkv;
@@ -514,49 +580,38 @@ static int64_t left_of(const dm_attention_desc *d) {
     return left < span ? (int64_t)left : -1;
 }
 
-}  // namespace dm
-
-using namespace dm;
-
-extern "C" {
-
-size_t dm_attention_decode_workspace(const dm_attention_desc *d) {
-    if (!d || !split_takes(d)) return 0;
-    const size_t parts = (size_t)(d->b * d->hq) * nsplit_of(d);
-    return align_up(parts * d->d * sizeof(float)) + align_up(parts * sizeof(float));
-}
-
-int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k, const void *v,
-                        const int32_t *lengths, void *o, void *workspace, size_t workspace_bytes,
-                        void *stream) {
-    if (!d) return refuse("attention_decode: null descriptor");
+// The checks both entry points share; returns DM_OK or the refusal.
+static int check_decode(const char *op, const dm_attention_desc *d) {
+    const std::string o(op);
+    if (!d) return refuse(o + ": null descriptor");
     if (d->b < 0 || d->tk < 0 || d->hq < 0 || d->hkv <= 0 || d->d < 0)
-        return refuse("attention_decode: bad dimensions");
+        return refuse(o + ": bad dimensions");
     if (d->hq % d->hkv != 0)
-        return refuse("attention_decode: the query heads (" + std::to_string(d->hq) +
+        return refuse(o + ": the query heads (" + std::to_string(d->hq) +
                       ") must be a multiple of the key-value heads (" + std::to_string(d->hkv) +
                       ")");
     if (d->dtype != DM_F32 && d->dtype != DM_BF16 && d->dtype != DM_F16)
-        return refuse("attention_decode: dtype must be f32, bf16 or f16");
-    if (d->d > 256) return refuse("attention_decode: head dimension above 256 is not implemented");
-    if (workspace_bytes < dm_attention_decode_workspace(d))
-        return refuse("attention_decode: the workspace is smaller than dm_attention_decode_workspace");
-    hipStream_t st = (hipStream_t)stream;
+        return refuse(o + ": dtype must be f32, bf16 or f16");
+    if (d->d > 256) return refuse(o + ": head dimension above 256 is not implemented");
+    return DM_OK;
+}
+
+// Launches the generic kernel, or the split pass and the merge.
+static int run_decode(const char *op, const dm_attention_desc *d, bool split, bool paged,
+                      const void *q, const void *k, const void *v, const int32_t *lengths,
+                      const KvMap &map, void *o, void *workspace, hipStream_t st) {
+    const std::string opn(op);
     const int64_t rows = d->b * d->hq;
-    if (rows == 0 || d->d == 0) return DM_OK;
     const float scale = scale_of(d);
     const int64_t left = left_of(d);
-    if (d->tk == 0) {
-        fill_zero(o, rows * d->d * dtype_bytes(d->dtype), st);
-        DM_LAUNCH_CHECK("attention_decode: fill");
-        return DM_OK;
-    }
-    if (!split_takes(d)) {
+    if (!split) {
         const int npl = d->d <= 64 ? 1 : (d->d <= 128 ? 2 : 4);
         dim3 grid((unsigned)((rows + 3) / 4));
-#define DEC_GEN(DT, NPL)                                                                    \
-    decode_generic<DT, NPL><<<grid, 256, 0, st>>>(d->b, d->tk, d->hq, d->hkv, d->d, left,   \
-                                                  scale, q, k, v, lengths, o)
+#define DEC_GEN2(DT, NPL, PG)                                                               \
+    decode_generic<DT, NPL, PG><<<grid, 256, 0, st>>>(d->b, d->tk, d->hq, d->hkv, d->d, left, \
+                                                      scale, q, k, v, lengths, map, o)
+#define DEC_GEN(DT, NPL)                                 \
+    if (paged) DEC_GEN2(DT, NPL, true); else DEC_GEN2(DT, NPL, false)
         if (d->dtype == DM_F32) {
             if (npl == 1) DEC_GEN(DM_F32, 1); else if (npl == 2) DEC_GEN(DM_F32, 2); else DEC_GEN(DM_F32, 4);
         } else if (d->dtype == DM_BF16) {
@@ -565,8 +620,9 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
             if (npl == 1) DEC_GEN(DM_F16, 1); else if (npl == 2) DEC_GEN(DM_F16, 2); else DEC_GEN(DM_F16, 4);
         }
 #undef DEC_GEN
+#undef DEC_GEN2
         probe_add(DM_PROBE_ATTN_FWD_GENERIC);
-        DM_LAUNCH_CHECK("attention_decode: launch");
+        DM_LAUNCH_CHECK((opn + ": launch").c_str());
         return DM_OK;
     }
     const int nsplit = nsplit_of(d), span = span_of(d);
@@ -580,7 +636,7 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
     const int g = (int)(d->hq / d->hkv);
 #define DEC_SPLIT(DT, DD, GG)                                                               \
     decode_split<DT, DD, GG><<<grid, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, span, \
-                                                   q, k, v, lengths, part_o, part_lse)
+                                                   q, k, v, lengths, map, part_o, part_lse)
 #define DEC_G(DT, DD)                                \
     switch (g) {                                     \
         case 1: DEC_SPLIT(DT, DD, 1); break;         \
@@ -588,9 +644,12 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         case 4: DEC_SPLIT(DT, DD, 4); break;         \
         default: DEC_SPLIT(DT, DD, 8); break;        \
     }
-#define DEC_MFMA(DT, GG)                                                                    \
-    decode_split_mfma<DT, GG><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, \
-                                                    span, q, k, v, lengths, part_o, part_lse)
+#define DEC_MFMA2(DT, GG, PG)                                                               \
+    decode_split_mfma<DT, GG, PG><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale,  \
+                                                           nsplit, span, q, k, v, lengths, map, \
+                                                           part_o, part_lse)
+#define DEC_MFMA(DT, GG)                             \
+    if (paged) DEC_MFMA2(DT, GG, true); else DEC_MFMA2(DT, GG, false)
 #define DEC_G128(DT)                                 \
     switch (g) {                                     \
         case 1: DEC_MFMA(DT, 1); break;              \
@@ -616,12 +675,92 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
 #undef DEC_D
 #undef DEC_G128
 #undef DEC_MFMA
+#undef DEC_MFMA2
 #undef DEC_G
 #undef DEC_SPLIT
     probe_add(DM_PROBE_DECODE_SPLIT);
     probe_add(DM_PROBE_DECODE_MERGE);
-    DM_LAUNCH_CHECK("attention_decode: launch");
+    DM_LAUNCH_CHECK((opn + ": launch").c_str());
     return DM_OK;
+}
+
+static size_t decode_workspace(const dm_attention_desc *d, bool split) {
+    if (!d || !split) return 0;
+    const size_t parts = (size_t)(d->b * d->hq) * nsplit_of(d);
+    return align_up(parts * d->d * sizeof(float)) + align_up(parts * sizeof(float));
+}
+
+}  // namespace dm
+
+using namespace dm;
+
+extern "C" {
+
+size_t dm_attention_decode_workspace(const dm_attention_desc *d) {
+    return d && d->hkv > 0 ? decode_workspace(d, split_takes(d)) : 0;
+}
+
+int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k, const void *v,
+                        const int32_t *lengths, void *o, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+    const char *op = "attention_decode";
+    if (int rc = check_decode(op, d)) return rc;
+    KvMap map{};
+    if (d->cu_seqlens_k) {
+        if (d->nseq != d->b)
+            return refuse("attention_decode: a packed cache takes cu_seqlens_k [B + 1] with "
+                          "nseq = B");
+        map.offsets = d->cu_seqlens_k;
+    }
+    if (workspace_bytes < dm_attention_decode_workspace(d))
+        return refuse("attention_decode: the workspace is smaller than dm_attention_decode_workspace");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t rows = d->b * d->hq;
+    if (rows == 0 || d->d == 0) return DM_OK;
+    if (d->tk == 0) {
+        fill_zero(o, rows * d->d * dtype_bytes(d->dtype), st);
+        DM_LAUNCH_CHECK("attention_decode: fill");
+        return DM_OK;
+    }
+    return run_decode(op, d, split_takes(d), false, q, k, v, lengths, map, o, workspace, st);
+}
+
+size_t dm_attention_decode_paged_workspace(const dm_attention_desc *d, int64_t page_size) {
+    return d && d->hkv > 0 ? decode_workspace(d, paged_split_takes(d, page_size)) : 0;
+}
+
+int dm_attention_decode_paged(const dm_attention_desc *d, const void *q, const void *k_pages,
+                              const void *v_pages, int64_t num_pages, int64_t page_size,
+                              const int32_t *block_table, int64_t max_pages,
+                              const int32_t *lengths, void *o, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+    const char *op = "attention_decode_paged";
+    if (int rc = check_decode(op, d)) return rc;
+    if (page_size < 1 || max_pages < 0 || num_pages < 0)
+        return refuse("attention_decode_paged: page_size must be positive, max_pages and "
+                      "num_pages not negative");
+    if (d->tk != max_pages * page_size)
+        return refuse("attention_decode_paged: desc->tk (" + std::to_string(d->tk) +
+                      ") must be max_pages * page_size (" + std::to_string(max_pages * page_size) +
+                      ")");
+    if (d->cu_seqlens_k)
+        return refuse("attention_decode_paged: a paged cache takes a block table, not cu_seqlens_k");
+    if (d->tk > 0 && d->b > 0 && !block_table)
+        return refuse("attention_decode_paged: the block table is [B, max_pages] int32");
+    if (workspace_bytes < dm_attention_decode_paged_workspace(d, page_size))
+        return refuse("attention_decode_paged: the workspace is smaller than "
+                      "dm_attention_decode_paged_workspace");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t rows = d->b * d->hq;
+    if (rows == 0 || d->d == 0) return DM_OK;
+    if (d->tk == 0) {
+        fill_zero(o, rows * d->d * dtype_bytes(d->dtype), st);
+        DM_LAUNCH_CHECK("attention_decode_paged: fill");
+        return DM_OK;
+    }
+    KvMap map{nullptr, block_table, page_size, max_pages, num_pages};
+    return run_decode(op, d, paged_split_takes(d, page_size), true, q, k_pages, v_pages, lengths,
+                      map, o, workspace, st);
 }
 
 }  // extern "C"

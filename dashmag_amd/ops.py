@@ -199,6 +199,110 @@ def attention_decode(query, key, value, lengths=None, options=None):
     return out
 
 
+def _decode_desc(op, query, key, value, tk, options):
+    """The descriptor of a decode over a cache whose rows are ``key.shape[-2:] = [Hkv, D]``."""
+    if query.dim() != 3:
+        raise Unsupported(f"{op}: query is [B, Hq, D]")
+    if tuple(key.shape) != tuple(value.shape):
+        raise Unsupported(f"{op}: key and value must have one shape")
+    b, hq, d = query.shape
+    hkv, dk = key.shape[-2], key.shape[-1]
+    if d != dk:
+        raise Unsupported(f"{op}: query and key must have one head dimension")
+    if hkv == 0 or hq % hkv != 0:
+        raise Unsupported(f"{op}: the query heads ({hq}) must be a multiple of the key-value "
+                          f"heads ({hkv})")
+    if not (query.dtype == key.dtype == value.dtype):
+        raise Unsupported(f"{op}: query, key and value must share one dtype")
+    desc = _lib.AttentionDesc(b=b, tq=1, tk=tk, hq=hq, hkv=hkv, d=d, dtype=_dtype(op, query),
+                              mask_kind=_lib.DM_MASK_NONE)
+    o = desc.options
+    o.has_scale = int(options.scale is not None)
+    o.scale = float(options.scale) if options.scale is not None else 0.0
+    o.has_window = int(options.window is not None)
+    if options.window is not None:
+        o.window_left = min(int(options.window.left), UNBOUNDED)
+        o.window_right = min(int(options.window.right), UNBOUNDED)
+    return desc
+
+
+def _cache_lengths(op, lengths, b, device):
+    if lengths is None:
+        return None
+    lt = torch.as_tensor(lengths)
+    if tuple(lt.shape) != (b,):
+        raise Unsupported(f"{op}: the cache lengths are [B] = [{b}]")
+    return _offsets(lt, device)
+
+
+def attention_decode_packed(query, key, value, cu_seqlens_k, lengths=None, options=None,
+                            max_len=None):
+    """Decoding against a packed cache ``key, value [N, Hkv, D]``: sequence ``b``'s keys are rows
+    ``cu_seqlens_k[b] .. cu_seqlens_k[b + 1] - 1``, the first ``lengths[b]`` of them (all
+    without lengths). The same operation as ``attention_decode`` (attention.rs:732) over a
+    cache that keeps each sequence at an offset; ``max_len`` bounds every sequence's span (by
+    default the longest span of ``cu_seqlens_k``)."""
+    op = "attention_decode"
+    options = options or AttentionOptions()
+    _device(op, query, key, value)
+    if key.dim() != 3:
+        raise Unsupported(f"{op}: a packed key cache is [N, Hkv, D]")
+    b = query.shape[0] if query.dim() == 3 else -1
+    cu = torch.as_tensor(cu_seqlens_k)
+    if cu.dim() != 1 or cu.shape[0] != b + 1:
+        raise Unsupported(f"{op}: cu_seqlens_k is [B + 1] = [{b + 1}]")
+    if max_len is None:
+        host = cu.detach().to("cpu", torch.int64)
+        max_len = int((host[1:] - host[:-1]).max()) if b > 0 else 0
+        if int(host.min()) < 0 or int(host.max()) > key.shape[0]:
+            raise Unsupported(f"{op}: cu_seqlens_k must lie within the cache's {key.shape[0]} "
+                              "rows")
+    desc = _decode_desc(op, query, key, value, max(int(max_len), 0), options)
+    cu = _offsets(cu, query.device)
+    desc.cu_seqlens_k, desc.nseq = cu.data_ptr(), b
+    ln = _cache_lengths(op, lengths, b, query.device)
+    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
+    out = torch.empty_like(q)
+    nbytes = _lib.lib().dm_attention_decode_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_attention_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
+                                              _ptr(ln), _ptr(out), _ptr(ws), nbytes, _stream()))
+    return out
+
+
+def attention_decode_paged(query, key_pages, value_pages, block_table, lengths=None,
+                           options=None):
+    """Decoding against a paged cache ``key_pages, value_pages [P, page_size, Hkv, D]``: key
+    ``j`` of sequence ``b`` is row ``j % page_size`` of page ``block_table[b, j // page_size]``
+    (``block_table [B, max_pages]`` int). The same operation as ``attention_decode``
+    (attention.rs:732) over the dense cache this table describes; sequence ``b`` holds its
+    first ``lengths[b]`` keys (all ``max_pages * page_size`` without lengths)."""
+    op = "attention_decode_paged"
+    options = options or AttentionOptions()
+    _device(op, query, key_pages, value_pages)
+    if key_pages.dim() != 4:
+        raise Unsupported(f"{op}: the key pages are [P, page_size, Hkv, D]")
+    b = query.shape[0] if query.dim() == 3 else -1
+    bt = torch.as_tensor(block_table)
+    if bt.dim() != 2 or bt.shape[0] != b:
+        raise Unsupported(f"{op}: the block table is [B, max_pages] with B = {b}")
+    npages, page_size = key_pages.shape[0], key_pages.shape[1]
+    if page_size < 1:
+        raise Unsupported(f"{op}: pages hold at least one key")
+    max_pages = bt.shape[1]
+    desc = _decode_desc(op, query, key_pages, value_pages, max_pages * page_size, options)
+    bt = _offsets(bt, query.device)
+    ln = _cache_lengths(op, lengths, b, query.device)
+    q, k, v = query.contiguous(), key_pages.contiguous(), value_pages.contiguous()
+    out = torch.empty_like(q)
+    nbytes = _lib.lib().dm_attention_decode_paged_workspace(ctypes.byref(desc), page_size)
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_attention_decode_paged(
+        ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v), npages, page_size, _ptr(bt), max_pages,
+        _ptr(ln), _ptr(out), _ptr(ws), nbytes, _stream()))
+    return out
+
+
 # ------------------------------------------------------------------------------------------
 # Gated delta rule
 # ------------------------------------------------------------------------------------------

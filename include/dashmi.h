@@ -7,6 +7,7 @@
  *                        (public fn attention_with_lse          crates/dash-ops/src/attention.rs:660)
  *   dm_attention_bwd     AttentionBackend::attention_backward   crates/dash-ops/src/attention.rs:689
  *   dm_attention_decode  AttentionBackend::attention_decode     crates/dash-ops/src/attention.rs:732
+ *   dm_attention_decode_paged  (none: the decode over a paged cache)
  *   dm_gdr_chunk_fwd     ChunkGatedDeltaBackend::chunk_gated_delta_forward
  *                                                               crates/dash-ops/src/gated_delta/chunk.rs:340-425, :856
  *   dm_gdr_chunk_bwd     ChunkGatedDeltaBackend::chunk_gated_delta_backward (the Autodiff node's
@@ -185,11 +186,33 @@ int dm_attention_bwd(const dm_attention_desc *desc, const void *q, const void *k
 /* Decoding: q [B, Hq, D] against the cache k, v [B, S, Hkv, D], sequence b holding its first
  * lengths[b] keys (all S when lengths is NULL); the options' scale and window left apply.
  * o [B, Hq, D] in dtype. Replaces attention.rs:732 / cube.rs:1126. `desc->tq` is unused,
- * desc->tk is S. */
+ * desc->tk is S.
+ * A packed cache (desc->cu_seqlens_k set, desc->nseq = B): k, v [N, Hkv, D], sequence b's keys in
+ * rows cu_seqlens_k[b] .. cu_seqlens_k[b + 1] - 1, the first lengths[b] of them (all when
+ * lengths is NULL), at most desc->tk = S of them (S bounds every sequence's span). The contract
+ * has only the dense form (crates/dash-contract/src/attention.rs:61-71); the packed form is the
+ * same operation over a cache that keeps each sequence's rows at an offset, and a dense cache is
+ * the packed one with offsets b * S. */
 size_t dm_attention_decode_workspace(const dm_attention_desc *desc);
 int dm_attention_decode(const dm_attention_desc *desc, const void *q, const void *k,
                         const void *v, const int32_t *lengths, void *o, void *workspace,
                         size_t workspace_bytes, void *stream);
+
+/* Decoding against a paged cache (no counterpart in the reference, whose decode takes the dense
+ * cache of crates/dash-contract/src/attention.rs:61-71; this is the same operation, with the
+ * dense cache's key j of sequence b stored at row j % page_size of page
+ * block_table[b * max_pages + j / page_size]): k_pages, v_pages [num_pages, page_size, Hkv, D],
+ * block_table [B, max_pages] int32, lengths [B] int32 or NULL (all max_pages * page_size keys).
+ * desc->tk must be max_pages * page_size; desc->cu_seqlens_k must be NULL. Only the pages that
+ * hold visible keys are read. A page index outside [0, num_pages) for a visible key reads as
+ * zeros (a wrong result, never an access outside the pages). D = 128 with pages of a multiple of
+ * 16 keys runs the split pass on MFMA; other shapes run the generic kernel. */
+size_t dm_attention_decode_paged_workspace(const dm_attention_desc *desc, int64_t page_size);
+int dm_attention_decode_paged(const dm_attention_desc *desc, const void *q, const void *k_pages,
+                              const void *v_pages, int64_t num_pages, int64_t page_size,
+                              const int32_t *block_table, int64_t max_pages,
+                              const int32_t *lengths, void *o, void *workspace,
+                              size_t workspace_bytes, void *stream);
 
 /* The chunked gated delta rule forward: out [B, T, H, Dv] in dtype and, if final_state is not
  * NULL, each sequence's final state [S, H, Dk, Dv] f32; h0 [S, H, Dk, Dv] f32 or NULL (zeros).

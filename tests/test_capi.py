@@ -81,3 +81,33 @@ def test_refusal_names_the_operation():
     rc = _lib.lib().dm_attention_fwd(ctypes.byref(d), None, None, None, None, None, None, 0, None)
     assert rc == _lib.DM_ERR_REFUSED
     assert _lib.last_error().startswith("attention: the query heads (3)")
+
+
+def test_paged_decode_refusals():
+    """The paged decode refuses before any launch: capacity and page size disagree, a packed
+    offset array instead of a block table, a missing block table."""
+    lb = _lib.lib()
+    d, _ = _desc(1, 64, False, None, None, _lib.DM_MASK_NONE)
+    d.dtype = _lib.DM_BF16
+    call = lambda ps, bt, mp: lb.dm_attention_decode_paged(  # noqa: E731
+        ctypes.byref(d), None, None, None, 4, ps, bt, mp, None, None, None, 0, None)
+    assert call(16, None, 3) == _lib.DM_ERR_REFUSED
+    assert _lib.last_error().startswith("attention_decode_paged: desc->tk (64)")
+    assert call(0, None, 4) == _lib.DM_ERR_REFUSED
+    assert "page_size must be positive" in _lib.last_error()
+    assert call(16, None, 4) == _lib.DM_ERR_REFUSED
+    assert "block table" in _lib.last_error()
+    ck = np.zeros(2, np.int32)
+    d.cu_seqlens_k = ck.ctypes.data
+    assert call(16, None, 4) == _lib.DM_ERR_REFUSED
+    assert "not cu_seqlens_k" in _lib.last_error()
+
+
+def test_packed_decode_refuses_a_wrong_sequence_count():
+    d, _ = _desc(1, 8, False, None, None, _lib.DM_MASK_NONE)
+    ck = np.zeros(3, np.int32)
+    d.cu_seqlens_k, d.nseq = ck.ctypes.data, 2
+    rc = _lib.lib().dm_attention_decode(ctypes.byref(d), None, None, None, None, None, None, 0,
+                                        None)
+    assert rc == _lib.DM_ERR_REFUSED
+    assert _lib.last_error().startswith("attention_decode: a packed cache")
