@@ -294,3 +294,35 @@ def conv1d_update(x, weight, bias, state, silu=False, precision="f32"):
            _p(state), _p(out), _p(nxt))
     assert rc == 0
     return out, nxt
+
+
+class _Logprob(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_int64), ("v", ctypes.c_int64), ("d", ctypes.c_int64),
+        ("targets", ctypes.c_void_p), ("masked", ctypes.c_void_p), ("n_masked", ctypes.c_int64),
+        ("vocab_chunk", ctypes.c_int64), ("row_chunk", ctypes.c_int64),
+    ]
+
+
+def chosen_logprob(hidden, weight, targets, masked=(), vocab_chunk=0, row_chunk=3072,
+                   with_grad=True, precision="f32"):
+    """The chosen-token log-probability and entropy (logprob/reference.rs:64-287): ``hidden``
+    ``[n, D]``, ``weight`` ``[V, D]``, ``targets`` ``[n]``, ``masked`` token ids (any order,
+    each ``< V``); returns ``(logprob [n], entropy [n], grad [n, D] or None)``, ``grad`` the
+    gradient of each ``logprob[i]`` with respect to ``hidden[i]``."""
+    hidden, weight = _f32(hidden), _f32(weight)
+    targets = _i64(targets)
+    n, d = hidden.shape
+    v = weight.shape[0]
+    ids = np.unique(np.asarray(masked, np.int64)).astype(np.uint32)
+    assert np.all(ids < v), "masked ids lie below V"
+    assert row_chunk >= 1
+    s = _Logprob(n=n, v=v, d=d, targets=targets.ctypes.data, masked=ids.ctypes.data if ids.size
+                 else None, n_masked=ids.size, vocab_chunk=int(vocab_chunk),
+                 row_chunk=int(row_chunk))
+    lp, ent = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    grad = np.zeros((n, d), np.float32) if with_grad else None
+    rc = getattr(lib(), f"dmo_logprob_{precision}")(ctypes.byref(s), _p(hidden), _p(weight),
+                                                   _p(lp), _p(ent), _p(grad))
+    assert rc == 0
+    return lp, ent, grad

@@ -2,7 +2,8 @@
  *
  * TEST INFRASTRUCTURE ONLY: a plain-C restatement of dash-ops' reference implementations
  * (crates/dash-ops/src/attention/reference.rs, crates/dash-ops/src/gated_delta/chunk/reference.rs,
- * crates/dash-ops/src/gated_delta/recurrent.rs:309-404, crates/dash-ops/src/conv1d/reference.rs),
+ * crates/dash-ops/src/gated_delta/recurrent.rs:309-404, crates/dash-ops/src/conv1d/reference.rs,
+ * crates/dash-ops/src/logprob/reference.rs),
  * compiled in f32 (the reference's own
  * precision, suffix _f32) and in f64 (suffix _f64). Only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg load it, as the checker and as the timed CPU baseline; the product
@@ -58,6 +59,16 @@ typedef struct {
     int64_t w_out;
 } dmo_conv1d;
 
+/* One chosen-token log-probability call (crates/dash-contract/src/logprob.rs): hidden [n, D],
+ * weight [V, D], targets [n]; masked sorted and free of repeats; LogprobOptions. */
+typedef struct {
+    int64_t n, v, d;
+    const int64_t *targets;
+    const uint32_t *masked;
+    int64_t n_masked;
+    int64_t vocab_chunk, row_chunk;
+} dmo_logprob;
+
 /* The sequence of `n` positions cut by `cu` [s + 1] that holds position `at`: the number of
  * ends at or before it, clamped into 0..s (reference.rs:118-159 `sequences`), and whether any
  * sequence holds it. */
@@ -107,6 +118,7 @@ int dmo_attention_visible(const dmo_attention *a, int64_t b, int64_t i, int64_t 
 #define SQRT sqrtf
 #include "oracle_body.h"
 #include "oracle_conv1d.h"
+#include "oracle_logprob.h"
 #undef R
 #undef FN
 #undef EXP
@@ -120,6 +132,7 @@ int dmo_attention_visible(const dmo_attention *a, int64_t b, int64_t i, int64_t 
 #define SQRT sqrt
 #include "oracle_body.h"
 #include "oracle_conv1d.h"
+#include "oracle_logprob.h"
 #undef R
 #undef FN
 #undef EXP
