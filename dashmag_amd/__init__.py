@@ -1,5 +1,5 @@
-"""dashmag_amd: dash-ops' attention, gated-delta-rule and causal-conv1d hot path, native to
-MI355X (gfx950).
+"""dashmag_amd: dash-ops' attention, gated-delta-rule, causal-conv1d and chosen-token
+log-probability hot path, native to MI355X (gfx950).
 
 The operations run as hand-written HIP kernels in ``libdashmi.so`` behind the C ABI of
 ``include/dashmi.h``; this package is the host-side mirror of dash-ops' operation interface
@@ -7,18 +7,20 @@ The operations run as hand-written HIP kernels in ``libdashmi.so`` behind the C 
 """
 from .contract import (Activation, AttentionMask, AttentionOptions, CausalConv1dOptions,
                        CausalConv1dStepOptions, ChunkGatedDeltaOptions, DType,
-                       GatedDeltaStepOptions, UNBOUNDED, Unsupported, Window)
+                       GatedDeltaStepOptions, LogprobOptions, UNBOUNDED, Unsupported, Window)
 from .ops import (attention, attention_backward, attention_decode, attention_decode_packed,
                   attention_decode_paged, attention_with_lse,
-                  causal_conv1d, causal_conv1d_backward, causal_conv1d_update,
+                  causal_conv1d, causal_conv1d_backward, causal_conv1d_update, chosen_logprob,
+                  chosen_logprob_with_grad,
                   chunk_gated_delta_rule, chunk_gated_delta_rule_backward, gated_delta_step)
 
 __all__ = [
     "Activation", "AttentionMask", "AttentionOptions", "CausalConv1dOptions",
     "CausalConv1dStepOptions", "ChunkGatedDeltaOptions", "DType",
-    "GatedDeltaStepOptions", "UNBOUNDED", "Unsupported", "Window",
+    "GatedDeltaStepOptions", "LogprobOptions", "UNBOUNDED", "Unsupported", "Window",
     "attention", "attention_backward", "attention_decode", "attention_decode_packed",
     "attention_decode_paged", "attention_with_lse",
-    "causal_conv1d", "causal_conv1d_backward", "causal_conv1d_update",
+    "causal_conv1d", "causal_conv1d_backward", "causal_conv1d_update", "chosen_logprob",
+    "chosen_logprob_with_grad",
     "chunk_gated_delta_rule", "chunk_gated_delta_rule_backward", "gated_delta_step",
 ]

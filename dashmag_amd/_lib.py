@@ -16,7 +16,7 @@ DM_UNBOUNDED = (1 << 64) - 1
 
 PROBES = ["attn_fwd_mfma", "attn_fwd_generic", "attn_bwd_mfma", "attn_bwd_generic",
           "decode_split", "decode_merge", "gdr_chunk_fwd", "gdr_chunk_bwd", "gdr_step",
-          "conv1d_fwd", "conv1d_bwd", "conv1d_update"]
+          "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob"]
 DM_ACT_NONE, DM_ACT_SILU = 0, 1
 
 
@@ -54,10 +54,17 @@ class Conv1dDesc(ctypes.Structure):
                 ("has_final", ctypes.c_int32), ("w_out", ctypes.c_int64)]
 
 
+class LogprobDesc(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_int64), ("v", ctypes.c_int64), ("d", ctypes.c_int64),
+                ("hidden_dtype", ctypes.c_int32), ("weight_dtype", ctypes.c_int32),
+                ("vocab_chunk", ctypes.c_int64), ("row_chunk", ctypes.c_int64)]
+
+
 #: Every symbol include/dashmi.h declares, with (restype, argtypes).
 _VP, _SZ, _I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64
 _AD, _GD = ctypes.POINTER(AttentionDesc), ctypes.POINTER(GdrDesc)
 _CD = ctypes.POINTER(Conv1dDesc)
+_LD = ctypes.POINTER(LogprobDesc)
 SIGNATURES = {
     "dm_last_error": (ctypes.c_char_p, []),
     "dm_describe": (ctypes.c_int, [ctypes.c_char_p, _SZ]),
@@ -75,6 +82,9 @@ SIGNATURES = {
                                         _SZ, _VP]),
     "dm_attention_decode_workspace": (_SZ, [_AD]),
     "dm_attention_decode": (ctypes.c_int, [_AD, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "dm_chosen_logprob_workspace": (_SZ, [_LD, ctypes.c_int]),
+    "dm_chosen_logprob": (ctypes.c_int, [_LD, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP,
+                                         _SZ, _VP]),
     "dm_attention_decode_paged_workspace": (_SZ, [_AD, ctypes.c_int64]),
     "dm_attention_decode_paged": (ctypes.c_int, [_AD, _VP, _VP, _VP, ctypes.c_int64,
                                                  ctypes.c_int64, _VP, ctypes.c_int64, _VP, _VP,
@@ -130,7 +140,7 @@ def probe_reset() -> None:
 
 KERNELS = ["attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "decode_split", "gdr_prep", "gdr_state",
            "gdr_output", "gdr_step", "gdr_bwd_pre", "gdr_bwd_state", "gdr_bwd_grads",
-           "conv1d_fwd", "conv1d_bwd", "conv1d_update"]
+           "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob_stats"]
 
 
 def kernel_timing(enable: bool) -> None:

@@ -179,6 +179,16 @@ class CausalConv1dStepOptions:
         return CausalConv1dStepOptions(options.activation)
 
 
+@dataclasses.dataclass(frozen=True)
+class LogprobOptions:
+    """How the vocabulary and the rows are chunked (crates/dash-contract/src/logprob.rs:33-56):
+    ``vocab_chunk`` tokens per chunk (0: 4096 for row blocks below 2304 rows, else 8192,
+    crates/dash-ops/src/logprob.rs:90-101), ``row_chunk`` the most rows per block."""
+
+    vocab_chunk: int = 0
+    row_chunk: int = 3072
+
+
 def query_scale(scale: Optional[float], dk: int) -> float:
     """The gated delta rule's query scale: ``1/sqrt(Dk)`` unless given
     (crates/dash-ops/src/gated_delta.rs:17)."""

@@ -19,7 +19,7 @@ import torch
 from . import _lib
 from .contract import (Activation, AttentionMask, AttentionOptions, CausalConv1dOptions,
                        CausalConv1dStepOptions, ChunkGatedDeltaOptions, GatedDeltaStepOptions,
-                       UNBOUNDED, Unsupported)
+                       LogprobOptions, UNBOUNDED, Unsupported)
 
 _DT = {torch.float32: _lib.DM_F32, torch.bfloat16: _lib.DM_BF16, torch.float16: _lib.DM_F16}
 
@@ -611,3 +611,59 @@ def causal_conv1d_update(x, weight, bias, state,
                                                   _ptr(bc), _ptr(st_in), _ptr(out), _ptr(st_out),
                                                   _stream()))
     return out, st_out
+
+
+# ------------------------------------------------------------------------------------------
+# Chosen-token log-probability
+# ------------------------------------------------------------------------------------------
+
+def _logprob(hidden, weight, targets, masked, options, with_grad):
+    op = "chosen_logprob"
+    options = options or LogprobOptions()
+    _device(op, hidden, weight)
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise Unsupported(f"{op}: hidden [n, D] and weight [V, D] must share D, got "
+                          f"{list(hidden.shape)}, {list(weight.shape)}")
+    for t in (hidden, weight):
+        if t.dtype not in (torch.bfloat16, torch.float32):
+            raise Unsupported(f"{op}: the log-probability takes bf16 or f32")
+    n, d = hidden.shape
+    v = weight.shape[0]
+    tg = torch.as_tensor(targets)
+    if tuple(tg.shape) != (n,):
+        raise Unsupported(f"{op}: targets must be [n] = [{n}]")
+    tg = tg.to(device=hidden.device, dtype=torch.int64).contiguous()
+    ids = [int(i) for i in masked]
+    if any(i < 0 for i in ids):
+        raise Unsupported(f"{op}: masked token ids are not negative")
+    ids_c = (ctypes.c_uint32 * max(len(ids), 1))(*ids)
+    desc = _lib.LogprobDesc(n=n, v=v, d=d, hidden_dtype=_dtype(op, hidden),
+                            weight_dtype=_dtype(op, weight),
+                            vocab_chunk=int(options.vocab_chunk), row_chunk=int(options.row_chunk))
+    h, w = hidden.contiguous(), weight.contiguous()
+    lp = torch.empty(n, dtype=torch.float32, device=h.device)
+    ent = torch.empty(n, dtype=torch.float32, device=h.device)
+    grad = torch.empty(n, d, dtype=torch.float32, device=h.device) if with_grad else None
+    nbytes = _lib.lib().dm_chosen_logprob_workspace(ctypes.byref(desc), int(with_grad))
+    ws = _workspace(nbytes, h.device)
+    _check(op, _lib.lib().dm_chosen_logprob(ctypes.byref(desc), _ptr(h), _ptr(w), _ptr(tg),
+                                            ctypes.cast(ids_c, ctypes.c_void_p), len(ids),
+                                            _ptr(lp), _ptr(ent), _ptr(grad), _ptr(ws), nbytes,
+                                            _stream()))
+    return lp, ent, grad
+
+
+def chosen_logprob(hidden, weight, targets, masked=(), options=None):
+    """``(logprob [n], entropy [n])`` f32 of ``targets`` under ``softmax(hidden weightᵀ)`` without
+    the ``masked`` token ids (crates/dash-ops/src/logprob.rs:127-138; the contract's definition,
+    crates/dash-contract/src/logprob.rs:4-15): ``hidden`` ``[n, D]``, ``weight`` ``[V, D]``, bf16
+    or f32; a masked or out-of-range target gives ``-inf``."""
+    lp, ent, _ = _logprob(hidden, weight, targets, masked, options, False)
+    return lp, ent
+
+
+def chosen_logprob_with_grad(hidden, weight, targets, masked=(), options=None):
+    """``(logprob, entropy, grad [n, D] f32)``, ``grad[i]`` the gradient of ``logprob[i]`` with
+    respect to ``hidden[i]`` (logprob.rs:140-160); the backward of the log-probability is
+    ``upstream[:, None] * grad``, cast to ``hidden``'s dtype (logprob.rs:160-190)."""
+    return _logprob(hidden, weight, targets, masked, options, True)

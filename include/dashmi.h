@@ -18,6 +18,8 @@
  *                                                               crates/dash-ops/src/conv1d.rs:300-329
  *   dm_causal_conv1d_update  CausalConv1dBackend::causal_conv1d_update
  *                                                               crates/dash-ops/src/conv1d.rs:331-360, :750
+ *   dm_chosen_logprob    ChosenLogprobBackend::chosen_logprob{,_with_grad}
+ *                                                               crates/dash-ops/src/logprob.rs:127-160
  *
  * Conventions (crates/dash-contract/src/lib.rs:38-91):
  *   - Every tensor is a device pointer to a contiguous array in the contract's layout:
@@ -109,6 +111,17 @@ typedef struct {
     int64_t w_out;
 } dm_conv1d_desc;
 
+/* One chosen-token log-probability call (crates/dash-contract/src/logprob.rs:17-56): hidden
+ * [n, D], weight [V, D], each DM_BF16 or DM_F32 (bf16 arithmetic where both are bf16, else both
+ * taken as f32); LogprobOptions (logprob.rs:33-56): vocab_chunk tokens per chunk (0: 4096 for
+ * row blocks below 2304 rows, else 8192, crates/dash-ops/src/logprob.rs:90-101), row_chunk the
+ * most rows per block (at least 1; dash-ops' default 3072). */
+typedef struct {
+    int64_t n, v, d;
+    int32_t hidden_dtype, weight_dtype;
+    int64_t vocab_chunk, row_chunk;
+} dm_logprob_desc;
+
 /* The message of this thread's last refusal or error. */
 const char *dm_last_error(void);
 
@@ -132,6 +145,7 @@ typedef enum {
     DM_PROBE_CONV1D_FWD,
     DM_PROBE_CONV1D_BWD,
     DM_PROBE_CONV1D_UPDATE,
+    DM_PROBE_LOGPROB,
     DM_PROBE_COUNT
 } dm_probe;
 uint64_t dm_probe_count(int probe);
@@ -156,6 +170,7 @@ typedef enum {
     DM_KERNEL_CONV1D_FWD,     /* causal conv1d forward */
     DM_KERNEL_CONV1D_BWD,     /* causal conv1d backward: the input gradient and the partial sums */
     DM_KERNEL_CONV1D_UPDATE,  /* causal conv1d decoding step */
+    DM_KERNEL_LOGPROB_STATS,  /* chosen-token log-probability: the per-chunk statistics */
     DM_KERNEL_COUNT
 } dm_kernel;
 int dm_kernel_timing(int enable);
@@ -265,6 +280,22 @@ int dm_causal_conv1d_bwd(const dm_conv1d_desc *desc, const void *x, const void *
 int dm_causal_conv1d_update(const dm_conv1d_desc *desc, const void *x, const void *weight,
                             const void *bias, const float *state, void *out, float *next_state,
                             void *stream);
+
+/* The chosen-token log-probability and entropy (crates/dash-contract/src/logprob.rs:4-15):
+ * logits z = hidden weight^T over the vocabulary minus the masked ids, never all held;
+ * logprob [n] f32 = z[t] - logsumexp z (-inf where the target is masked or outside [0, V)),
+ * entropy [n] f32; with grad (not NULL), grad [n, D] f32 = d logprob[i] / d hidden[i], which the
+ * caller scales by the upstream gradient (the backward of logprob.rs:160-190). targets [n] int64
+ * on the device; masked: n_masked token ids on the HOST (the reference's Vec<u32>), any order,
+ * each below V, at least one token left unmasked. Replaces ChosenLogprobBackend::chosen_logprob
+ * and chosen_logprob_with_grad (logprob.rs:127-160). The logits' and the gradient's products
+ * run as rocBLAS GEMMs on the stream; the online log-sum-exp between them as this library's
+ * kernels. */
+size_t dm_chosen_logprob_workspace(const dm_logprob_desc *desc, int with_grad);
+int dm_chosen_logprob(const dm_logprob_desc *desc, const void *hidden, const void *weight,
+                      const int64_t *targets, const uint32_t *masked, int64_t n_masked,
+                      float *logprob, float *entropy, float *grad, void *workspace,
+                      size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -111,3 +111,31 @@ def test_packed_decode_refuses_a_wrong_sequence_count():
                                         None)
     assert rc == _lib.DM_ERR_REFUSED
     assert _lib.last_error().startswith("attention_decode: a packed cache")
+
+
+def test_logprob_refusals():
+    """The log-probability refuses before any launch: a masked id outside the vocabulary, every
+    token masked, an f16 operand, a zero row_chunk."""
+    lb = _lib.lib()
+    d = _lib.LogprobDesc(n=4, v=5, d=8, hidden_dtype=_lib.DM_BF16, weight_dtype=_lib.DM_BF16,
+                         vocab_chunk=0, row_chunk=3072)
+
+    def call(ids):
+        arr = (ctypes.c_uint32 * max(len(ids), 1))(*ids)
+        return lb.dm_chosen_logprob(ctypes.byref(d), None, None, None,
+                                    ctypes.cast(arr, ctypes.c_void_p), len(ids), None, None,
+                                    None, None, 0, None)
+
+    assert call([7]) == _lib.DM_ERR_REFUSED
+    assert _lib.last_error() == ("chosen_logprob: masked token id 7 is not below the "
+                                 "vocabulary size 5")
+    assert call([4, 3, 2, 1, 0, 0]) == _lib.DM_ERR_REFUSED
+    assert _lib.last_error() == "chosen_logprob: at least one token must stay unmasked"
+    assert call([1, 1]) == _lib.DM_ERR_REFUSED  # passes the ids, stops at the workspace
+    assert "workspace" in _lib.last_error()
+    d.hidden_dtype = _lib.DM_F16
+    assert call([]) == _lib.DM_ERR_REFUSED
+    assert _lib.last_error() == "chosen_logprob: the log-probability takes bf16 or f32"
+    d.hidden_dtype, d.row_chunk = _lib.DM_BF16, 0
+    assert call([]) == _lib.DM_ERR_REFUSED
+    assert _lib.last_error() == "chosen_logprob: row_chunk must be at least 1"
