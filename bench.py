@@ -39,7 +39,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step,conv1d")
+    p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step,conv1d,logprob")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (torch copy_), 5 times: the known-size "
                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
@@ -399,6 +399,44 @@ def main():
               f"{ms_b * 1e3:.1f} us ({bwd_bytes / ms_b / 1e6:.0f} GB/s), step {ms_u * 1e3:.1f} us",
               file=sys.stderr, flush=True)
         del c, x, go, out, gx
+
+    # ---- chosen-token log-probability, config 7 (after the model: the next row) ----
+    if want("logprob"):
+        c = syn.logprob_config(dev)
+        h, wt, tg, masked = c["hidden"], c["weight"], c["targets"], c["masked"]
+        n, d = h.shape
+        v = wt.shape[0]
+        desc = _lib.LogprobDesc(n=n, v=v, d=d, hidden_dtype=_lib.DM_BF16,
+                                weight_dtype=_lib.DM_BF16, vocab_chunk=0, row_chunk=3072)
+        ids = (ctypes.c_uint32 * len(masked))(*masked)
+        lp = torch.empty(n, dtype=torch.float32, device=dev)
+        ent, grad = torch.empty_like(lp), torch.empty(n, d, dtype=torch.float32, device=dev)
+        nb = lib.dm_chosen_logprob_workspace(ctypes.byref(desc), 1)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        P = lambda tt: None if tt is None else ctypes.c_void_p(tt.data_ptr())  # noqa: E731
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+        def lp_call(g):
+            check(lib.dm_chosen_logprob(ctypes.byref(desc), P(h), P(wt), P(tg),
+                                        ctypes.cast(ids, ctypes.c_void_p), len(masked), P(lp),
+                                        P(ent), P(g), P(ws), nb, st), lib)
+
+        tfw, tgr = Timed(torch, lambda: lp_call(None)), Timed(torch, lambda: lp_call(grad))
+        ms_f = tfw.run(max(args.steps, 5), args.warmup)
+        ms_g = tgr.run(max(args.steps, 5), args.warmup)
+        # algorithmic flops: the logits (2 n V D) and, with the gradient, its product (2 n V D)
+        fl = 2 * n * v * d
+        kus = {k: round(v_[0] * 1e3, 2) for k, v_ in tgr.kernel_ms.items()}
+        secondary["logprob"] = dict(
+            unit="TFLOP/s", workload=f"chosen-token logprob, bf16, n={n}, D={d}, V={v}, "
+            f"{len(masked)} masked ids, default chunking",
+            fwd_ms=ms_f, fwd_TFLOPs=fl / ms_f / 1e9, fwd_frac_of_mfma_peak=fl / ms_f / 1e9 / BF16_PEAK_TFLOPS,
+            grad_ms=ms_g, grad_TFLOPs=2 * fl / ms_g / 1e9,
+            grad_frac_of_mfma_peak=2 * fl / ms_g / 1e9 / BF16_PEAK_TFLOPS,
+            rows_per_s=n / ms_g * 1e3, kernel_us=kus)
+        print(f"logprob: fwd {ms_f:.2f} ms ({fl / ms_f / 1e9:.0f} TFLOP/s), with gradient "
+              f"{ms_g:.2f} ms ({2 * fl / ms_g / 1e9:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+        del c, h, wt, grad, ws
 
     # ---- CPU baseline: the oracle on a bounded sample of config 2 ----
     cpu = None

@@ -51,10 +51,10 @@ def build(verbose=False, jobs=8) -> str:
                 print(err, file=sys.stderr)
     objs = [o for o, _ in results]
     tmp = LIB + ".tmp"
-    # rocBLAS for the log-probability's plain GEMMs (the logits and the gradient's products)
+    # hipBLASLt for the log-probability's plain GEMMs (the logits and the gradient's products)
     rocm_lib = os.path.join(os.path.dirname(os.path.dirname(HIPCC)), "lib")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-           f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lrocblas"]
+           f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lhipblaslt"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

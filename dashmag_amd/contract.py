@@ -182,8 +182,9 @@ class CausalConv1dStepOptions:
 @dataclasses.dataclass(frozen=True)
 class LogprobOptions:
     """How the vocabulary and the rows are chunked (crates/dash-contract/src/logprob.rs:33-56):
-    ``vocab_chunk`` tokens per chunk (0: 4096 for row blocks below 2304 rows, else 8192,
-    crates/dash-ops/src/logprob.rs:90-101), ``row_chunk`` the most rows per block."""
+    ``vocab_chunk`` tokens per chunk (0: the implementation's own choice, 8192 tokens here;
+    dash-ops takes 4096 below 2304 rows, crates/dash-ops/src/logprob.rs:90-101), ``row_chunk``
+    the most rows per block."""
 
     vocab_chunk: int = 0
     row_chunk: int = 3072

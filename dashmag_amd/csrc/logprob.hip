@@ -3,7 +3,7 @@
 // crates/dash-ops/src/logprob.rs:1-56, logprob/reference.rs:64-287).
 //
 // For a block of rows and a chunk of C vocabulary tokens:
-//   1. Z [rows, C] f32 = hidden · weight_cᵀ, one library GEMM (rocBLAS, bf16 operands with f32
+//   1. Z [rows, C] f32 = hidden · weight_cᵀ, one library GEMM (hipBLASLt, bf16 operands with f32
 //      accumulation, or f32 throughout): the logits are never held for more than one chunk;
 //   2. lp_stats, one workgroup per row: the masked online log-sum-exp of the chunk (running
 //      maximum m, s = Σ e^{z-m}, a = Σ e^{z-m}(z-m) for the entropy, r = s without the target's
@@ -20,7 +20,7 @@
 //
 // Roofline: two GEMMs of 2 n V D flops each (one without the gradient; the remainder's GEMM is a
 // third), bound by MFMA; lp_stats moves 12 bytes per logit (Z read, E written as two bf16 parts).
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <cfloat>
 #include <algorithm>
@@ -36,6 +36,7 @@ namespace dm {
 enum { LP_M = 0, LP_S, LP_R, LP_A, LP_ZT, LP_FOUND, LP_NSTATE };
 
 constexpr int kLpThreads = 256;
+constexpr int64_t kLpMaxChunk = 8192;  // 1024 columns per register group, 8 groups
 
 __device__ __forceinline__ bool lp_masked(const uint32_t *bits, int64_t tok) {
     return (bits[tok >> 5] >> (tok & 31)) & 1u;
@@ -70,23 +71,57 @@ __global__ __launch_bounds__(kLpThreads) void lp_init(int64_t rows, int64_t D, f
         for (int64_t e = threadIdx.x; e < D; e += kLpThreads) o[row * D + e] = 0.f;
 }
 
-// The masked words of the vocabulary: bit j of word j / 32 set for a masked token.
+// One row's statistics for one chunk, each logit read once: thread t holds columns
+// 4 t + 1024 i + q (i < NV, q < 4) in registers (16-byte loads when the chunk width is a multiple
+// of 4), so a chunk of up to 1024 NV columns is read from memory once. `bits` holds the masked
+// words of the vocabulary (bit j of word j / 32 set for a masked token).
 // EK: 0 no gradient, 1 the weights as bf16 part + remainder, 2 the weights in f32.
-template <int EK>
+template <int EK, int NV>
 __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw, int64_t c0,
                                                        int64_t D, const float *__restrict__ Z,
                                                        const int64_t *__restrict__ targets,
                                                        const uint32_t *__restrict__ bits,
                                                        float *__restrict__ st, int64_t nst,
-                                                       void *__restrict__ E, float *__restrict__ o) {
+                                                       void *__restrict__ E, void *__restrict__ E2,
+                                                       float *__restrict__ o) {
     __shared__ float sm[4];
     const int64_t row = blockIdx.x;
     if (row >= rows) return;
     const float *z = Z + row * cw;
+    const bool vec = (cw & 3) == 0;
+    float x[NV][4];
+    uint32_t live = 0;  // bit 4 i + q: column 4 t + 1024 i + q is in the chunk and unmasked
     // the chunk's maximum over the unmasked tokens
     float mx = -FLT_MAX;
-    for (int64_t j = threadIdx.x; j < cw; j += kLpThreads)
-        if (!lp_masked(bits, c0 + j)) mx = fmaxf(mx, z[j]);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int64_t j = 4 * (int64_t)threadIdx.x + 1024 * i;
+        if (vec && j < cw) {
+            const float4 v = *(const float4 *)(z + j);
+            x[i][0] = v.x, x[i][1] = v.y, x[i][2] = v.z, x[i][3] = v.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) x[i][q] = j + q < cw ? z[j + q] : -FLT_MAX;
+        }
+        // the masked bits of the 4 columns: one word when they share it
+        const int64_t tok = c0 + j;
+        uint32_t mb = 0;
+        if (j < cw) {
+            if ((tok & 31) <= 28) {
+                mb = bits[tok >> 5] >> (tok & 31);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (j + q < cw) mb |= (uint32_t)lp_masked(bits, tok + q) << q;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (j + q < cw && !((mb >> q) & 1u)) {
+                live |= 1u << (4 * i + q);
+                mx = fmaxf(mx, x[i][q]);
+            }
+    }
     mx = lp_block_max(mx, sm);
     const float m = st[LP_M * nst + row];
     const float m_new = mx > m ? mx : m;
@@ -96,30 +131,56 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
     const bool has_t = tl >= 0 && tl < cw && !lp_masked(bits, t);
     // the chunk's sums; the weights of the next product (0 for the target and masked tokens)
     float se = 0.f, sa = 0.f, sr = 0.f;
-    for (int64_t j = threadIdx.x; j < cw; j += kLpThreads) {
-        float e = 0.f;
-        if (!lp_masked(bits, c0 + j)) {
-            const float dz = z[j] - m_new;
-            e = expf(dz);
-            se += e;
-            sa += e * dz;
-            if (j == tl) e = 0.f;
-            sr += e;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int64_t j = 4 * (int64_t)threadIdx.x + 1024 * i;
+        if (j >= cw) continue;
+        float e[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            e[q] = 0.f;
+            if ((live >> (4 * i + q)) & 1u) {
+                const float dz = x[i][q] - m_new;
+                e[q] = expf(dz);
+                se += e[q];
+                sa += e[q] * dz;
+                if (j + q == tl) e[q] = 0.f;
+                sr += e[q];
+            }
         }
         if constexpr (EK == 1) {
-            const uint16_t hi = f32_to_bf16(e);
-            const uint16_t lo = f32_to_bf16(e - bf16_to_f32(hi));
-            ((uint16_t *)E)[row * cw + j] = hi;
-            ((uint16_t *)E)[rows * cw + row * cw + j] = lo;
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                hi[q] = f32_to_bf16(e[q]);
+                lo[q] = f32_to_bf16(e[q] - bf16_to_f32(hi[q]));
+            }
+            uint16_t *eh = (uint16_t *)E + row * cw + j, *el = (uint16_t *)E2 + row * cw + j;
+            if (vec) {
+                *(uint2 *)eh = make_uint2(hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16);
+                *(uint2 *)el = make_uint2(lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (j + q < cw) eh[q] = hi[q], el[q] = lo[q];
+            }
         } else if constexpr (EK == 2) {
-            ((float *)E)[row * cw + j] = e;
+            float *ef = (float *)E + row * cw + j;
+            if (vec) {
+                *(float4 *)ef = make_float4(e[0], e[1], e[2], e[3]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (j + q < cw) ef[q] = e[q];
+            }
         }
     }
     se = lp_block_sum(se, sm);
     sa = lp_block_sum(sa, sm);
     sr = lp_block_sum(sr, sm);
     if constexpr (EK != 0) {
-        if (alpha != 1.f)
+        // o is still zero while nothing has been summed (the first chunk)
+        if (alpha != 1.f && st[LP_S * nst + row] != 0.f)
             for (int64_t e = threadIdx.x; e < D; e += kLpThreads) o[row * D + e] *= alpha;
     }
     if (threadIdx.x == 0) {
@@ -172,33 +233,96 @@ __global__ void lp_widen(int64_t count, const uint16_t *__restrict__ x, float *_
         y[i] = bf16_to_f32(x[i]);
 }
 
-// One rocBLAS handle per (thread, device); each call sets its stream.
-static rocblas_handle lp_handle(hipStream_t st) {
-    thread_local std::map<int, rocblas_handle> handles;
+// hipBLASLt: one handle per (thread, device); per GEMM shape, the descriptors and the
+// heuristic's first algorithm, kept for the process.
+constexpr size_t kLtWorkspace = 64u << 20;  // the library's workspace, part of ours
+
+struct LtGemm {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    bool ok = false;
+};
+
+static hipblasLtHandle_t lt_handle() {
+    thread_local std::map<int, hipblasLtHandle_t> handles;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     auto it = handles.find(dev);
     if (it == handles.end()) {
-        rocblas_handle h = nullptr;
-        if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+        hipblasLtHandle_t h = nullptr;
+        if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return nullptr;
         it = handles.emplace(dev, h).first;
     }
-    if (rocblas_set_stream(it->second, st) != rocblas_status_success) return nullptr;
     return it->second;
+}
+
+// Column-major D (m x n, ld m) = op(A) op(B) + beta D, f32 out, f32 accumulation; A and B of
+// type `t`, A stored m x k (ta = N, lda m) or k x m (ta = T, lda k), B k x n (ld k).
+static int lt_gemm(hipStream_t st, bool ta, int64_t m, int64_t n, int64_t k, const void *A,
+                   const void *B, hipDataType t, float beta, float *Dm, void *ws) {
+    hipblasLtHandle_t h = lt_handle();
+    if (!h) {
+        set_error("chosen_logprob: no hipBLASLt handle");
+        return DM_ERR_HIP;
+    }
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    thread_local std::map<std::vector<int64_t>, LtGemm> cache;
+    const std::vector<int64_t> key{dev, ta, m, n, k, (int64_t)t, beta != 0.f};
+    LtGemm &g = cache[key];
+    if (!g.desc) {
+        const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = HIPBLAS_OP_N;
+        bool good = hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+        good = good && hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa,
+                                                       sizeof(opa)) == HIPBLAS_STATUS_SUCCESS;
+        good = good && hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb,
+                                                       sizeof(opb)) == HIPBLAS_STATUS_SUCCESS;
+        good = good && hipblasLtMatrixLayoutCreate(&g.a, t, ta ? k : m, ta ? m : k, ta ? k : m) == HIPBLAS_STATUS_SUCCESS;
+        good = good && hipblasLtMatrixLayoutCreate(&g.b, t, k, n, k) == HIPBLAS_STATUS_SUCCESS;
+        good = good && hipblasLtMatrixLayoutCreate(&g.c, HIP_R_32F, m, n, m) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulPreference_t pref = nullptr;
+        good = good && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+        const uint64_t wsb = kLtWorkspace;
+        good = good && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                             &wsb, sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulHeuristicResult_t res[1];
+        int found = 0;
+        good = good && hipblasLtMatmulAlgoGetHeuristic(h, g.desc, g.a, g.b, g.c, g.c, pref, 1, res,
+                                                       &found) == HIPBLAS_STATUS_SUCCESS;
+        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        g.ok = good && found > 0 && res[0].workspaceSize <= kLtWorkspace;
+        if (g.ok) g.algo = res[0].algo;
+    }
+    if (!g.ok) {
+        set_error("chosen_logprob: hipBLASLt has no algorithm for a " + std::to_string(m) + " x " +
+                  std::to_string(n) + " x " + std::to_string(k) + " product");
+        return DM_ERR_HIP;
+    }
+    const float one = 1.f;
+    const hipblasStatus_t s = hipblasLtMatmul(h, g.desc, &one, A, g.a, B, g.b, &beta, Dm, g.c, Dm,
+                                              g.c, &g.algo, ws, kLtWorkspace, st);
+    if (s != HIPBLAS_STATUS_SUCCESS) {
+        set_error("chosen_logprob: hipBLASLt matmul failed (status " + std::to_string((int)s) + ")");
+        return DM_ERR_HIP;
+    }
+    return DM_OK;
 }
 
 struct LpPlan {
     int64_t block, chunk;  // rows per block, vocabulary tokens per chunk
     bool bf16;             // both operands bf16 (else both taken as f32)
-    size_t off_bits, off_state, off_z, off_e, off_h, off_w, total;
+    size_t off_bits, off_state, off_z, off_e, off_h, off_w, off_lt, total;
 };
 
 static LpPlan lp_plan(const dm_logprob_desc *d, bool grad) {
     LpPlan p{};
     const int64_t nb = d->n > 0 ? (d->n + d->row_chunk - 1) / d->row_chunk : 1;
     p.block = std::max<int64_t>(1, (d->n + nb - 1) / nb);
-    p.chunk = d->vocab_chunk > 0 ? d->vocab_chunk : (p.block < 2304 ? 4096 : 8192);
-    p.chunk = std::min<int64_t>(p.chunk, std::max<int64_t>(d->v, 1));
+    // 0: 8192 tokens (measured best on MI355X for every block size); wider chunks are walked
+    // 8192 tokens at a time (the statistics kernel holds a chunk's logits in registers)
+    p.chunk = d->vocab_chunk > 0 ? d->vocab_chunk : kLpMaxChunk;
+    p.chunk = std::min<int64_t>({p.chunk, kLpMaxChunk, std::max<int64_t>(d->v, 1)});
     p.bf16 = d->hidden_dtype == DM_BF16 && d->weight_dtype == DM_BF16;
     size_t o = 0;
     p.off_bits = o;
@@ -208,11 +332,13 @@ static LpPlan lp_plan(const dm_logprob_desc *d, bool grad) {
     p.off_z = o;
     o += align_up((size_t)p.block * p.chunk * 4);
     p.off_e = o;
-    if (grad) o += align_up((size_t)p.block * p.chunk * 4);  // two bf16 parts or one f32
+    if (grad) o += align_up((size_t)p.block * p.chunk * 4) + 256;  // two bf16 parts or one f32
     p.off_h = o;
     if (!p.bf16 && d->hidden_dtype == DM_BF16) o += align_up((size_t)d->n * d->d * 4);
     p.off_w = o;
     if (!p.bf16 && d->weight_dtype == DM_BF16) o += align_up((size_t)d->v * d->d * 4);
+    p.off_lt = o;
+    o += kLtWorkspace;
     p.total = o;
     return p;
 }
@@ -222,20 +348,16 @@ static int lp_check(const dm_logprob_desc *d) {
     if (d->n < 0 || d->v < 1 || d->d < 1)
         return refuse("chosen_logprob: hidden is [n, D] and weight [V, D] with V, D >= 1");
     if (d->row_chunk < 1) return refuse("chosen_logprob: row_chunk must be at least 1");
+    if (d->d % 8 != 0)
+        return refuse("chosen_logprob: hidden widths D that are not a multiple of 8 are not "
+                      "implemented");
     if (d->vocab_chunk < 0) return refuse("chosen_logprob: vocab_chunk must not be negative");
     for (int dt : {d->hidden_dtype, d->weight_dtype})
         if (dt != DM_BF16 && dt != DM_F32)
             return refuse("chosen_logprob: the log-probability takes bf16 or f32");
-    if (d->d > INT32_MAX || d->v > INT32_MAX)
-        return refuse("chosen_logprob: V and D must fit the GEMMs' 32-bit sizes");
     return DM_OK;
 }
 
-static int lp_gemm_status(rocblas_status s) {
-    if (s == rocblas_status_success) return DM_OK;
-    set_error(std::string("chosen_logprob: rocBLAS GEMM failed: ") + rocblas_status_to_string(s));
-    return DM_ERR_HIP;
-}
 
 }  // namespace dm
 
@@ -299,15 +421,9 @@ int dm_chosen_logprob(const dm_logprob_desc *d, const void *hidden, const void *
         }
         DM_LAUNCH_CHECK("chosen_logprob: widen");
     }
-    const rocblas_datatype op_t = p.bf16 ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
+    const hipDataType op_t = p.bf16 ? HIP_R_16BF : HIP_R_32F;
     const size_t esz = p.bf16 ? 2 : 4;
-    rocblas_handle h = lp_handle(st);
-    if (!h) {
-        set_error("chosen_logprob: no rocBLAS handle");
-        return DM_ERR_HIP;
-    }
-    const float one = 1.f, zero = 0.f;
-    const int D = (int)d->d;
+    void *lt_ws = ws + p.off_lt;
     for (int64_t r0 = 0; r0 < d->n; r0 += p.block) {
         const int64_t rows = std::min<int64_t>(p.block, d->n - r0);
         float *o = want_grad ? grad + r0 * d->d : nullptr;
@@ -315,39 +431,36 @@ int dm_chosen_logprob(const dm_logprob_desc *d, const void *hidden, const void *
         DM_LAUNCH_CHECK("chosen_logprob: init");
         const char *Hb = (const char *)H + (size_t)r0 * d->d * esz;
         for (int64_t c0 = 0; c0 < d->v; c0 += p.chunk) {
-            const int cw = (int)std::min<int64_t>(p.chunk, d->v - c0);
+            const int64_t cw = std::min<int64_t>(p.chunk, d->v - c0);
+            // the bf16 remainder after the part, at an aligned offset
+            void *E2 = (char *)E + align_up((size_t)rows * cw * 2);
             const char *Wc = (const char *)W + (size_t)c0 * d->d * esz;
-            // Z (column-major cw x rows, i.e. [rows, cw] row-major) = W_c H^T
-            int rc = lp_gemm_status(rocblas_gemm_ex(
-                h, rocblas_operation_transpose, rocblas_operation_none, cw, (int)rows, D, &one, Wc,
-                op_t, D, Hb, op_t, D, &zero, Z, rocblas_datatype_f32_r, cw, Z,
-                rocblas_datatype_f32_r, cw, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
-                rocblas_gemm_flags_none));
-            if (rc) return rc;
+            // Z (column-major cw x rows, i.e. [rows, cw] row-major) = W_c H^T: W_c is stored
+            // D x cw column-major, so op(A) = T
+            if (int rc = lt_gemm(st, true, cw, rows, d->d, Wc, Hb, op_t, 0.f, Z, lt_ws)) return rc;
             {
                 KernelTimer timer(DM_KERNEL_LOGPROB_STATS, st);
-                if (!want_grad)
-                    lp_stats<0><<<(unsigned)rows, kLpThreads, 0, st>>>(
-                        rows, cw, c0, d->d, Z, targets + r0, dbits, state + r0, d->n, nullptr, nullptr);
-                else if (p.bf16)
-                    lp_stats<1><<<(unsigned)rows, kLpThreads, 0, st>>>(
-                        rows, cw, c0, d->d, Z, targets + r0, dbits, state + r0, d->n, E, o);
-                else
-                    lp_stats<2><<<(unsigned)rows, kLpThreads, 0, st>>>(
-                        rows, cw, c0, d->d, Z, targets + r0, dbits, state + r0, d->n, E, o);
+                const int nv = (int)((cw + 1023) / 1024);
+#define LP_STATS(EK, NV, EE, OO)                                                                   lp_stats<EK, NV><<<(unsigned)rows, kLpThreads, 0, st>>>(rows, cw, c0, d->d, Z, targets + r0,                                                             dbits, state + r0, d->n, EE, E2, OO)
+#define LP_NV(EK, EE, OO)                                                                          if (nv <= 1) LP_STATS(EK, 1, EE, OO);                                                          else if (nv <= 2) LP_STATS(EK, 2, EE, OO);                                                     else if (nv <= 4) LP_STATS(EK, 4, EE, OO);                                                     else LP_STATS(EK, 8, EE, OO)
+                if (!want_grad) {
+                    LP_NV(0, nullptr, nullptr);
+                } else if (p.bf16) {
+                    LP_NV(1, E, o);
+                } else {
+                    LP_NV(2, E, o);
+                }
+#undef LP_NV
+#undef LP_STATS
             }
             DM_LAUNCH_CHECK("chosen_logprob: stats");
             if (want_grad) {
-                // o (column-major D x rows) += W_c^T-as-stored (D x cw) E^T (cw x rows)
+                // o (column-major D x rows) += W_c as stored (D x cw) E^T (cw x rows)
                 const int parts = p.bf16 ? 2 : 1;
                 for (int part = 0; part < parts; part++) {
-                    const char *Ep = (const char *)E + (size_t)part * rows * cw * 2;
-                    rc = lp_gemm_status(rocblas_gemm_ex(
-                        h, rocblas_operation_none, rocblas_operation_none, D, (int)rows, cw, &one,
-                        Wc, op_t, D, Ep, op_t, cw, &one, o, rocblas_datatype_f32_r, D, o,
-                        rocblas_datatype_f32_r, D, rocblas_datatype_f32_r,
-                        rocblas_gemm_algo_standard, 0, rocblas_gemm_flags_none));
-                    if (rc) return rc;
+                    const void *Ep = part ? E2 : E;
+                    if (int rc = lt_gemm(st, false, d->d, rows, cw, Wc, Ep, op_t, 1.f, o, lt_ws))
+                        return rc;
                 }
             }
         }

@@ -179,6 +179,19 @@ def conv1d_config(device="cpu", dtype=torch.bfloat16, c=6144, k=4, w=3, b_step=1
                 step_state=state)
 
 
+def logprob_config(device="cpu", dtype=torch.bfloat16, n=4096, d=4096, v=151936, n_masked=64):
+    """Config 7: the chosen-token log-probability after a model's last layer. hidden [n, D]
+    N(0, 1), the output weight [V, D] N(0, 0.02^2) (V = 151936, a Qwen-family vocabulary; logits
+    of standard deviation about 1.3), targets uniform in [0, V), n_masked distinct masked ids
+    (tensor indices: hidden 0, weight 1, targets 7, masked ids 2)."""
+    hidden = as_input(normal(seed_of(7, Q), (n, d), device), dtype)
+    weight = as_input(normal(seed_of(7, K), (v, d), device, std=0.02), dtype)
+    targets = (uniform(seed_of(7, LENGTHS), n, device) * v).to(torch.int64).clamp_(0, v - 1)
+    order = torch.argsort(uniform(seed_of(7, V), v))
+    masked = sorted(order[:n_masked].tolist())
+    return dict(hidden=hidden, weight=weight, targets=targets, masked=masked)
+
+
 def _config4_cuts(total=32768, nseq=8):
     """Config 4's sequence boundaries (see config4)."""
     u = uniform(seed_of(4, LENGTHS), 1024).tolist()

@@ -113,9 +113,10 @@ typedef struct {
 
 /* One chosen-token log-probability call (crates/dash-contract/src/logprob.rs:17-56): hidden
  * [n, D], weight [V, D], each DM_BF16 or DM_F32 (bf16 arithmetic where both are bf16, else both
- * taken as f32); LogprobOptions (logprob.rs:33-56): vocab_chunk tokens per chunk (0: 4096 for
- * row blocks below 2304 rows, else 8192, crates/dash-ops/src/logprob.rs:90-101), row_chunk the
- * most rows per block (at least 1; dash-ops' default 3072). */
+ * taken as f32); LogprobOptions (logprob.rs:33-56): vocab_chunk tokens per chunk (0: this
+ * implementation's own choice, 8192; dash-ops' is 4096 below 2304 rows,
+ * crates/dash-ops/src/logprob.rs:90-101), row_chunk the most rows per block (at least 1;
+ * dash-ops' default 3072). */
 typedef struct {
     int64_t n, v, d;
     int32_t hidden_dtype, weight_dtype;
@@ -289,8 +290,9 @@ int dm_causal_conv1d_update(const dm_conv1d_desc *desc, const void *x, const voi
  * on the device; masked: n_masked token ids on the HOST (the reference's Vec<u32>), any order,
  * each below V, at least one token left unmasked. Replaces ChosenLogprobBackend::chosen_logprob
  * and chosen_logprob_with_grad (logprob.rs:127-160). The logits' and the gradient's products
- * run as rocBLAS GEMMs on the stream; the online log-sum-exp between them as this library's
- * kernels. */
+ * run as hipBLASLt GEMMs on the stream; the online log-sum-exp between them as this library's
+ * kernels. vocab_chunk 0 walks 8192 tokens a chunk, and wider chunks are walked 8192 tokens at a
+ * time. D must be a multiple of 8. */
 size_t dm_chosen_logprob_workspace(const dm_logprob_desc *desc, int with_grad);
 int dm_chosen_logprob(const dm_logprob_desc *desc, const void *hidden, const void *weight,
                       const int64_t *targets, const uint32_t *masked, int64_t n_masked,
