@@ -326,3 +326,52 @@ def chosen_logprob(hidden, weight, targets, masked=(), vocab_chunk=0, row_chunk=
                                                    _p(lp), _p(ent), _p(grad))
     assert rc == 0
     return lp, ent, grad
+
+
+class _Lce(ctypes.Structure):
+    _fields_ = [("lp", _Logprob), ("ignore_index", ctypes.c_int64), ("eps", ctypes.c_float),
+                ("lam", ctypes.c_float), ("entropy", ctypes.c_int32)]
+
+
+def _lce(hidden, weight, targets, masked, vocab_chunk, row_chunk, ignore_index, eps, lam,
+         entropy):
+    hidden, weight = _f32(hidden), _f32(weight)
+    targets = _i64(targets)
+    ids = np.unique(np.asarray(masked, np.int64)).astype(np.uint32)
+    assert np.all(ids < weight.shape[0])
+    lp = _Logprob(n=hidden.shape[0], v=weight.shape[0], d=hidden.shape[1],
+                  targets=targets.ctypes.data, masked=ids.ctypes.data if ids.size else None,
+                  n_masked=ids.size, vocab_chunk=int(vocab_chunk), row_chunk=int(row_chunk))
+    s = _Lce(lp=lp, ignore_index=int(ignore_index), eps=float(eps), lam=float(lam),
+             entropy=int(bool(entropy)))
+    return s, hidden, weight, (targets, ids)
+
+
+def linear_cross_entropy_fwd(hidden, weight, targets, masked=(), vocab_chunk=0, row_chunk=3072,
+                             ignore_index=-100, eps=0.0, lam=0.0, entropy=False,
+                             precision="f32"):
+    """The fused linear cross-entropy's per-row outputs (loss.rs:411-525): ``rows`` ``[8, n]``
+    f32 = loss, logprob, entropy, lse, q (1 - p(target)), s, counted, found."""
+    s, hidden, weight, keep = _lce(hidden, weight, targets, masked, vocab_chunk, row_chunk,
+                                   ignore_index, eps, lam, entropy)
+    rows = np.zeros((8, hidden.shape[0]), np.float32)
+    rc = getattr(lib(), f"dmo_lce_fwd_{precision}")(ctypes.byref(s), _p(hidden), _p(weight),
+                                                   _p(rows))
+    assert rc == 0
+    return rows
+
+
+def linear_cross_entropy_bwd(hidden, weight, targets, rows, upstream, masked=(), vocab_chunk=0,
+                             row_chunk=3072, ignore_index=-100, eps=0.0, lam=0.0, entropy=False,
+                             precision="f32"):
+    """Its gradients (loss.rs:527-668 and logprob/reference.rs:289-380) from ``rows`` and the
+    upstream gradients ``[3, n]`` of the loss, logprob and entropy rows: ``(grad_hidden [n, D],
+    grad_weight [V, D])`` f32."""
+    s, hidden, weight, keep = _lce(hidden, weight, targets, masked, vocab_chunk, row_chunk,
+                                   ignore_index, eps, lam, entropy)
+    rows, upstream = _f32(rows), _f32(upstream)
+    gh, gw = np.zeros_like(hidden), np.zeros_like(weight)
+    rc = getattr(lib(), f"dmo_lce_bwd_{precision}")(ctypes.byref(s), _p(hidden), _p(weight),
+                                                   _p(rows), _p(upstream), _p(gh), _p(gw))
+    assert rc == 0
+    return gh, gw

@@ -3,7 +3,7 @@
  * TEST INFRASTRUCTURE ONLY: a plain-C restatement of dash-ops' reference implementations
  * (crates/dash-ops/src/attention/reference.rs, crates/dash-ops/src/gated_delta/chunk/reference.rs,
  * crates/dash-ops/src/gated_delta/recurrent.rs:309-404, crates/dash-ops/src/conv1d/reference.rs,
- * crates/dash-ops/src/logprob/reference.rs),
+ * crates/dash-ops/src/logprob/reference.rs, crates/dash-ops/src/loss.rs),
  * compiled in f32 (the reference's own
  * precision, suffix _f32) and in f64 (suffix _f64). Only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg load it, as the checker and as the timed CPU baseline; the product
@@ -69,6 +69,15 @@ typedef struct {
     int64_t vocab_chunk, row_chunk;
 } dmo_logprob;
 
+/* One fused linear cross-entropy call (crates/dash-contract/src/loss.rs): the log-probability's
+ * shapes, ids and chunks, and CrossEntropyOptions (reduction aside: the rows are per row). */
+typedef struct {
+    dmo_logprob lp;
+    int64_t ignore_index;
+    float eps, lambda;
+    int32_t entropy;
+} dmo_lce;
+
 /* The sequence of `n` positions cut by `cu` [s + 1] that holds position `at`: the number of
  * ends at or before it, clamped into 0..s (reference.rs:118-159 `sequences`), and whether any
  * sequence holds it. */
@@ -119,6 +128,7 @@ int dmo_attention_visible(const dmo_attention *a, int64_t b, int64_t i, int64_t 
 #include "oracle_body.h"
 #include "oracle_conv1d.h"
 #include "oracle_logprob.h"
+#include "oracle_loss.h"
 #undef R
 #undef FN
 #undef EXP
@@ -133,6 +143,7 @@ int dmo_attention_visible(const dmo_attention *a, int64_t b, int64_t i, int64_t 
 #include "oracle_body.h"
 #include "oracle_conv1d.h"
 #include "oracle_logprob.h"
+#include "oracle_loss.h"
 #undef R
 #undef FN
 #undef EXP
