@@ -16,7 +16,7 @@ DM_UNBOUNDED = (1 << 64) - 1
 
 PROBES = ["attn_fwd_mfma", "attn_fwd_generic", "attn_bwd_mfma", "attn_bwd_generic",
           "decode_split", "decode_merge", "gdr_chunk_fwd", "gdr_chunk_bwd", "gdr_step",
-          "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob"]
+          "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob", "lce_fwd", "lce_bwd"]
 DM_ACT_NONE, DM_ACT_SILU = 0, 1
 
 
@@ -60,11 +60,18 @@ class LogprobDesc(ctypes.Structure):
                 ("vocab_chunk", ctypes.c_int64), ("row_chunk", ctypes.c_int64)]
 
 
+class LceDesc(ctypes.Structure):
+    _fields_ = [("lp", LogprobDesc), ("ignore_index", ctypes.c_int64),
+                ("label_smoothing", ctypes.c_float), ("z_loss", ctypes.c_float),
+                ("entropy", ctypes.c_int32)]
+
+
 #: Every symbol include/dashmi.h declares, with (restype, argtypes).
 _VP, _SZ, _I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64
 _AD, _GD = ctypes.POINTER(AttentionDesc), ctypes.POINTER(GdrDesc)
 _CD = ctypes.POINTER(Conv1dDesc)
 _LD = ctypes.POINTER(LogprobDesc)
+_XD = ctypes.POINTER(LceDesc)
 SIGNATURES = {
     "dm_last_error": (ctypes.c_char_p, []),
     "dm_describe": (ctypes.c_int, [ctypes.c_char_p, _SZ]),
@@ -82,6 +89,11 @@ SIGNATURES = {
                                         _SZ, _VP]),
     "dm_attention_decode_workspace": (_SZ, [_AD]),
     "dm_attention_decode": (ctypes.c_int, [_AD, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "dm_linear_cross_entropy_workspace": (_SZ, [_XD, ctypes.c_int]),
+    "dm_linear_cross_entropy_fwd": (ctypes.c_int, [_XD, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _SZ,
+                                                   _VP]),
+    "dm_linear_cross_entropy_bwd": (ctypes.c_int, [_XD, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP,
+                                                   _VP, _VP, _SZ, _VP]),
     "dm_chosen_logprob_workspace": (_SZ, [_LD, ctypes.c_int]),
     "dm_chosen_logprob": (ctypes.c_int, [_LD, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP,
                                          _SZ, _VP]),

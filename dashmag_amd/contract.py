@@ -190,6 +190,29 @@ class LogprobOptions:
     row_chunk: int = 3072
 
 
+class Reduction(enum.Enum):
+    """How linear_cross_entropy reduces the rows' losses, as torch's ``reduction``
+    (crates/dash-contract/src/loss.rs:52-63)."""
+
+    MEAN = "mean"
+    SUM = "sum"
+    NONE = "none"
+
+
+@dataclasses.dataclass(frozen=True)
+class CrossEntropyOptions:
+    """crates/dash-contract/src/loss.rs:65-95: torch's ``F.cross_entropy`` defaults (the mean,
+    ignore index -100, no label smoothing), no z-loss, no masked id, no entropy."""
+
+    reduction: Reduction = Reduction.MEAN
+    ignore_index: int = -100
+    label_smoothing: float = 0.0
+    z_loss: float = 0.0
+    masked: tuple = ()
+    entropy: bool = False
+    chunks: LogprobOptions = LogprobOptions()
+
+
 def query_scale(scale: Optional[float], dk: int) -> float:
     """The gated delta rule's query scale: ``1/sqrt(Dk)`` unless given
     (crates/dash-ops/src/gated_delta.rs:17)."""

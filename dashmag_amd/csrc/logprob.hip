@@ -22,8 +22,10 @@
 // third), bound by MFMA; lp_stats moves 12 bytes per logit (Z read, E written as two bf16 parts).
 #include <hipblaslt/hipblaslt.h>
 
-#include <cfloat>
 #include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <functional>
 #include <map>
 #include <string>
 #include <vector>
@@ -33,7 +35,7 @@
 
 namespace dm {
 
-enum { LP_M = 0, LP_S, LP_R, LP_A, LP_ZT, LP_FOUND, LP_NSTATE };
+enum { LP_M = 0, LP_S, LP_R, LP_A, LP_ZT, LP_FOUND, LP_ZSUM, LP_NSTATE };
 
 constexpr int kLpThreads = 256;
 constexpr int64_t kLpMaxChunk = 8192;  // 1024 columns per register group, 8 groups
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
     const int64_t tl = t - c0;
     const bool has_t = tl >= 0 && tl < cw && !lp_masked(bits, t);
     // the chunk's sums; the weights of the next product (0 for the target and masked tokens)
-    float se = 0.f, sa = 0.f, sr = 0.f;
+    float se = 0.f, sa = 0.f, sr = 0.f, sz = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int64_t j = 4 * (int64_t)threadIdx.x + 1024 * i;
@@ -144,6 +146,7 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
                 e[q] = expf(dz);
                 se += e[q];
                 sa += e[q] * dz;
+                sz += x[i][q];
                 if (j + q == tl) e[q] = 0.f;
                 sr += e[q];
             }
@@ -176,6 +179,7 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
         }
     }
     se = lp_block_sum(se, sm);
+    sz = lp_block_sum(sz, sm);
     sa = lp_block_sum(sa, sm);
     sr = lp_block_sum(sr, sm);
     if constexpr (EK != 0) {
@@ -193,6 +197,7 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
             st[LP_FOUND * nst + row] += 1.f;
         }
         st[LP_M * nst + row] = m_new;
+        st[LP_ZSUM * nst + row] += sz;
     }
 }
 
@@ -233,6 +238,121 @@ __global__ void lp_widen(int64_t count, const uint16_t *__restrict__ x, float *_
         y[i] = bf16_to_f32(x[i]);
 }
 
+// ------------------------------------------------------------------------------------------
+// The fused linear cross-entropy (crates/dash-contract/src/loss.rs; crates/dash-ops/src/loss.rs)
+// ------------------------------------------------------------------------------------------
+
+enum { LCE_LOSS = 0, LCE_LOGPROB, LCE_ENTROPY, LCE_LSE, LCE_Q, LCE_S, LCE_COUNTED, LCE_FOUND };
+enum { LC_A = 0, LC_T, LC_E, LC_C, LC_COUNT };
+
+// The rows' outputs from the pass's sums (loss.rs:456-525 finish): rows [8, n] = loss, logprob,
+// entropy (0 on an ignored row), lse, q = r / s (1 - p(target)), s, counted, found.
+__global__ void lce_finish(int64_t n, const float *__restrict__ st, const int64_t *__restrict__ targets,
+                           int64_t ignore_index, float eps, float lam, float inv_classes,
+                           float *__restrict__ rows) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float m = st[LP_M * n + i], s = st[LP_S * n + i], r = st[LP_R * n + i];
+    const float a = st[LP_A * n + i], zt = st[LP_ZT * n + i], zsum = st[LP_ZSUM * n + i];
+    const bool seen = st[LP_FOUND * n + i] > 0.5f, counted = targets[i] != ignore_index;
+    const float ln_s = logf(s), lse = m + ln_s;
+    float loss = 0.f;
+    if (eps < 1.f) loss = (1.f - eps) * (seen ? lse - zt : INFINITY);
+    if (eps != 0.f) loss += eps * (lse - zsum * inv_classes);
+    if (lam != 0.f) loss += lam * (lse * lse);
+    rows[LCE_LOSS * n + i] = counted ? loss : 0.f;
+    rows[LCE_LOGPROB * n + i] = counted ? (seen ? zt - lse : -INFINITY) : 0.f;
+    rows[LCE_ENTROPY * n + i] = counted ? ln_s - a / s : 0.f;
+    rows[LCE_LSE * n + i] = lse;
+    rows[LCE_Q * n + i] = r / s;
+    rows[LCE_S * n + i] = s;
+    rows[LCE_COUNTED * n + i] = counted ? 1.f : 0.f;
+    rows[LCE_FOUND * n + i] = seen ? 1.f : 0.f;
+}
+
+// The gradient pass's coefficients per row (loss.rs:597-668) from the upstream gradients of the
+// loss, logprob and entropy rows (0 on an ignored row): A = gl (1 + 2 lambda lse) - gp - ge H,
+// the target's value T + C (T = gl (eps + 2 lambda lse) - q (gl (1 + 2 lambda lse) - gp)
+// - (1 - q)(ge H + ge logprob) where found), E = ge (with the entropy), C = -gl eps / K.
+__global__ void lce_coef(int64_t n, const float *__restrict__ rows,
+                         const float *__restrict__ upstream, float eps, float lam,
+                         float inv_classes, int entropy, float *__restrict__ coef) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const bool counted = rows[LCE_COUNTED * n + i] > 0.5f;
+    const float gl = counted ? upstream[i] : 0.f, gp = counted ? upstream[n + i] : 0.f;
+    const float ge = entropy && counted ? upstream[2 * n + i] : 0.f;
+    const float lse = rows[LCE_LSE * n + i], q = rows[LCE_Q * n + i];
+    float soft = gl - gp;
+    if (lam != 0.f) soft += gl * (lse * 2.f * lam);
+    float tgt = -q * soft;
+    float glt = gl * eps;
+    if (lam != 0.f) glt += gl * (lse * 2.f * lam);
+    tgt += glt;
+    if (entropy) {
+        const float ent = ge * rows[LCE_ENTROPY * n + i];
+        soft -= ent;
+        const float pt = 1.f - q;
+        tgt -= pt * ent + ge * pt * rows[LCE_LOGPROB * n + i];
+    }
+    const float c = -gl * eps * inv_classes;
+    coef[LC_A * n + i] = soft;
+    coef[LC_T * n + i] = (rows[LCE_FOUND * n + i] > 0.5f ? tgt : 0.f) + c;
+    coef[LC_E * n + i] = ge;
+    coef[LC_C * n + i] = c;
+}
+
+// The logits' gradient of a chunk (logprob/reference.rs:345-366): g = e^{z - lse}(A - E (z - lse))
+// + C, T + C at the target, 0 at a masked id; written as bf16 (BF = true, the products' operand,
+// as torch's bf16 linear layer rounds its output's gradient) or f32. One row per workgroup.
+template <bool BF>
+__global__ __launch_bounds__(kLpThreads) void lce_dz(int64_t rows, int64_t cw, int64_t c0,
+                                                     const float *__restrict__ Z,
+                                                     const int64_t *__restrict__ targets,
+                                                     const uint32_t *__restrict__ bits,
+                                                     const float *__restrict__ rowsv,
+                                                     const float *__restrict__ coef, int64_t n,
+                                                     void *__restrict__ G) {
+    const int64_t row = blockIdx.x;
+    if (row >= rows) return;
+    const float lse = rowsv[LCE_LSE * n + row], A = coef[LC_A * n + row];
+    const float T = coef[LC_T * n + row], E = coef[LC_E * n + row], C = coef[LC_C * n + row];
+    const int64_t tl = targets[row] - c0;
+    const float *z = Z + row * cw;
+    for (int64_t j = threadIdx.x; j < cw; j += kLpThreads) {
+        float g;
+        if (lp_masked(bits, c0 + j)) {
+            g = 0.f;
+        } else if (j == tl) {
+            g = T;
+        } else {
+            const float dz = z[j] - lse;
+            g = expf(dz) * (A - E * dz) + C;
+        }
+        if constexpr (BF)
+            ((uint16_t *)G)[row * cw + j] = f32_to_bf16(g);
+        else
+            ((float *)G)[row * cw + j] = g;
+    }
+}
+
+// f32 -> the dtype (a copy for f32), and fills with zeros.
+__global__ void lp_cast(int64_t count, const float *__restrict__ x, void *__restrict__ y, int dt) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x)
+        st_any(dt, y, i, x[i]);
+}
+__global__ void lp_zero(int64_t count, float *__restrict__ x) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = 0.f;
+}
+__global__ void lp_widen16(int64_t count, const _Float16 *__restrict__ x, float *__restrict__ y) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = (float)x[i];
+}
+
 // hipBLASLt: one handle per (thread, device); per GEMM shape, the descriptors and the
 // heuristic's first algorithm, kept for the process.
 constexpr size_t kLtWorkspace = 64u << 20;  // the library's workspace, part of ours
@@ -258,28 +378,31 @@ static hipblasLtHandle_t lt_handle() {
 }
 
 // Column-major D (m x n, ld m) = op(A) op(B) + beta D, f32 out, f32 accumulation; A and B of
-// type `t`, A stored m x k (ta = N, lda m) or k x m (ta = T, lda k), B k x n (ld k).
-static int lt_gemm(hipStream_t st, bool ta, int64_t m, int64_t n, int64_t k, const void *A,
-                   const void *B, hipDataType t, float beta, float *Dm, void *ws) {
+// type `t`, A stored m x k (ta = N, lda m) or k x m (ta = T, lda k), B stored k x n (tb = N,
+// ldb k) or n x k (tb = T, ldb n).
+static int lt_gemm(hipStream_t st, bool ta, bool tb, int64_t m, int64_t n, int64_t k,
+                   const void *A, const void *B, hipDataType t, float beta, float *Dm, void *ws) {
     hipblasLtHandle_t h = lt_handle();
     if (!h) {
-        set_error("chosen_logprob: no hipBLASLt handle");
+        set_error("no hipBLASLt handle");
         return DM_ERR_HIP;
     }
     int dev = 0;
     (void)hipGetDevice(&dev);
     thread_local std::map<std::vector<int64_t>, LtGemm> cache;
-    const std::vector<int64_t> key{dev, ta, m, n, k, (int64_t)t, beta != 0.f};
+    const std::vector<int64_t> key{dev, ta, tb, m, n, k, (int64_t)t, beta != 0.f};
     LtGemm &g = cache[key];
     if (!g.desc) {
-        const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = HIPBLAS_OP_N;
+        const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+        const hipblasOperation_t opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
         bool good = hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
         good = good && hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa,
                                                        sizeof(opa)) == HIPBLAS_STATUS_SUCCESS;
         good = good && hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb,
                                                        sizeof(opb)) == HIPBLAS_STATUS_SUCCESS;
         good = good && hipblasLtMatrixLayoutCreate(&g.a, t, ta ? k : m, ta ? m : k, ta ? k : m) == HIPBLAS_STATUS_SUCCESS;
-        good = good && hipblasLtMatrixLayoutCreate(&g.b, t, k, n, k) == HIPBLAS_STATUS_SUCCESS;
+        good = good && hipblasLtMatrixLayoutCreate(&g.b, t, tb ? n : k, tb ? k : n, tb ? n : k) ==
+                           HIPBLAS_STATUS_SUCCESS;
         good = good && hipblasLtMatrixLayoutCreate(&g.c, HIP_R_32F, m, n, m) == HIPBLAS_STATUS_SUCCESS;
         hipblasLtMatmulPreference_t pref = nullptr;
         good = good && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
@@ -295,7 +418,7 @@ static int lt_gemm(hipStream_t st, bool ta, int64_t m, int64_t n, int64_t k, con
         if (g.ok) g.algo = res[0].algo;
     }
     if (!g.ok) {
-        set_error("chosen_logprob: hipBLASLt has no algorithm for a " + std::to_string(m) + " x " +
+        set_error("hipBLASLt has no algorithm for a " + std::to_string(m) + " x " +
                   std::to_string(n) + " x " + std::to_string(k) + " product");
         return DM_ERR_HIP;
     }
@@ -303,7 +426,7 @@ static int lt_gemm(hipStream_t st, bool ta, int64_t m, int64_t n, int64_t k, con
     const hipblasStatus_t s = hipblasLtMatmul(h, g.desc, &one, A, g.a, B, g.b, &beta, Dm, g.c, Dm,
                                               g.c, &g.algo, ws, kLtWorkspace, st);
     if (s != HIPBLAS_STATUS_SUCCESS) {
-        set_error("chosen_logprob: hipBLASLt matmul failed (status " + std::to_string((int)s) + ")");
+        set_error("hipBLASLt matmul failed (status " + std::to_string((int)s) + ")");
         return DM_ERR_HIP;
     }
     return DM_OK;
@@ -312,10 +435,14 @@ static int lt_gemm(hipStream_t st, bool ta, int64_t m, int64_t n, int64_t k, con
 struct LpPlan {
     int64_t block, chunk;  // rows per block, vocabulary tokens per chunk
     bool bf16;             // both operands bf16 (else both taken as f32)
-    size_t off_bits, off_state, off_z, off_e, off_h, off_w, off_lt, total;
+    size_t off_bits, off_state, off_z, off_e, off_h, off_w, off_lt, off_coef, off_gh, off_gw;
+    size_t total;
 };
 
-static LpPlan lp_plan(const dm_logprob_desc *d, bool grad) {
+// What a call holds: grad (the log-probability's softmax weights, two bf16 parts or f32),
+// dz (the loss's logits gradient, bf16 or f32), and the loss's f32 gradient accumulators when
+// the gradients' dtype is not f32.
+static LpPlan lp_plan(const dm_logprob_desc *d, bool grad, bool dz, bool gh32, bool gw32) {
     LpPlan p{};
     const int64_t nb = d->n > 0 ? (d->n + d->row_chunk - 1) / d->row_chunk : 1;
     p.block = std::max<int64_t>(1, (d->n + nb - 1) / nb);
@@ -324,125 +451,145 @@ static LpPlan lp_plan(const dm_logprob_desc *d, bool grad) {
     p.chunk = d->vocab_chunk > 0 ? d->vocab_chunk : kLpMaxChunk;
     p.chunk = std::min<int64_t>({p.chunk, kLpMaxChunk, std::max<int64_t>(d->v, 1)});
     p.bf16 = d->hidden_dtype == DM_BF16 && d->weight_dtype == DM_BF16;
+    const int64_t n1 = std::max<int64_t>(d->n, 1);
     size_t o = 0;
     p.off_bits = o;
     o += align_up((size_t)((d->v + 31) / 32) * 4);
     p.off_state = o;
-    o += align_up((size_t)LP_NSTATE * std::max<int64_t>(d->n, 1) * 4);
+    o += align_up((size_t)LP_NSTATE * n1 * 4);
     p.off_z = o;
     o += align_up((size_t)p.block * p.chunk * 4);
     p.off_e = o;
-    if (grad) o += align_up((size_t)p.block * p.chunk * 4) + 256;  // two bf16 parts or one f32
+    if (grad || dz) o += align_up((size_t)p.block * p.chunk * 4) + 256;
     p.off_h = o;
-    if (!p.bf16 && d->hidden_dtype == DM_BF16) o += align_up((size_t)d->n * d->d * 4);
+    if (!p.bf16 && d->hidden_dtype != DM_F32) o += align_up((size_t)d->n * d->d * 4);
     p.off_w = o;
-    if (!p.bf16 && d->weight_dtype == DM_BF16) o += align_up((size_t)d->v * d->d * 4);
+    if (!p.bf16 && d->weight_dtype != DM_F32) o += align_up((size_t)d->v * d->d * 4);
+    p.off_coef = o;
+    if (dz) o += align_up((size_t)LC_COUNT * n1 * 4);
+    p.off_gh = o;
+    if (gh32) o += align_up((size_t)d->n * d->d * 4);
+    p.off_gw = o;
+    if (gw32) o += align_up((size_t)d->v * d->d * 4);
     p.off_lt = o;
     o += kLtWorkspace;
     p.total = o;
     return p;
 }
 
-static int lp_check(const dm_logprob_desc *d) {
-    if (!d) return refuse("chosen_logprob: null descriptor");
+static int lp_check(const std::string &op, const dm_logprob_desc *d, bool f16) {
+    if (!d) return refuse(op + ": null descriptor");
     if (d->n < 0 || d->v < 1 || d->d < 1)
-        return refuse("chosen_logprob: hidden is [n, D] and weight [V, D] with V, D >= 1");
-    if (d->row_chunk < 1) return refuse("chosen_logprob: row_chunk must be at least 1");
+        return refuse(op + ": hidden is [n, D] and weight [V, D] with V, D >= 1");
+    if (d->row_chunk < 1) return refuse(op + ": row_chunk must be at least 1");
     if (d->d % 8 != 0)
-        return refuse("chosen_logprob: hidden widths D that are not a multiple of 8 are not "
-                      "implemented");
-    if (d->vocab_chunk < 0) return refuse("chosen_logprob: vocab_chunk must not be negative");
+        return refuse(op + ": hidden widths D that are not a multiple of 8 are not implemented");
+    if (d->vocab_chunk < 0) return refuse(op + ": vocab_chunk must not be negative");
     for (int dt : {d->hidden_dtype, d->weight_dtype})
-        if (dt != DM_BF16 && dt != DM_F32)
-            return refuse("chosen_logprob: the log-probability takes bf16 or f32");
+        if (dt != DM_BF16 && dt != DM_F32 && !(f16 && dt == DM_F16))
+            return refuse(op + (f16 ? ": the loss takes f32, bf16 or f16"
+                                    : ": the log-probability takes bf16 or f32"));
     return DM_OK;
 }
 
-
-}  // namespace dm
-
-using namespace dm;
-
-extern "C" {
-
-size_t dm_chosen_logprob_workspace(const dm_logprob_desc *d, int with_grad) {
-    if (lp_check(d) != DM_OK) return 0;
-    return lp_plan(d, with_grad != 0).total;
-}
-
-int dm_chosen_logprob(const dm_logprob_desc *d, const void *hidden, const void *weight,
-                      const int64_t *targets, const uint32_t *masked, int64_t n_masked,
-                      float *logprob, float *entropy, float *grad, void *workspace,
-                      size_t workspace_bytes, void *stream) {
-    if (int rc = lp_check(d)) return rc;
-    if (n_masked < 0 || (n_masked > 0 && !masked))
-        return refuse("chosen_logprob: masked ids need a host array of n_masked ids");
-    // the masked ids as words of bits, on the host (the ids are a host list, as the
-    // reference's Vec<u32>): each below V, at least one token left
-    std::vector<uint32_t> bits((size_t)(d->v + 31) / 32, 0u);
+// The masked ids as words of bits, on the host (the ids are a host list, as the reference's
+// Vec<u32>): each below V, at least one token left. Returns the number of distinct ids, or -1
+// after a refusal.
+static int64_t lp_bits(const std::string &op, const dm_logprob_desc *d, const uint32_t *masked,
+                       int64_t n_masked, std::vector<uint32_t> &bits) {
+    if (n_masked < 0 || (n_masked > 0 && !masked)) {
+        refuse(op + ": masked ids need a host array of n_masked ids");
+        return -1;
+    }
+    bits.assign((size_t)(d->v + 31) / 32, 0u);
     int64_t distinct = 0;
     for (int64_t i = 0; i < n_masked; i++) {
         const uint32_t id = masked[i];
-        if ((int64_t)id >= d->v)
-            return refuse("chosen_logprob: masked token id " + std::to_string(id) +
-                          " is not below the vocabulary size " + std::to_string(d->v));
+        if ((int64_t)id >= d->v) {
+            refuse(op + ": masked token id " + std::to_string(id) +
+                   " is not below the vocabulary size " + std::to_string(d->v));
+            return -1;
+        }
         uint32_t &w = bits[id >> 5];
         if (!((w >> (id & 31)) & 1u)) distinct++;
         w |= 1u << (id & 31);
     }
-    if (distinct >= d->v) return refuse("chosen_logprob: at least one token must stay unmasked");
-    const bool want_grad = grad != nullptr;
-    const LpPlan p = lp_plan(d, want_grad);
-    if (workspace_bytes < p.total)
-        return refuse("chosen_logprob: the workspace is smaller than dm_chosen_logprob_workspace");
-    if (d->n == 0) return DM_OK;
-    hipStream_t st = (hipStream_t)stream;
-    char *ws = (char *)workspace;
-    uint32_t *dbits = (uint32_t *)(ws + p.off_bits);
+    if (distinct >= d->v) {
+        refuse(op + ": at least one token must stay unmasked");
+        return -1;
+    }
+    return distinct;
+}
+
+// The operands in one arithmetic: both bf16, or both f32 (a bf16 or f16 one widened into the
+// workspace).
+static int lp_operands(const dm_logprob_desc *d, const LpPlan &p, const void *hidden,
+                       const void *weight, char *ws, hipStream_t st, const void **H,
+                       const void **W) {
+    *H = hidden;
+    *W = weight;
+    if (p.bf16) return DM_OK;
+    const void *src[2] = {hidden, weight};
+    const int dts[2] = {d->hidden_dtype, d->weight_dtype};
+    const int64_t counts[2] = {d->n * d->d, d->v * d->d};
+    float *dst[2] = {(float *)(ws + p.off_h), (float *)(ws + p.off_w)};
+    const void **out[2] = {H, W};
+    for (int k = 0; k < 2; k++) {
+        if (dts[k] == DM_F32) continue;
+        if (dts[k] == DM_BF16)
+            lp_widen<<<1024, 256, 0, st>>>(counts[k], (const uint16_t *)src[k], dst[k]);
+        else
+            lp_widen16<<<1024, 256, 0, st>>>(counts[k], (const _Float16 *)src[k], dst[k]);
+        *out[k] = dst[k];
+    }
+    DM_LAUNCH_CHECK("widening the operands");
+    return DM_OK;
+}
+
+// One block's logits of one chunk: Z (column-major cw x rows, i.e. [rows, cw] row-major) =
+// W_c H_b^T; W_c is stored D x cw column-major, so op(A) = T.
+static int lp_logits(const dm_logprob_desc *d, const LpPlan &p, const void *H, const void *W,
+                     int64_t r0, int64_t rows, int64_t c0, int64_t cw, float *Z, void *lt_ws,
+                     hipStream_t st) {
+    const size_t esz = p.bf16 ? 2 : 4;
+    return lt_gemm(st, true, false, cw, rows, d->d, (const char *)W + (size_t)c0 * d->d * esz,
+                   (const char *)H + (size_t)r0 * d->d * esz, p.bf16 ? HIP_R_16BF : HIP_R_32F,
+                   0.f, Z, lt_ws);
+}
+
+// The pass over the vocabulary (reference.rs:121-287): per block of rows and chunk, the logits
+// and the statistics; with `grad`, o += E W_c in grad's rows. State [LP_NSTATE, n].
+static int lp_pass(const dm_logprob_desc *d, const LpPlan &p, const void *H, const void *W,
+                   const int64_t *targets, const uint32_t *dbits, char *ws, float *grad,
+                   hipStream_t st, const std::function<int(int64_t, int64_t)> &after_block) {
     float *state = (float *)(ws + p.off_state);
     float *Z = (float *)(ws + p.off_z);
     void *E = ws + p.off_e;
-    if (hipMemcpyAsync(dbits, bits.data(), bits.size() * 4, hipMemcpyHostToDevice, st) !=
-        hipSuccess)
-        return hip_status(hipGetLastError(), "chosen_logprob: copying the masked ids");
-
-    // operands in one arithmetic: both bf16, or both f32 (a bf16 one widened)
-    const void *H = hidden, *W = weight;
-    if (!p.bf16) {
-        if (d->hidden_dtype == DM_BF16) {
-            lp_widen<<<1024, 256, 0, st>>>(d->n * d->d, (const uint16_t *)hidden,
-                                           (float *)(ws + p.off_h));
-            H = ws + p.off_h;
-        }
-        if (d->weight_dtype == DM_BF16) {
-            lp_widen<<<1024, 256, 0, st>>>(d->v * d->d, (const uint16_t *)weight,
-                                           (float *)(ws + p.off_w));
-            W = ws + p.off_w;
-        }
-        DM_LAUNCH_CHECK("chosen_logprob: widen");
-    }
+    void *lt_ws = ws + p.off_lt;
     const hipDataType op_t = p.bf16 ? HIP_R_16BF : HIP_R_32F;
     const size_t esz = p.bf16 ? 2 : 4;
-    void *lt_ws = ws + p.off_lt;
+    const bool want_grad = grad != nullptr;
     for (int64_t r0 = 0; r0 < d->n; r0 += p.block) {
         const int64_t rows = std::min<int64_t>(p.block, d->n - r0);
         float *o = want_grad ? grad + r0 * d->d : nullptr;
         lp_init<<<(unsigned)rows, kLpThreads, 0, st>>>(rows, d->d, state + r0, d->n, o);
-        DM_LAUNCH_CHECK("chosen_logprob: init");
-        const char *Hb = (const char *)H + (size_t)r0 * d->d * esz;
+        DM_LAUNCH_CHECK("init");
         for (int64_t c0 = 0; c0 < d->v; c0 += p.chunk) {
             const int64_t cw = std::min<int64_t>(p.chunk, d->v - c0);
             // the bf16 remainder after the part, at an aligned offset
             void *E2 = (char *)E + align_up((size_t)rows * cw * 2);
-            const char *Wc = (const char *)W + (size_t)c0 * d->d * esz;
-            // Z (column-major cw x rows, i.e. [rows, cw] row-major) = W_c H^T: W_c is stored
-            // D x cw column-major, so op(A) = T
-            if (int rc = lt_gemm(st, true, cw, rows, d->d, Wc, Hb, op_t, 0.f, Z, lt_ws)) return rc;
+            if (int rc = lp_logits(d, p, H, W, r0, rows, c0, cw, Z, lt_ws, st)) return rc;
             {
                 KernelTimer timer(DM_KERNEL_LOGPROB_STATS, st);
                 const int nv = (int)((cw + 1023) / 1024);
-#define LP_STATS(EK, NV, EE, OO)                                                                   lp_stats<EK, NV><<<(unsigned)rows, kLpThreads, 0, st>>>(rows, cw, c0, d->d, Z, targets + r0,                                                             dbits, state + r0, d->n, EE, E2, OO)
-#define LP_NV(EK, EE, OO)                                                                          if (nv <= 1) LP_STATS(EK, 1, EE, OO);                                                          else if (nv <= 2) LP_STATS(EK, 2, EE, OO);                                                     else if (nv <= 4) LP_STATS(EK, 4, EE, OO);                                                     else LP_STATS(EK, 8, EE, OO)
+#define LP_STATS(EK, NV, EE, OO)                                                               \
+    lp_stats<EK, NV><<<(unsigned)rows, kLpThreads, 0, st>>>(rows, cw, c0, d->d, Z, targets + r0, \
+                                                            dbits, state + r0, d->n, EE, E2, OO)
+#define LP_NV(EK, EE, OO)                          \
+    if (nv <= 1) LP_STATS(EK, 1, EE, OO);          \
+    else if (nv <= 2) LP_STATS(EK, 2, EE, OO);     \
+    else if (nv <= 4) LP_STATS(EK, 4, EE, OO);     \
+    else LP_STATS(EK, 8, EE, OO)
                 if (!want_grad) {
                     LP_NV(0, nullptr, nullptr);
                 } else if (p.bf16) {
@@ -453,28 +600,212 @@ int dm_chosen_logprob(const dm_logprob_desc *d, const void *hidden, const void *
 #undef LP_NV
 #undef LP_STATS
             }
-            DM_LAUNCH_CHECK("chosen_logprob: stats");
+            DM_LAUNCH_CHECK("statistics");
             if (want_grad) {
                 // o (column-major D x rows) += W_c as stored (D x cw) E^T (cw x rows)
-                const int parts = p.bf16 ? 2 : 1;
-                for (int part = 0; part < parts; part++) {
-                    const void *Ep = part ? E2 : E;
-                    if (int rc = lt_gemm(st, false, d->d, rows, cw, Wc, Ep, op_t, 1.f, o, lt_ws))
+                const char *Wc = (const char *)W + (size_t)c0 * d->d * esz;
+                for (int part = 0; part < (p.bf16 ? 2 : 1); part++)
+                    if (int rc = lt_gemm(st, false, false, d->d, rows, cw, Wc, part ? E2 : E,
+                                         op_t, 1.f, o, lt_ws))
                         return rc;
-                }
             }
         }
-        if (p.bf16 || d->weight_dtype == DM_BF16)
-            lp_finish<DM_BF16><<<(unsigned)rows, kLpThreads, 0, st>>>(
-                rows, d->v, d->d, state + r0, d->n, targets + r0, weight, logprob + r0,
-                entropy + r0, o);
-        else
-            lp_finish<DM_F32><<<(unsigned)rows, kLpThreads, 0, st>>>(
-                rows, d->v, d->d, state + r0, d->n, targets + r0, weight, logprob + r0,
-                entropy + r0, o);
-        DM_LAUNCH_CHECK("chosen_logprob: finish");
+        if (int rc = after_block(r0, rows)) return rc;
     }
+    return DM_OK;
+}
+
+static int lp_upload_bits(const std::vector<uint32_t> &bits, char *ws, const LpPlan &p,
+                          hipStream_t st) {
+    if (hipMemcpyAsync(ws + p.off_bits, bits.data(), bits.size() * 4, hipMemcpyHostToDevice, st) !=
+        hipSuccess)
+        return hip_status(hipGetLastError(), "copying the masked ids");
+    return DM_OK;
+}
+
+static int lce_check(const dm_lce_desc *d) {
+    const std::string op = "linear_cross_entropy";
+    if (!d) return refuse(op + ": null descriptor");
+    if (int rc = lp_check(op, &d->lp, true)) return rc;
+    if (d->lp.hidden_dtype != d->lp.weight_dtype)
+        return refuse(op + ": hidden and weight share one dtype");
+    if (!(d->label_smoothing >= 0.f && d->label_smoothing <= 1.f))
+        return refuse(op + ": label_smoothing must be in 0..=1, got " +
+                      std::to_string(d->label_smoothing));
+    if (!(std::isfinite(d->z_loss) && d->z_loss >= 0.f))
+        return refuse(op + ": z_loss must be finite and at least 0, got " +
+                      std::to_string(d->z_loss));
+    return DM_OK;
+}
+
+}  // namespace dm
+
+using namespace dm;
+
+extern "C" {
+
+size_t dm_chosen_logprob_workspace(const dm_logprob_desc *d, int with_grad) {
+    if (lp_check("chosen_logprob", d, false) != DM_OK) return 0;
+    return lp_plan(d, with_grad != 0, false, false, false).total;
+}
+
+int dm_chosen_logprob(const dm_logprob_desc *d, const void *hidden, const void *weight,
+                      const int64_t *targets, const uint32_t *masked, int64_t n_masked,
+                      float *logprob, float *entropy, float *grad, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+    const std::string op = "chosen_logprob";
+    if (int rc = lp_check(op, d, false)) return rc;
+    std::vector<uint32_t> bits;
+    if (lp_bits(op, d, masked, n_masked, bits) < 0) return DM_ERR_REFUSED;
+    const bool want_grad = grad != nullptr;
+    const LpPlan p = lp_plan(d, want_grad, false, false, false);
+    if (workspace_bytes < p.total)
+        return refuse(op + ": the workspace is smaller than dm_chosen_logprob_workspace");
+    if (d->n == 0) return DM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    if (int rc = lp_upload_bits(bits, ws, p, st)) return rc;
+    const void *H, *W;
+    if (int rc = lp_operands(d, p, hidden, weight, ws, st, &H, &W)) return rc;
+    const float *state = (const float *)(ws + p.off_state);
+    int rc = lp_pass(d, p, H, W, targets, (const uint32_t *)(ws + p.off_bits), ws, grad, st,
+                     [&](int64_t r0, int64_t rows) -> int {
+                         float *o = want_grad ? grad + r0 * d->d : nullptr;
+                         if (d->weight_dtype == DM_BF16)
+                             lp_finish<DM_BF16><<<(unsigned)rows, kLpThreads, 0, st>>>(
+                                 rows, d->v, d->d, state + r0, d->n, targets + r0, weight,
+                                 logprob + r0, entropy + r0, o);
+                         else
+                             lp_finish<DM_F32><<<(unsigned)rows, kLpThreads, 0, st>>>(
+                                 rows, d->v, d->d, state + r0, d->n, targets + r0, weight,
+                                 logprob + r0, entropy + r0, o);
+                         DM_LAUNCH_CHECK("chosen_logprob: finish");
+                         return DM_OK;
+                     });
+    if (rc) return rc;
     probe_add(DM_PROBE_LOGPROB);
+    return DM_OK;
+}
+
+size_t dm_linear_cross_entropy_workspace(const dm_lce_desc *d, int backward) {
+    if (lce_check(d) != DM_OK) return 0;
+    const bool f32 = d->lp.hidden_dtype == DM_F32;
+    return lp_plan(&d->lp, false, backward != 0, backward && !f32, backward && !f32).total;
+}
+
+int dm_linear_cross_entropy_fwd(const dm_lce_desc *d, const void *hidden, const void *weight,
+                                const int64_t *targets, const uint32_t *masked, int64_t n_masked,
+                                float *rows, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    const std::string op = "linear_cross_entropy";
+    if (int rc = lce_check(d)) return rc;
+    const dm_logprob_desc *lp = &d->lp;
+    std::vector<uint32_t> bits;
+    const int64_t nmask = lp_bits(op, lp, masked, n_masked, bits);
+    if (nmask < 0) return DM_ERR_REFUSED;
+    const LpPlan p = lp_plan(lp, false, false, false, false);
+    if (workspace_bytes < p.total)
+        return refuse(op + ": the workspace is smaller than dm_linear_cross_entropy_workspace");
+    if (lp->n == 0) return DM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    if (int rc = lp_upload_bits(bits, ws, p, st)) return rc;
+    const void *H, *W;
+    if (int rc = lp_operands(lp, p, hidden, weight, ws, st, &H, &W)) return rc;
+    if (int rc = lp_pass(lp, p, H, W, targets, (const uint32_t *)(ws + p.off_bits), ws, nullptr,
+                         st, [](int64_t, int64_t) { return (int)DM_OK; }))
+        return rc;
+    const float inv_classes = 1.f / (float)(lp->v - nmask);
+    lce_finish<<<(unsigned)((lp->n + 255) / 256), 256, 0, st>>>(
+        lp->n, (const float *)(ws + p.off_state), targets, d->ignore_index, d->label_smoothing,
+        d->z_loss, inv_classes, rows);
+    DM_LAUNCH_CHECK("linear_cross_entropy: finish");
+    probe_add(DM_PROBE_LCE_FWD);
+    return DM_OK;
+}
+
+int dm_linear_cross_entropy_bwd(const dm_lce_desc *d, const void *hidden, const void *weight,
+                                const int64_t *targets, const uint32_t *masked, int64_t n_masked,
+                                const float *rows, const float *upstream, void *grad_hidden,
+                                void *grad_weight, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    const std::string op = "linear_cross_entropy";
+    if (int rc = lce_check(d)) return rc;
+    const dm_logprob_desc *lp = &d->lp;
+    std::vector<uint32_t> bits;
+    const int64_t nmask = lp_bits(op, lp, masked, n_masked, bits);
+    if (nmask < 0) return DM_ERR_REFUSED;
+    const bool f32 = lp->hidden_dtype == DM_F32;
+    const LpPlan p = lp_plan(lp, false, true, !f32, !f32);
+    if (workspace_bytes < p.total)
+        return refuse(op + ": the workspace is smaller than dm_linear_cross_entropy_workspace");
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    float *gh = grad_hidden ? (f32 ? (float *)grad_hidden : (float *)(ws + p.off_gh)) : nullptr;
+    float *gw = grad_weight ? (f32 ? (float *)grad_weight : (float *)(ws + p.off_gw)) : nullptr;
+    if (gw) {
+        lp_zero<<<1024, 256, 0, st>>>(lp->v * lp->d, gw);
+        DM_LAUNCH_CHECK("linear_cross_entropy: zero");
+    }
+    if (lp->n == 0) {
+        if (grad_weight && !f32) {
+            lp_cast<<<1024, 256, 0, st>>>(lp->v * lp->d, gw, grad_weight, lp->weight_dtype);
+            DM_LAUNCH_CHECK("linear_cross_entropy: cast");
+        }
+        return DM_OK;
+    }
+    if (gh) {
+        lp_zero<<<1024, 256, 0, st>>>(lp->n * lp->d, gh);
+        DM_LAUNCH_CHECK("linear_cross_entropy: zero");
+    }
+    if (int rc = lp_upload_bits(bits, ws, p, st)) return rc;
+    const void *H, *W;
+    if (int rc = lp_operands(lp, p, hidden, weight, ws, st, &H, &W)) return rc;
+    const float inv_classes = 1.f / (float)(lp->v - nmask);
+    float *coef = (float *)(ws + p.off_coef);
+    lce_coef<<<(unsigned)((lp->n + 255) / 256), 256, 0, st>>>(
+        lp->n, rows, upstream, d->label_smoothing, d->z_loss, inv_classes, d->entropy, coef);
+    DM_LAUNCH_CHECK("linear_cross_entropy: coefficients");
+    // the gradient pass (logprob/reference.rs:289-380): the logits again, the logits' gradient,
+    // then grad_hidden_b += G W_c and grad_weight_c += G^T H_b
+    float *Z = (float *)(ws + p.off_z);
+    void *G = ws + p.off_e, *lt_ws = ws + p.off_lt;
+    const hipDataType op_t = p.bf16 ? HIP_R_16BF : HIP_R_32F;
+    const size_t esz = p.bf16 ? 2 : 4;
+    const uint32_t *dbits = (const uint32_t *)(ws + p.off_bits);
+    for (int64_t r0 = 0; r0 < lp->n; r0 += p.block) {
+        const int64_t rows_b = std::min<int64_t>(p.block, lp->n - r0);
+        for (int64_t c0 = 0; c0 < lp->v; c0 += p.chunk) {
+            const int64_t cw = std::min<int64_t>(p.chunk, lp->v - c0);
+            if (int rc = lp_logits(lp, p, H, W, r0, rows_b, c0, cw, Z, lt_ws, st)) return rc;
+            if (p.bf16)
+                lce_dz<true><<<(unsigned)rows_b, kLpThreads, 0, st>>>(
+                    rows_b, cw, c0, Z, targets + r0, dbits, rows + r0, coef + r0, lp->n, G);
+            else
+                lce_dz<false><<<(unsigned)rows_b, kLpThreads, 0, st>>>(
+                    rows_b, cw, c0, Z, targets + r0, dbits, rows + r0, coef + r0, lp->n, G);
+            DM_LAUNCH_CHECK("linear_cross_entropy: logits gradient");
+            const char *Wc = (const char *)W + (size_t)c0 * lp->d * esz;
+            // grad_hidden (column-major D x rows) += W_c as stored (D x cw) G^T (cw x rows)
+            if (gh)
+                if (int rc = lt_gemm(st, false, false, lp->d, rows_b, cw, Wc, G, op_t, 1.f,
+                                     gh + r0 * lp->d, lt_ws))
+                    return rc;
+            // grad_weight_c (column-major D x cw) += H_b as stored (D x rows) G (rows x cw; G
+            // is stored cw x rows, so op(B) = T)
+            if (gw)
+                if (int rc = lt_gemm(st, false, true, lp->d, cw, rows_b,
+                                     (const char *)H + (size_t)r0 * lp->d * esz, G, op_t, 1.f,
+                                     gw + c0 * lp->d, lt_ws))
+                    return rc;
+        }
+    }
+    if (!f32) {
+        if (grad_hidden) lp_cast<<<1024, 256, 0, st>>>(lp->n * lp->d, gh, grad_hidden, lp->hidden_dtype);
+        if (grad_weight) lp_cast<<<1024, 256, 0, st>>>(lp->v * lp->d, gw, grad_weight, lp->weight_dtype);
+        DM_LAUNCH_CHECK("linear_cross_entropy: cast");
+    }
+    probe_add(DM_PROBE_LCE_BWD);
     return DM_OK;
 }
 

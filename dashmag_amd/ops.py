@@ -19,7 +19,7 @@ import torch
 from . import _lib
 from .contract import (Activation, AttentionMask, AttentionOptions, CausalConv1dOptions,
                        CausalConv1dStepOptions, ChunkGatedDeltaOptions, GatedDeltaStepOptions,
-                       LogprobOptions, UNBOUNDED, Unsupported)
+                       CrossEntropyOptions, LogprobOptions, Reduction, UNBOUNDED, Unsupported)
 
 _DT = {torch.float32: _lib.DM_F32, torch.bfloat16: _lib.DM_BF16, torch.float16: _lib.DM_F16}
 
@@ -667,3 +667,85 @@ def chosen_logprob_with_grad(hidden, weight, targets, masked=(), options=None):
     respect to ``hidden[i]`` (logprob.rs:140-160); the backward of the log-probability is
     ``upstream[:, None] * grad``, cast to ``hidden``'s dtype (logprob.rs:160-190)."""
     return _logprob(hidden, weight, targets, masked, options, True)
+
+
+# ------------------------------------------------------------------------------------------
+# Fused linear cross-entropy
+# ------------------------------------------------------------------------------------------
+
+_LCE_ROWS = ("loss", "logprob", "entropy", "lse", "q", "s", "counted", "found")
+
+
+def _lce_desc(op, hidden, weight, targets, options):
+    _device(op, hidden, weight)
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise Unsupported(f"{op}: hidden [n, D] and weight [V, D] must share D, got "
+                          f"{list(hidden.shape)}, {list(weight.shape)}")
+    if hidden.dtype != weight.dtype:
+        raise Unsupported(f"{op}: hidden and weight share one dtype")
+    n, d = hidden.shape
+    tg = torch.as_tensor(targets)
+    if tuple(tg.shape) != (n,):
+        raise Unsupported(f"{op}: targets must be [n] = [{n}]")
+    tg = tg.to(device=hidden.device, dtype=torch.int64).contiguous()
+    ids = [int(i) for i in options.masked]
+    if any(i < 0 for i in ids):
+        raise Unsupported(f"{op}: masked token ids are not negative")
+    ids_c = (ctypes.c_uint32 * max(len(ids), 1))(*ids)
+    dt = _dtype(op, hidden)
+    lp = _lib.LogprobDesc(n=n, v=weight.shape[0], d=d, hidden_dtype=dt, weight_dtype=dt,
+                          vocab_chunk=int(options.chunks.vocab_chunk),
+                          row_chunk=int(options.chunks.row_chunk))
+    desc = _lib.LceDesc(lp=lp, ignore_index=int(options.ignore_index),
+                        label_smoothing=float(options.label_smoothing),
+                        z_loss=float(options.z_loss), entropy=int(bool(options.entropy)))
+    return desc, tg, ids_c, len(ids)
+
+
+def linear_cross_entropy(hidden, weight, targets, options=None):
+    """torch's ``F.cross_entropy(F.linear(hidden, weight), targets)`` with label smoothing, a
+    z-loss and masked ids, without the n x V logits (crates/dash-ops/src/loss.rs:820-895;
+    crates/dash-contract/src/loss.rs): ``(loss, logprob [n], entropy [n] or None, rows)``, the
+    loss ``[1]`` (mean, sum) or ``[n]`` (none), all f32; ``rows`` ``[8, n]`` (loss, logprob,
+    entropy, lse, q, s, counted, found) is what ``linear_cross_entropy_backward`` takes."""
+    op = "linear_cross_entropy"
+    options = options or CrossEntropyOptions()
+    desc, tg, ids_c, nid = _lce_desc(op, hidden, weight, targets, options)
+    h, w = hidden.contiguous(), weight.contiguous()
+    n = h.shape[0]
+    rows = torch.zeros(len(_LCE_ROWS), n, dtype=torch.float32, device=h.device)
+    nbytes = _lib.lib().dm_linear_cross_entropy_workspace(ctypes.byref(desc), 0)
+    ws = _workspace(nbytes, h.device)
+    _check(op, _lib.lib().dm_linear_cross_entropy_fwd(
+        ctypes.byref(desc), _ptr(h), _ptr(w), _ptr(tg), ctypes.cast(ids_c, ctypes.c_void_p), nid,
+        _ptr(rows), _ptr(ws), nbytes, _stream()))
+    if options.reduction == Reduction.NONE:
+        loss = rows[0]
+    elif options.reduction == Reduction.SUM:
+        loss = rows[0].sum().reshape(1)
+    else:  # the mean over the counted rows (NaN when every row is ignored, as torch)
+        loss = (rows[0].sum() / rows[6].sum()).reshape(1)
+    return loss, rows[1], (rows[2] if options.entropy else None), rows
+
+
+def linear_cross_entropy_backward(hidden, weight, targets, rows, upstream, options=None,
+                                  grad_hidden=True, grad_weight=True):
+    """The gradients for ``hidden`` and ``weight`` (crates/dash-ops/src/loss.rs:157-200,
+    :527-668): ``upstream`` ``[3, n]`` f32 holds the gradients of the loss, logprob and entropy
+    rows (for a reduced loss: the mean's 1 / counted or the sum's 1 on each row). Returns
+    ``(grad_hidden, grad_weight)`` in the inputs' dtype, each None when not asked for."""
+    op = "linear_cross_entropy"
+    options = options or CrossEntropyOptions()
+    desc, tg, ids_c, nid = _lce_desc(op, hidden, weight, targets, options)
+    h, w = hidden.contiguous(), weight.contiguous()
+    up = torch.as_tensor(upstream, dtype=torch.float32).to(h.device).contiguous()
+    if tuple(up.shape) != (3, h.shape[0]):
+        raise Unsupported(f"{op}: upstream is [3, n]")
+    gh = torch.empty_like(h) if grad_hidden else None
+    gw = torch.empty_like(w) if grad_weight else None
+    nbytes = _lib.lib().dm_linear_cross_entropy_workspace(ctypes.byref(desc), 1)
+    ws = _workspace(nbytes, h.device)
+    _check(op, _lib.lib().dm_linear_cross_entropy_bwd(
+        ctypes.byref(desc), _ptr(h), _ptr(w), _ptr(tg), ctypes.cast(ids_c, ctypes.c_void_p), nid,
+        _ptr(rows.contiguous()), _ptr(up), _ptr(gh), _ptr(gw), _ptr(ws), nbytes, _stream()))
+    return gh, gw

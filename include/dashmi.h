@@ -20,6 +20,10 @@
  *                                                               crates/dash-ops/src/conv1d.rs:331-360, :750
  *   dm_chosen_logprob    ChosenLogprobBackend::chosen_logprob{,_with_grad}
  *                                                               crates/dash-ops/src/logprob.rs:127-160
+ *   dm_linear_cross_entropy_fwd  LinearCrossEntropyBackend::linear_cross_entropy
+ *                                                               crates/dash-ops/src/loss.rs:134-160
+ *   dm_linear_cross_entropy_bwd  LinearCrossEntropyBackend::linear_cross_entropy_backward
+ *                                                               crates/dash-ops/src/loss.rs:157-200
  *
  * Conventions (crates/dash-contract/src/lib.rs:38-91):
  *   - Every tensor is a device pointer to a contiguous array in the contract's layout:
@@ -123,6 +127,18 @@ typedef struct {
     int64_t vocab_chunk, row_chunk;
 } dm_logprob_desc;
 
+/* One fused linear cross-entropy call (crates/dash-contract/src/loss.rs:52-95): the
+ * log-probability's shapes and chunks (hidden and weight of one dtype: f32, bf16 or f16) and
+ * CrossEntropyOptions but the reduction and the masked ids: ignore_index (torch's -100 by
+ * default), label_smoothing eps in 0..=1, z_loss lambda >= 0, entropy (whether the entropy takes
+ * a gradient). */
+typedef struct {
+    dm_logprob_desc lp;
+    int64_t ignore_index;
+    float label_smoothing, z_loss;
+    int32_t entropy;
+} dm_lce_desc;
+
 /* The message of this thread's last refusal or error. */
 const char *dm_last_error(void);
 
@@ -147,6 +163,8 @@ typedef enum {
     DM_PROBE_CONV1D_BWD,
     DM_PROBE_CONV1D_UPDATE,
     DM_PROBE_LOGPROB,
+    DM_PROBE_LCE_FWD,
+    DM_PROBE_LCE_BWD,
     DM_PROBE_COUNT
 } dm_probe;
 uint64_t dm_probe_count(int probe);
@@ -298,6 +316,31 @@ int dm_chosen_logprob(const dm_logprob_desc *desc, const void *hidden, const voi
                       const int64_t *targets, const uint32_t *masked, int64_t n_masked,
                       float *logprob, float *entropy, float *grad, void *workspace,
                       size_t workspace_bytes, void *stream);
+
+/* The fused linear cross-entropy (crates/dash-contract/src/loss.rs:1-50), forward: rows [8, n]
+ * f32 per row = loss, logprob, entropy (each 0 on an ignored row; loss +inf and logprob -inf
+ * where the target is masked or outside [0, V)), lse, q = 1 - p(target) summed over the other
+ * tokens, s, counted, found (crates/dash-ops/src/loss.rs:96-116). The caller reduces the loss row
+ * (mean over the counted rows, sum, or none, loss.rs:872-877). targets [n] int64 on the device;
+ * masked: n_masked ids on the HOST, any order, each below V, at least one token left. Replaces
+ * LinearCrossEntropyBackend::linear_cross_entropy (loss.rs:134-160; the written-out backward is
+ * always taken, as with a weight that trains). */
+size_t dm_linear_cross_entropy_workspace(const dm_lce_desc *desc, int backward);
+int dm_linear_cross_entropy_fwd(const dm_lce_desc *desc, const void *hidden, const void *weight,
+                                const int64_t *targets, const uint32_t *masked, int64_t n_masked,
+                                float *rows, void *workspace, size_t workspace_bytes,
+                                void *stream);
+/* Its backward from the forward's rows and upstream [3, n] f32 (the gradients of the loss,
+ * logprob and entropy rows; the entropy's is read only with desc->entropy): grad_hidden [n, D]
+ * and grad_weight [V, D] in the inputs' dtype, either NULL when not wanted. A second pass over
+ * the vocabulary recomputes each chunk's logits; the logits' gradient is rounded to bf16 for the
+ * products from bf16 inputs. Replaces LinearCrossEntropyBackend::linear_cross_entropy_backward
+ * (loss.rs:157-200). */
+int dm_linear_cross_entropy_bwd(const dm_lce_desc *desc, const void *hidden, const void *weight,
+                                const int64_t *targets, const uint32_t *masked, int64_t n_masked,
+                                const float *rows, const float *upstream, void *grad_hidden,
+                                void *grad_weight, void *workspace, size_t workspace_bytes,
+                                void *stream);
 
 #ifdef __cplusplus
 }
