@@ -436,7 +436,35 @@ def main():
             rows_per_s=n / ms_g * 1e3, kernel_us=kus)
         print(f"logprob: fwd {ms_f:.2f} ms ({fl / ms_f / 1e9:.0f} TFLOP/s), with gradient "
               f"{ms_g:.2f} ms ({2 * fl / ms_g / 1e9:.0f} TFLOP/s)", file=sys.stderr, flush=True)
-        del c, h, wt, grad, ws
+        del grad, ws
+
+        # the fused linear cross-entropy on the same inputs: label smoothing 0.1, z-loss 1e-4,
+        # the 64 masked ids; forward, then the gradients of hidden and of a trained weight
+        opts = dm.CrossEntropyOptions(label_smoothing=0.1, z_loss=1e-4, masked=tuple(masked))
+        up = torch.zeros(3, n)
+        up[0] = 1.0 / n
+        rows_box = {}
+
+        def lce_fwd():
+            rows_box["rows"] = dm.linear_cross_entropy(h, wt, tg, opts)[3]
+
+        def lce_step():
+            lce_fwd()
+            dm.linear_cross_entropy_backward(h, wt, tg, rows_box["rows"], up, opts)
+
+        tlf, tls = Timed(torch, lce_fwd), Timed(torch, lce_step)
+        ms_lf = tlf.run(max(args.steps, 5), args.warmup)
+        ms_ls = tls.run(max(args.steps, 5), args.warmup)
+        # forward: the logits (2 n V D); backward: the logits again, grad_hidden and grad_weight
+        secondary["linear_cross_entropy"] = dict(
+            unit="TFLOP/s", workload=f"fused linear cross-entropy, bf16, n={n}, D={d}, V={v}, "
+            "label smoothing 0.1, z-loss 1e-4, 64 masked ids, gradients of hidden and weight",
+            fwd_ms=ms_lf, fwd_TFLOPs=fl / ms_lf / 1e9, step_ms=ms_ls,
+            step_TFLOPs=4 * fl / ms_ls / 1e9,
+            step_frac_of_mfma_peak=4 * fl / ms_ls / 1e9 / BF16_PEAK_TFLOPS)
+        print(f"linear cross-entropy: fwd {ms_lf:.2f} ms, fwd+bwd {ms_ls:.2f} ms "
+              f"({4 * fl / ms_ls / 1e9:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+        del c, h, wt, rows_box
 
     # ---- CPU baseline: the oracle on a bounded sample of config 2 ----
     cpu = None
