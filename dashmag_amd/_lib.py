@@ -16,7 +16,8 @@ DM_UNBOUNDED = (1 << 64) - 1
 
 PROBES = ["attn_fwd_mfma", "attn_fwd_generic", "attn_bwd_mfma", "attn_bwd_generic",
           "decode_split", "decode_merge", "gdr_chunk_fwd", "gdr_chunk_bwd", "gdr_step",
-          "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob", "lce_fwd", "lce_bwd"]
+          "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob", "lce_fwd", "lce_bwd",
+          "gdr_chunk_fwd_mfma", "gdr_chunk_bwd_mfma"]
 DM_ACT_NONE, DM_ACT_SILU = 0, 1
 
 

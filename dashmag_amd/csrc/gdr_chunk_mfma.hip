@@ -1602,6 +1602,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
     }
     probe_add(DM_PROBE_GDR_CHUNK_FWD, 4);
+    probe_add(DM_PROBE_GDR_CHUNK_FWD_MFMA, 4);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule: MFMA launch");
     return DM_OK;
 }
@@ -1658,6 +1659,7 @@ int launch_gdr_mfma_bwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         gdr_mfma_bwd_kernels<DM_F16>(a, w, chunks, seqs, h0, d_out, d_final, dq, dk, dv, dg,
                                      dbeta, dh0, st);
     probe_add(DM_PROBE_GDR_CHUNK_BWD, 6);
+    probe_add(DM_PROBE_GDR_CHUNK_BWD_MFMA, 6);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule_backward: MFMA launch");
     return DM_OK;
 }

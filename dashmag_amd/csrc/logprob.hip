@@ -32,6 +32,7 @@
 
 #include "attention_kernels.h"
 #include "dm_common.h"
+#include "mfma.h"
 
 namespace dm {
 
@@ -125,7 +126,11 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
             }
     }
     mx = lp_block_max(mx, sm);
+    // this row's running state, read by every thread before the block reductions below (thread
+    // 0 rewrites it after them)
     const float m = st[LP_M * nst + row];
+    const float s_old = st[LP_S * nst + row], a_old = st[LP_A * nst + row];
+    const float r_old = st[LP_R * nst + row];
     const float m_new = mx > m ? mx : m;
     const float shift = m - m_new, alpha = expf(shift);
     const int64_t t = targets[row];
@@ -184,14 +189,13 @@ __global__ __launch_bounds__(kLpThreads) void lp_stats(int64_t rows, int64_t cw,
     sr = lp_block_sum(sr, sm);
     if constexpr (EK != 0) {
         // o is still zero while nothing has been summed (the first chunk)
-        if (alpha != 1.f && st[LP_S * nst + row] != 0.f)
+        if (alpha != 1.f && s_old != 0.f)
             for (int64_t e = threadIdx.x; e < D; e += kLpThreads) o[row * D + e] *= alpha;
     }
     if (threadIdx.x == 0) {
-        const float s = st[LP_S * nst + row], a = st[LP_A * nst + row];
-        st[LP_A * nst + row] = alpha * (a + s * shift) + sa;
-        st[LP_S * nst + row] = s * alpha + se;
-        st[LP_R * nst + row] = st[LP_R * nst + row] * alpha + sr;
+        st[LP_A * nst + row] = alpha * (a_old + s_old * shift) + sa;
+        st[LP_S * nst + row] = s_old * alpha + se;
+        st[LP_R * nst + row] = r_old * alpha + sr;
         if (has_t) {
             st[LP_ZT * nst + row] += z[tl];
             st[LP_FOUND * nst + row] += 1.f;
@@ -337,9 +341,29 @@ __global__ __launch_bounds__(kLpThreads) void lce_dz(int64_t rows, int64_t cw, i
 }
 
 // f32 -> the dtype (a copy for f32), and fills with zeros.
+// f32 -> the dtype, 8 elements a thread per pass (two 16-byte loads, one 16-byte store for a
+// 16-bit dtype); the tail past a multiple of 8 element by element.
 __global__ void lp_cast(int64_t count, const float *__restrict__ x, void *__restrict__ y, int dt) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
-         i += (int64_t)gridDim.x * blockDim.x)
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t n8 = count / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const f32x4_t av = __builtin_nontemporal_load((const f32x4_t *)x + 2 * i);
+        const f32x4_t bv = __builtin_nontemporal_load((const f32x4_t *)x + 2 * i + 1);
+        const float4 a = make_float4(av[0], av[1], av[2], av[3]);
+        const float4 b = make_float4(bv[0], bv[1], bv[2], bv[3]);
+        if (dt == DM_F32) {
+            ((float4 *)y)[2 * i] = a;
+            ((float4 *)y)[2 * i + 1] = b;
+        } else if (dt == DM_BF16) {
+            ((uint4 *)y)[i] = make_uint4(pack2<DM_BF16>(a.x, a.y), pack2<DM_BF16>(a.z, a.w),
+                                         pack2<DM_BF16>(b.x, b.y), pack2<DM_BF16>(b.z, b.w));
+        } else {
+            ((uint4 *)y)[i] = make_uint4(pack2<DM_F16>(a.x, a.y), pack2<DM_F16>(a.z, a.w),
+                                         pack2<DM_F16>(b.x, b.y), pack2<DM_F16>(b.z, b.w));
+        }
+    }
+    for (int64_t i = 8 * n8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += stride)
         st_any(dt, y, i, x[i]);
 }
 __global__ void lp_zero(int64_t count, float *__restrict__ x) {
@@ -690,7 +714,8 @@ int dm_chosen_logprob(const dm_logprob_desc *d, const void *hidden, const void *
 size_t dm_linear_cross_entropy_workspace(const dm_lce_desc *d, int backward) {
     if (lce_check(d) != DM_OK) return 0;
     const bool f32 = d->lp.hidden_dtype == DM_F32;
-    return lp_plan(&d->lp, false, backward != 0, backward && !f32, backward && !f32).total;
+    // backward 1: both gradients; 2: the hidden's alone (no weight-gradient accumulator)
+    return lp_plan(&d->lp, false, backward != 0, backward && !f32, backward == 1 && !f32).total;
 }
 
 int dm_linear_cross_entropy_fwd(const dm_lce_desc *d, const void *hidden, const void *weight,
@@ -736,7 +761,9 @@ int dm_linear_cross_entropy_bwd(const dm_lce_desc *d, const void *hidden, const 
     const int64_t nmask = lp_bits(op, lp, masked, n_masked, bits);
     if (nmask < 0) return DM_ERR_REFUSED;
     const bool f32 = lp->hidden_dtype == DM_F32;
-    const LpPlan p = lp_plan(lp, false, true, !f32, !f32);
+    // the weight-gradient accumulator (16-bit inputs) is reserved only when that gradient is
+    // asked for: dm_linear_cross_entropy_workspace(desc, 2) sizes a call without it
+    const LpPlan p = lp_plan(lp, false, true, !f32, !f32 && grad_weight != nullptr);
     if (workspace_bytes < p.total)
         return refuse(op + ": the workspace is smaller than dm_linear_cross_entropy_workspace");
     hipStream_t st = (hipStream_t)stream;

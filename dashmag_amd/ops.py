@@ -57,10 +57,36 @@ def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def _offsets(t, device):
-    """Offsets of any int dtype as the int32 device array the kernels read."""
+_I32_MAX = (1 << 31) - 1
+
+
+def _offsets(t, device, op=None, what="offsets"):
+    """Offsets of any int dtype as the int32 device array the kernels read; with ``op``, values
+    outside int32 are refused rather than wrapped by the cast."""
     t = torch.as_tensor(t)
+    if op is not None and t.numel() and t.dtype not in (torch.int32, torch.int16, torch.uint8,
+                                                       torch.int8):
+        lo, hi = int(t.min()), int(t.max())
+        if lo < -_I32_MAX - 1 or hi > _I32_MAX:
+            raise Unsupported(f"{op}: {what} must fit in int32, got values in [{lo}, {hi}]")
     return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _cu_seqlens(op, t, device, tokens, exact=True, what="cu_seqlens"):
+    """Sequence offsets, checked on the host as dash-ops' ``read_cu_seqlens`` checks them
+    (crates/dash-ops/src/sequences.rs:49-67): they start at 0 and do not decrease, and they end
+    at ``tokens`` (``exact``) or, for attention's packed mask, at most there (positions past the
+    last offset belong to no sequence, crates/dash-contract/src/attention.rs:49-54). Offsets the
+    kernels would index rows with are never passed on unchecked. Returns the int32 device
+    array."""
+    host = torch.as_tensor(t).detach().to("cpu", torch.int64)
+    cu = host.tolist()
+    ok = (len(cu) >= 1 and cu[0] == 0 and all(a <= b for a, b in zip(cu, cu[1:]))
+          and (cu[-1] == tokens if exact else cu[-1] <= tokens))
+    if not ok:
+        end = f"T = {tokens}" if exact else f"at most T = {tokens}"
+        raise Unsupported(f"{op}: {what} must go from 0 to {end} without decreasing, got {cu}")
+    return _offsets(host, device, op, what)
 
 
 # ------------------------------------------------------------------------------------------
@@ -101,7 +127,8 @@ def _attention_desc(op, q, k, v, mask: AttentionMask, options: AttentionOptions,
         if cq.dim() != 1 or ck.dim() != 1 or cq.shape != ck.shape or cq.shape[0] < 1:
             raise Unsupported(f"{op}: cu_seqlens_q and cu_seqlens_k are [S + 1], one S, got "
                               f"{list(cq.shape)}, {list(ck.shape)}")
-        cq, ck = _offsets(cq, q.device), _offsets(ck, q.device)
+        cq = _cu_seqlens(op, cq, q.device, tq, exact=False, what="cu_seqlens_q")
+        ck = _cu_seqlens(op, ck, q.device, tk, exact=False, what="cu_seqlens_k")
         keep += [cq, ck]
         desc.mask_kind = _lib.DM_MASK_PACKED
         desc.cu_seqlens_q, desc.cu_seqlens_k = cq.data_ptr(), ck.data_ptr()
@@ -189,7 +216,7 @@ def attention_decode(query, key, value, lengths=None, options=None):
         lt = torch.as_tensor(lengths)
         if tuple(lt.shape) != (b,):
             raise Unsupported(f"{op}: the cache lengths are [B] = [{b}]")
-        ln = _offsets(lt, query.device)
+        ln = _cache_lengths(op, lt, b, query.device)
     q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
     out = torch.empty_like(q)
     nbytes = _lib.lib().dm_attention_decode_workspace(ctypes.byref(desc))
@@ -232,7 +259,9 @@ def _cache_lengths(op, lengths, b, device):
     lt = torch.as_tensor(lengths)
     if tuple(lt.shape) != (b,):
         raise Unsupported(f"{op}: the cache lengths are [B] = [{b}]")
-    return _offsets(lt, device)
+    if lt.numel() and int(lt.min()) < 0:
+        raise Unsupported(f"{op}: the cache lengths are not negative")
+    return _offsets(lt, device, op, "the cache lengths")
 
 
 def attention_decode_packed(query, key, value, cu_seqlens_k, lengths=None, options=None,
@@ -251,14 +280,15 @@ def attention_decode_packed(query, key, value, cu_seqlens_k, lengths=None, optio
     cu = torch.as_tensor(cu_seqlens_k)
     if cu.dim() != 1 or cu.shape[0] != b + 1:
         raise Unsupported(f"{op}: cu_seqlens_k is [B + 1] = [{b + 1}]")
+    host = cu.detach().to("cpu", torch.int64)
+    if b > 0 and (int(host.min()) < 0 or int(host.max()) > key.shape[0]
+                  or bool((host[1:] < host[:-1]).any())):
+        raise Unsupported(f"{op}: cu_seqlens_k must lie within the cache's {key.shape[0]} "
+                          "rows without decreasing")
     if max_len is None:
-        host = cu.detach().to("cpu", torch.int64)
         max_len = int((host[1:] - host[:-1]).max()) if b > 0 else 0
-        if int(host.min()) < 0 or int(host.max()) > key.shape[0]:
-            raise Unsupported(f"{op}: cu_seqlens_k must lie within the cache's {key.shape[0]} "
-                              "rows")
     desc = _decode_desc(op, query, key, value, max(int(max_len), 0), options)
-    cu = _offsets(cu, query.device)
+    cu = _offsets(cu, query.device, op, "cu_seqlens_k")
     desc.cu_seqlens_k, desc.nseq = cu.data_ptr(), b
     ln = _cache_lengths(op, lengths, b, query.device)
     q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
@@ -291,7 +321,7 @@ def attention_decode_paged(query, key_pages, value_pages, block_table, lengths=N
         raise Unsupported(f"{op}: pages hold at least one key")
     max_pages = bt.shape[1]
     desc = _decode_desc(op, query, key_pages, value_pages, max_pages * page_size, options)
-    bt = _offsets(bt, query.device)
+    bt = _offsets(bt, query.device, op, "the block table")
     ln = _cache_lengths(op, lengths, b, query.device)
     q, k, v = query.contiguous(), key_pages.contiguous(), value_pages.contiguous()
     out = torch.empty_like(q)
@@ -357,7 +387,7 @@ def _gdr_desc(op, q, k, v, g, beta, cu_seqlens, qk_l2norm, scale, step, keep):
         if cu.dim() != 1 or cu.shape[0] < 2:
             raise Unsupported(f"{op}: cu_seqlens must hold S + 1 >= 2 offsets, got "
                               f"{cu.shape[0] if cu.dim() == 1 else list(cu.shape)}")
-        cu = _offsets(cu, q.device)
+        cu = _cu_seqlens(op, cu, q.device, t if not step else b)
         keep.append(cu)
         desc.cu_seqlens, desc.nseq = cu.data_ptr(), cu.shape[0] - 1
         nseq = cu.shape[0] - 1
@@ -494,9 +524,10 @@ def _conv1d_desc(op, x, weight, bias, states, cu_seqlens, activation, keep):
         if x.shape[0] != 1:
             raise Unsupported(f"{op}: packed sequences lie along T of a batch of one, "
                               f"got B = {x.shape[0]}")
-        cu = _offsets(cu_seqlens, x.device)
-        if cu.numel() < 2:
-            raise Unsupported(f"{op}: cu_seqlens must hold N + 1 >= 2 offsets, got {cu.numel()}")
+        n_off = torch.as_tensor(cu_seqlens).numel()
+        if n_off < 2:
+            raise Unsupported(f"{op}: cu_seqlens must hold N + 1 >= 2 offsets, got {n_off}")
+        cu = _cu_seqlens(op, cu_seqlens, x.device, desc.t)
         keep.append(cu)
         desc.cu_seqlens = cu.data_ptr()
         desc.nseq = nseq = cu.numel() - 1
@@ -617,6 +648,18 @@ def causal_conv1d_update(x, weight, bias, state,
 # Chosen-token log-probability
 # ------------------------------------------------------------------------------------------
 
+def _masked_ids(op, masked, v):
+    """The masked token ids as a list, each checked against the vocabulary here, before the
+    uint32 array the C ABI takes is built (a larger id would wrap in that cast)."""
+    ids = [int(i) for i in masked]
+    if any(i < 0 for i in ids):
+        raise Unsupported(f"{op}: masked token ids are not negative")
+    for i in ids:
+        if i >= v:
+            raise Unsupported(f"{op}: masked token id {i} is not below the vocabulary size {v}")
+    return ids
+
+
 def _logprob(hidden, weight, targets, masked, options, with_grad):
     op = "chosen_logprob"
     options = options or LogprobOptions()
@@ -633,9 +676,7 @@ def _logprob(hidden, weight, targets, masked, options, with_grad):
     if tuple(tg.shape) != (n,):
         raise Unsupported(f"{op}: targets must be [n] = [{n}]")
     tg = tg.to(device=hidden.device, dtype=torch.int64).contiguous()
-    ids = [int(i) for i in masked]
-    if any(i < 0 for i in ids):
-        raise Unsupported(f"{op}: masked token ids are not negative")
+    ids = _masked_ids(op, masked, v)
     ids_c = (ctypes.c_uint32 * max(len(ids), 1))(*ids)
     desc = _lib.LogprobDesc(n=n, v=v, d=d, hidden_dtype=_dtype(op, hidden),
                             weight_dtype=_dtype(op, weight),
@@ -688,9 +729,7 @@ def _lce_desc(op, hidden, weight, targets, options):
     if tuple(tg.shape) != (n,):
         raise Unsupported(f"{op}: targets must be [n] = [{n}]")
     tg = tg.to(device=hidden.device, dtype=torch.int64).contiguous()
-    ids = [int(i) for i in options.masked]
-    if any(i < 0 for i in ids):
-        raise Unsupported(f"{op}: masked token ids are not negative")
+    ids = _masked_ids(op, options.masked, weight.shape[0])
     ids_c = (ctypes.c_uint32 * max(len(ids), 1))(*ids)
     dt = _dtype(op, hidden)
     lp = _lib.LogprobDesc(n=n, v=weight.shape[0], d=d, hidden_dtype=dt, weight_dtype=dt,
@@ -743,7 +782,8 @@ def linear_cross_entropy_backward(hidden, weight, targets, rows, upstream, optio
         raise Unsupported(f"{op}: upstream is [3, n]")
     gh = torch.empty_like(h) if grad_hidden else None
     gw = torch.empty_like(w) if grad_weight else None
-    nbytes = _lib.lib().dm_linear_cross_entropy_workspace(ctypes.byref(desc), 1)
+    nbytes = _lib.lib().dm_linear_cross_entropy_workspace(ctypes.byref(desc),
+                                                          1 if grad_weight else 2)
     ws = _workspace(nbytes, h.device)
     _check(op, _lib.lib().dm_linear_cross_entropy_bwd(
         ctypes.byref(desc), _ptr(h), _ptr(w), _ptr(tg), ctypes.cast(ids_c, ctypes.c_void_p), nid,

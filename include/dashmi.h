@@ -120,7 +120,9 @@ typedef struct {
  * taken as f32); LogprobOptions (logprob.rs:33-56): vocab_chunk tokens per chunk (0: this
  * implementation's own choice, 8192; dash-ops' is 4096 below 2304 rows,
  * crates/dash-ops/src/logprob.rs:90-101), row_chunk the most rows per block (at least 1;
- * dash-ops' default 3072). */
+ * dash-ops' default 3072). A vocab_chunk above 8192 is walked 8192 tokens at a time (the
+ * statistics kernel holds one chunk's logits in registers), so the order of the online sums is
+ * that of 8192-token chunks; results stay within the contract's bounds either way. */
 typedef struct {
     int64_t n, v, d;
     int32_t hidden_dtype, weight_dtype;
@@ -165,6 +167,8 @@ typedef enum {
     DM_PROBE_LOGPROB,
     DM_PROBE_LCE_FWD,
     DM_PROBE_LCE_BWD,
+    DM_PROBE_GDR_CHUNK_FWD_MFMA, /* the MFMA kernels of the chunked forward (a subset of the above) */
+    DM_PROBE_GDR_CHUNK_BWD_MFMA, /* the MFMA kernels of the chunked backward */
     DM_PROBE_COUNT
 } dm_probe;
 uint64_t dm_probe_count(int probe);
@@ -324,7 +328,10 @@ int dm_chosen_logprob(const dm_logprob_desc *desc, const void *hidden, const voi
  * (mean over the counted rows, sum, or none, loss.rs:872-877). targets [n] int64 on the device;
  * masked: n_masked ids on the HOST, any order, each below V, at least one token left. Replaces
  * LinearCrossEntropyBackend::linear_cross_entropy (loss.rs:134-160; the written-out backward is
- * always taken, as with a weight that trains). */
+ * always taken, as with a weight that trains). The workspace query's `backward`: 0 for the
+ * forward, 1 for a backward with both gradients, 2 for a backward without grad_weight (a frozen
+ * output weight: no V x D f32 accumulator is reserved; the backward then refuses a non-NULL
+ * grad_weight with that smaller workspace). */
 size_t dm_linear_cross_entropy_workspace(const dm_lce_desc *desc, int backward);
 int dm_linear_cross_entropy_fwd(const dm_lce_desc *desc, const void *hidden, const void *weight,
                                 const int64_t *targets, const uint32_t *masked, int64_t n_masked,

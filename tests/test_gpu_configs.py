@@ -12,7 +12,7 @@ import torch
 
 import dashmag_amd as dm
 import oracle
-from dashmag_amd import synthetic as syn
+from dashmag_amd import _lib, synthetic as syn
 from fixtures import errors
 
 pytestmark = pytest.mark.gpu
@@ -144,6 +144,32 @@ def test_config4_chunk_backward_slice():
         rr = rel(host(a_), e_)
         print(f"config 4 (2048 tokens) {name}: rel {rr:.2e}")
         assert rr <= BF16_TOL
+
+
+def test_config4_chunk_backward_full():
+    """The backward at config 4's full size (32768 tokens, 8 sequences, H = 16), checked on
+    oracle slices of two sequences x two heads: sequences and heads are independent, so each
+    slice's gradients (and its initial state's) are that sequence's own backward."""
+    c = syn.config4("cuda")
+    opts = dm.ChunkGatedDeltaOptions(output_final_state=True)
+    args = [c[x] for x in ("q", "k", "v", "g", "beta")]
+    dfin = syn.normal(78, tuple(c["h0"].shape), "cuda", std=0.1)
+    _lib.probe_reset()
+    r = dm.chunk_gated_delta_rule_backward(*args, c["h0"], c["cu_seqlens"], c["do"], dfin, opts)
+    torch.cuda.synchronize()
+    assert _lib.probe_counts()["gdr_chunk_bwd_mfma"] > 0, "the MFMA backward did not run"
+    cu = c["cu_seqlens"].tolist()
+    for s in [1, 6]:
+        a, b = cu[s], cu[s + 1]
+        for h in [2, 13]:
+            sl = lambda x: host(x[:, a:b, h:h + 1])  # noqa: E731
+            e = oracle.gdr_chunk_bwd(*(sl(x) for x in args), host(c["h0"][s:s + 1, h:h + 1]),
+                                     sl(c["do"]), host(dfin[s:s + 1, h:h + 1]))
+            got = [sl(x) for x in r[:5]] + [host(r[5][s:s + 1, h:h + 1])]
+            for name, a_, e_ in zip(["dq", "dk", "dv", "dg", "dbeta", "dh0"], got, e):
+                rr = rel(a_, e_)
+                print(f"config 4 seq {s} ({b - a} tokens) head {h} {name}: rel {rr:.2e}")
+                assert rr <= BF16_TOL, (s, h, name, rr)
 
 
 def test_config5_step():

@@ -44,7 +44,7 @@ def test_mfma_forward_matches_oracle(dtype, lens, l2norm, h0):
     opts = dm.ChunkGatedDeltaOptions(qk_l2norm=l2norm, output_final_state=True)
     out, fin = dm.chunk_gated_delta_rule(q, k, v, g, beta, st, cu.cuda(), opts)
     torch.cuda.synchronize()
-    assert _lib.probe_counts()["gdr_chunk_fwd"] > 0
+    assert _lib.probe_counts()["gdr_chunk_fwd_mfma"] > 0, "the MFMA forward did not run"
     eo, ef = oracle.gdr_chunk_fwd(host(q), host(k), host(v), host(g), host(beta),
                                   None if st is None else host(st), cu.numpy(), l2norm,
                                   precision="f64")
@@ -108,7 +108,7 @@ def test_mfma_backward_matches_oracle(dtype, lens, h, l2norm, tol, states):
     opts = dm.ChunkGatedDeltaOptions(qk_l2norm=l2norm, output_final_state=True)
     r = dm.chunk_gated_delta_rule_backward(q, k, v, g, beta, h0, cu.cuda(), do, dfin, opts)
     torch.cuda.synchronize()
-    assert _lib.probe_counts()["gdr_chunk_bwd"] > 0
+    assert _lib.probe_counts()["gdr_chunk_bwd_mfma"] > 0, "the MFMA backward did not run"
     e = oracle.gdr_chunk_bwd(host(q), host(k), host(v), host(g), host(beta),
                              None if h0 is None else host(h0), host(do),
                              None if dfin is None else host(dfin), cu.numpy(), l2norm,
