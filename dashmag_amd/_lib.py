@@ -90,6 +90,7 @@ SIGNATURES = {
                                         _SZ, _VP]),
     "dm_attention_decode_workspace": (_SZ, [_AD]),
     "dm_attention_decode": (ctypes.c_int, [_AD, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "dm_attention_decode_noalloc": (ctypes.c_int, [_AD, _VP, _VP, _VP, _VP, _VP, _VP]),
     "dm_linear_cross_entropy_workspace": (_SZ, [_XD, ctypes.c_int]),
     "dm_linear_cross_entropy_fwd": (ctypes.c_int, [_XD, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _SZ,
                                                    _VP]),

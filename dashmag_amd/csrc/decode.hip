@@ -8,6 +8,7 @@
 // vector units (decode_split): each K/V row (D * 2 bytes) is read by D / 8 lanes with 16-byte
 // loads, one wavefront covering 64 * 8 / D rows per load, the dot products reduced across the
 // row's lanes with xor shuffles; f32 online softmax per lane group.
+#include <mutex>
 #include <string>
 
 #include "attention_kernels.h"
@@ -690,6 +691,37 @@ static size_t decode_workspace(const dm_attention_desc *d, bool split) {
     return align_up(parts * d->d * sizeof(float)) + align_up(parts * sizeof(float));
 }
 
+// The no-allocation entry point's scratch: one array per device, held from the library's load
+// until the process ends, for the split pass's partial outputs and log-sum-exps. Every call on a
+// device shares it (calls that overlap on one device race). The split pass writes every partial
+// it has, so nothing needs clearing between calls.
+constexpr size_t kDecodeScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+// The device address of this device's `scratch`, looked up once per device (the array's name in
+// host code is a host-side stand-in, never a device address).
+static int scratch_address(void **out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void *addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "attention_decode_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return refuse("attention_decode_noalloc: device index " + std::to_string(dev) +
+                      " beyond the library's table of " + std::to_string(kMaxDevices));
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return hip_status(e, "attention_decode_noalloc: hipGetSymbolAddress(scratch)");
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return DM_OK;
+}
+
 }  // namespace dm
 
 using namespace dm;
@@ -723,6 +755,20 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         return DM_OK;
     }
     return run_decode(op, d, split_takes(d), false, q, k, v, lengths, map, o, workspace, st);
+}
+
+int dm_attention_decode_noalloc(const dm_attention_desc *d, const void *q, const void *k,
+                                const void *v, const int32_t *lengths, void *o, void *stream) {
+    if (int rc = check_decode("attention_decode", d)) return rc;
+    const size_t need = dm_attention_decode_workspace(d);
+    if (need > kDecodeScratchBytes)
+        return refuse("attention_decode: the call needs " + std::to_string(need) +
+                      " bytes of scratch, above the no-allocation entry point's " +
+                      std::to_string(kDecodeScratchBytes) + "; use dm_attention_decode");
+    void *ws = nullptr;
+    if (need > 0)
+        if (int rc = scratch_address(&ws)) return rc;
+    return dm_attention_decode(d, q, k, v, lengths, o, ws, need, stream);
 }
 
 size_t dm_attention_decode_paged_workspace(const dm_attention_desc *d, int64_t page_size) {

@@ -236,6 +236,17 @@ int dm_attention_decode(const dm_attention_desc *desc, const void *q, const void
                         const void *v, const int32_t *lengths, void *o, void *workspace,
                         size_t workspace_bytes, void *stream);
 
+/* dm_attention_decode without a workspace and without allocating (no counterpart in the
+ * reference): for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The split pass's partials go to a
+ * static device array of 16 MiB per GPU, held until the process ends; a call whose
+ * dm_attention_decode_workspace exceeds 16 MiB is refused (about 64 sequences x 32 query heads
+ * x 16 splits at D = 128). Every call on one GPU shares that array: calls that overlap on one GPU
+ * (concurrent streams or threads) race. Same arguments, results and refusals as
+ * dm_attention_decode otherwise (dense or packed cache). */
+int dm_attention_decode_noalloc(const dm_attention_desc *desc, const void *q, const void *k,
+                                const void *v, const int32_t *lengths, void *o, void *stream);
+
 /* Decoding against a paged cache (no counterpart in the reference, whose decode takes the dense
  * cache of crates/dash-contract/src/attention.rs:61-71; this is the same operation, with the
  * dense cache's key j of sequence b stored at row j % page_size of page

@@ -139,3 +139,15 @@ def test_logprob_refusals():
     d.hidden_dtype, d.row_chunk = _lib.DM_BF16, 0
     assert call([]) == _lib.DM_ERR_REFUSED
     assert _lib.last_error() == "chosen_logprob: row_chunk must be at least 1"
+
+
+def test_noalloc_decode_refuses_calls_beyond_its_scratch():
+    """The no-allocation decode refuses, before touching the device, a call whose partials would
+    not fit its 16 MiB scratch (here 1024 x 64 rows of 256 f32 partials, 64 MiB)."""
+    d = _lib.AttentionDesc(b=1024, tq=1, tk=100_000, hq=64, hkv=8, d=256, dtype=_lib.DM_BF16,
+                           mask_kind=_lib.DM_MASK_NONE)
+    lb = _lib.lib()
+    assert lb.dm_attention_decode_workspace(ctypes.byref(d)) > (16 << 20)
+    rc = lb.dm_attention_decode_noalloc(ctypes.byref(d), None, None, None, None, None, None)
+    assert rc == _lib.DM_ERR_REFUSED
+    assert _lib.last_error().startswith("attention_decode: the call needs")
