@@ -28,13 +28,19 @@ class AttentionOptionsC(ctypes.Structure):
                 ("deterministic", ctypes.c_int32)]
 
 
+class Strides(ctypes.Structure):
+    _fields_ = [("b", ctypes.c_int64), ("t", ctypes.c_int64), ("h", ctypes.c_int64)]
+
+
 class AttentionDesc(ctypes.Structure):
     _fields_ = [("b", ctypes.c_int64), ("tq", ctypes.c_int64), ("tk", ctypes.c_int64),
                 ("hq", ctypes.c_int64), ("hkv", ctypes.c_int64), ("d", ctypes.c_int64),
                 ("dtype", ctypes.c_int32), ("mask_kind", ctypes.c_int32),
                 ("key_padding", ctypes.c_void_p), ("cu_seqlens_q", ctypes.c_void_p),
                 ("cu_seqlens_k", ctypes.c_void_p), ("nseq", ctypes.c_int64),
-                ("options", AttentionOptionsC)]
+                ("options", AttentionOptionsC), ("strided", ctypes.c_int32),
+                ("sq", Strides), ("sk", Strides), ("sv", Strides), ("so", Strides),
+                ("sdo", Strides)]
 
 
 class GdrDesc(ctypes.Structure):

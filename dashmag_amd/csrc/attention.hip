@@ -20,19 +20,21 @@ namespace dm {
 template <int DT, int NPL>
 __global__ __launch_bounds__(256) void attn_fwd_generic(MaskInfo m, int64_t B, int64_t Hq,
                                                         int64_t Hkv, int64_t D, float scale,
-                                                        const void *q, const void *k,
-                                                        const void *v, void *o, float *lse) {
+                                                        AttnStrides sd, const void *q,
+                                                        const void *k, const void *v, void *o,
+                                                        float *lse) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t Tq = m.tq, Tk = m.tk;
     if (row >= B * Tq * Hq) return;
     const int64_t h = row % Hq, i = (row / Hq) % Tq, b = row / (Hq * Tq);
     const int64_t kh = h / (Hq / Hkv);
+    const int64_t qo = b * sd.q.b + i * sd.q.t + h * sd.q.h;
     float qr[NPL], acc[NPL];
 #pragma unroll
     for (int e = 0; e < NPL; e++) {
         int64_t d = lane + 64 * e;
-        qr[e] = d < D ? ld<DT>(q, row * D + d) : 0.f;
+        qr[e] = d < D ? ld<DT>(q, qo + d) : 0.f;
         acc[e] = 0.f;
     }
     int64_t lo, hi;
@@ -40,7 +42,8 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(MaskInfo m, int64_t B, i
     float mx = -INFINITY, l = 0.f;
     for (int64_t j = lo; j < hi; j++) {
         if (m.pad && m.pad[b * Tk + j]) continue;
-        const int64_t kr = ((b * Tk + j) * Hkv + kh) * D;
+        const int64_t kr = b * sd.k.b + j * sd.k.t + kh * sd.k.h;
+        const int64_t vr = b * sd.v.b + j * sd.v.t + kh * sd.v.h;
         float s = 0.f;
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
@@ -54,7 +57,7 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(MaskInfo m, int64_t B, i
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
             int64_t d = lane + 64 * e;
-            float vv = d < D ? ld<DT>(v, kr + d) : 0.f;
+            float vv = d < D ? ld<DT>(v, vr + d) : 0.f;
             acc[e] = acc[e] * alpha + p * vv;
         }
         mx = mn;
@@ -76,17 +79,21 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(MaskInfo m, int64_t B, i
 // ------------------------------------------------------------------------------------------
 
 template <int DT, int NPL>
-__global__ __launch_bounds__(256) void attn_delta_generic(int64_t rows, int64_t D,
+__global__ __launch_bounds__(256) void attn_delta_generic(int64_t rows, int64_t Tq, int64_t Hq,
+                                                          int64_t D, AttnStrides sd,
                                                           const void *o, const void *d_o,
                                                           float *delta) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
+    const int64_t h = row % Hq, i = (row / Hq) % Tq, b = row / (Hq * Tq);
+    const int64_t oo = b * sd.o.b + i * sd.o.t + h * sd.o.h;
+    const int64_t go = b * sd.g.b + i * sd.g.t + h * sd.g.h;
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < NPL; e++) {
         int64_t d = lane + 64 * e;
-        if (d < D) s += ld<DT>(o, row * D + d) * ld<DT>(d_o, row * D + d);
+        if (d < D) s += ld<DT>(o, oo + d) * ld<DT>(d_o, go + d);
     }
     s = wave_sum(s);
     if (lane == 0) delta[row] = s;
@@ -95,22 +102,24 @@ __global__ __launch_bounds__(256) void attn_delta_generic(int64_t rows, int64_t 
 template <int DT, int NPL>
 __global__ __launch_bounds__(256) void attn_dq_generic(MaskInfo m, int64_t B, int64_t Hq,
                                                        int64_t Hkv, int64_t D, float scale,
-                                                       const void *q, const void *k,
-                                                       const void *v, const float *lse,
-                                                       const void *d_o, const float *delta,
-                                                       void *dq) {
+                                                       AttnStrides sd, const void *q,
+                                                       const void *k, const void *v,
+                                                       const float *lse, const void *d_o,
+                                                       const float *delta, void *dq) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t Tq = m.tq, Tk = m.tk;
     if (row >= B * Tq * Hq) return;
     const int64_t h = row % Hq, i = (row / Hq) % Tq, b = row / (Hq * Tq);
     const int64_t kh = h / (Hq / Hkv);
+    const int64_t qo = b * sd.q.b + i * sd.q.t + h * sd.q.h;
+    const int64_t go = b * sd.g.b + i * sd.g.t + h * sd.g.h;
     float qr[NPL], gr[NPL], acc[NPL];
 #pragma unroll
     for (int e = 0; e < NPL; e++) {
         int64_t d = lane + 64 * e;
-        qr[e] = d < D ? ld<DT>(q, row * D + d) : 0.f;
-        gr[e] = d < D ? ld<DT>(d_o, row * D + d) : 0.f;
+        qr[e] = d < D ? ld<DT>(q, qo + d) : 0.f;
+        gr[e] = d < D ? ld<DT>(d_o, go + d) : 0.f;
         acc[e] = 0.f;
     }
     const float ls = lse[row], dl = delta[row];
@@ -119,14 +128,15 @@ __global__ __launch_bounds__(256) void attn_dq_generic(MaskInfo m, int64_t B, in
     if (ls == -INFINITY) hi = lo;  // a query that sees no key: dq = 0
     for (int64_t j = lo; j < hi; j++) {
         if (m.pad && m.pad[b * Tk + j]) continue;
-        const int64_t kr = ((b * Tk + j) * Hkv + kh) * D;
+        const int64_t kr = b * sd.k.b + j * sd.k.t + kh * sd.k.h;
+        const int64_t vr = b * sd.v.b + j * sd.v.t + kh * sd.v.h;
         float s = 0.f, dp = 0.f;
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
             int64_t d = lane + 64 * e;
             if (d < D) {
                 s += qr[e] * ld<DT>(k, kr + d);
-                dp += gr[e] * ld<DT>(v, kr + d);
+                dp += gr[e] * ld<DT>(v, vr + d);
             }
         }
         s = wave_sum(s);
@@ -149,22 +159,25 @@ __global__ __launch_bounds__(256) void attn_dq_generic(MaskInfo m, int64_t B, in
 template <int DT, int NPL>
 __global__ __launch_bounds__(256) void attn_dkdv_generic(MaskInfo m, int64_t B, int64_t Hq,
                                                          int64_t Hkv, int64_t D, float scale,
-                                                         const void *q, const void *k,
-                                                         const void *v, const float *lse,
-                                                         const void *d_o, const float *delta,
-                                                         void *dk, void *dv) {
+                                                         AttnStrides sd, const void *q,
+                                                         const void *k, const void *v,
+                                                         const float *lse, const void *d_o,
+                                                         const float *delta, void *dk,
+                                                         void *dv) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t Tq = m.tq, Tk = m.tk;
     if (row >= B * Tk * Hkv) return;
     const int64_t kh = row % Hkv, j = (row / Hkv) % Tk, b = row / (Hkv * Tk);
     const int64_t group = Hq / Hkv;
+    const int64_t ko = b * sd.k.b + j * sd.k.t + kh * sd.k.h;
+    const int64_t vo = b * sd.v.b + j * sd.v.t + kh * sd.v.h;
     float kr[NPL], vr[NPL], ak[NPL], av[NPL];
 #pragma unroll
     for (int e = 0; e < NPL; e++) {
         int64_t d = lane + 64 * e;
-        kr[e] = d < D ? ld<DT>(k, row * D + d) : 0.f;
-        vr[e] = d < D ? ld<DT>(v, row * D + d) : 0.f;
+        kr[e] = d < D ? ld<DT>(k, ko + d) : 0.f;
+        vr[e] = d < D ? ld<DT>(v, vo + d) : 0.f;
         ak[e] = av[e] = 0.f;
     }
     const bool padded = m.pad && m.pad[b * Tk + j];
@@ -176,13 +189,15 @@ __global__ __launch_bounds__(256) void attn_dkdv_generic(MaskInfo m, int64_t B, 
             const int64_t qr = (b * Tq + i) * Hq + h;
             const float ls = lse[qr];
             if (ls == -INFINITY) continue;
+            const int64_t qo = b * sd.q.b + i * sd.q.t + h * sd.q.h;
+            const int64_t go = b * sd.g.b + i * sd.g.t + h * sd.g.h;
             float s = 0.f, dp = 0.f;
 #pragma unroll
             for (int e = 0; e < NPL; e++) {
                 int64_t d = lane + 64 * e;
                 if (d < D) {
-                    s += kr[e] * ld<DT>(q, qr * D + d);
-                    dp += vr[e] * ld<DT>(d_o, qr * D + d);
+                    s += kr[e] * ld<DT>(q, qo + d);
+                    dp += vr[e] * ld<DT>(d_o, go + d);
                 }
             }
             s = wave_sum(s);
@@ -193,8 +208,8 @@ __global__ __launch_bounds__(256) void attn_dkdv_generic(MaskInfo m, int64_t B, 
             for (int e = 0; e < NPL; e++) {
                 int64_t d = lane + 64 * e;
                 if (d < D) {
-                    ak[e] += ds * ld<DT>(q, qr * D + d);
-                    av[e] += p * ld<DT>(d_o, qr * D + d);
+                    ak[e] += ds * ld<DT>(q, qo + d);
+                    av[e] += p * ld<DT>(d_o, go + d);
                 }
             }
         }
@@ -232,6 +247,12 @@ int check_attention(const dm_attention_desc *d, const char *op) {
             return refuse(o + ": cu_seqlens_q and cu_seqlens_k are [S + 1], one S");
     }
     if (d->mask_kind < 0 || d->mask_kind > 2) return refuse(o + ": unknown mask kind");
+    if (d->strided) {
+        const AttnStrides s = attn_strides(d);
+        if (!strides_ok(s.q) || !strides_ok(s.k) || !strides_ok(s.v) || !strides_ok(s.o) ||
+            !strides_ok(s.g))
+            return refuse(o + ": strides must not be negative");
+    }
     if (d->d > 256)
         return refuse(o + ": head dimension " + std::to_string(d->d) +
                       " above 256 is not implemented");
@@ -262,7 +283,8 @@ int launch_attn_fwd_generic(const MaskInfo &m, const dm_attention_desc *d, float
     dim3 grid((unsigned)((rows + 3) / 4)), block(256);
     DM_DISPATCH_DT_NPL(d->dtype, npl_of(d->d),
                        attn_fwd_generic<DT, NPL><<<grid, block, 0, st>>>(
-                           m, d->b, d->hq, d->hkv, d->d, scale, q, k, v, o, lse));
+                           m, d->b, d->hq, d->hkv, d->d, scale, attn_strides(d), q, k, v, o,
+                           lse));
     probe_add(DM_PROBE_ATTN_FWD_GENERIC);
     DM_LAUNCH_CHECK("attention: forward launch");
     return DM_OK;
@@ -298,7 +320,8 @@ int dm_attention_fwd(const dm_attention_desc *desc, const void *q, const void *k
         DM_LAUNCH_CHECK("attention: fill");
         return DM_OK;
     }
-    if (mfma_fwd_takes(desc)) return launch_attn_fwd_mfma(m, desc, scale, q, k, v, o, lse, st);
+    if (mfma_fwd_takes(desc, q, k, v))
+        return launch_attn_fwd_mfma(m, desc, scale, q, k, v, o, lse, st);
     return launch_attn_fwd_generic(m, desc, scale, q, k, v, o, lse, st);
 }
 
@@ -332,18 +355,20 @@ int dm_attention_bwd(const dm_attention_desc *desc, const void *q, const void *k
     }
     float *delta = (float *)workspace;
     char *rest = (char *)workspace + align_up(qrows * sizeof(float));
-    if (mfma_bwd_takes(desc))
+    if (mfma_bwd_takes(desc, q, k, v, o, d_o))
         return launch_attn_bwd_mfma(m, desc, scale, q, k, v, o, lse, d_o, dq, dk, dv, delta,
                                     rest, st);
     const int npl = npl_of(desc->d);
+    const AttnStrides sd = attn_strides(desc);
     dim3 block(256);
     DM_DISPATCH_DT_NPL(desc->dtype, npl,
         attn_delta_generic<DT, NPL><<<dim3((unsigned)((qrows + 3) / 4)), block, 0, st>>>(
-            qrows, desc->d, o, d_o, delta);
+            qrows, desc->tq, desc->hq, desc->d, sd, o, d_o, delta);
         attn_dq_generic<DT, NPL><<<dim3((unsigned)((qrows + 3) / 4)), block, 0, st>>>(
-            m, desc->b, desc->hq, desc->hkv, desc->d, scale, q, k, v, lse, d_o, delta, dq);
+            m, desc->b, desc->hq, desc->hkv, desc->d, scale, sd, q, k, v, lse, d_o, delta, dq);
         attn_dkdv_generic<DT, NPL><<<dim3((unsigned)((krows + 3) / 4)), block, 0, st>>>(
-            m, desc->b, desc->hq, desc->hkv, desc->d, scale, q, k, v, lse, d_o, delta, dk, dv));
+            m, desc->b, desc->hq, desc->hkv, desc->d, scale, sd, q, k, v, lse, d_o, delta, dk,
+            dv));
     probe_add(DM_PROBE_ATTN_BWD_GENERIC, 3);
     DM_LAUNCH_CHECK("attention_backward: launch");
     return DM_OK;

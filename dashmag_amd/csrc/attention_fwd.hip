@@ -63,7 +63,7 @@ __device__ uint64_t dm_trace_fwd[2][256][4];
 
 template <int DT, int D, bool PAD>
 __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, int64_t Hq,
-                                                      int64_t Hkv, float scale,
+                                                      int64_t Hkv, float scale, AttnStrides sd,
                                                       const uint16_t *__restrict__ q,
                                                       const uint16_t *__restrict__ k,
                                                       const uint16_t *__restrict__ v,
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     // this wavefront's queries as the B operand: col = query, k = head dimension
     Frag8 qf[KSTEPS];
     {
-        const uint16_t *qp = q + ((b * Tq + qi) * Hq + h) * D + half * 8;
+        const uint16_t *qp = q + b * sd.q.b + qi * sd.q.t + h * sd.q.h + half * 8;
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++)
             qf[s].u = qvalid ? *(const uint4 *)(qp + s * 16) : make_uint4(0, 0, 0, 0);
@@ -152,27 +152,30 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
 
     // staging: 16-byte chunks of one K and one V tile per thread, by buffer loads whose range
     // ends at the last key (rows past it read zeros)
-    const int32_t kvstride = (int32_t)(Hkv * D);
-    const uint32_t kvbytes = (uint32_t)(((Tk - 1) * Hkv + 1) * D * 2);
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + (b * Tk * Hkv + kh) * D, kvbytes);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + (b * Tk * Hkv + kh) * D, kvbytes);
+    // (row strides in elements; the host checked that every byte range fits 32 bits)
+    const int32_t kstride = (int32_t)sd.k.t, vstride = (int32_t)sd.v.t;
+    const uint32_t kbytes = (uint32_t)(((Tk - 1) * sd.k.t + D) * 2);
+    const uint32_t vbytes = (uint32_t)(((Tk - 1) * sd.v.t + D) * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + b * sd.k.b + kh * sd.k.h, kbytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + b * sd.v.b + kh * sd.v.h, vbytes);
     const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
     constexpr int CPR = D / 8;              // chunks per row
     constexpr int NCH = kFwdN * CPR / 512;   // chunks per thread per tensor
     constexpr int RSTEP = 512 / CPR;        // rows between a thread's chunks
     const int crow = tid / CPR, ccol = tid % CPR;
-    const uint32_t goff = (uint32_t)(crow * kvstride + ccol * 8) * 2;
+    const uint32_t koff = (uint32_t)(crow * kstride + ccol * 8) * 2;
+    const uint32_t voff = (uint32_t)(crow * vstride + ccol * 8) * 2;
     uint4 rk[NCH], rv[NCH];
     auto tile_key = [&](int32_t j) { return kv_lo + (j < nt ? j : 0) * kFwdN; };
     auto load_k = [&](int32_t j) __attribute__((always_inline)) {
-        const uint32_t base = (uint32_t)tile_key(j) * (uint32_t)kvstride * 2 + goff;
+        const uint32_t base = (uint32_t)tile_key(j) * (uint32_t)kstride * 2 + koff;
 #pragma unroll
-        for (int u = 0; u < NCH; u++) rk[u] = buf_load16(krs, base + (uint32_t)(u * RSTEP * kvstride * 2));
+        for (int u = 0; u < NCH; u++) rk[u] = buf_load16(krs, base + (uint32_t)(u * RSTEP * kstride * 2));
     };
     auto load_v = [&](int32_t j) __attribute__((always_inline)) {
-        const uint32_t base = (uint32_t)tile_key(j) * (uint32_t)kvstride * 2 + goff;
+        const uint32_t base = (uint32_t)tile_key(j) * (uint32_t)vstride * 2 + voff;
 #pragma unroll
-        for (int u = 0; u < NCH; u++) rv[u] = buf_load16(vrs, base + (uint32_t)(u * RSTEP * kvstride * 2));
+        for (int u = 0; u < NCH; u++) rv[u] = buf_load16(vrs, base + (uint32_t)(u * RSTEP * vstride * 2));
     };
     auto store_k = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
@@ -339,12 +342,22 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
             ltot > 0.f ? (float)((double)mc * 0.6931471805599453 + log((double)ltot)) : -INFINITY;
 }
 
-bool mfma_fwd_takes(const dm_attention_desc *d) {
+// Whether the 16-bit kernels' buffer loads reach `rows` rows of `x` (a row every x.t elements,
+// D wide) with 32-bit byte offsets from one (batch, head) base.
+bool rows_fit_32bit(const Strd &x, int64_t rows, int64_t d) {
+    return rows <= 0 || ((rows - 1) * x.t + d) * 2 < (1ll << 31);
+}
+
+bool mfma_fwd_takes(const dm_attention_desc *d, const void *q, const void *k, const void *v) {
     // a positive scale keeps the maximum of the raw scores the maximum of the scaled ones;
-    // buffer loads take 32-bit byte offsets within one batch row's keys and values
+    // buffer loads take 32-bit byte offsets within one (batch row, head)'s keys and values;
+    // 16-byte vector loads need 16-byte rows and bases
+    const AttnStrides s = attn_strides(d);
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) && (d->d == 64 || d->d == 128) &&
            d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
-           d->tk * d->hkv * d->d * 2 < (1ll << 31);
+           rows_fit_32bit(s.k, d->tk, d->d) && rows_fit_32bit(s.v, d->tk, d->d) &&
+           strides_16b(s.q) && strides_16b(s.k) && strides_16b(s.v) && aligned_16b(q) &&
+           aligned_16b(k) && aligned_16b(v);
 }
 
 #ifdef DM_TRACE_FWD
@@ -363,13 +376,14 @@ int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     dim3 grid((unsigned)nblocks), block(512);
     const uint16_t *qq = (const uint16_t *)q, *kk = (const uint16_t *)k, *vv = (const uint16_t *)v;
     uint16_t *oo = (uint16_t *)o;
+    const AttnStrides sd = attn_strides(d);
 #define FWD(DT, DD)                                                                           \
     if (m.pad)                                                                                \
-        attn_fwd_mfma<DT, DD, true><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq,  \
-                                                          kk, vv, oo, lse);                  \
+        attn_fwd_mfma<DT, DD, true><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd,  \
+                                                          qq, kk, vv, oo, lse);              \
     else                                                                                      \
-        attn_fwd_mfma<DT, DD, false><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
-                                                           kk, vv, oo, lse)
+        attn_fwd_mfma<DT, DD, false><<<grid, block, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
+                                                           qq, kk, vv, oo, lse)
     {
         KernelTimer timer(DM_KERNEL_ATTN_FWD, st);
         if (d->dtype == DM_BF16) {

@@ -17,11 +17,13 @@ int launch_attn_fwd_generic(const MaskInfo &m, const dm_attention_desc *d, float
                             hipStream_t st);
 
 // MFMA paths (attention_fwd.hip, attention_mfma_bwd.hip): bf16/f16, D in {64, 128}.
-bool mfma_fwd_takes(const dm_attention_desc *d);
+bool rows_fit_32bit(const Strd &x, int64_t rows, int64_t d);
+bool mfma_fwd_takes(const dm_attention_desc *d, const void *q, const void *k, const void *v);
 int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float scale,
                          const void *q, const void *k, const void *v, void *o, float *lse,
                          hipStream_t st);
-bool mfma_bwd_takes(const dm_attention_desc *d);
+bool mfma_bwd_takes(const dm_attention_desc *d, const void *q, const void *k, const void *v,
+                    const void *o, const void *d_o);
 size_t mfma_bwd_workspace(const dm_attention_desc *d);
 int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float scale,
                          const void *q, const void *k, const void *v, const void *o,

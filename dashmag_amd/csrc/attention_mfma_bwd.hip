@@ -87,7 +87,7 @@ static size_t bwd_layout(const dm_attention_desc *d, char *base, BwdWs *w) {
 // ------------------------------------------------------------------------------------------
 
 template <int DT, int D>
-__global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t Hq,
+__global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t Hq, AttnStrides sd,
                                                 const uint16_t *__restrict__ o,
                                                 const uint16_t *__restrict__ d_o,
                                                 const float *__restrict__ lse,
@@ -107,8 +107,8 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
     constexpr int CH = D / 8;  // 16-byte chunks per head row
     for (int64_t h = lane / CH; h < Hq; h += 64 / CH) {
         const int c = lane % CH;
-        const int64_t base = (row * Hq + h) * D + c * 8;
-        const uint4 a = *(const uint4 *)(o + base), g = *(const uint4 *)(d_o + base);
+        const uint4 a = *(const uint4 *)(o + b * sd.o.b + i * sd.o.t + h * sd.o.h + c * 8);
+        const uint4 g = *(const uint4 *)(d_o + b * sd.g.b + i * sd.g.t + h * sd.g.h + c * 8);
         float s = unpack_lo<DT>(a.x) * unpack_lo<DT>(g.x) + unpack_hi<DT>(a.x) * unpack_hi<DT>(g.x) +
                   unpack_lo<DT>(a.y) * unpack_lo<DT>(g.y) + unpack_hi<DT>(a.y) * unpack_hi<DT>(g.y) +
                   unpack_lo<DT>(a.z) * unpack_lo<DT>(g.z) + unpack_hi<DT>(a.z) * unpack_hi<DT>(g.z) +
@@ -121,7 +121,6 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
             w.lse2[row * Hq + h] = l == -INFINITY ? INFINITY : l * 1.4426950408889634f;
         }
     }
-    (void)b;
 }
 
 // Per tile of kRowTile rows: [union lo, union hi) of the rows' intervals, and [full lo, full hi), the
@@ -291,7 +290,7 @@ struct DkdvSmem {
 
 template <int DT, int D, bool PAD>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_t Hq,
-                                                   int64_t Hkv, float scale,
+                                                   int64_t Hkv, float scale, AttnStrides sd,
                                                    const uint16_t *__restrict__ q,
                                                    const uint16_t *__restrict__ k,
                                                    const uint16_t *__restrict__ v,
@@ -330,8 +329,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     // K (P waves) or V (dS waves) of this lane's key as B operands (col = key, k = head dim)
     Frag8 bf[KSTEPS];
     {
-        const uint16_t *src = pwave ? k : v;
-        const uint16_t *bp = src + ((b * Tk + key) * Hkv + kh) * D + half * 8;
+        const uint16_t *bp = (pwave ? k + b * sd.k.b + (int64_t)key * sd.k.t + kh * sd.k.h
+                                    : v + b * sd.v.b + (int64_t)key * sd.v.t + kh * sd.v.h) +
+                             half * 8;
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++)
             bf[s].u = kvalid ? *(const uint4 *)(bp + s * 16) : make_uint4(0, 0, 0, 0);
@@ -403,9 +403,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     // two register sets, a step's loads issued two steps before its store
     constexpr int CPR = D / 8, NCH = (kDkdvStep * CPR + 511) / 512, RSTEP = 512 / CPR;
     const int crow = tid / CPR, ccol = tid % CPR;  // crow >= kDkdvStep: no chunk (D = 64)
-    const uint32_t qrow_bytes = (uint32_t)(Hq * D * 2);
-    const uint32_t qbytes = (uint32_t)(((Tq - 1) * Hq + 1) * D * 2);
-    const uint32_t goff = crow * qrow_bytes + ccol * 16;
+    // (row strides in bytes; the host checked that every byte range fits 32 bits)
+    const uint32_t qrow_bytes = (uint32_t)(sd.q.t * 2), grow_bytes = (uint32_t)(sd.g.t * 2);
+    const uint32_t qbytes = (uint32_t)(((Tq - 1) * sd.q.t + D) * 2);
+    const uint32_t gbytes = (uint32_t)(((Tq - 1) * sd.g.t + D) * 2);
     struct Stage {
         uint4 q[NCH], g[NCH];
         float lse, delta;
@@ -420,15 +421,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     const __amdgpu_buffer_rsrc_t lrs = make_rsrc(w.rlo + b * Tq, (uint32_t)(Tq * 4));
     const __amdgpu_buffer_rsrc_t hrs = make_rsrc(w.rhi + b * Tq, (uint32_t)(Tq * 4));
     auto load = [&](Stage &x, int64_t h, int64_t t) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t qrs = make_rsrc(q + (b * Tq * Hq + h) * D, qbytes);
-        const __amdgpu_buffer_rsrc_t grs = make_rsrc(d_o + (b * Tq * Hq + h) * D, qbytes);
-        const uint32_t base = (uint32_t)(t * kDkdvStep) * qrow_bytes + ccol * 16;
+        const __amdgpu_buffer_rsrc_t qrs = make_rsrc(q + b * sd.q.b + h * sd.q.h, qbytes);
+        const __amdgpu_buffer_rsrc_t grs = make_rsrc(d_o + b * sd.g.b + h * sd.g.h, gbytes);
+        const uint32_t i0 = (uint32_t)(t * kDkdvStep);
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
             const int r = (crow + u * RSTEP) & (kDkdvStep - 1);
-            const uint32_t off = base + r * qrow_bytes;
-            x.q[u] = buf_load16(qrs, off);
-            x.g[u] = buf_load16(grs, off);
+            x.q[u] = buf_load16(qrs, (i0 + r) * qrow_bytes + ccol * 16);
+            x.g[u] = buf_load16(grs, (i0 + r) * grow_bytes + ccol * 16);
         }
         const uint32_t i = (uint32_t)(t * kDkdvStep) + (tid & (kDkdvStep - 1));
         const __amdgpu_buffer_rsrc_t srs = make_rsrc(w.lse2 + b * Tq * Hq + h, mbytes);
@@ -748,7 +748,8 @@ struct DqSmem {
 
 template <int DT, int D, bool PAD>
 __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t Hq, int64_t Hkv,
-                                                 float scale, const uint16_t *__restrict__ q,
+                                                 float scale, AttnStrides sd,
+                                                 const uint16_t *__restrict__ q,
                                                  const uint16_t *__restrict__ k,
                                                  const uint16_t *__restrict__ v,
                                                  const uint16_t *__restrict__ d_o,
@@ -812,11 +813,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     // Q (P waves) or dO (dS waves) of this lane's query as the B operand: col = query, k = d
     Frag8 bf[KSTEPS];
     {
-        const uint16_t *src = pwave ? q : d_o;
-        const int64_t off = ((b * Tq + qi) * Hq + h) * D + half * 8;
+        const uint16_t *src = (pwave ? q + b * sd.q.b + qi * sd.q.t + h * sd.q.h
+                                     : d_o + b * sd.g.b + qi * sd.g.t + h * sd.g.h) +
+                              half * 8;
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++)
-            bf[s].u = qvalid ? *(const uint4 *)(src + off + s * 16) : make_uint4(0, 0, 0, 0);
+            bf[s].u = qvalid ? *(const uint4 *)(src + s * 16) : make_uint4(0, 0, 0, 0);
     }
     f32x16_t acc[DT32];
 #pragma unroll
@@ -825,10 +827,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         for (int i = 0; i < 16; i++) acc[t][i] = 0.f;
     const float c2 = scale * 1.4426950408889634f;
     const float nlse = -lse2;
-    const int32_t kvstride = (int32_t)(Hkv * D);
-    const uint32_t kvbytes = (uint32_t)(((Tk - 1) * Hkv + 1) * D * 2);
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + (b * Tk * Hkv + kh) * D, kvbytes);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + (b * Tk * Hkv + kh) * D, kvbytes);
+    const int32_t kstride = (int32_t)sd.k.t, vstride = (int32_t)sd.v.t;
+    const uint32_t kbytes = (uint32_t)(((Tk - 1) * sd.k.t + D) * 2);
+    const uint32_t vbytes = (uint32_t)(((Tk - 1) * sd.v.t + D) * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + b * sd.k.b + kh * sd.k.h, kbytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + b * sd.v.b + kh * sd.v.h, vbytes);
     const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
 
     // staging: a tile's K and V rows in 16-byte chunks over the 512 threads, two register
@@ -845,9 +848,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
             const int r = (crow + u * RSTEP) & (kDqStep - 1);
-            const uint32_t off = (uint32_t)((j0 + r) * kvstride + ccol * 8) * 2;
-            x.k[u] = buf_load16(krs, off);
-            x.v[u] = buf_load16(vrs, off);
+            x.k[u] = buf_load16(krs, (uint32_t)((j0 + r) * kstride + ccol * 8) * 2);
+            x.v[u] = buf_load16(vrs, (uint32_t)((j0 + r) * vstride + ccol * 8) * 2);
         }
     };
     auto store = [&](const KvStage &x, DqSlot<D> &sl) __attribute__((always_inline)) {
@@ -1002,14 +1004,26 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 // Host side
 // ------------------------------------------------------------------------------------------
 
-bool mfma_bwd_takes(const dm_attention_desc *d) {
+// The shapes and strides the MFMA backward takes (its buffer loads use 32-bit byte offsets
+// from one (batch row, head) base; 16-byte vector loads need 16-byte rows).
+static bool mfma_bwd_shape_takes(const dm_attention_desc *d) {
+    const AttnStrides s = attn_strides(d);
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) && (d->d == 64 || d->d == 128) &&
            d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
-           d->tk * d->hkv * d->d * 2 < (1ll << 31) && d->tq * d->hq * d->d * 2 < (1ll << 31);
+           rows_fit_32bit(s.k, d->tk, d->d) && rows_fit_32bit(s.v, d->tk, d->d) &&
+           rows_fit_32bit(s.q, d->tq, d->d) && rows_fit_32bit(s.g, d->tq, d->d) &&
+           d->tq * d->hq < (1ll << 29) && strides_16b(s.q) && strides_16b(s.k) &&
+           strides_16b(s.v) && strides_16b(s.o) && strides_16b(s.g);
+}
+
+bool mfma_bwd_takes(const dm_attention_desc *d, const void *q, const void *k, const void *v,
+                    const void *o, const void *d_o) {
+    return mfma_bwd_shape_takes(d) && aligned_16b(q) && aligned_16b(k) && aligned_16b(v) &&
+           aligned_16b(o) && aligned_16b(d_o);
 }
 
 size_t mfma_bwd_workspace(const dm_attention_desc *d) {
-    return mfma_bwd_takes(d) ? bwd_layout(d, nullptr, nullptr) : 0;
+    return mfma_bwd_shape_takes(d) ? bwd_layout(d, nullptr, nullptr) : 0;
 }
 
 #ifdef DM_TRACE_DKDV
@@ -1033,28 +1047,29 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     if (nb_kv >= (1ll << 31) || nb_q >= (1ll << 31)) return refuse("attention_backward: too large");
     const uint16_t *qq = (const uint16_t *)q, *kk = (const uint16_t *)k, *vv = (const uint16_t *)v;
     const uint16_t *oo = (const uint16_t *)o, *gg = (const uint16_t *)d_o;
+    const AttnStrides sd = attn_strides(d);
 #define BWD(DT, DD)                                                                            \
-    bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, oo, gg, lse, \
-                                                                   delta, w);                  \
+    bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, sd, oo, gg,  \
+                                                                   lse, delta, w);             \
     bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
     bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, w);              \
     if (m.pad) {                                                                               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
-                                                                qq, kk, vv, gg, delta, w,      \
+                                                                sd, qq, kk, vv, gg, delta, w,      \
                                                                 (uint16_t *)dk, (uint16_t *)dv); } \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
-        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq,  \
-                                                             kk, vv, gg, delta, w,             \
+        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
+                                                             qq, kk, vv, gg, delta, w,             \
                                                              (uint16_t *)dq); }                \
     } else {                                                                                   \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, false><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
-                                                                 qq, kk, vv, gg, delta, w,     \
+                                                                 sd, qq, kk, vv, gg, delta, w,     \
                                                                  (uint16_t *)dk, (uint16_t *)dv); } \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
-        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, qq, \
-                                                              kk, vv, gg, delta, w,            \
+        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
+                                                              qq, kk, vv, gg, delta, w,            \
                                                               (uint16_t *)dq); }               \
     }
     if (d->dtype == DM_BF16) {

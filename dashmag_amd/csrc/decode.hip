@@ -31,10 +31,15 @@ struct Bf16x8 {
 // (offsets = cu_seqlens_k, [B + 1] int32), at most S of them. Paged: key j of sequence b is row
 // j % page_size of page block_table[b * max_pages + j / page_size] of k, v
 // [num_pages, page_size, Hkv, D]; a page index outside [0, num_pages) reads as zeros.
+//
+// Element strides: the query's along (batch, head); the cache's along (batch row or page, key,
+// head), the key's t stride also the distance between a packed cache's rows.
 struct KvMap {
     const int32_t *offsets;
     const int32_t *block_table;
     int64_t page_size, max_pages, num_pages;
+    int64_t qb, qh;
+    int64_t kb, kt, kh, vb, vt, vh;
 };
 
 // Sequence b's first cache row (dense and packed) and the number of keys it holds: lengths[b]
@@ -54,10 +59,19 @@ __device__ __forceinline__ void kv_extent(const KvMap &m, int64_t b, int64_t S,
     if (len < 0) len = 0;
 }
 
-// Paged caches: the cache row of key j of sequence b, or -1 when its page index is out of range.
-__device__ __forceinline__ int64_t kv_page_row(const KvMap &m, int64_t b, int64_t j) {
+// Element offsets of sequence b's key 0 in the key and value caches (dense and packed), for
+// row0 from kv_extent.
+__device__ __forceinline__ int64_t kv_base_k(const KvMap &m, int64_t b, int64_t row0) {
+    return m.offsets ? row0 * m.kt : b * m.kb;
+}
+__device__ __forceinline__ int64_t kv_base_v(const KvMap &m, int64_t b, int64_t row0) {
+    return m.offsets ? row0 * m.vt : b * m.vb;
+}
+
+// Paged caches: the page holding key j of sequence b, or -1 when its index is out of range.
+__device__ __forceinline__ int64_t kv_page(const KvMap &m, int64_t b, int64_t j) {
     const int64_t pg = m.block_table[b * m.max_pages + j / m.page_size];
-    return pg >= 0 && pg < m.num_pages ? pg * m.page_size + j % m.page_size : -1;
+    return pg >= 0 && pg < m.num_pages ? pg : -1;
 }
 
 template <int DT>
@@ -141,7 +155,7 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const int64_t h = kh * G + g;
-        qp[g] = *(const uint4 *)((const char *)q + ((b * Hq + h) * D + seg * 8) * 2);
+        qp[g] = *(const uint4 *)((const uint16_t *)q + b * map.qb + h * map.qh + seg * 8);
     }
 
     float mx[G], l[G], acc[G][8];
@@ -153,9 +167,9 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
         for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
     }
 
-    const int64_t row_stride = Hkv * D * 2;  // bytes between consecutive keys
-    const char *kb = (const char *)k + (row0 * Hkv + kh) * D * 2 + seg * 16;
-    const char *vb = (const char *)v + (row0 * Hkv + kh) * D * 2 + seg * 16;
+    const int64_t row_stride = map.kt * 2;  // bytes between consecutive keys (and values)
+    const char *kb = (const char *)k + (kv_base_k(map, b, row0) + kh * map.kh) * 2 + seg * 16;
+    const char *vb = (const char *)v + (kv_base_v(map, b, row0) + kh * map.vh) * 2 + seg * 16;
 
     // each wavefront sweeps a contiguous quarter of the split, kDecodeRows rows per lane group
     // per step; the next step's rows are loaded before this step's are used
@@ -322,8 +336,8 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
 #pragma unroll
     for (int st = 0; st < 8; st++) {
         if (col < G) {
-            const uint16_t *qp =
-                (const uint16_t *)q + (b * Hq + kh * G + col) * D + st * 16 + half * 4;
+            const uint16_t *qp = (const uint16_t *)q + b * map.qb + (kh * G + col) * map.qh +
+                                 st * 16 + half * 4;
             const uint2 a = *(const uint2 *)qp, c = *(const uint2 *)(qp + 8);
             qf[st].u = make_uint4(a.x, a.y, c.x, c.y);
         } else {
@@ -332,9 +346,9 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     }
     const float qscale = scale * 1.4426950408889634f;
 
-    const int64_t row_stride = Hkv * D * 2;
-    const char *kb = (const char *)k + ((PAGED ? 0 : row0) * Hkv + kh) * D * 2;
-    const char *vb = (const char *)v + ((PAGED ? 0 : row0) * Hkv + kh) * D * 2;
+    const int64_t row_stride = map.kt * 2;  // bytes between consecutive keys (and values)
+    const char *kb = (const char *)k + ((PAGED ? 0 : kv_base_k(map, b, row0)) + kh * map.kh) * 2;
+    const char *vb = (const char *)v + ((PAGED ? 0 : kv_base_v(map, b, row0)) + kh * map.vh) * 2;
     // each wavefront sweeps a contiguous quarter of the split
     const int64_t per_wave = span / NW;
     const int64_t w0 = start + wave * per_wave;
@@ -355,11 +369,13 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
             for (int h = 0; h < 2; h++) {
                 const int64_t h0 = j0 + 16 * h;
                 const int64_t first = max(h0, w0), last = min(h0 + 16, w1);
-                int64_t row = first < last ? kv_page_row(map, b, first) : -1;
-                const uint32_t bytes = row >= 0 ? (uint32_t)((last - first) * row_stride) : 0u;
-                if (row < 0) row = 0;
-                const __amdgpu_buffer_rsrc_t kh_rs = make_rsrc(kb + row * row_stride, bytes);
-                const __amdgpu_buffer_rsrc_t vh_rs = make_rsrc(vb + row * row_stride, bytes);
+                const int64_t pg = first < last ? kv_page(map, b, first) : -1;
+                const uint32_t bytes = pg >= 0 ? (uint32_t)((last - first) * row_stride) : 0u;
+                // the half's first visible key within its page
+                const int64_t kofs = pg >= 0 ? (pg * map.kb + first % map.page_size * map.kt) * 2 : 0;
+                const int64_t vofs = pg >= 0 ? (pg * map.vb + first % map.page_size * map.vt) * 2 : 0;
+                const __amdgpu_buffer_rsrc_t kh_rs = make_rsrc(kb + kofs, bytes);
+                const __amdgpu_buffer_rsrc_t vh_rs = make_rsrc(vb + vofs, bytes);
 #pragma unroll
                 for (int u = 4 * h; u < 4 * h + 4; u++) {
                     const int64_t key = j0 + 4 * u + (lane >> 4);
@@ -515,21 +531,33 @@ __global__ __launch_bounds__(256) void decode_generic(int64_t B, int64_t S, int6
     int64_t lo = left >= 0 ? len - 1 - left : 0;
     if (lo < 0) lo = 0;
     float qr[NPL], acc[NPL];
+    const int64_t qo = b * map.qb + h * map.qh;
 #pragma unroll
     for (int e = 0; e < NPL; e++) {
         int64_t d = lane + 64 * e;
-        qr[e] = d < D ? ld<DT>(q, row * D + d) : 0.f;
+        qr[e] = d < D ? ld<DT>(q, qo + d) : 0.f;
         acc[e] = 0.f;
     }
+    const int64_t kseq = kv_base_k(map, b, row0) + kh * map.kh;
+    const int64_t vseq = kv_base_v(map, b, row0) + kh * map.vh;
     float mx = -INFINITY, l = 0.f;
     for (int64_t j = lo; j < len; j++) {
-        const int64_t cr = PAGED ? kv_page_row(map, b, j) : row0 + j;
-        const int64_t kr = (cr * Hkv + kh) * D;
+        int64_t kr, vr;
+        bool cr = true;  // false: a page index out of range (the key counts as zeros)
+        if constexpr (PAGED) {
+            const int64_t pg = kv_page(map, b, j), r = j % map.page_size;
+            cr = pg >= 0;
+            kr = pg * map.kb + r * map.kt + kh * map.kh;
+            vr = pg * map.vb + r * map.vt + kh * map.vh;
+        } else {
+            kr = kseq + j * map.kt;
+            vr = vseq + j * map.vt;
+        }
         float s = 0.f;
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
             int64_t d = lane + 64 * e;
-            if (d < D && cr >= 0) s += qr[e] * ld<DT>(k, kr + d);
+            if (d < D && cr) s += qr[e] * ld<DT>(k, kr + d);
         }
         s = wave_sum(s) * scale;
         const float mn = fmaxf(mx, s);
@@ -538,7 +566,7 @@ __global__ __launch_bounds__(256) void decode_generic(int64_t B, int64_t S, int6
 #pragma unroll
         for (int e = 0; e < NPL; e++) {
             int64_t d = lane + 64 * e;
-            acc[e] = acc[e] * alpha + p * (d < D && cr >= 0 ? ld<DT>(v, kr + d) : 0.f);
+            acc[e] = acc[e] * alpha + p * (d < D && cr ? ld<DT>(v, vr + d) : 0.f);
         }
         mx = mn;
     }
@@ -550,16 +578,39 @@ __global__ __launch_bounds__(256) void decode_generic(int64_t B, int64_t S, int6
     }
 }
 
-static bool split_takes(const dm_attention_desc *d) {
+// The call's strides (elements): the descriptor's, or the contiguous layouts' (q [B, Hq, D];
+// a dense cache [B, S, Hkv, D], a packed one [N, Hkv, D], pages [P, page_size, Hkv, D]).
+static KvMap kv_strides(const dm_attention_desc *d, int64_t page_size) {
+    KvMap m{};
+    if (d->strided) {
+        m.qb = d->sq.b, m.qh = d->sq.h;
+        m.kb = d->sk.b, m.kt = d->sk.t, m.kh = d->sk.h;
+        m.vb = d->sv.b, m.vt = d->sv.t, m.vh = d->sv.h;
+    } else {
+        const int64_t row = d->hkv * d->d, rows = page_size > 0 ? page_size : d->tk;
+        m.qb = d->hq * d->d, m.qh = d->d;
+        m.kb = m.vb = rows * row, m.kt = m.vt = row, m.kh = m.vh = d->d;
+    }
+    return m;
+}
+
+// The split kernels read keys and values with one row stride of at least a row, in 16-byte
+// pieces; their shapes as below.
+static bool split_takes(const dm_attention_desc *d, int64_t page_size = 0) {
     const int64_t g = d->hq / d->hkv;
+    const KvMap m = kv_strides(d, page_size);
+    const bool rows = m.kt == m.vt && m.kt >= d->d && m.qh % 8 == 0 && m.qb % 8 == 0 &&
+                      m.kb % 8 == 0 && m.kt % 8 == 0 && m.kh % 8 == 0 && m.vb % 8 == 0 &&
+                      m.vh % 8 == 0;
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) &&
-           (d->d == 64 || d->d == 128 || d->d == 256) && (g == 1 || g == 2 || g == 4 || g == 8);
+           (d->d == 64 || d->d == 128 || d->d == 256) && (g == 1 || g == 2 || g == 4 || g == 8) &&
+           rows;
 }
 
 // A paged cache runs the split pass on MFMA for D = 128 and pages of a multiple of 16 keys; every
 // other paged call takes the generic kernel.
 static bool paged_split_takes(const dm_attention_desc *d, int64_t page_size) {
-    return split_takes(d) && d->d == 128 && page_size % 16 == 0;
+    return split_takes(d, page_size) && d->d == 128 && page_size % 16 == 0;
 }
 
 static int span_of(const dm_attention_desc *d) {
@@ -594,6 +645,9 @@ static int check_decode(const char *op, const dm_attention_desc *d) {
     if (d->dtype != DM_F32 && d->dtype != DM_BF16 && d->dtype != DM_F16)
         return refuse(o + ": dtype must be f32, bf16 or f16");
     if (d->d > 256) return refuse(o + ": head dimension above 256 is not implemented");
+    if (d->strided && (d->sq.b < 0 || d->sq.h < 0 || !strides_ok(Strd{d->sk.b, d->sk.t, d->sk.h}) ||
+                       !strides_ok(Strd{d->sv.b, d->sv.t, d->sv.h})))
+        return refuse(o + ": strides must not be negative");
     return DM_OK;
 }
 
@@ -737,7 +791,7 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
                         void *stream) {
     const char *op = "attention_decode";
     if (int rc = check_decode(op, d)) return rc;
-    KvMap map{};
+    KvMap map = kv_strides(d, 0);
     if (d->cu_seqlens_k) {
         if (d->nseq != d->b)
             return refuse("attention_decode: a packed cache takes cu_seqlens_k [B + 1] with "
@@ -754,7 +808,8 @@ int dm_attention_decode(const dm_attention_desc *d, const void *q, const void *k
         DM_LAUNCH_CHECK("attention_decode: fill");
         return DM_OK;
     }
-    return run_decode(op, d, split_takes(d), false, q, k, v, lengths, map, o, workspace, st);
+    const bool split = split_takes(d) && aligned_16b(q) && aligned_16b(k) && aligned_16b(v);
+    return run_decode(op, d, split, false, q, k, v, lengths, map, o, workspace, st);
 }
 
 int dm_attention_decode_noalloc(const dm_attention_desc *d, const void *q, const void *k,
@@ -804,9 +859,14 @@ int dm_attention_decode_paged(const dm_attention_desc *d, const void *q, const v
         DM_LAUNCH_CHECK("attention_decode_paged: fill");
         return DM_OK;
     }
-    KvMap map{nullptr, block_table, page_size, max_pages, num_pages};
-    return run_decode(op, d, paged_split_takes(d, page_size), true, q, k_pages, v_pages, lengths,
-                      map, o, workspace, st);
+    KvMap map = kv_strides(d, page_size);
+    map.block_table = block_table;
+    map.page_size = page_size;
+    map.max_pages = max_pages;
+    map.num_pages = num_pages;
+    const bool split = paged_split_takes(d, page_size) && aligned_16b(q) && aligned_16b(k_pages) &&
+                       aligned_16b(v_pages);
+    return run_decode(op, d, split, true, q, k_pages, v_pages, lengths, map, o, workspace, st);
 }
 
 }  // extern "C"

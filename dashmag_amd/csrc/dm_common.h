@@ -221,4 +221,30 @@ inline float scale_of(const dm_attention_desc *d) {
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
 
+// Element strides of an input along (batch, time, head); the last dimension is contiguous.
+struct Strd {
+    int64_t b, t, h;
+};
+// The attention inputs' strides: q, k, v, and the backward's o and d_o (g). Contiguous
+// [B, T, H, D] unless the descriptor gives others.
+struct AttnStrides {
+    Strd q, k, v, o, g;
+};
+
+inline AttnStrides attn_strides(const dm_attention_desc *d) {
+    const Strd cq{d->tq * d->hq * d->d, d->hq * d->d, d->d};
+    const Strd ck{d->tk * d->hkv * d->d, d->hkv * d->d, d->d};
+    AttnStrides s{cq, ck, ck, cq, cq};
+    if (d->strided) {
+        auto cv = [](const dm_strides &x) { return Strd{x.b, x.t, x.h}; };
+        s = AttnStrides{cv(d->sq), cv(d->sk), cv(d->sv), cv(d->so), cv(d->sdo)};
+    }
+    return s;
+}
+
+inline bool strides_ok(const Strd &x) { return x.b >= 0 && x.t >= 0 && x.h >= 0; }
+// 16-byte rows for the 16-bit kernels' vector loads: every stride a multiple of 8 elements
+inline bool strides_16b(const Strd &x) { return x.b % 8 == 0 && x.t % 8 == 0 && x.h % 8 == 0; }
+inline bool aligned_16b(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 }  // namespace dm

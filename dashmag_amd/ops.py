@@ -53,6 +53,28 @@ def _check(op, rc):
     raise RuntimeError(msg)
 
 
+def _readable(t):
+    """``t`` as the kernels read it in place: a view whose last dimension is contiguous, and for
+    16-bit dtypes strides that are multiples of 8 elements on a 16-byte aligned base (what the
+    MFMA and split kernels' vector loads take); otherwise a contiguous copy, as dash-ops copies
+    what its kernels cannot read in place (crates/dash-ops/src/attention.rs:85-93)."""
+    if t.dim() == 0 or t.numel() == 0:
+        return t.contiguous()
+    st = t.stride()
+    if st[-1] != 1 and t.shape[-1] > 1:
+        return t.contiguous()
+    if t.element_size() == 2 and (any(x % 8 for x in st[:-1]) or t.data_ptr() % 16):
+        return t.contiguous()
+    return t
+
+
+def _set_strides(field, t, dims):
+    """Fills a ``dm_strides`` from ``t``'s strides along ``dims`` (``b``, ``t``, ``h`` in that
+    order; None for an axis the tensor lacks)."""
+    st = t.stride()
+    field.b, field.t, field.h = (0 if i is None else st[i] for i in dims)
+
+
 def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
@@ -155,8 +177,11 @@ def attention_with_lse(query, key, value, mask: Optional[AttentionMask] = None,
     _device(op, query, key, value)
     keep = []
     desc = _attention_desc(op, query, key, value, mask, options, keep)
-    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
-    out = torch.empty_like(q)
+    q, k, v = _readable(query), _readable(key), _readable(value)
+    desc.strided = 1
+    for f, t in ((desc.sq, q), (desc.sk, k), (desc.sv, v)):
+        _set_strides(f, t, (0, 1, 2))
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
     nbytes = _lib.lib().dm_attention_fwd_workspace(ctypes.byref(desc))
     ws = _workspace(nbytes, q.device)
@@ -183,11 +208,14 @@ def attention_backward(query, key, value, output, lse, grad_output, mask=None, o
         raise Unsupported(f"{op}: the output and its gradient are [B, Tq, Hq, D]")
     if tuple(lse.shape) != tuple(query.shape[:3]):
         raise Unsupported(f"{op}: the log-sum-exp is [B, Tq, Hq]")
-    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
-    o = output.to(q.dtype).contiguous()
-    g = grad_output.to(q.dtype).contiguous()
+    q, k, v = _readable(query), _readable(key), _readable(value)
+    o = _readable(output.to(q.dtype))
+    g = _readable(grad_output.to(q.dtype))
     ls = lse.to(torch.float32).contiguous()
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    desc.strided = 1
+    for f, t in ((desc.sq, q), (desc.sk, k), (desc.sv, v), (desc.so, o), (desc.sdo, g)):
+        _set_strides(f, t, (0, 1, 2))
+    dq, dk, dv = (torch.empty(x.shape, dtype=x.dtype, device=x.device) for x in (q, k, v))
     nbytes = _lib.lib().dm_attention_bwd_workspace(ctypes.byref(desc))
     ws = _workspace(nbytes, q.device)
     _check(op, _lib.lib().dm_attention_bwd(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
@@ -217,8 +245,9 @@ def attention_decode(query, key, value, lengths=None, options=None):
         if tuple(lt.shape) != (b,):
             raise Unsupported(f"{op}: the cache lengths are [B] = [{b}]")
         ln = _cache_lengths(op, lt, b, query.device)
-    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
-    out = torch.empty_like(q)
+    q, k, v = _readable(query), _readable(key), _readable(value)
+    _decode_strides(desc, q, k, v, (0, 1, 2))
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     nbytes = _lib.lib().dm_attention_decode_workspace(ctypes.byref(desc))
     ws = _workspace(nbytes, q.device)
     _check(op, _lib.lib().dm_attention_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
@@ -251,6 +280,13 @@ def _decode_desc(op, query, key, value, tk, options):
         o.window_left = min(int(options.window.left), UNBOUNDED)
         o.window_right = min(int(options.window.right), UNBOUNDED)
     return desc
+
+
+def _decode_strides(desc, q, k, v, cache_dims):
+    desc.strided = 1
+    _set_strides(desc.sq, q, (0, None, 1))
+    _set_strides(desc.sk, k, cache_dims)
+    _set_strides(desc.sv, v, cache_dims)
 
 
 def _cache_lengths(op, lengths, b, device):
@@ -291,8 +327,9 @@ def attention_decode_packed(query, key, value, cu_seqlens_k, lengths=None, optio
     cu = _offsets(cu, query.device, op, "cu_seqlens_k")
     desc.cu_seqlens_k, desc.nseq = cu.data_ptr(), b
     ln = _cache_lengths(op, lengths, b, query.device)
-    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
-    out = torch.empty_like(q)
+    q, k, v = _readable(query), _readable(key), _readable(value)
+    _decode_strides(desc, q, k, v, (None, 0, 1))
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     nbytes = _lib.lib().dm_attention_decode_workspace(ctypes.byref(desc))
     ws = _workspace(nbytes, q.device)
     _check(op, _lib.lib().dm_attention_decode(ctypes.byref(desc), _ptr(q), _ptr(k), _ptr(v),
@@ -323,8 +360,9 @@ def attention_decode_paged(query, key_pages, value_pages, block_table, lengths=N
     desc = _decode_desc(op, query, key_pages, value_pages, max_pages * page_size, options)
     bt = _offsets(bt, query.device, op, "the block table")
     ln = _cache_lengths(op, lengths, b, query.device)
-    q, k, v = query.contiguous(), key_pages.contiguous(), value_pages.contiguous()
-    out = torch.empty_like(q)
+    q, k, v = _readable(query), _readable(key_pages), _readable(value_pages)
+    _decode_strides(desc, q, k, v, (0, 1, 2))
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     nbytes = _lib.lib().dm_attention_decode_paged_workspace(ctypes.byref(desc), page_size)
     ws = _workspace(nbytes, q.device)
     _check(op, _lib.lib().dm_attention_decode_paged(

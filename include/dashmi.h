@@ -26,9 +26,16 @@
  *                                                               crates/dash-ops/src/loss.rs:157-200
  *
  * Conventions (crates/dash-contract/src/lib.rs:38-91):
- *   - Every tensor is a device pointer to a contiguous array in the contract's layout:
- *     [B, T, H, D] for queries/keys/values/outputs, [B, T, H] for lse, g and beta,
- *     [S, H, Dk, Dv] f32 for states. The caller makes strided inputs contiguous.
+ *   - Every tensor is a device pointer to an array in the contract's layout: [B, T, H, D] for
+ *     queries/keys/values/outputs, [B, T, H] for lse, g and beta, [S, H, Dk, Dv] f32 for
+ *     states. Outputs are contiguous (freshly allocated by the caller, as the reference's are).
+ *     The attention, decode and chunked gated-delta-rule inputs may be strided views (a slice
+ *     of one fused projection, a [B, H, T, D] tensor seen through a permutation): with
+ *     `strided` set in the descriptor, each such input's (batch, time, head) strides in
+ *     elements are given and its last dimension is contiguous; the kernels read it in place
+ *     (crates/dash-ops/src/attention.rs:85-93, attention/cube.rs:428-461). The fast kernels
+ *     take strides that are multiples of 16 bytes and 16-byte aligned bases (other calls run
+ *     the generic kernels, which take any). Without `strided`, every input is contiguous.
  *   - Floating inputs of a call share one dtype (dm_dtype); lse and states are f32; g and beta
  *     of the gated delta rule may each be f32 or the inputs' dtype.
  *   - Sequence boundaries (cu_seqlens) and cache lengths are int32 device arrays.
@@ -73,6 +80,11 @@ typedef struct {
     int32_t deterministic;              /* 1: the query gradient in a fixed summation order */
 } dm_attention_options;
 
+/* An input's strides in elements along (batch, time, head); its last dimension is contiguous. */
+typedef struct {
+    int64_t b, t, h;
+} dm_strides;
+
 /* One attention call's shapes, dtype and mask (check_shapes, attention.rs:551-590). */
 typedef struct {
     int64_t b, tq, tk, hq, hkv, d;
@@ -82,6 +94,11 @@ typedef struct {
     const int32_t *cu_seqlens_q, *cu_seqlens_k;
     int64_t nseq;
     dm_attention_options options;
+    /* 0: every input contiguous. 1: the strides below (each >= 0). Decode reads sq.b and sq.h
+     * of q [B, Hq, D], and of the cache sk/sv: dense [B, S, Hkv, D] (b, t, h); packed
+     * [N, Hkv, D] (t, h; b unused); paged [P, page_size, Hkv, D] (b = the page stride). */
+    int32_t strided;
+    dm_strides sq, sk, sv, so, sdo; /* q, k, v; the backward's o and d_o */
 } dm_attention_desc;
 
 /* The gated delta rule's shapes and options (chunk.rs:771 check_inputs, recurrent.rs:258). */
