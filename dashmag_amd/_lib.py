@@ -49,7 +49,9 @@ class GdrDesc(ctypes.Structure):
                 ("g_dtype", ctypes.c_int32), ("beta_dtype", ctypes.c_int32),
                 ("cu_seqlens", ctypes.c_void_p), ("nseq", ctypes.c_int64),
                 ("qk_l2norm", ctypes.c_int32), ("has_scale", ctypes.c_int32),
-                ("scale", ctypes.c_float)]
+                ("scale", ctypes.c_float), ("strided", ctypes.c_int32), ("sq", Strides),
+                ("sk", Strides), ("sv", Strides), ("sg", Strides), ("sbeta", Strides),
+                ("sdo", Strides)]
 
 
 class Conv1dDesc(ctypes.Structure):

@@ -25,15 +25,15 @@ namespace dm {
 // index up to the host's bound n_max that no sequence uses gets a count of 0.
 // ------------------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void gdr_plan(int64_t nseq, int64_t T, int64_t n_max,
-                                                const int32_t *__restrict__ cu,
-                                                int32_t *__restrict__ seq_chunk0,
-                                                int32_t *__restrict__ chunk_seq,
-                                                int32_t *__restrict__ chunk_tok0,
-                                                int32_t *__restrict__ chunk_len) {
-    __shared__ int32_t part[256];
+__global__ __launch_bounds__(1024) void gdr_plan(int64_t nseq, int64_t T, int64_t n_max,
+                                                 const int32_t *__restrict__ cu,
+                                                 int32_t *__restrict__ seq_chunk0,
+                                                 int32_t *__restrict__ chunk_seq,
+                                                 int32_t *__restrict__ chunk_tok0,
+                                                 int32_t *__restrict__ chunk_len) {
+    __shared__ int32_t part[1024];
     const int tid = threadIdx.x;
-    const int64_t per = (nseq + 255) / 256;
+    const int64_t per = (nseq + 1023) / 1024;
     const int64_t s0 = tid * per, s1 = s0 + per < nseq ? s0 + per : nseq;
     auto span = [&](int64_t s, int64_t *a, int64_t *b) {
         if (cu) {
@@ -47,6 +47,7 @@ __global__ __launch_bounds__(256) void gdr_plan(int64_t nseq, int64_t T, int64_t
             *b = s * T + T;
         }
     };
+    // chunks per thread's sequences, then an inclusive scan over the threads
     int32_t local = 0;
     for (int64_t s = s0; s < s1; s++) {
         int64_t a, b;
@@ -55,35 +56,44 @@ __global__ __launch_bounds__(256) void gdr_plan(int64_t nseq, int64_t T, int64_t
     }
     part[tid] = local;
     __syncthreads();
-    if (tid == 0) {
-        int32_t run = 0;
-        for (int x = 0; x < 256; x++) {
-            int32_t c = part[x];
-            part[x] = run;
-            run += c;
-        }
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int32_t y = tid >= o ? part[tid - o] : 0;
+        __syncthreads();
+        part[tid] += y;
+        __syncthreads();
     }
-    __syncthreads();
-    int32_t c = part[tid];
+    int32_t c = part[tid] - local;
     for (int64_t s = s0; s < s1; s++) {
         int64_t a, b;
         span(s, &a, &b);
-        seq_chunk0[s] = c;
-        for (int64_t t = a; t < b; t += kChunk, c++) {
-            if (c >= n_max) break;
-            chunk_seq[c] = (int32_t)s;
-            chunk_tok0[c] = (int32_t)t;
-            chunk_len[c] = (int32_t)(b - t < kChunk ? b - t : kChunk);
-        }
+        seq_chunk0[s] = c < n_max ? c : (int32_t)n_max;
+        c += (int32_t)((b - a + kChunk - 1) / kChunk);
     }
-    if (tid == 255) seq_chunk0[nseq] = c;
-    __syncthreads();
-    // chunks no sequence uses
-    const int32_t used = seq_chunk0[nseq];
-    for (int64_t x = used + tid; x < n_max; x += 256) {
-        chunk_seq[x] = 0;
-        chunk_tok0[x] = 0;
-        chunk_len[x] = 0;
+    const int32_t used = part[1023] < n_max ? part[1023] : (int32_t)n_max;
+    if (tid == 0) seq_chunk0[nseq] = used;
+    __syncthreads();  // (orders the global writes above for the whole workgroup)
+    // every chunk in parallel: its sequence is the last whose first chunk is at or before it
+    for (int64_t x = tid; x < n_max; x += 1024) {
+        if (x >= used) {
+            chunk_seq[x] = 0;
+            chunk_tok0[x] = 0;
+            chunk_len[x] = 0;
+            continue;
+        }
+        int64_t lo = 0, hi = nseq - 1;  // seq_chunk0[lo] <= x
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if (seq_chunk0[mid] <= x)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        int64_t a, b;
+        span(lo, &a, &b);
+        const int64_t t = a + (x - seq_chunk0[lo]) * kChunk;
+        chunk_seq[x] = (int32_t)lo;
+        chunk_tok0[x] = (int32_t)t;
+        chunk_len[x] = (int32_t)(b - t < kChunk ? b - t : kChunk);
     }
 }
 
@@ -108,17 +118,17 @@ __global__ __launch_bounds__(256) void gdr_prep(GdrArgs a, GdrWs w, int keep_ta)
     if (tid < kChunk) {
         const bool ok = tid < len;
         const int64_t t = tok0 + tid;
-        G[tid] = ok ? ld_any(a.g_dt, a.g, t * a.H + h) : 0.f;
-        bet[tid] = ok ? ld_any(a.beta_dt, a.beta, t * a.H + h) : 0.f;
+        G[tid] = ok ? ld_any(a.g_dt, a.g, g_at(a, t, h)) : 0.f;
+        bet[tid] = ok ? ld_any(a.beta_dt, a.beta, b_at(a, t, h)) : 0.f;
     }
     // rows: one wavefront per row, lanes along the head
     for (int i = wave; i < kChunk; i += 4) {
         const bool ok = i < len;
-        const int64_t base = ((tok0 + i) * a.H + h) * Dk;
+        const int64_t qb = q_at(a, tok0 + i, h), kb = k_at(a, tok0 + i, h);
         float sq = 0.f, sk = 0.f;
         for (int64_t x = lane; x < Dk; x += 64) {
-            const float qv = ok ? ld<DT>(a.q, base + x) : 0.f;
-            const float kv = ok ? ld<DT>(a.k, base + x) : 0.f;
+            const float qv = ok ? ld<DT>(a.q, qb + x) : 0.f;
+            const float kv = ok ? ld<DT>(a.k, kb + x) : 0.f;
             sq += qv * qv;
             sk += kv * kv;
         }
@@ -128,8 +138,8 @@ __global__ __launch_bounds__(256) void gdr_prep(GdrArgs a, GdrWs w, int keep_ta)
             ki = 1.f / sqrtf(wave_sum(sk) + 1e-6f);
         }
         for (int64_t x = lane; x < Dk; x += 64) {
-            const float qv = ok ? ld<DT>(a.q, base + x) : 0.f;
-            const float kv = ok ? ld<DT>(a.k, base + x) : 0.f;
+            const float qv = ok ? ld<DT>(a.q, qb + x) : 0.f;
+            const float kv = ok ? ld<DT>(a.k, kb + x) : 0.f;
             Qn[i * Dk + x] = (a.l2norm ? qv * qi : qv) * a.scale;
             Kn[i * Dk + x] = a.l2norm ? kv * ki : kv;
         }
@@ -192,7 +202,7 @@ __global__ __launch_bounds__(256) void gdr_prep(GdrArgs a, GdrWs w, int keep_ta)
         const int64_t y = idx % Dv;
         float s = 0.f;
         for (int j = 0; j <= i && j < len; j++)
-            s += Tm[i][j] * (ld<DT>(a.v, ((tok0 + j) * a.H + h) * Dv + y) * bet[j]);
+            s += Tm[i][j] * (ld<DT>(a.v, v_at(a, tok0 + j, h) + y) * bet[j]);
         U[idx] = s;
     }
 }
@@ -316,7 +326,7 @@ __global__ __launch_bounds__(256) void gdr_dvlocal(GdrArgs a, GdrWs w, const voi
         const int j = (int)(idx / Dv);
         const int64_t y = idx % Dv;
         float s = 0.f;
-        for (int i = j; i < len; i++) s += P[i][j] * ld<DT>(d_out, ((tok0 + i) * a.H + h) * Dv + y);
+        for (int i = j; i < len; i++) s += P[i][j] * ld<DT>(d_out, o_at(a, tok0 + i, h) + y);
         dvl[idx] = s;
     }
 }
@@ -356,7 +366,7 @@ __global__ __launch_bounds__(256) void gdr_state_bwd(GdrArgs a, GdrWs w, const v
             const int64_t x = idx / Dv, y = idx % Dv;
             float qdo = 0.f, wdv = 0.f;
             for (int i = 0; i < kChunk; i++) {
-                const float d_o = i < len ? ld<DT>(d_out, ((tok0 + i) * a.H + h) * Dv + y) : 0.f;
+                const float d_o = i < len ? ld<DT>(d_out, o_at(a, tok0 + i, h) + y) : 0.f;
                 qdo += Qn[i * Dk + x] * expf(G[i]) * d_o;
                 wdv += W[i * Dk + x] * dVn[i * Dv + y];
             }
@@ -396,14 +406,14 @@ __global__ __launch_bounds__(256) void gdr_grads(GdrArgs a, GdrWs w, const void 
     const float *Tm = w.Tm + ch * C * C, *Am = w.Am + ch * C * C;
     float *DQ = w.gq + ch * C * Dk, *DK = w.gk + ch * C * Dk, *X = w.gx + ch * C * (Dk > Dv ? Dk : Dv);
     auto dO = [&](int i, int64_t y) -> float {
-        return i < len ? ld<DT>(d_out, ((tok0 + i) * a.H + h) * Dv + y) : 0.f;
+        return i < len ? ld<DT>(d_out, o_at(a, tok0 + i, h) + y) : 0.f;
     };
     auto Vin = [&](int i, int64_t y) -> float {
-        return i < len ? ld<DT>(a.v, ((tok0 + i) * a.H + h) * Dv + y) : 0.f;
+        return i < len ? ld<DT>(a.v, v_at(a, tok0 + i, h) + y) : 0.f;
     };
     if (tid < C) {
         G[tid] = w.G[ch * C + tid];
-        bet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
+        bet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, b_at(a, tok0 + tid, h)) : 0.f;
     }
     __syncthreads();
     if (tid < C) {
@@ -613,20 +623,21 @@ __global__ __launch_bounds__(256) void gdr_grads(GdrArgs a, GdrWs w, const void 
     }
     // dq (scaled), dk, through the l2 normalisation (l2norm_backward :246-252)
     for (int i = wave; i < len; i += 4) {
-        const int64_t base = ((tok0 + i) * a.H + h) * Dk;
+        const int64_t base = ((tok0 + i) * a.H + h) * Dk;  // the gradients' (contiguous)
+        const int64_t qb = q_at(a, tok0 + i, h), kb = k_at(a, tok0 + i, h);
         float qi = 1.f, ki = 1.f, sq = 0.f, sk = 0.f;
         if (a.l2norm) {
             float nq = 0.f, nk = 0.f;
             for (int64_t x = lane; x < Dk; x += 64) {
-                const float qv = ld<DT>(a.q, base + x), kv = ld<DT>(a.k, base + x);
+                const float qv = ld<DT>(a.q, qb + x), kv = ld<DT>(a.k, kb + x);
                 nq += qv * qv;
                 nk += kv * kv;
             }
             qi = 1.f / sqrtf(wave_sum(nq) + 1e-6f);
             ki = 1.f / sqrtf(wave_sum(nk) + 1e-6f);
             for (int64_t x = lane; x < Dk; x += 64) {
-                sq += ld<DT>(a.q, base + x) * qi * DQ[i * Dk + x] * a.scale;
-                sk += ld<DT>(a.k, base + x) * ki * DK[i * Dk + x];
+                sq += ld<DT>(a.q, qb + x) * qi * DQ[i * Dk + x] * a.scale;
+                sk += ld<DT>(a.k, kb + x) * ki * DK[i * Dk + x];
             }
             sq = wave_sum(sq);
             sk = wave_sum(sk);
@@ -634,8 +645,8 @@ __global__ __launch_bounds__(256) void gdr_grads(GdrArgs a, GdrWs w, const void 
         for (int64_t x = lane; x < Dk; x += 64) {
             const float gq = DQ[i * Dk + x] * a.scale, gk = DK[i * Dk + x];
             if (a.l2norm) {
-                st<DT>(dq, base + x, qi * (gq - ld<DT>(a.q, base + x) * qi * sq));
-                st<DT>(dk, base + x, ki * (gk - ld<DT>(a.k, base + x) * ki * sk));
+                st<DT>(dq, base + x, qi * (gq - ld<DT>(a.q, qb + x) * qi * sq));
+                st<DT>(dk, base + x, ki * (gk - ld<DT>(a.k, kb + x) * ki * sk));
             } else {
                 st<DT>(dq, base + x, gq);
                 st<DT>(dk, base + x, gk);
@@ -694,9 +705,41 @@ size_t gdr_ws_layout(const dm_gdr_desc *d, bool backward, char *base, GdrWs *w) 
     return off;
 }
 
+bool gdr_strides_ok(const dm_gdr_desc *d, bool step) {
+    if (!d->strided) return true;
+    const int64_t T = step ? 1 : d->t;
+    for (const dm_strides *x : {&d->sq, &d->sk, &d->sv, &d->sg, &d->sbeta, &d->sdo}) {
+        if (x->b < 0 || x->t < 0 || x->h < 0) return false;
+        if (!step && d->b > 1 && x->b != T * x->t) return false;
+    }
+    return true;
+}
+
+bool gdr_strides_16b(const dm_gdr_desc *d) {
+    if (!d->strided) return true;
+    for (const dm_strides *x : {&d->sq, &d->sk, &d->sv, &d->sdo})
+        if (x->b % 8 || x->t % 8 || x->h % 8) return false;
+    return true;
+}
+
 GdrArgs gdr_args(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
-                 const void *g, const void *beta) {
+                 const void *g, const void *beta, bool step) {
     GdrArgs a;
+    // contiguous rows unless given: [rows, H, D] and [rows, H]; the step's rows are its batch
+    // (t stride = b stride)
+    const int64_t H = d->h;
+    a.q_t = a.k_t = H * d->dk, a.q_h = a.k_h = d->dk;
+    a.v_t = a.o_t = H * d->dv, a.v_h = a.o_h = d->dv;
+    a.g_t = a.b_t = H, a.g_h = a.b_h = 1;
+    if (d->strided) {
+        auto rowst = [&](const dm_strides &x) { return step ? x.b : x.t; };
+        a.q_t = rowst(d->sq), a.q_h = d->sq.h;
+        a.k_t = rowst(d->sk), a.k_h = d->sk.h;
+        a.v_t = rowst(d->sv), a.v_h = d->sv.h;
+        a.g_t = rowst(d->sg), a.g_h = d->sg.h;
+        a.b_t = rowst(d->sbeta), a.b_h = d->sbeta.h;
+        a.o_t = rowst(d->sdo), a.o_h = d->sdo.h;
+    }
     a.H = d->h;
     a.rows = d->b * d->t;
     a.Dk = d->dk;
@@ -716,7 +759,7 @@ GdrArgs gdr_args(const dm_gdr_desc *d, const void *q, const void *k, const void 
 int launch_plan(const dm_gdr_desc *d, int32_t *seq_chunk0, int32_t *chunk_seq,
                 int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st) {
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
-    gdr_plan<<<1, 256, 0, st>>>(S, d->t, nc, d->cu_seqlens, seq_chunk0, chunk_seq, chunk_tok0,
+    gdr_plan<<<1, 1024, 0, st>>>(S, d->t, nc, d->cu_seqlens, seq_chunk0, chunk_seq, chunk_tok0,
                                 chunk_len);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule: plan");
     return DM_OK;

@@ -122,10 +122,10 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
-            const int64_t off = ((tok0 + (r < len ? r : len - 1)) * a.H + h) * kD + c * 8;
-            vreg[u] = *(const uint4 *)(vin + off);
-            qraw[u] = *(const uint4 *)(qin + off);
-            kraw[u] = *(const uint4 *)(kin + off);
+            const int64_t tok = tok0 + (r < len ? r : len - 1);
+            vreg[u] = *(const uint4 *)(vin + v_at(a, tok, h) + c * 8);
+            qraw[u] = *(const uint4 *)(qin + q_at(a, tok, h) + c * 8);
+            kraw[u] = *(const uint4 *)(kin + k_at(a, tok, h) + c * 8);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -136,8 +136,8 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     // the gates (after the rows' loads: their reads wait on the memory counter)
     if (tid < kC) {
         const bool ok = tid < len;
-        sm.g[tid] = ok ? ld_any(a.g_dt, a.g, (tok0 + tid) * a.H + h) : 0.f;
-        sm.bet[tid] = ok ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
+        sm.g[tid] = ok ? ld_any(a.g_dt, a.g, g_at(a, tok0 + tid, h)) : 0.f;
+        sm.bet[tid] = ok ? ld_any(a.beta_dt, a.beta, b_at(a, tok0 + tid, h)) : 0.f;
     }
     // queries and keys: 16 lanes per row, zero past the chunk's tokens; normalised in f32 and
     // rounded back to the dtype when asked
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
         if (a.l2norm)
             qv = *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8);
         else
-            qv = r < len ? *(const uint4 *)((const uint16_t *)a.q + ((tok0 + r) * a.H + h) * kD + c * 8)
+            qv = r < len ? *(const uint4 *)((const uint16_t *)a.q + q_at(a, tok0 + r, h) + c * 8)
                          : make_uint4(0, 0, 0, 0);
         uint2 *qp = (uint2 *)(qs + r * kRowB + c * 8);
         qp[0] = make_uint2(qv.x, qv.y);
@@ -800,10 +800,10 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int x = tid + 256 * u, r = x / 16, c = x % 16;
-        const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
-        dv[u] = *(const uint4 *)(dob + row * kD + c * 8);
+        const int64_t tok = tok0 + (r < len ? r : len - 1);
+        dv[u] = *(const uint4 *)(dob + o_at(a, tok, h) + c * 8);
         qv[u] = a.l2norm ? *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8)
-                         : *(const uint4 *)(qin + row * kD + c * 8);
+                         : *(const uint4 *)(qin + q_at(a, tok, h) + c * 8);
     }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -1056,8 +1056,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int x = tid + 512 * u, r = x / 16, c = x % 16;
-            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
-            s4[u] = *(const uint4 *)(dob + row * kD + c * 8);
+            s4[u] = *(const uint4 *)(dob + o_at(a, tok0 + (r < len ? r : len - 1), h) + c * 8);
         }
         s5 = *(const uint4 *)(w.Aqk + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
         // per-token values (after the rows' loads: these reads wait on the memory counter)
@@ -1066,7 +1065,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             tG[tid] = gv;
             tGam[tid] = __expf(gv);
             tLam[tid] = __expf(w.G[ch * kC + kC - 1] - gv);
-            tBet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, (tok0 + tid) * a.H + h) : 0.f;
+            tBet[tid] = tid < len ? ld_any(a.beta_dt, a.beta, b_at(a, tok0 + tid, h)) : 0.f;
         }
         // fragment (dv tile p, dk step st), lane l: column dv = 32 p + l % 32 (a row of X^T),
         // dk runs 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4)
@@ -1167,10 +1166,10 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int x = tid + 512 * u, r = x / 16, c = x % 16;
-            const int64_t row = (tok0 + (r < len ? r : len - 1)) * a.H + h;
-            q2[u] = *(const uint4 *)(qin + row * kD + c * 8);
-            k2[u] = *(const uint4 *)(kin + row * kD + c * 8);
-            v2[u] = *(const uint4 *)(vin + row * kD + c * 8);
+            const int64_t tok = tok0 + (r < len ? r : len - 1);
+            q2[u] = *(const uint4 *)(qin + q_at(a, tok, h) + c * 8);
+            k2[u] = *(const uint4 *)(kin + k_at(a, tok, h) + c * 8);
+            v2[u] = *(const uint4 *)(vin + v_at(a, tok, h) + c * 8);
         }
         t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
     }
@@ -1544,9 +1543,9 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 // ------------------------------------------------------------------------------------------
 
 bool gdr_mfma_takes(const dm_gdr_desc *d) {
-    // (the state pass addresses the keys through a 32-bit buffer range)
+    // (the state pass addresses the keys through a 32-bit buffer range; 16-byte row loads)
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk == kD && d->dv == kD &&
-           d->b * d->t * d->h * kD * 2 < (1ll << 32);
+           d->b * d->t * d->h * kD * 2 < (1ll << 32) && gdr_strides_16b(d);
 }
 
 size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { return mfma_layout(d, nullptr, nullptr); }
@@ -1556,20 +1555,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
                         float *final_state, void *workspace, hipStream_t st) {
     MfmaWs w;
     mfma_layout(d, (char *)workspace, &w);
-    GdrArgs a;
-    a.H = d->h;
-    a.rows = d->b * d->t;
-    a.Dk = d->dk;
-    a.Dv = d->dv;
-    a.g_dt = d->g_dtype;
-    a.beta_dt = d->beta_dtype;
-    a.l2norm = d->qk_l2norm;
-    a.scale = d->has_scale ? d->scale : (float)(1.0 / std::sqrt((double)d->dk));
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.g = g;
-    a.beta = beta;
+    const GdrArgs a = gdr_args(d, q, k, v, g, beta);
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
     int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st);
     if (rc) return rc;

@@ -18,10 +18,12 @@ namespace dm {
 //   S <- S + k delta^T;  out <- S^T q.
 template <int DT, int MAXR>
 __global__ __launch_bounds__(256) void gdr_step_kernel(
-    int64_t nseq, int64_t H, int64_t Dk, int64_t Dv, int ncs, const int32_t *__restrict__ cu, int g_dt,
-    int beta_dt, int l2norm, float scale, const void *__restrict__ q, const void *__restrict__ k,
-    const void *__restrict__ v, const void *__restrict__ g, const void *__restrict__ beta,
+    GdrArgs a, int64_t nseq, int64_t Dk, int64_t Dv, int ncs, const int32_t *__restrict__ cu,
     const float *state_in, float *state_out, void *__restrict__ out) {
+    const int64_t H = a.H;
+    const int g_dt = a.g_dt, beta_dt = a.beta_dt, l2norm = a.l2norm;
+    const float scale = a.scale;
+    const void *q = a.q, *k = a.k, *v = a.v, *g = a.g, *beta = a.beta;
     // the state's columns are independent: ncs workgroups share a (sequence, head), each
     // taking Dv / ncs columns (every one recomputes the token's normalisation)
     const int64_t sh = blockIdx.x / ncs;
@@ -64,15 +66,15 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     }
 
     for (int64_t t = t0; t < t1; t++) {
-        const int64_t qk_off = (t * H + h) * Dk;
+        const int64_t q_off = q_at(a, t, h), k_off = k_at(a, t, h);
         // load q, k (f32), normalise
         float pq = 0.f, pk = 0.f;
         for (int64_t x = tid; x < Dk; x += 256) {
-            const float a = ld<DT>(q, qk_off + x), b = ld<DT>(k, qk_off + x);
-            qs[x] = a;
-            ks[x] = b;
-            pq += a * a;
-            pk += b * b;
+            const float qv = ld<DT>(q, q_off + x), kv = ld<DT>(k, k_off + x);
+            qs[x] = qv;
+            ks[x] = kv;
+            pq += qv * qv;
+            pk += kv * kv;
         }
         if (l2norm) {
             pq = wave_sum(pq);
@@ -91,8 +93,8 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
             qmul = (1.f / sqrtf(norm2[0] + 1e-6f));
             kmul = 1.f / sqrtf(norm2[1] + 1e-6f);
         }
-        const float decay = expf(ld_any(g_dt, g, t * H + h));
-        const float bt = ld_any(beta_dt, beta, t * H + h);
+        const float decay = expf(ld_any(g_dt, g, g_at(a, t, h)));
+        const float bt = ld_any(beta_dt, beta, b_at(a, t, h));
 
         // S <- exp(g) S ; partial S^T k
         float part[4] = {0.f, 0.f, 0.f, 0.f};
@@ -115,7 +117,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
         for (int c = 0; c < 4; c++) {
             float kv = 0.f;
             for (int x = 0; x < NKG; x++) kv += red[x * Dw + quad * 4 + c];
-            delta[c] = (ld<DT>(v, (t * H + h) * Dv + c0 + quad * 4 + c) - kv) * bt;
+            delta[c] = (ld<DT>(v, v_at(a, t, h) + c0 + quad * 4 + c) - kv) * bt;
         }
         __syncthreads();
         // S <- S + k delta^T ; partial S^T q
@@ -176,6 +178,9 @@ int check_gdr(const dm_gdr_desc *d, const char *op, bool step) {
     }
     if (d->dk > 256 || d->dv > 256)
         return refuse(o + ": heads wider than 256 are not implemented");
+    if (!gdr_strides_ok(d, step))
+        return refuse(o + ": strides must not be negative, and each batch stride must be T times "
+                          "its time stride (the host copies other views)");
     return DM_OK;
 }
 
@@ -203,13 +208,10 @@ extern "C" int dm_gdr_step(const dm_gdr_desc *d, const void *q, const void *k, c
     const int nkg = 256 / nq;
     const int rows = (int)((d->dk + nkg - 1) / nkg);
     const size_t smem = (size_t)(2 * d->dk + nkg * dw) * sizeof(float);
-    const float scale =
-        d->has_scale ? d->scale : (float)(1.0 / std::sqrt((double)d->dk));
-    const int l2 = d->qk_l2norm ? 1 : 0;
+    const GdrArgs a = gdr_args(d, q, k, v, g, beta, true);
 #define STEP(DT, R)                                                                          \
     gdr_step_kernel<DT, R><<<(unsigned)blocks, 256, smem, st>>>(                             \
-        nseq, d->h, d->dk, d->dv, ncs, d->cu_seqlens, d->g_dtype, d->beta_dtype, l2, scale, q, k, v, \
-        g, beta, state_in, state_out, out)
+        a, nseq, d->dk, d->dv, ncs, d->cu_seqlens, state_in, state_out, out)
 #define STEP_R(DT)                                  \
     if (rows <= 4) STEP(DT, 4);                     \
     else if (rows <= 8) STEP(DT, 8);                \

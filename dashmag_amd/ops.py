@@ -68,6 +68,23 @@ def _readable(t):
     return t
 
 
+def _gdr_view(t, rows_b, fast):
+    """A gated-delta-rule input as the kernels read it in place: ``_readable`` for q, k, v and
+    d_out (``fast``), any view for g and beta; and, for a batch of more than one, rows that
+    follow one another (b stride = T x t stride), else a contiguous copy."""
+    t = _readable(t) if fast else t
+    if rows_b and t.dim() >= 2 and t.shape[0] > 1 and t.stride(0) != t.shape[1] * t.stride(1):
+        t = t.contiguous()
+    return t
+
+
+def _gdr_strides(desc, step, **tensors):
+    desc.strided = 1
+    dims = (0, None, 1) if step else (0, 1, 2)
+    for name, t in tensors.items():
+        _set_strides(getattr(desc, name), t, dims)
+
+
 def _set_strides(field, t, dims):
     """Fills a ``dm_strides`` from ``t``'s strides along ``dims`` (``b``, ``t``, ``h`` in that
     order; None for an axis the tensor lacks)."""
@@ -444,7 +461,9 @@ def chunk_gated_delta_rule(q, k, v, g, beta, initial_state=None, cu_seqlens=None
                                               options.qk_l2norm, options.scale, False, keep)
     if initial_state is not None and tuple(initial_state.shape) != (nseq, h, dk, dv):
         raise Unsupported(f"{op}: the initial state must be [S, H, Dk, Dv], one per sequence")
-    qc, kc, vc, gc, bc = (x.contiguous() for x in (q, k, v, g, beta))
+    qc, kc, vc = (_gdr_view(x, True, True) for x in (q, k, v))
+    gc, bc = (_gdr_view(x, True, False) for x in (g, beta))
+    _gdr_strides(desc, False, sq=qc, sk=kc, sv=vc, sg=gc, sbeta=bc)
     h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
     out = torch.empty((b, t, h, dv), dtype=q.dtype, device=q.device)
     fin = torch.empty((nseq, h, dk, dv), dtype=torch.float32, device=q.device) \
@@ -473,12 +492,14 @@ def chunk_gated_delta_rule_backward(q, k, v, g, beta, initial_state, cu_seqlens,
         raise Unsupported(f"{op}: the output's gradient is [B, T, H, Dv]")
     if d_final_state is not None and tuple(d_final_state.shape) != (nseq, h, dk, dv):
         raise Unsupported(f"{op}: the final state's gradient is [S, H, Dk, Dv]")
-    qc, kc, vc, gc, bc = (x.contiguous() for x in (q, k, v, g, beta))
+    qc, kc, vc = (_gdr_view(x, True, True) for x in (q, k, v))
+    gc, bc = (_gdr_view(x, True, False) for x in (g, beta))
+    do = _gdr_view(d_out.to(q.dtype), True, True)
+    _gdr_strides(desc, False, sq=qc, sk=kc, sv=vc, sg=gc, sbeta=bc, sdo=do)
     h0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
-    do = d_out.to(q.dtype).contiguous()
     dfin = None if d_final_state is None else d_final_state.to(torch.float32).contiguous()
-    dq, dk_, dv_ = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
-    dg, db = torch.empty_like(gc), torch.empty_like(bc)
+    dq, dk_, dv_ = (torch.empty(x.shape, dtype=x.dtype, device=x.device) for x in (qc, kc, vc))
+    dg, db = (torch.empty(x.shape, dtype=x.dtype, device=x.device) for x in (gc, bc))
     dh0 = torch.empty((nseq, h, dk, dv), dtype=torch.float32, device=q.device) \
         if initial_state is not None else None
     nbytes = _lib.lib().dm_gdr_chunk_bwd_workspace(ctypes.byref(desc))
@@ -506,7 +527,9 @@ def gated_delta_step(q, k, v, g, beta, state, cu_seqlens=None,
         raise Unsupported(f"{op}: state must be [S, H, Dk, Dv], one per sequence")
     if state.dtype != torch.float32:
         raise Unsupported(f"{op}: the state is f32")
-    qc, kc, vc, gc, bc = (x.contiguous() for x in (q, k, v, g, beta))
+    qc, kc, vc = (_gdr_view(x, False, True) for x in (q, k, v))
+    _gdr_strides(desc, True, sq=qc, sk=kc, sv=vc, sg=g, sbeta=beta)
+    gc, bc = g, beta
     if in_place:
         if not state.is_contiguous():
             raise Unsupported(f"{op}: an in-place state must be contiguous")

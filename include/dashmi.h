@@ -112,6 +112,13 @@ typedef struct {
     int32_t qk_l2norm;
     int32_t has_scale;
     float scale;
+    /* 0: every input contiguous. 1: the strides below (elements, each >= 0) along (batch, time,
+     * head) of q, k, v [B, T, H, D] (the step: [B, H, D], t unused), g and beta [B, T, H], and
+     * the backward's d_out. The kernels index tokens as the flattened b * T + t, so each b
+     * stride must be T times the t stride (or B = 1); calls whose strides are not of that form
+     * are refused (the caller copies them). */
+    int32_t strided;
+    dm_strides sq, sk, sv, sg, sbeta, sdo;
 } dm_gdr_desc;
 
 /* The causal conv1d's activation (crates/dash-contract/src/conv1d.rs:81-90). */

@@ -118,3 +118,61 @@ def test_decode_packed_cache_view():
     o2 = dm.attention_decode_packed(q, k.contiguous(), v.contiguous(), cu)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+def _gdr_inputs(t, h, dk, dv, dtype, seed, fused=True):
+    """q, k, v as slices of one fused projection [1, T, H (2 Dk + Dv)] (or [1, H, T, D]
+    permutations), g and beta as slices of one [1, T, 2 H] f32 tensor."""
+    if fused:
+        qkv = syn.normal(seed, (1, t, h * (2 * dk + dv)), "cuda").to(dtype)
+        q = qkv[..., :h * dk].unflatten(-1, (h, dk))
+        k = qkv[..., h * dk:2 * h * dk].unflatten(-1, (h, dk))
+        v = qkv[..., 2 * h * dk:].unflatten(-1, (h, dv))
+    else:
+        q = syn.normal(seed, (1, h, t, dk), "cuda").to(dtype).transpose(1, 2)
+        k = syn.normal(seed + 1, (1, h, t, dk), "cuda").to(dtype).transpose(1, 2)
+        v = syn.normal(seed + 2, (1, h, t, dv), "cuda").to(dtype).transpose(1, 2)
+    gb = syn.normal(seed + 3, (1, t, 2 * h), "cuda")
+    gb = torch.cat([-torch.nn.functional.softplus(gb[..., :h]), torch.sigmoid(gb[..., h:])], -1)
+    return q, k, v, gb[..., :h], gb[..., h:]
+
+
+@pytest.mark.parametrize("dtype,fused", [(torch.bfloat16, True), (torch.bfloat16, False),
+                                         (torch.float32, True), (torch.float32, False)])
+def test_gdr_chunk_views(dtype, fused):
+    lens = [70, 1, 200, 64]
+    cu = torch.tensor([0, 70, 71, 271, 335], dtype=torch.int32, device="cuda")
+    t, h, d = sum(lens), 2, 128 if dtype != torch.float32 else 32
+    q, k, v, g, beta = _gdr_inputs(t, h, d, d, dtype, 31, fused)
+    assert not q.is_contiguous() and not g.is_contiguous()
+    h0 = syn.normal(37, (len(lens), h, d, d), "cuda", std=0.1)
+    do = syn.normal(38, (1, h, t, d), "cuda").to(dtype).transpose(1, 2)
+    opts = dm.ChunkGatedDeltaOptions(qk_l2norm=True, output_final_state=True)
+    _lib.probe_reset()
+    r1 = dm.chunk_gated_delta_rule(q, k, v, g, beta, h0, cu, opts)
+    b1 = dm.chunk_gated_delta_rule_backward(q, k, v, g, beta, h0, cu, do, None, opts)
+    if dtype != torch.float32:
+        pc = _lib.probe_counts()
+        assert pc["gdr_chunk_fwd_mfma"] > 0 and pc["gdr_chunk_bwd_mfma"] > 0, pc
+    c = [x.contiguous() for x in (q, k, v, g, beta)]
+    r2 = dm.chunk_gated_delta_rule(*c, h0, cu, opts)
+    b2 = dm.chunk_gated_delta_rule_backward(*c, h0, cu, do.contiguous(), None, opts)
+    torch.cuda.synchronize()
+    for a_, e_ in zip(list(r1) + list(b1), list(r2) + list(b2)):
+        assert torch.equal(a_, e_)
+
+
+def test_gdr_step_views():
+    b, h, d = 5, 3, 128
+    x = syn.normal(41, (b, 3 * h, d), "cuda").bfloat16()
+    q, k, v = x[:, :h], x[:, h:2 * h], x[:, 2 * h:]
+    gb = syn.normal(42, (b, 2 * h), "cuda")
+    gb = torch.cat([-torch.nn.functional.softplus(gb[:, :h]), torch.sigmoid(gb[:, h:])], -1)
+    g, beta = gb[:, :h], gb[:, h:]
+    st = syn.normal(43, (b, h, d, d), "cuda", std=0.1)
+    opts = dm.GatedDeltaStepOptions(True)
+    o1, s1 = dm.gated_delta_step(q, k, v, g, beta, st, None, opts)
+    o2, s2 = dm.gated_delta_step(q.contiguous(), k.contiguous(), v.contiguous(), g.contiguous(),
+                                 beta.contiguous(), st, None, opts)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
