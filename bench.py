@@ -39,7 +39,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list: attn,attn4096,decode,gdr,step,conv1d,logprob")
+    p.add_argument("--only", default="", help="comma list: attn,attn4096,attn256,decode,gdr,step,conv1d,logprob")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (torch copy_), 5 times: the known-size "
                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
@@ -188,6 +188,30 @@ def main():
               f"{secondary['attention_fwd_bwd_T4096']['value']:.1f} TFLOP/s", file=sys.stderr,
               flush=True)
         del c
+
+    # ---- the reference's own attention shape: T=6144, Hq=8, Hkv=2, D=256, causal ----
+    if want("attn256"):
+        c = syn.config2_single(dev, t=6144, hq=8, hkv=2, d=256)
+        P = syn.visible_pairs([6144])
+        q, k, v, do = c["q"], c["k"], c["v"], c["do"]
+        opts = dm.AttentionOptions(causal=True)
+        keep = []
+        desc = ops._attention_desc("attention", q, k, v, dm.AttentionMask.none(), opts, keep)
+        o = torch.empty_like(q)
+        lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        pp = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o, lse)]
+        fwd = lambda: check(lib.dm_attention_fwd(ctypes.byref(desc), *pp, None, 0, st), lib)  # noqa: E731
+        t = Timed(torch, fwd)
+        ms = t.run(args.steps, args.warmup)
+        kus = {k_: round(v_[0] * 1e3, 2) for k_, v_ in t.kernel_ms.items()}
+        secondary["attention_fwd_T6144_D256"] = dict(
+            unit="TFLOP/s", value=4 * P * 256 * 8 / ms / 1e9, ms=ms,
+            frac_of_bf16_peak=4 * P * 256 * 8 / ms / 1e9 / BF16_PEAK_TFLOPS, kernel_us=kus,
+            shape="causal, T=6144, Hq=8, Hkv=2, D=256, bf16 (crates/dash-ops/README.md:83-84)")
+        print(f"attention fwd T=6144 D=256: {ms:.3f} ms, {4 * P * 256 * 8 / ms / 1e9:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
+        del c, q, k, v, do, o
 
     # ---- decode, config 3 ----
     if want("decode"):

@@ -23,7 +23,11 @@
 
 namespace dm {
 
-constexpr int kFwdM = 256;  // queries per workgroup
+// queries per workgroup: 32 per wavefront, 8 wavefronts (ping-pong pairs) at D 64 and 128, 4 at
+// D 256 (one per SIMD: 32 queries' O^T over 256 columns and their Q fragments take 192
+// registers, more than two wavefronts per SIMD hold)
+template <int D>
+constexpr int fwd_waves() { return D == 256 ? 4 : 8; }
 constexpr int kFwdN = 64;   // keys per tile
 
 // Row strides (elements) of the LDS tiles: K rows are read along D by ds_read_b128 (16 lanes on
@@ -62,7 +66,7 @@ __device__ uint64_t dm_trace_fwd[2][256][4];
 #endif
 
 template <int DT, int D, bool PAD>
-__global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, int64_t Hq,
+__global__ __launch_bounds__(64 * fwd_waves<D>(), 1) void attn_fwd_mfma(MaskInfo m, int64_t B, int64_t Hq,
                                                       int64_t Hkv, float scale, AttnStrides sd,
                                                       const uint16_t *__restrict__ q,
                                                       const uint16_t *__restrict__ k,
@@ -73,6 +77,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     __shared__ FwdSmem<D> sm;
     constexpr int KSTEPS = D / 16;  // k-steps of S^T over the head dimension
     constexpr int DT32 = D / 32;    // 32-row tiles of O^T
+    constexpr int NW = fwd_waves<D>(), NT = 64 * NW, kFwdM = 32 * NW;
     const int64_t Tq = m.tq, Tk = m.tk;
     const int64_t ntiles = (Tq + kFwdM - 1) / kFwdM;
     const int64_t nwork = ntiles * Hq * B;
@@ -87,7 +92,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     const int64_t b = work / (Hq * ntiles);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool first = wave < 4;  // products first in each step
+    const bool first = NW == 4 || wave < 4;  // products first in each step
     const int col = lane & 31, half = lane >> 5;
     const int64_t qi = tile * kFwdM + wave * 32 + col;  // this lane's query row
     const bool qvalid = qi < Tq;
@@ -118,7 +123,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     __syncthreads();
     int32_t kv_lo = INT32_MAX, kv_hi = INT32_MIN;
 #pragma unroll
-    for (int w = 0; w < 8; w++) {
+    for (int w = 0; w < NW; w++) {
         kv_lo = min(kv_lo, sm.lo[w]);
         kv_hi = max(kv_hi, sm.hi[w]);
     }
@@ -160,8 +165,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_mfma(MaskInfo m, int64_t B, i
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + b * sd.v.b + kh * sd.v.h, vbytes);
     const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
     constexpr int CPR = D / 8;              // chunks per row
-    constexpr int NCH = kFwdN * CPR / 512;   // chunks per thread per tensor
-    constexpr int RSTEP = 512 / CPR;        // rows between a thread's chunks
+    constexpr int NCH = kFwdN * CPR / NT;    // chunks per thread per tensor
+    constexpr int RSTEP = NT / CPR;         // rows between a thread's chunks
     const int crow = tid / CPR, ccol = tid % CPR;
     const uint32_t koff = (uint32_t)(crow * kstride + ccol * 8) * 2;
     const uint32_t voff = (uint32_t)(crow * vstride + ccol * 8) * 2;
@@ -353,9 +358,9 @@ bool mfma_fwd_takes(const dm_attention_desc *d, const void *q, const void *k, co
     // buffer loads take 32-bit byte offsets within one (batch row, head)'s keys and values;
     // 16-byte vector loads need 16-byte rows and bases
     const AttnStrides s = attn_strides(d);
-    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && (d->d == 64 || d->d == 128) &&
-           d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
-           rows_fit_32bit(s.k, d->tk, d->d) && rows_fit_32bit(s.v, d->tk, d->d) &&
+    return (d->dtype == DM_BF16 || d->dtype == DM_F16) &&
+           (d->d == 64 || d->d == 128 || d->d == 256) && d->tq < (1ll << 30) &&
+           d->tk < (1ll << 30) && scale_of(d) > 0.f && rows_fit_32bit(s.k, d->tk, d->d) && rows_fit_32bit(s.v, d->tk, d->d) &&
            strides_16b(s.q) && strides_16b(s.k) && strides_16b(s.v) && aligned_16b(q) &&
            aligned_16b(k) && aligned_16b(v);
 }
@@ -369,11 +374,13 @@ extern "C" int dm_debug_trace_fwd(void *host, size_t bytes) {
 int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float scale,
                          const void *q, const void *k, const void *v, void *o, float *lse,
                          hipStream_t st) {
-    const int64_t ntiles = (d->tq + kFwdM - 1) / kFwdM;
+    const int nw = d->d == 256 ? fwd_waves<256>() : fwd_waves<128>();
+    const int64_t per = 32 * nw;  // queries per workgroup
+    const int64_t ntiles = (d->tq + per - 1) / per;
     const int64_t nwork = ntiles * d->hq * d->b;
     const int64_t nblocks = (nwork + 7) / 8 * 8;
     if (nblocks >= (1ll << 31)) return refuse("attention: too many query tiles");
-    dim3 grid((unsigned)nblocks), block(512);
+    dim3 grid((unsigned)nblocks), block(64 * nw);
     const uint16_t *qq = (const uint16_t *)q, *kk = (const uint16_t *)k, *vv = (const uint16_t *)v;
     uint16_t *oo = (uint16_t *)o;
     const AttnStrides sd = attn_strides(d);
@@ -387,9 +394,9 @@ int launch_attn_fwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     {
         KernelTimer timer(DM_KERNEL_ATTN_FWD, st);
         if (d->dtype == DM_BF16) {
-            if (d->d == 64) { FWD(DM_BF16, 64); } else { FWD(DM_BF16, 128); }
+            if (d->d == 64) { FWD(DM_BF16, 64); } else if (d->d == 128) { FWD(DM_BF16, 128); } else { FWD(DM_BF16, 256); }
         } else {
-            if (d->d == 64) { FWD(DM_F16, 64); } else { FWD(DM_F16, 128); }
+            if (d->d == 64) { FWD(DM_F16, 64); } else if (d->d == 128) { FWD(DM_F16, 128); } else { FWD(DM_F16, 256); }
         }
     }
 #undef FWD

@@ -420,15 +420,23 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     const uint32_t mbytes = (uint32_t)(((Tq - 1) * Hq + 1) * 4);
     const __amdgpu_buffer_rsrc_t lrs = make_rsrc(w.rlo + b * Tq, (uint32_t)(Tq * 4));
     const __amdgpu_buffer_rsrc_t hrs = make_rsrc(w.rhi + b * Tq, (uint32_t)(Tq * 4));
+    // each chunk's byte offset within a step's rows (loop-invariant)
+    uint32_t qoff[NCH], goff[NCH];
+#pragma unroll
+    for (int u = 0; u < NCH; u++) {
+        const uint32_t r = (uint32_t)((crow + u * RSTEP) & (kDkdvStep - 1));
+        qoff[u] = r * qrow_bytes + ccol * 16;
+        goff[u] = r * grow_bytes + ccol * 16;
+    }
     auto load = [&](Stage &x, int64_t h, int64_t t) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t qrs = make_rsrc(q + b * sd.q.b + h * sd.q.h, qbytes);
         const __amdgpu_buffer_rsrc_t grs = make_rsrc(d_o + b * sd.g.b + h * sd.g.h, gbytes);
         const uint32_t i0 = (uint32_t)(t * kDkdvStep);
+        const uint32_t qb = i0 * qrow_bytes, gb = i0 * grow_bytes;
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            const int r = (crow + u * RSTEP) & (kDkdvStep - 1);
-            x.q[u] = buf_load16(qrs, (i0 + r) * qrow_bytes + ccol * 16);
-            x.g[u] = buf_load16(grs, (i0 + r) * grow_bytes + ccol * 16);
+            x.q[u] = buf_load16(qrs, qb + qoff[u]);
+            x.g[u] = buf_load16(grs, gb + goff[u]);
         }
         const uint32_t i = (uint32_t)(t * kDkdvStep) + (tid & (kDkdvStep - 1));
         const __amdgpu_buffer_rsrc_t srs = make_rsrc(w.lse2 + b * Tq * Hq + h, mbytes);
@@ -843,13 +851,20 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     };
     KvStage st0, st1;
     const int nsteps = kv_lo < kv_hi ? (kv_hi - kv_lo + kDqStep - 1) / kDqStep : 0;
+    uint32_t koff[NCH], voff[NCH];  // each chunk's byte offset within a step's rows
+#pragma unroll
+    for (int u = 0; u < NCH; u++) {
+        const int r = (crow + u * RSTEP) & (kDqStep - 1);
+        koff[u] = (uint32_t)(r * kstride + ccol * 8) * 2;
+        voff[u] = (uint32_t)(r * vstride + ccol * 8) * 2;
+    }
     auto load = [&](KvStage &x, int n) __attribute__((always_inline)) {
         const int32_t j0 = kv_lo + (n < nsteps ? n : 0) * kDqStep;
+        const uint32_t kb = (uint32_t)(j0 * kstride) * 2, vb = (uint32_t)(j0 * vstride) * 2;
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            const int r = (crow + u * RSTEP) & (kDqStep - 1);
-            x.k[u] = buf_load16(krs, (uint32_t)((j0 + r) * kstride + ccol * 8) * 2);
-            x.v[u] = buf_load16(vrs, (uint32_t)((j0 + r) * vstride + ccol * 8) * 2);
+            x.k[u] = buf_load16(krs, kb + koff[u]);
+            x.v[u] = buf_load16(vrs, vb + voff[u]);
         }
     };
     auto store = [&](const KvStage &x, DqSlot<D> &sl) __attribute__((always_inline)) {

@@ -153,3 +153,40 @@ def test_mfma_attention_nondeterministic_flag_matches():
     assert torch.equal(r1[1], r2[1]) and torch.equal(r1[2], r2[2])
     err = errors(host(r2[0]), host(r1[0]))[1]
     assert err <= 2 * BF16.masks[2]
+
+
+D256_CASES = [c for c in CASES if c[0] in (
+    "none_129", "causal_1", "causal_31", "causal_127_scale", "causal_tq127_tk33_empty_rows",
+    "window_both_300", "key_padding_160", "packed_cross", "packed_no_causal")]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", D256_CASES, ids=[c[0] for c in D256_CASES])
+def test_mfma_attention_d256_matches_oracle(case, dtype):
+    """Head width 256 (the reference's published attention shapes): the forward on MFMA (a
+    probe shows it), the backward on the generic kernels; both against the f64 oracle."""
+    print(f"case {case[0]} {dtype} D=256", flush=True)
+    seed = 3000 + 17 * CASES.index(case)
+    (q, k, v, do), mask, opts, mk = _build(case, dtype, 256, seed)
+    _lib.probe_reset()
+    o, lse = dm.attention_with_lse(q, k, v, mask, opts)
+    torch.cuda.synchronize()
+    pc = _lib.probe_counts()
+    assert pc["attn_fwd_mfma"] > 0 and pc["attn_fwd_generic"] == 0, pc
+    dq, dk, dv = dm.attention_backward(q, k, v, o, lse, do, mask, opts)
+    torch.cuda.synchronize()
+    call = mk(host(q), host(k), host(v))
+    eo, el = oracle.attention_fwd(call, "f64")
+    gq, gk, gv = oracle.attention_bwd(call, host(o), host(lse), host(do), "f64")
+    bounds = (BF16 if dtype == torch.bfloat16 else F16).masks
+    got = [host(o), host(lse), host(dq), host(dk), host(dv)]
+    for name, a, e, bound in zip(PARTS, got, [eo, el, gq, gk, gv], bounds):
+        ab, err = errors(a, e)
+        if name != "lse" and np.max(np.abs(e[np.isfinite(e)]), initial=0.0) < 1e-3:
+            err = ab
+        tol = 2 * bound * (max(1.0, np.sqrt(k.shape[1] / 64)) if name == "lse" else 1.0)
+        print(f"  {name}: rel {err:.2e} (bound {tol:.1e})")
+        assert err <= tol, (case[0], name, err)
+    empty = el == -np.inf
+    if empty.any():
+        assert np.all(got[0][empty] == 0.0) and np.all(got[2][empty] == 0.0)
