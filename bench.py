@@ -192,26 +192,20 @@ def main():
     # ---- the reference's own attention shape: T=6144, Hq=8, Hkv=2, D=256, causal ----
     if want("attn256"):
         c = syn.config2_single(dev, t=6144, hq=8, hkv=2, d=256)
+        ms, mf, mb, _, kms = bench_attention(torch, dm, ops, lib, c, args.steps, args.warmup)
         P = syn.visible_pairs([6144])
-        q, k, v, do = c["q"], c["k"], c["v"], c["do"]
-        opts = dm.AttentionOptions(causal=True)
-        keep = []
-        desc = ops._attention_desc("attention", q, k, v, dm.AttentionMask.none(), opts, keep)
-        o = torch.empty_like(q)
-        lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
-        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        pp = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o, lse)]
-        fwd = lambda: check(lib.dm_attention_fwd(ctypes.byref(desc), *pp, None, 0, st), lib)  # noqa: E731
-        t = Timed(torch, fwd)
-        ms = t.run(args.steps, args.warmup)
-        kus = {k_: round(v_[0] * 1e3, 2) for k_, v_ in t.kernel_ms.items()}
-        secondary["attention_fwd_T6144_D256"] = dict(
-            unit="TFLOP/s", value=4 * P * 256 * 8 / ms / 1e9, ms=ms,
-            frac_of_bf16_peak=4 * P * 256 * 8 / ms / 1e9 / BF16_PEAK_TFLOPS, kernel_us=kus,
+        fl = lambda n: n * P * 256 * 8  # noqa: E731
+        secondary["attention_fwd_bwd_T6144_D256"] = dict(
+            unit="TFLOP/s", value=fl(14) / ms / 1e9, ms_per_step=ms, ms_fwd=mf, ms_bwd=mb,
+            fwd_tflops=fl(4) / mf / 1e9, bwd_tflops=fl(10) / mb / 1e9,
+            frac_of_bf16_peak=fl(14) / ms / 1e9 / BF16_PEAK_TFLOPS,
+            kernel_us={k_: round(v_[0] * 1e3, 2) for k_, v_ in kms.items()},
             shape="causal, T=6144, Hq=8, Hkv=2, D=256, bf16 (crates/dash-ops/README.md:83-84)")
-        print(f"attention fwd T=6144 D=256: {ms:.3f} ms, {4 * P * 256 * 8 / ms / 1e9:.1f} TFLOP/s",
-              file=sys.stderr, flush=True)
-        del c, q, k, v, do, o
+        print("attention T=6144 D=256 kernels: " + ", ".join(
+            f"{k_} {v_[0] * 1e3:.1f} us" for k_, v_ in kms.items()), file=sys.stderr, flush=True)
+        print(f"attention T=6144 D=256: {ms:.3f} ms/step (fwd {mf:.3f} = {fl(4) / mf / 1e9:.1f}, "
+              f"bwd {mb:.3f} = {fl(10) / mb / 1e9:.1f} TFLOP/s)", file=sys.stderr, flush=True)
+        del c
 
     # ---- decode, config 3 ----
     if want("decode"):

@@ -1,4 +1,4 @@
-// MFMA attention backward for gfx950 (bf16/f16, head width 64 or 128), deterministic: the
+// MFMA attention backward for gfx950 (bf16/f16, head width 64, 128 or 256), deterministic: the
 // query gradient is summed over the key tiles in a fixed order by its own sweep, as the
 // reference's default does (crates/dash-ops/src/attention/kernels.rs:999-2058; the contract's
 // `deterministic`, crates/dash-contract/src/attention.rs:100-105).
@@ -13,6 +13,7 @@
 //              dK += dS^T Q, whose B operands come from transposed LDS copies of the tile.
 //   bwd_dq     per (tile of 128 queries, query head): sweeps the key tiles as the forward does,
 //              recomputing S^T and dP^T, dQ^T += K^T dS^T.
+//   bwd_dkdv_w4, bwd_dq_w4   head width 256: one wavefront per SIMD, dV and dK in two passes.
 #include <string>
 #include <type_traits>
 
@@ -1016,6 +1017,516 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 }
 
 // ------------------------------------------------------------------------------------------
+// Head width 256: single-role wavefronts
+// ------------------------------------------------------------------------------------------
+//
+// At D = 256 a wavefront's 32 keys need dK and dV accumulators of 128 registers each, and the
+// products' outputs share the accumulator registers with them: both gradients at once do not
+// fit beside the S and dP outputs. The gradients are then two launches of one kernel, each
+// workgroup 4 wavefronts (one per SIMD) taking 32 keys each through every step:
+//   dV pass: S = Q K^T, P, dV += P^T dO                      (32 products of 32x32x16 a step)
+//   dK pass: S = Q K^T, P, dP = dO V^T, dS = P (dP - delta), dK += dS^T Q     (48 a step)
+// (80 products against the 64 of a single pass: S is computed twice). The tiles a pass reads
+// rotate through two LDS slots, staged one step ahead through registers. The work list, the
+// schedule ring and the query-head split are the 8-wavefront kernel's.
+constexpr int kDkdvDV = 0, kDkdvDK = 1;
+
+template <int D>
+struct Dkdv4Smem {
+    DkdvSlot<D> slot[2];
+    int4 sched[kDkdvRing];
+};
+
+template <int DT, int D, bool PAD, int MODE>
+__global__ __launch_bounds__(256, 1) void bwd_dkdv_w4(MaskInfo m, int64_t B, int64_t Hq,
+                                                      int64_t Hkv, float scale, AttnStrides sd,
+                                                      const uint16_t *__restrict__ q,
+                                                      const uint16_t *__restrict__ k,
+                                                      const uint16_t *__restrict__ v,
+                                                      const uint16_t *__restrict__ d_o,
+                                                      const float *__restrict__ delta,
+                                                      BwdWs w, uint16_t *__restrict__ out) {
+    constexpr bool DK = MODE == kDkdvDK;
+    constexpr int RS = BwdStrides<D>::ROW, TS = BwdStrides<D>::TR;
+    __shared__ Dkdv4Smem<D> sm;
+    constexpr int KSTEPS = D / 16, DT32 = D / 32;
+    const int64_t Tq = m.tq, Tk = m.tk;
+    const int64_t nkb = (Tk + kKvBlock - 1) / kKvBlock;
+    const int hs = w.hsplit;
+    const int64_t nwork = nkb * Hkv * B * hs;
+    if ((int64_t)blockIdx.x >= nwork) return;
+    const int64_t work = w.order[blockIdx.x];
+    const int64_t kh = work % Hkv, part = (work / Hkv) % hs;
+    const int64_t kb = (work / (Hkv * hs)) % nkb, b = work / (Hkv * hs * nkb);
+    const int64_t group = Hq / Hkv;
+    const int64_t h_first = kh * group + part * (group / hs);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kw = wave;
+    const int col = lane & 31, half = lane >> 5;
+    const int32_t j0 = (int32_t)(kb * kKvBlock);
+    const int32_t key = j0 + kw * 32 + col;
+    const bool kvalid = key < Tk;
+    const bool kpad = PAD && kvalid && m.pad[b * Tk + key];
+    const int32_t mkey = kpad ? -1 : key;
+    const float c2 = scale * 1.4426950408889634f;
+
+    // K (and, for dK, V) of this lane's key as B operands (col = key, k = head dim)
+    Frag8 bk[KSTEPS], bv[DK ? KSTEPS : 1];
+    {
+        const uint16_t *kp = k + b * sd.k.b + (int64_t)key * sd.k.t + kh * sd.k.h + half * 8;
+        const uint16_t *vp = v + b * sd.v.b + (int64_t)key * sd.v.t + kh * sd.v.h + half * 8;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            bk[st].u = kvalid ? *(const uint4 *)(kp + st * 16) : make_uint4(0, 0, 0, 0);
+            if constexpr (DK) bv[st].u = kvalid ? *(const uint4 *)(vp + st * 16) : make_uint4(0, 0, 0, 0);
+        }
+    }
+    f32x16_t acc[DT32];
+#pragma unroll
+    for (int t = 0; t < DT32; t++) acc[t] = zero16();
+
+    const int64_t ntiles = (Tq + kDkdvStep - 1) / kDkdvStep;
+    const int32_t *tr = w.trange + b * ntiles * 4;
+    const int32_t j1 = j0 + kKvBlock < Tk ? j0 + kKvBlock : (int32_t)Tk;
+    const int32_t hend = (int32_t)(h_first + group / hs);
+    struct TileIter {
+        int32_t h, t, c0;
+        uint64_t pending, cut;
+        bool masked;
+    };
+    auto scan = [&](TileIter &it) {
+        const int32_t tt = it.c0 + lane;
+        const int4 r = *(const int4 *)(tr + (tt < ntiles ? tt : ntiles - 1) * 4);
+        const bool in = tt < ntiles;
+        const bool see = in & (r.x < j1) & (r.y > j0);
+        const bool pcut = PAD | (r.z > j0) | (r.w < j0 + kKvBlock);
+        it.pending = __ballot(see);
+        it.cut = __ballot(pcut);
+    };
+    auto next = [&](TileIter &it) {
+        while (it.h < hend) {
+            if (it.pending) {
+                const int bit = __builtin_ctzll(it.pending);
+                it.pending &= it.pending - 1;
+                it.t = __builtin_amdgcn_readfirstlane(it.c0 + bit);
+                it.masked = (it.cut >> bit) & 1;
+                return;
+            }
+            it.c0 += 64;
+            if (it.c0 >= ntiles) {
+                it.h++;
+                it.c0 = 0;
+                if (it.h >= hend) return;
+            }
+            scan(it);
+        }
+    };
+    TileIter it;
+    auto publish = [&](const int kk) __attribute__((always_inline)) {
+        if (lane == 0)
+            sm.sched[kk % kDkdvRing] = make_int4(it.h, it.t, it.masked ? 1 : 0, it.h < hend ? 1 : 0);
+        if (it.h < hend) next(it);
+    };
+    if (wave == 0) {
+        it.h = (int32_t)h_first;
+        it.c0 = 0;
+        it.t = -1;
+        if (j0 >= Tk) {
+            it.h = hend;
+        } else {
+            scan(it);
+            next(it);
+        }
+        for (int kk = 0; kk < 4; kk++) publish(kk);
+    }
+    __syncthreads();
+    struct Entry {
+        int32_t h, t;
+        bool masked, valid;
+    };
+    auto entry = [&](const int kk) __attribute__((always_inline)) -> Entry {
+        const int4 e = sm.sched[kk % kDkdvRing];
+        Entry x;
+        x.h = __builtin_amdgcn_readfirstlane(e.x);
+        x.t = __builtin_amdgcn_readfirstlane(e.y);
+        x.masked = __builtin_amdgcn_readfirstlane(e.z) != 0;
+        x.valid = __builtin_amdgcn_readfirstlane(e.w) != 0;
+        return x;
+    };
+
+    // staging: a step's Q and dO rows, 16-byte chunks over the 256 threads
+    constexpr int CPR = D / 8, NCH = kDkdvStep * CPR / 256, RSTEP = 256 / CPR;
+    const int crow = tid / CPR, ccol = tid % CPR;
+    const uint32_t qrow_bytes = (uint32_t)(sd.q.t * 2), grow_bytes = (uint32_t)(sd.g.t * 2);
+    const uint32_t qbytes = (uint32_t)(((Tq - 1) * sd.q.t + D) * 2);
+    const uint32_t gbytes = (uint32_t)(((Tq - 1) * sd.g.t + D) * 2);
+    const uint32_t mbytes = (uint32_t)(((Tq - 1) * Hq + 1) * 4);
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(w.rlo + b * Tq, (uint32_t)(Tq * 4));
+    const __amdgpu_buffer_rsrc_t hrs = make_rsrc(w.rhi + b * Tq, (uint32_t)(Tq * 4));
+    struct Stage {
+        uint4 q[NCH], g[NCH];
+        float lse, delta;
+        int32_t lo, hi;
+    };
+    Stage stg;
+    auto load = [&](int64_t h, int64_t t) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t qrs = make_rsrc(q + b * sd.q.b + h * sd.q.h, qbytes);
+        const __amdgpu_buffer_rsrc_t grs = make_rsrc(d_o + b * sd.g.b + h * sd.g.h, gbytes);
+        const uint32_t i0 = (uint32_t)(t * kDkdvStep);
+#pragma unroll
+        for (int u = 0; u < NCH; u++) {
+            const uint32_t r = i0 + (uint32_t)(crow + u * RSTEP);
+            stg.q[u] = buf_load16(qrs, r * qrow_bytes + ccol * 16);
+            stg.g[u] = buf_load16(grs, r * grow_bytes + ccol * 16);
+        }
+        const uint32_t i = i0 + (tid & (kDkdvStep - 1));
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(w.lse2 + b * Tq * Hq + h, mbytes);
+        stg.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, i * (uint32_t)Hq * 4, 0, 0));
+        if constexpr (DK) {
+            const __amdgpu_buffer_rsrc_t drs = make_rsrc(delta + b * Tq * Hq + h, mbytes);
+            stg.delta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drs, i * (uint32_t)Hq * 4, 0, 0));
+        }
+        stg.lo = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, i * 4, 0, 0);
+        stg.hi = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(hrs, i * 4, 0, 0);
+    };
+    // the dV pass reads Q by rows and dO transposed; the dK pass Q both ways and dO by rows
+    auto store = [&](DkdvSlot<D> &sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NCH; u++) {
+            const int r = crow + u * RSTEP;
+            sl.q[r * (RS / 8) + ccol] = stg.q[u];
+            if constexpr (DK) {
+                sl.qt[r * (TS / 8) + ccol] = stg.q[u];
+                sl.g[r * (RS / 8) + ccol] = stg.g[u];
+            } else {
+                sl.gt[r * (TS / 8) + ccol] = stg.g[u];
+            }
+        }
+        if (tid < kDkdvStep) {
+            sl.lse2[tid] = stg.lse;
+            if constexpr (DK) sl.delta[tid] = stg.delta;
+            sl.rlo[tid] = stg.lo;
+            sl.rhi[tid] = max(stg.hi - stg.lo, 0);
+        }
+    };
+    auto load_entry = [&](const Entry &e) __attribute__((always_inline)) {
+        load(e.valid ? e.h : h_first, e.valid ? e.t : 0);
+    };
+
+    // one 32-query step on slot sl, this wavefront's keys
+    auto step = [&](const DkdvSlot<D> &sl, const bool masked_flag) __attribute__((always_inline)) {
+        const uint16_t *sq = (const uint16_t *)sl.q;
+        // S = Q K^T (A = the query rows, B = this lane's key)
+        f32x16_t s = zero16();
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(sq + col * RS + half * 8 + st * 16);
+            s = mfma32<DT>(a, bk[st], s);
+            if (st % 4 == 3) __builtin_amdgcn_sched_barrier(0);  // reads at most 4 ahead
+        }
+        // P = exp2(S c - lse2), masked on the tiles the intervals cut; element i is query
+        // 8 (i / 4) + 4 h + i % 4
+        float p[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r0 = j * 8 + half * 4;
+            const float4 l4 = *(const float4 *)(sl.lse2 + r0);
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+            int lo4[4] = {0, 0, 0, 0}, hi4[4] = {0, 0, 0, 0};
+            if (masked_flag) {
+                const int4 a4 = *(const int4 *)(sl.rlo + r0);
+                const int4 b4 = *(const int4 *)(sl.rhi + r0);
+                lo4[0] = a4.x; lo4[1] = a4.y; lo4[2] = a4.z; lo4[3] = a4.w;
+                hi4[0] = b4.x; hi4[1] = b4.y; hi4[2] = b4.z; hi4[3] = b4.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float x = fast_exp2(fmaf(s[4 * j + e], c2, -lv[e]));
+                if (masked_flag) x = (uint32_t)(mkey - lo4[e]) < (uint32_t)hi4[e] ? x : 0.f;
+                p[4 * j + e] = x;
+            }
+        }
+        if constexpr (DK) {
+            // dP = dO V^T, dS = P (dP - delta)
+            const uint16_t *sg = (const uint16_t *)sl.g;
+            f32x16_t dp = zero16();
+#pragma unroll
+            for (int st = 0; st < KSTEPS; st++) {
+                Frag8 a;
+                a.u = *(const uint4 *)(sg + col * RS + half * 8 + st * 16);
+                dp = mfma32<DT>(a, bv[st], dp);
+                if (st % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 d4 = *(const float4 *)(sl.delta + j * 8 + half * 4);
+                p[4 * j + 0] *= dp[4 * j + 0] - d4.x;
+                p[4 * j + 1] *= dp[4 * j + 1] - d4.y;
+                p[4 * j + 2] *= dp[4 * j + 2] - d4.z;
+                p[4 * j + 3] *= dp[4 * j + 3] - d4.w;
+            }
+        }
+        // dV += P^T dO or dK += dS^T Q: A = P (dS) in the products' output layout (row = key,
+        // k = query), B = dO (Q) by transposed reads of the row-major tile
+        const uint16_t *sb = DK ? (const uint16_t *)sl.qt : (const uint16_t *)sl.gt;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            Frag8 pf;
+            pf.u = make_uint4(pack2<DT>(p[8 * u], p[8 * u + 1]), pack2<DT>(p[8 * u + 2], p[8 * u + 3]),
+                              pack2<DT>(p[8 * u + 4], p[8 * u + 5]), pack2<DT>(p[8 * u + 6], p[8 * u + 7]));
+#pragma unroll
+            for (int dt = 0; dt < DT32; dt++) {
+                acc[dt] = mfma32<DT>(pf, lds_tr_frag(sb, TS, u * 16, dt * 32, lane), acc[dt]);
+                if (dt % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    // prologue: step 0 in slot 0, step 1 loading; iteration n stores step n + 1 into the other
+    // slot, loads step n + 2 and computes step n
+    {
+        const Entry e0 = entry(0);
+        load_entry(e0);
+        if (e0.valid) store(sm.slot[0]);
+        load_entry(entry(1));
+    }
+    __syncthreads();
+    // the step count up front (a counted loop keeps the accumulators in place across it): the
+    // tiles whose rows see the block, once per query head of the item
+    int32_t nsee = 0;
+    if (j0 < Tk) {
+        for (int64_t c0 = 0; c0 < ntiles; c0 += 64) {
+            const int64_t tt = c0 + lane;
+            const int4 r = *(const int4 *)(tr + (tt < ntiles ? tt : ntiles - 1) * 4);
+            nsee += __builtin_popcountll(__ballot((tt < ntiles) & (r.x < j1) & (r.y > j0)));
+        }
+    }
+    const int32_t nsteps = __builtin_amdgcn_readfirstlane(nsee * (hend - (int32_t)h_first));
+    for (int n = 0; n < nsteps; n++) {
+        const Entry e = entry(n);
+        if (n + 1 < nsteps) store(sm.slot[(n + 1) & 1]);
+        load_entry(entry(n + 2));
+        step(sm.slot[n & 1], e.masked);
+        if (wave == 0) publish(n + 4);
+        __syncthreads();
+    }
+
+    // dK (scaled) or dV: lane holds column d = 32 dt + col, rows = keys 32 kw + crow(i)
+    const int32_t nrows = (int32_t)(Tk - j0) - kw * 32;  // rows of this wavefront's keys in range
+    const int64_t base = ((b * Tk + j0 + kw * 32) * Hkv + kh) * D + col;
+    const int32_t rstride = (int32_t)(Hkv * D);
+    const float f = DK ? scale : 1.f;
+    if (hs == 1) {
+        uint16_t *po = out + base;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = dm::crow(i, lane);
+            if (r < nrows) {
+#pragma unroll
+                for (int dt = 0; dt < DT32; dt++)
+                    po[r * rstride + dt * 32] = (uint16_t)(pack2<DT>(acc[dt][i] * f, 0.f) & 0xffffu);
+            }
+        }
+    } else {
+        const int64_t n = B * Tk * Hkv * D;
+        float *po = w.kvpart + (part * 2 + (DK ? 0 : 1)) * n + base;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = dm::crow(i, lane);
+            if (r < nrows) {
+#pragma unroll
+                for (int dt = 0; dt < DT32; dt++) po[r * rstride + dt * 32] = acc[dt][i] * f;
+            }
+        }
+    }
+}
+
+// dQ at D = 256: 4 wavefronts of 32 queries (128 per workgroup), each holding its queries' Q
+// and dO fragments and dQ^T (256 x 32) over the key steps: S^T = K Q^T, dP^T = V dO^T,
+// dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T (48 products per 32-key step). Key and value tiles
+// rotate through two LDS slots, staged one step ahead.
+template <int D>
+struct Dq4Smem {
+    DqSlot<D> slot[2];
+    int32_t lo[4], hi[4];
+};
+
+template <int DT, int D, bool PAD>
+__global__ __launch_bounds__(256, 1) void bwd_dq_w4(MaskInfo m, int64_t B, int64_t Hq, int64_t Hkv,
+                                                    float scale, AttnStrides sd,
+                                                    const uint16_t *__restrict__ q,
+                                                    const uint16_t *__restrict__ k,
+                                                    const uint16_t *__restrict__ v,
+                                                    const uint16_t *__restrict__ d_o,
+                                                    const float *__restrict__ delta, BwdWs w,
+                                                    uint16_t *__restrict__ dq) {
+    constexpr int RS = BwdStrides<D>::ROW, TS = BwdStrides<D>::TR;
+    __shared__ Dq4Smem<D> sm;
+    constexpr int KSTEPS = D / 16, DT32 = D / 32;
+    const int64_t Tq = m.tq, Tk = m.tk;
+    const int64_t ntiles = (Tq + kDqM - 1) / kDqM;
+    const int64_t nwork = ntiles * Hq * B;
+    const int64_t work = blockIdx.x;
+    if (work >= nwork) return;
+    const int64_t kh = work % Hkv;
+    const int64_t h = kh * (Hq / Hkv) + (work / Hkv) % (Hq / Hkv);
+    const int64_t tile = ntiles - 1 - (work / Hq) % ntiles;
+    const int64_t b = work / (Hq * ntiles);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const int64_t qi = tile * kDqM + wave * 32 + col;
+    const bool qvalid = qi < Tq;
+    int32_t lo = 0, hi = 0;
+    float lse2 = INFINITY, dl = 0.f;
+    if (qvalid) {
+        lo = w.rlo[b * Tq + qi];
+        hi = w.rhi[b * Tq + qi];
+        lse2 = w.lse2[(b * Tq + qi) * Hq + h];
+        dl = delta[(b * Tq + qi) * Hq + h];
+    }
+    if (lse2 == INFINITY) hi = lo;  // a query that sees no key: dq = 0
+    {
+        int32_t wl = lo < hi ? lo : INT32_MAX, wh = lo < hi ? hi : INT32_MIN;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            wl = min(wl, __shfl_xor(wl, off, 64));
+            wh = max(wh, __shfl_xor(wh, off, 64));
+        }
+        if (lane == 0) {
+            sm.lo[wave] = wl;
+            sm.hi[wave] = wh;
+        }
+    }
+    __syncthreads();
+    const int32_t kv_lo = min(min(sm.lo[0], sm.lo[1]), min(sm.lo[2], sm.lo[3]));
+    const int32_t kv_hi = max(max(sm.hi[0], sm.hi[1]), max(sm.hi[2], sm.hi[3]));
+    const int32_t span = hi - lo;
+
+    Frag8 qf[KSTEPS], gf[KSTEPS];  // B operands: col = query, k = d
+    {
+        const uint16_t *qp = q + b * sd.q.b + qi * sd.q.t + h * sd.q.h + half * 8;
+        const uint16_t *gp = d_o + b * sd.g.b + qi * sd.g.t + h * sd.g.h + half * 8;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            qf[st].u = qvalid ? *(const uint4 *)(qp + st * 16) : make_uint4(0, 0, 0, 0);
+            gf[st].u = qvalid ? *(const uint4 *)(gp + st * 16) : make_uint4(0, 0, 0, 0);
+        }
+    }
+    f32x16_t acc[DT32];
+#pragma unroll
+    for (int t = 0; t < DT32; t++) acc[t] = zero16();
+    const float c2 = scale * 1.4426950408889634f;
+    const float nlse = -lse2;
+    const int32_t kstride = (int32_t)sd.k.t, vstride = (int32_t)sd.v.t;
+    const uint32_t kbytes = (uint32_t)(((Tk - 1) * sd.k.t + D) * 2);
+    const uint32_t vbytes = (uint32_t)(((Tk - 1) * sd.v.t + D) * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + b * sd.k.b + kh * sd.k.h, kbytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v + b * sd.v.b + kh * sd.v.h, vbytes);
+    const uint8_t *pad = PAD ? m.pad + b * Tk : nullptr;
+
+    constexpr int CPR = D / 8, NCH = kDqStep * CPR / 256, RSTEP = 256 / CPR;
+    const int crow = tid / CPR, ccol = tid % CPR;
+    uint32_t koff[NCH], voff[NCH];
+#pragma unroll
+    for (int u = 0; u < NCH; u++) {
+        const int r = crow + u * RSTEP;
+        koff[u] = (uint32_t)(r * kstride + ccol * 8) * 2;
+        voff[u] = (uint32_t)(r * vstride + ccol * 8) * 2;
+    }
+    struct KvStage {
+        uint4 k[NCH], v[NCH];
+    };
+    KvStage stg;
+    const int nsteps = kv_lo < kv_hi ? (kv_hi - kv_lo + kDqStep - 1) / kDqStep : 0;
+    auto load = [&](int n) __attribute__((always_inline)) {
+        const int32_t jj = kv_lo + (n < nsteps ? n : 0) * kDqStep;
+        const uint32_t kb = (uint32_t)(jj * kstride) * 2, vb = (uint32_t)(jj * vstride) * 2;
+#pragma unroll
+        for (int u = 0; u < NCH; u++) {
+            stg.k[u] = buf_load16(krs, kb + koff[u]);
+            stg.v[u] = buf_load16(vrs, vb + voff[u]);
+        }
+    };
+    auto store = [&](DqSlot<D> &sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NCH; u++) {
+            const int r = crow + u * RSTEP;
+            sl.k[r * (RS / 8) + ccol] = stg.k[u];
+            sl.kt[r * (TS / 8) + ccol] = stg.k[u];
+            sl.v[r * (RS / 8) + ccol] = stg.v[u];
+        }
+    };
+    auto step = [&](const int n, const DqSlot<D> &sl) __attribute__((always_inline)) {
+        const int32_t jb = kv_lo + n * kDqStep;
+        const uint16_t *ka = (const uint16_t *)sl.k + col * RS + half * 8;
+        const uint16_t *va = (const uint16_t *)sl.v + col * RS + half * 8;
+        f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(ka + st * 16);
+            s = mfma32<DT>(a, qf[st], s);
+        }
+#pragma unroll
+        for (int st = 0; st < KSTEPS; st++) {
+            Frag8 a;
+            a.u = *(const uint4 *)(va + st * 16);
+            dp = mfma32<DT>(a, gf[st], dp);
+        }
+        // element i is key jb + 8 (i / 4) + 4 h + i % 4
+        float ds[16];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * jj + e;
+                const int32_t j = jb + jj * 8 + half * 4 + e;
+                float x = fast_exp2(fmaf(s[i], c2, nlse));
+                bool vis = (uint32_t)(j - lo) < (uint32_t)span;
+                if constexpr (PAD) vis = vis & (pad[j < Tk ? j : Tk - 1] == 0);
+                ds[i] = vis ? x * (dp[i] - dl) : 0.f;
+            }
+        Frag8 df[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            df[u].u = make_uint4(pack2<DT>(ds[8 * u], ds[8 * u + 1]), pack2<DT>(ds[8 * u + 2], ds[8 * u + 3]),
+                                 pack2<DT>(ds[8 * u + 4], ds[8 * u + 5]), pack2<DT>(ds[8 * u + 6], ds[8 * u + 7]));
+        const uint16_t *skt = (const uint16_t *)sl.kt;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int dt = 0; dt < DT32; dt++)
+                acc[dt] = mfma32<DT>(lds_tr_frag(skt, TS, u * 16, dt * 32, lane), df[u], acc[dt]);
+    };
+    load(0);
+    if (nsteps > 0) store(sm.slot[0]);
+    load(1);
+    __syncthreads();
+    for (int n = 0; n < nsteps; n++) {
+        if (n + 1 < nsteps) store(sm.slot[(n + 1) & 1]);
+        load(n + 2);
+        step(n, sm.slot[n & 1]);
+        __syncthreads();
+    }
+    if (qvalid) {
+        uint16_t *op = dq + ((b * Tq + qi) * Hq + h) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT32; dt++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const int d = dt * 32 + g4 * 8 + half * 4;
+                uint2 wv;
+                wv.x = pack2<DT>(acc[dt][g4 * 4 + 0] * scale, acc[dt][g4 * 4 + 1] * scale);
+                wv.y = pack2<DT>(acc[dt][g4 * 4 + 2] * scale, acc[dt][g4 * 4 + 3] * scale);
+                *(uint2 *)(op + d) = wv;
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------
 
@@ -1023,8 +1534,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 // from one (batch row, head) base; 16-byte vector loads need 16-byte rows).
 static bool mfma_bwd_shape_takes(const dm_attention_desc *d) {
     const AttnStrides s = attn_strides(d);
-    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && (d->d == 64 || d->d == 128) &&
-           d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
+    return (d->dtype == DM_BF16 || d->dtype == DM_F16) &&
+           (d->d == 64 || d->d == 128 || d->d == 256) && d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
            rows_fit_32bit(s.k, d->tk, d->d) && rows_fit_32bit(s.v, d->tk, d->d) &&
            rows_fit_32bit(s.q, d->tq, d->d) && rows_fit_32bit(s.g, d->tq, d->d) &&
            d->tq * d->hq < (1ll << 29) && strides_16b(s.q) && strides_16b(s.k) &&
@@ -1087,14 +1598,39 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
                                                               qq, kk, vv, gg, delta, w,            \
                                                               (uint16_t *)dq); }               \
     }
+#define DKDV4(DT, P, MODE, OUT)                                                                \
+    bwd_dkdv_w4<DT, 256, P, MODE><<<(unsigned)nb_kv, 256, 0, st>>>(                            \
+        m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)(OUT))
+#define BWD4(DT)                                                                               \
+    bwd_prep<DT, 256><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, sd, oo, gg, \
+                                                                    lse, delta, w);            \
+    bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
+    bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, w);              \
+    if (m.pad) {                                                                               \
+        { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
+          DKDV4(DT, true, kDkdvDV, dv);                                                        \
+          DKDV4(DT, true, kDkdvDK, dk); }                                                      \
+        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
+        bwd_dq_w4<DT, 256, true><<<(unsigned)nb_q, 256, 0, st>>>(                             \
+            m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)dq); }    \
+    } else {                                                                                   \
+        { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
+          DKDV4(DT, false, kDkdvDV, dv);                                                       \
+          DKDV4(DT, false, kDkdvDK, dk); }                                                     \
+        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
+        bwd_dq_w4<DT, 256, false><<<(unsigned)nb_q, 256, 0, st>>>(                            \
+            m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)dq); }    \
+    }
     if (d->dtype == DM_BF16) {
-        if (d->d == 64) { BWD(DM_BF16, 64); } else { BWD(DM_BF16, 128); }
+        if (d->d == 64) { BWD(DM_BF16, 64); } else if (d->d == 128) { BWD(DM_BF16, 128); } else { BWD4(DM_BF16); }
     } else {
-        if (d->d == 64) { BWD(DM_F16, 64); } else { BWD(DM_F16, 128); }
+        if (d->d == 64) { BWD(DM_F16, 64); } else if (d->d == 128) { BWD(DM_F16, 128); } else { BWD4(DM_F16); }
     }
 #undef BWD
+#undef BWD4
+#undef DKDV4
     if (w.hsplit > 1) {
-        const int64_t n = d->b * d->tk * d->hkv * d->d;  // a multiple of 4 (D is 64 or 128)
+        const int64_t n = d->b * d->tk * d->hkv * d->d;  // a multiple of 4 (D is 64, 128 or 256)
         const unsigned blocks = (unsigned)((n / 4 + 255) / 256);
         if (d->dtype == DM_BF16)
             bwd_kv_reduce<DM_BF16><<<blocks, 256, 0, st>>>(n, w.hsplit, w.kvpart, (uint16_t *)dk,

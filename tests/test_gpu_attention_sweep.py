@@ -163,8 +163,8 @@ D256_CASES = [c for c in CASES if c[0] in (
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", D256_CASES, ids=[c[0] for c in D256_CASES])
 def test_mfma_attention_d256_matches_oracle(case, dtype):
-    """Head width 256 (the reference's published attention shapes): the forward on MFMA (a
-    probe shows it), the backward on the generic kernels; both against the f64 oracle."""
+    """Head width 256 (the reference's published attention shapes): forward and backward on the
+    MFMA kernels (4-wavefront forms; probes show them), against the f64 oracle."""
     print(f"case {case[0]} {dtype} D=256", flush=True)
     seed = 3000 + 17 * CASES.index(case)
     (q, k, v, do), mask, opts, mk = _build(case, dtype, 256, seed)
@@ -175,6 +175,8 @@ def test_mfma_attention_d256_matches_oracle(case, dtype):
     assert pc["attn_fwd_mfma"] > 0 and pc["attn_fwd_generic"] == 0, pc
     dq, dk, dv = dm.attention_backward(q, k, v, o, lse, do, mask, opts)
     torch.cuda.synchronize()
+    pc = _lib.probe_counts()
+    assert pc["attn_bwd_mfma"] > 0 and pc["attn_bwd_generic"] == 0, pc
     call = mk(host(q), host(k), host(v))
     eo, el = oracle.attention_fwd(call, "f64")
     gq, gk, gv = oracle.attention_bwd(call, host(o), host(lse), host(do), "f64")

@@ -36,7 +36,7 @@ def _both(q, k, v, do, mask, opts):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 64, 256])
 def test_fused_projection_slices(dtype, d):
     b, t, hq, hkv = 2, 300, 8, 2
     q, k, v = _fused(b, t, hq, hkv, d, 5, dtype)
