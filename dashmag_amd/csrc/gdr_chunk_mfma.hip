@@ -1,4 +1,7 @@
-// The chunked gated delta rule forward on gfx950 MFMA: bf16/f16 inputs, Dk = Dv = 128, f32 state
+// The chunked gated delta rule forward on gfx950 MFMA: bf16/f16 inputs, Dk and Dv multiples of 8
+// up to 128 (the products are 128 wide: columns past a head width are loaded as zeros, which
+// add nothing to any product or norm, keep the state's extra rows and columns at zero, and are
+// never stored), f32 state
 // and accumulation, the intermediates that only feed products rounded to the inputs' dtype (W, U,
 // T, S, V' and Q K^T o decay, as fla's and the reference's tensor-core kernels round them,
 // crates/dash-ops/src/gated_delta/chunk/cube/tc.rs:1-12).
@@ -24,7 +27,7 @@
 
 namespace dm {
 
-constexpr int kD = 128;         // Dk = Dv of this kernel set
+constexpr int kD = 128;         // the products' Dk = Dv (the heads' widths are at most this)
 constexpr int kC = kChunk;      // 64 tokens
 constexpr int kRowS = kD + 8;   // row stride read by ds_read_b128 rows
 constexpr int kRowB = kD + 4;   // row stride read by ds_read_b64 rows (32 rows per half wave)
@@ -123,9 +126,9 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         for (int u = 0; u < 4; u++) {
             const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
             const int64_t tok = tok0 + (r < len ? r : len - 1);
-            vreg[u] = *(const uint4 *)(vin + v_at(a, tok, h) + c * 8);
-            qraw[u] = *(const uint4 *)(qin + q_at(a, tok, h) + c * 8);
-            kraw[u] = *(const uint4 *)(kin + k_at(a, tok, h) + c * 8);
+            vreg[u] = c * 8 < a.Dv ? *(const uint4 *)(vin + v_at(a, tok, h) + c * 8) : zero4();
+            qraw[u] = c * 8 < a.Dk ? *(const uint4 *)(qin + q_at(a, tok, h) + c * 8) : zero4();
+            kraw[u] = c * 8 < a.Dk ? *(const uint4 *)(kin + k_at(a, tok, h) + c * 8) : zero4();
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -503,12 +506,14 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
     // S_p: tile r holds rows 32 (RT p + r) + crow(i) of column dv
     f32x16_t S[RT];
     {
-        const float *src = h0 ? h0 + sh * kD * kD : nullptr;
+        const float *src = h0 ? h0 + sh * a.Dk * a.Dv : nullptr;
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                S[r][i] = src ? src[((RT * p + r) * 32 + crow(i, lane)) * kD + dv] : 0.f;
+            for (int i = 0; i < 16; i++) {
+                const int row = (RT * p + r) * 32 + crow(i, lane);
+                S[r][i] = src && row < a.Dk && dv < a.Dv ? src[row * a.Dv + dv] : 0.f;
+            }
     }
     auto load = [&](int c, HalfOps &x) __attribute__((always_inline)) {
         c = c < c1 ? c : c1 - 1;
@@ -621,11 +626,14 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
         load(c + 3, ob);
     }
     if (final_state) {
-        float *dst = final_state + sh * kD * kD;
+        float *dst = final_state + sh * a.Dk * a.Dv;
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) dst[((RT * p + r) * 32 + crow(i, lane)) * kD + dv] = S[r][i];
+            for (int i = 0; i < 16; i++) {
+                const int row = (RT * p + r) * 32 + crow(i, lane);
+                if (row < a.Dk && dv < a.Dv) dst[row * a.Dv + dv] = S[r][i];
+            }
     }
 }
 
@@ -666,8 +674,9 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
         if (a.l2norm)
             qv = *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8);
         else
-            qv = r < len ? *(const uint4 *)((const uint16_t *)a.q + q_at(a, tok0 + r, h) + c * 8)
-                         : make_uint4(0, 0, 0, 0);
+            qv = r < len && c * 8 < a.Dk
+                     ? *(const uint4 *)((const uint16_t *)a.q + q_at(a, tok0 + r, h) + c * 8)
+                     : zero4();
         uint2 *qp = (uint2 *)(qs + r * kRowB + c * 8);
         qp[0] = make_uint2(qv.x, qv.y);
         qp[1] = make_uint2(qv.z, qv.w);
@@ -728,9 +737,9 @@ __global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int x = tid + 256 * u, r = x / 16, c = x % 16;
-        if (r < len) {
+        if (r < len && c * 8 < a.Dv) {
             const uint2 *src = (const uint2 *)(orow + r * kRowB + c * 8);
-            *(uint4 *)((uint16_t *)out + ((tok0 + r) * a.H + h) * kD + c * 8) =
+            *(uint4 *)((uint16_t *)out + ((tok0 + r) * a.H + h) * a.Dv + c * 8) =
                 make_uint4(src[0].x, src[0].y, src[1].x, src[1].y);
         }
     }
@@ -801,9 +810,10 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
     for (int u = 0; u < 4; u++) {
         const int x = tid + 256 * u, r = x / 16, c = x % 16;
         const int64_t tok = tok0 + (r < len ? r : len - 1);
-        dv[u] = *(const uint4 *)(dob + o_at(a, tok, h) + c * 8);
-        qv[u] = a.l2norm ? *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8)
-                         : *(const uint4 *)(qin + q_at(a, tok, h) + c * 8);
+        dv[u] = c * 8 < a.Dv ? *(const uint4 *)(dob + o_at(a, tok, h) + c * 8) : zero4();
+        qv[u] = a.l2norm      ? *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8)
+                : c * 8 < a.Dk ? *(const uint4 *)(qin + q_at(a, tok, h) + c * 8)
+                               : zero4();
     }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -889,7 +899,11 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
     for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int i = 0; i < 16; i++)
-            D[r][i] = d_final ? d_final[sh * kD * kD + (p * 64 + r * 32 + crow(i, lane)) * kD + dv] : 0.f;
+            {
+                const int row = p * 64 + r * 32 + crow(i, lane);
+                D[r][i] = d_final && row < a.Dk && dv < a.Dv
+                              ? d_final[sh * a.Dk * a.Dv + row * a.Dv + dv] : 0.f;
+            }
     // a chunk before the sequence's first loads the first again (every call the same loads)
     auto load = [&](int c, BwdHalfOps &x) __attribute__((always_inline)) {
         c = c >= c0 ? c : c0;
@@ -988,8 +1002,10 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
 #pragma unroll
         for (int r = 0; r < 2; r++)
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                dh0[sh * kD * kD + (p * 64 + r * 32 + crow(i, lane)) * kD + dv] = D[r][i];
+            for (int i = 0; i < 16; i++) {
+                const int row = p * 64 + r * 32 + crow(i, lane);
+                if (row < a.Dk && dv < a.Dv) dh0[sh * a.Dk * a.Dv + row * a.Dv + dv] = D[r][i];
+            }
     }
 }
 
@@ -1056,7 +1072,9 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int x = tid + 512 * u, r = x / 16, c = x % 16;
-            s4[u] = *(const uint4 *)(dob + o_at(a, tok0 + (r < len ? r : len - 1), h) + c * 8);
+            s4[u] = c * 8 < a.Dv
+                        ? *(const uint4 *)(dob + o_at(a, tok0 + (r < len ? r : len - 1), h) + c * 8)
+                        : zero4();
         }
         s5 = *(const uint4 *)(w.Aqk + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
         // per-token values (after the rows' loads: these reads wait on the memory counter)
@@ -1167,9 +1185,9 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         for (int u = 0; u < 2; u++) {
             const int x = tid + 512 * u, r = x / 16, c = x % 16;
             const int64_t tok = tok0 + (r < len ? r : len - 1);
-            q2[u] = *(const uint4 *)(qin + q_at(a, tok, h) + c * 8);
-            k2[u] = *(const uint4 *)(kin + k_at(a, tok, h) + c * 8);
-            v2[u] = *(const uint4 *)(vin + v_at(a, tok, h) + c * 8);
+            q2[u] = c * 8 < a.Dk ? *(const uint4 *)(qin + q_at(a, tok, h) + c * 8) : zero4();
+            k2[u] = c * 8 < a.Dk ? *(const uint4 *)(kin + k_at(a, tok, h) + c * 8) : zero4();
+            v2[u] = c * 8 < a.Dv ? *(const uint4 *)(vin + v_at(a, tok, h) + c * 8) : zero4();
         }
         t2 = *(const uint4 *)(w.Tm + ch * kC * kC + (tid / 8) * kC + (tid % 8) * 8);
     }
@@ -1530,10 +1548,13 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     for (int u = 0; u < 2; u++) {
         const int x = tid + 512 * u, r = x / 16, c = x % 16;
         if (r < len) {
-            const int64_t o = ((tok0 + r) * a.H + h) * kD + c * 8;
-            *(uint4 *)((uint16_t *)dq + o) = *(const uint4 *)(oq + r * kR + c * 8);
-            *(uint4 *)((uint16_t *)dk + o) = *(const uint4 *)(ok_ + r * kR + c * 8);
-            *(uint4 *)((uint16_t *)dv + o) = *(const uint4 *)(ov + r * kR + c * 8);
+            const int64_t ok = ((tok0 + r) * a.H + h) * a.Dk + c * 8;
+            const int64_t ov_ = ((tok0 + r) * a.H + h) * a.Dv + c * 8;
+            if (c * 8 < a.Dk) {
+                *(uint4 *)((uint16_t *)dq + ok) = *(const uint4 *)(oq + r * kR + c * 8);
+                *(uint4 *)((uint16_t *)dk + ok) = *(const uint4 *)(ok_ + r * kR + c * 8);
+            }
+            if (c * 8 < a.Dv) *(uint4 *)((uint16_t *)dv + ov_) = *(const uint4 *)(ov + r * kR + c * 8);
         }
     }
 }
@@ -1544,7 +1565,11 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 
 bool gdr_mfma_takes(const dm_gdr_desc *d) {
     // (the state pass addresses the keys through a 32-bit buffer range; 16-byte row loads)
-    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk == kD && d->dv == kD &&
+    // head widths below 128 run the same products with the columns past the width held at
+    // zero (loaded as zeros, never stored): a zero key or query column adds nothing to any
+    // product or norm, and the state's rows and columns past the widths stay zero
+    return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk % 8 == 0 && d->dv % 8 == 0 &&
+           d->dk >= 8 && d->dv >= 8 && d->dk <= kD && d->dv <= kD &&
            d->b * d->t * d->h * kD * 2 < (1ll << 32) && gdr_strides_16b(d);
 }
 

@@ -57,7 +57,8 @@ int launch_plan(const dm_gdr_desc *d, int32_t *seq_chunk0, int32_t *chunk_seq,
 int64_t gdr_nseq(const dm_gdr_desc *d);
 int64_t gdr_chunk_bound(const dm_gdr_desc *d);
 
-// MFMA forward (gdr_chunk_mfma.hip): bf16/f16, Dk = Dv = 128.
+// MFMA forward and backward (gdr_chunk_mfma.hip): bf16/f16, Dk and Dv multiples of 8 up to 128
+// (the products are 128 wide; columns past a width are held at zero).
 bool gdr_mfma_takes(const dm_gdr_desc *d);
 size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d);
 int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,

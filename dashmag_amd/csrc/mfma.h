@@ -186,6 +186,8 @@ __device__ __forceinline__ float round_to(float x) {
     return unpack_lo<DT>(pack2<DT>(x, 0.f));
 }
 
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
+
 __device__ __forceinline__ f32x16_t zero16() {
     f32x16_t z;
 #pragma unroll
