@@ -50,11 +50,13 @@ class Timed:
     """Times a C-ABI call on the current stream: `steps` back-to-back calls between two HIP
     events, after `warmup` untimed ones. Over the same timed region the library's kernel timers
     (HIP event pairs around each launch, on the launch stream) give each kernel's average launch
-    duration, in ``kernel_ms`` {name: (ms per launch, launches)}."""
+    duration, in ``kernel_ms`` {name: (ms per launch, launches)}. A second run of as many calls
+    with the kernel timers off gives ``ms_plain``, the timers' cost check."""
 
     def __init__(self, torch, fn):
         self.torch, self.fn = torch, fn
         self.kernel_ms = {}
+        self.ms_plain = None
 
     def run(self, steps, warmup):
         from dashmag_amd import _lib
@@ -72,7 +74,14 @@ class Timed:
         torch.cuda.synchronize()
         self.kernel_ms = {k: (ms / n, n) for k, (ms, n) in _lib.kernel_times().items() if n}
         _lib.kernel_timing(False)
-        return start.elapsed_time(end) / steps  # ms per call
+        ms = start.elapsed_time(end) / steps  # ms per call
+        start.record()
+        for _ in range(steps):
+            self.fn()
+        end.record()
+        torch.cuda.synchronize()
+        self.ms_plain = start.elapsed_time(end) / steps
+        return ms
 
 
 def measured_traffic(kernel):
@@ -126,6 +135,7 @@ def bench_attention(torch, dm, ops, lib, data, steps, warmup, cu=None):
     ms_bwd = Timed(torch, bwd).run(steps, warmup)
     t = Timed(torch, step)
     ms_step = t.run(steps, warmup)
+    bench_attention.ms_plain = t.ms_plain
     return ms_step, ms_fwd, ms_bwd, _lib.probe_counts(), t.kernel_ms
 
 
@@ -166,6 +176,8 @@ def main():
         ms, mf, mb, probes, kms = bench_attention(torch, dm, ops, lib, c2, args.steps, args.warmup,
                                              c2["cu_seqlens"])
         head = dict(ms=ms, ms_fwd=mf, ms_bwd=mb, probes=probes, kernel_ms=kms)
+        secondary["attention_config2_ms_per_step_kernel_timers_off"] = round(
+            bench_attention.ms_plain, 4)
         secondary["attention_config2_kernel_us"] = {k: round(v[0] * 1e3, 2)
                                                     for k, v in kms.items()}
         print("attention config 2 kernels: " + ", ".join(
