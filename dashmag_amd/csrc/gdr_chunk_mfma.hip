@@ -89,22 +89,26 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd 
 // Prep
 // ------------------------------------------------------------------------------------------
 
-// 77 KB: two workgroups per CU. The query tile's space later holds T (f32), and the key tile's
-// beta V (for U's product, staged while T is computed); the key tile's space then stages the W
-// rows for the fragment stores.
+// 52 KB: three workgroups per CU. The query tile's space later holds T (f32); the key tile's
+// space keeps the keys until W = (T diag(beta gamma)) K, then holds beta V for U = T (beta V),
+// then stages the W rows for the fragment stores. A is kept as its ten lower 16 x 16 blocks.
 struct PrepSmem {
     uint4 k[kC * kRowS / 8];  // keys, rows; later beta V rows; later W rows
-    uint4 q[kC * kRowS / 8];  // queries, rows; later T (f32); later U rows
-    uint4 x[kC * kTrS / 8];   // beta gamma K: rows read transposed
-    float a[kC][kC + 4];      // A (strictly lower), f32, 16-byte aligned rows
+    uint4 q[kC * kRowS / 8];  // queries, rows; later T (f32)
+    float a[10][16][20];      // A's blocks (bi, bj), bi >= bj, at bi (bi + 1) / 2 + bj; f32
     float mm[3][16][20];      // T's off-diagonal block products
     float g[kC], gam[kC], bet[kC], lam[kC];
 };
 static_assert(sizeof(float) * kC * (kC + 4) <= sizeof(uint4) * kC * kRowS / 8, "T in q");
-static_assert(sizeof(PrepSmem) <= 80 * 1024, "two workgroups per compute unit");
+static_assert(sizeof(PrepSmem) <= 160 * 1024 / 3, "three workgroups per compute unit");
+// element (r, c) of A, in a lower block (r / 16 >= c / 16)
+__device__ __forceinline__ float &a_at(PrepSmem &sm, int r, int c) {
+    const int bi = r >> 4, bj = c >> 4;
+    return sm.a[bi * (bi + 1) / 2 + bj][r & 15][c & 15];
+}
 
 template <int DT>
-__global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
+__global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     __shared__ PrepSmem sm;
     const int64_t ch = blockIdx.x, n = ch / a.H, h = ch % a.H;
     const int len = w.chunk_len[n];
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     const int64_t tok0 = w.chunk_tok0[n];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
-    uint16_t *ks = (uint16_t *)sm.k, *qs = (uint16_t *)sm.q, *xs = (uint16_t *)sm.x;
+    uint16_t *ks = (uint16_t *)sm.k, *qs = (uint16_t *)sm.q;
     float(*tt)[kC + 4] = (float(*)[kC + 4])sm.q;  // T, in the query tile's space
     float(*mm)[16][20] = sm.mm;
 
@@ -194,18 +198,6 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         w.G[ch * kC + lane] = x;
     }
     __syncthreads();
-    // beta gamma K rows for the transposed reads of W's product
-    for (int xx = tid; xx < kC * 16; xx += 256) {
-        const int r = xx / 16, c = xx % 16;
-        const uint4 kv = sm.k[r * (kRowS / 8) + c];
-        const float fk = sm.bet[r] * sm.gam[r];
-        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-        uint32_t ko[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            ko[e] = pack2<DT>(unpack_lo<DT>(kw[e]) * fk, unpack_hi<DT>(kw[e]) * fk);
-        sm.x[r * (kTrS / 8) + c] = make_uint4(ko[0], ko[1], ko[2], ko[3]);
-    }
     // (lam K)^T as the state pass's A fragments: fragment (dk tile r, token step st), lane l
     // holds dk = 32 r + l % 32 at tokens 16 st + 8 j + 4 (l / 32) + e in slot 4 j + e (the k
     // order of the V' fragments it meets): transposed reads of the key rows, then lam per token
@@ -271,31 +263,17 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
             // masked before the exponential (above the diagonal G_i - G_j > 0)
             const float dec = r >= j ? __expf(sm.g[r] - sm.g[j]) : 0.f;
-            sm.a[r][j] = r > j ? sm.bet[r] * kk[i] * dec : 0.f;
+            if ((r >> 4) >= (j >> 4)) a_at(sm, r, j) = r > j ? sm.bet[r] * kk[i] * dec : 0.f;
             const uint32_t p2 = pack2<DT>(r >= j ? qk[i] * dec * a.scale : 0.f, 0.f);
             aq_out[r * kC + j] = (uint16_t)(p2 & 0xffffu);
         }
     } else {
         for (int xx = lane; xx < 32 * 32; xx += 64) {
             const int r = xx / 32, j = 32 + xx % 32;
-            sm.a[r][j] = 0.f;
             aq_out[r * kC + j] = 0;
         }
     }
-    __syncthreads();  // the query and key tiles are dead from here
-    // beta V rows for U's product, in the key tile's space
-    uint16_t *vs = ks;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
-        const float fv = sm.bet[r];
-        const uint32_t vw[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
-        uint32_t vo[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            vo[e] = pack2<DT>(unpack_lo<DT>(vw[e]) * fv, unpack_hi<DT>(vw[e]) * fv);
-        *(uint4 *)(vs + r * kRowS + c * 8) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
-    }
+    __syncthreads();  // the query tile is dead from here; the key tile lives until W
 
     // T = (I + A)^-1 by 16 x 16 blocks. Diagonal block b (wave b), row by row, lane c holding
     // column c in registers: T[i][c] = [i == c] - sum_{x < i} A[i][x] T[x][c] (rows of A read
@@ -308,7 +286,7 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             float s = 0.f;
 #pragma unroll
             for (int x4 = 0; x4 < i; x4 += 4) {
-                const float4 a4 = *(const float4 *)&sm.a[16 * b + i][16 * b + x4];
+                const float4 a4 = *(const float4 *)&a_at(sm, 16 * b + i, 16 * b + x4);
                 const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                 for (int e = 0; e < 4; e++)
@@ -347,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
                     for (int e = 0; e < 4; e++)
 #pragma unroll
                         for (int y4 = 0; y4 < 16; y4 += 4) {
-                            const float4 a4 = *(const float4 *)&sm.a[16 * bi + r0 + e][16 * kb_ + y4];
+                            const float4 a4 = *(const float4 *)&a_at(sm, 16 * bi + r0 + e, 16 * kb_ + y4);
                             acc[e] += a4.x * tcol[y4] + a4.y * tcol[y4 + 1] + a4.z * tcol[y4 + 2] +
                                       a4.w * tcol[y4 + 3];
                         }
@@ -379,23 +357,55 @@ __global__ __launch_bounds__(256, 2) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         level(std::integral_constant<int, 3>{});
     }
 
-    // W = T (beta gamma K) and U = T (beta V) in one pass: 8 output tiles each (2 token rows x 4
-    // columns of 32), wave w taking column tile w. A = T rows (f32 -> dtype) with k slots
-    // 16 st + 8 j + 4 h + e, B = the scaled rows read transposed (k = token, col = column).
+    // W = (T diag(beta gamma)) K, then U = T (beta V): 8 output tiles each (2 token rows x 4
+    // columns of 32), wave w taking column tile w. A = T rows (f32 -> dtype; for W each column
+    // scaled by its token's beta gamma) with k slots 16 st + 8 j + 4 h + e, B = the key rows,
+    // then the beta V rows, read transposed (k = token, col = column).
     f32x16_t wt[2], ut[2];
+    auto tfrag = [&](int ti, int st, bool bg) __attribute__((always_inline)) {
+        const int c0 = st * 16 + half * 4;
+        const float *tr = &tt[ti * 32 + col][c0];
+        float f[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+        if (bg) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                f[e] = sm.bet[c0 + e] * sm.gam[c0 + e];
+                f[4 + e] = sm.bet[c0 + 8 + e] * sm.gam[c0 + 8 + e];
+            }
+        }
+        Frag8 at;
+        at.u = make_uint4(pack2<DT>(tr[0] * f[0], tr[1] * f[1]), pack2<DT>(tr[2] * f[2], tr[3] * f[3]),
+                          pack2<DT>(tr[8] * f[4], tr[9] * f[5]), pack2<DT>(tr[10] * f[6], tr[11] * f[7]));
+        return at;
+    };
 #pragma unroll
     for (int ti = 0; ti < 2; ti++) {
         wt[ti] = zero16();
+#pragma unroll
+        for (int st = 0; st < kC / 16; st++)
+            wt[ti] = mfma32<DT>(tfrag(ti, st, true), lds_tr_frag(ks, kRowS, st * 16, wave * 32, lane), wt[ti]);
+    }
+    __syncthreads();  // the key tile is dead from here
+    // beta V rows for U's product, in the key tile's space
+    uint16_t *vs = ks;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int xx = tid + 256 * u, r = xx / 16, c = xx % 16;
+        const float fv = sm.bet[r];
+        const uint32_t vw[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+        uint32_t vo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            vo[e] = pack2<DT>(unpack_lo<DT>(vw[e]) * fv, unpack_hi<DT>(vw[e]) * fv);
+        *(uint4 *)(vs + r * kRowS + c * 8) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ti = 0; ti < 2; ti++) {
         ut[ti] = zero16();
 #pragma unroll
-        for (int st = 0; st < kC / 16; st++) {
-            Frag8 at;
-            const float *tr = &tt[ti * 32 + col][st * 16 + half * 4];
-            at.u = make_uint4(pack2<DT>(tr[0], tr[1]), pack2<DT>(tr[2], tr[3]),
-                              pack2<DT>(tr[8], tr[9]), pack2<DT>(tr[10], tr[11]));
-            wt[ti] = mfma32<DT>(at, lds_tr_frag(xs, kTrS, st * 16, wave * 32, lane), wt[ti]);
-            ut[ti] = mfma32<DT>(at, lds_tr_frag(vs, kRowS, st * 16, wave * 32, lane), ut[ti]);
-        }
+        for (int st = 0; st < kC / 16; st++)
+            ut[ti] = mfma32<DT>(tfrag(ti, st, false), lds_tr_frag(vs, kRowS, st * 16, wave * 32, lane), ut[ti]);
     }
     __syncthreads();
     // for the backward: T, row-major in the dtype
