@@ -305,6 +305,30 @@ def main():
               f"{nbytes / ms_g / 1e6:.0f} GB/s", file=sys.stderr, flush=True)
         del c, k, v, kpg, vpg
 
+        # the reference's attention head shape (Hq = 8, Hkv = 2, D = 256) over config 3's cache
+        # lengths
+        c = syn.config3(dev, hq=8, hkv=2, d=256)
+        q, k, v, lens = c["q"], c["k"], c["v"], c["lengths"]
+        desc = ops._attention_desc("attention_decode", q.unsqueeze(1), k, v,
+                                   dm.AttentionMask.none(), dm.AttentionOptions(), keep)
+        o = torch.empty_like(q)
+        nb = lib.dm_attention_decode_workspace(ctypes.byref(desc))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        ptrs = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, lens, o, ws)]
+        fn = lambda: check(lib.dm_attention_decode(ctypes.byref(desc), *ptrs[:5], ptrs[5], nb,  # noqa
+                                                   st), lib)
+        tm = Timed(torch, fn)
+        ms = tm.run(max(args.steps, 50), args.warmup)
+        nbytes = 4 * 2 * 256 * int(lens.sum()) + 4 * 64 * 8 * 256 + 4 * 64
+        secondary["decode_d256"] = dict(
+            unit="GB/s", value=nbytes / ms / 1e6, us_per_call=ms * 1e3, bytes=nbytes,
+            frac_of_hbm_peak=nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            kernel_us={k_: round(v_[0] * 1e3, 2) for k_, v_ in tm.kernel_ms.items()},
+            shape="config 3's lengths, B=64, S=8192, Hq=8, Hkv=2, D=256, bf16")
+        print(f"decode D=256 (Hq=8, Hkv=2): {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s",
+              file=sys.stderr, flush=True)
+        del c, q, k, v, o, ws
+
     # ---- gated delta rule chunked, config 4 ----
     if want("gdr"):
         c = syn.config4(dev)

@@ -4,10 +4,10 @@
 // all the query heads of a key-value head's group (the GQA reuse), and writes a normalised
 // partial output and its log-sum-exp in f32. Pass 2 merges the spans by their log-sum-exp.
 //
-// Bandwidth-bound. D = 128 runs its products on MFMA (decode_split_mfma); D = 64 and 256 on the
-// vector units (decode_split): each K/V row (D * 2 bytes) is read by D / 8 lanes with 16-byte
-// loads, one wavefront covering 64 * 8 / D rows per load, the dot products reduced across the
-// row's lanes with xor shuffles; f32 online softmax per lane group.
+// Bandwidth-bound. The split pass runs its products on MFMA (decode_split_mfma) at D = 64, 128
+// and 256 for bf16/f16: a GQA group's query heads read the same key rows, so the scores of a block
+// of keys are one small product, cheaper on the matrix units than as per-head dot products on the
+// vector units. f32 and other shapes take decode_generic.
 #include <mutex>
 #include <string>
 
@@ -17,14 +17,8 @@
 
 namespace dm {
 
-constexpr int kDecodeRows = 4;        // K/V rows each lane group loads per step
-constexpr int kDecodeMinSpan = 512;    // fewest keys a workgroup takes
-constexpr int kDecodeWorkgroups = 1024;  // the split count aims at about this many workgroups
-constexpr int kDecodeWorkgroupsMfma = 4096;  // the same for the MFMA kernel (shorter per key)
-
-struct Bf16x8 {
-    uint4 raw;
-};
+constexpr int kDecodeMinSpan = 512;          // fewest keys a workgroup takes
+constexpr int kDecodeWorkgroupsMfma = 4096;  // the split count aims at about this many workgroups
 
 // Where the cache keeps sequence b's keys. Dense: rows b * S .. b * S + S - 1 of k, v
 // [B, S, Hkv, D]. Packed: rows offsets[b] .. offsets[b + 1] - 1 of k, v [N, Hkv, D]
@@ -74,224 +68,9 @@ __device__ __forceinline__ int64_t kv_page(const KvMap &m, int64_t b, int64_t j)
     return pg >= 0 && pg < m.num_pages ? pg : -1;
 }
 
-template <int DT>
-__device__ __forceinline__ void unpack8(const uint4 &r, float *x) {
-    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        if (DT == DM_BF16) {
-            x[2 * e] = __uint_as_float(w[e] << 16);
-            x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-        } else {
-            union {
-                uint32_t u;
-                _Float16 h[2];
-            } c;
-            c.u = w[e];
-            x[2 * e] = (float)c.h[0];
-            x[2 * e + 1] = (float)c.h[1];
-        }
-    }
-}
-
-typedef __bf16 dec_bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 dec_f16x2 __attribute__((ext_vector_type(2)));
-
-// The dot product of 8 16-bit pairs in f32: v_dot2_f32_bf16 / v_dot2_f32_f16.
-template <int DT>
-__device__ __forceinline__ float dot8(const uint4 &a, const uint4 &b) {
-    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-    float t = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        if constexpr (DT == DM_BF16) {
-            dec_bf16x2 x, y;
-            __builtin_memcpy(&x, &aw[e], 4);
-            __builtin_memcpy(&y, &bw[e], 4);
-            t = __builtin_amdgcn_fdot2_f32_bf16(x, y, t, false);
-        } else {
-            dec_f16x2 x, y;
-            __builtin_memcpy(&x, &aw[e], 4);
-            __builtin_memcpy(&y, &bw[e], 4);
-            t = __builtin_amdgcn_fdot2(x, y, t, false);
-        }
-    }
-    return t;
-}
-
-// One split of one (sequence, key-value head): keys [base + split * span, ...) of the keys the
-// sequence's query sees, [lo, hi). Writes part_o [B, Hq, nsplit, D] (normalised) and part_lse
-// [B, Hq, nsplit] (-inf for a split that sees nothing).
-template <int DT, int D, int G>
-__global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64_t Hkv,
-                                                    int64_t left, float scale, int nsplit, int span,
-                                                    const void *__restrict__ q,
-                                                    const void *__restrict__ k,
-                                                    const void *__restrict__ v,
-                                                    const int32_t *__restrict__ lengths, KvMap map,
-                                                    float *__restrict__ part_o,
-                                                    float *__restrict__ part_lse) {
-    constexpr int LPR = D / 8;       // lanes per K/V row
-    constexpr int RPW = 64 / LPR;    // rows per wavefront per step
-    constexpr int NW = 4;            // wavefronts
-    const int split = blockIdx.x, kh = blockIdx.y;
-    const int64_t b = blockIdx.z;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = lane / LPR, seg = lane % LPR;
-
-    int64_t row0, len;
-    kv_extent(map, b, S, lengths, row0, len);
-    int64_t lo = left >= 0 ? len - 1 - left : 0;
-    if (lo < 0) lo = 0;
-    const int64_t start = lo + (int64_t)split * span;
-    int64_t end = start + span;
-    if (end > len) end = len;
-
-    // queries of the group, this lane's 8 elements as 4 packed pairs (the dot products run on
-    // v_dot2_f32_{bf16,f16} with f32 accumulation); scale * log2(e) applied to the f32 sum
-    const float qscale = scale * 1.4426950408889634f;
-    uint4 qp[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        const int64_t h = kh * G + g;
-        qp[g] = *(const uint4 *)((const uint16_t *)q + b * map.qb + h * map.qh + seg * 8);
-    }
-
-    float mx[G], l[G], acc[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        mx[g] = -INFINITY;
-        l[g] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-    }
-
-    const int64_t row_stride = map.kt * 2;  // bytes between consecutive keys (and values)
-    const char *kb = (const char *)k + (kv_base_k(map, b, row0) + kh * map.kh) * 2 + seg * 16;
-    const char *vb = (const char *)v + (kv_base_v(map, b, row0) + kh * map.vh) * 2 + seg * 16;
-
-    // each wavefront sweeps a contiguous quarter of the split, kDecodeRows rows per lane group
-    // per step; the next step's rows are loaded before this step's are used
-    constexpr int ROWS = kDecodeRows;
-    const int64_t per_wave = span / NW;
-    const int64_t w0 = start + wave * per_wave;
-    const int64_t w1 = min(w0 + per_wave, end);
-    uint4 kr[ROWS], vr[ROWS], kn[ROWS], vn[ROWS];
-    // rows past the wavefront's range load row w1 - 1 again (a visible row, so the loads need no
-    // branch and the compiler can keep the next step's loads in flight); their scores are -inf.
-    // Buffer loads from the wavefront's first row keep the two register sets' loads apart (plain
-    // loads of both sets get merged into one load at the loop head, which waits at once).
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb - seg * 16 + w0 * row_stride, 0xffffffffu);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb - seg * 16 + w0 * row_stride, 0xffffffffu);
-    auto load = [&](int64_t j0, uint4 *kk, uint4 *vv) {
-#pragma unroll
-        for (int u = 0; u < ROWS; u++) {
-            const uint32_t off =
-                (uint32_t)((min(j0 + u * RPW + r, w1 - 1) - w0) * row_stride) + seg * 16;
-            kk[u] = buf_load16_nt(krs, off);
-            vv[u] = buf_load16_nt(vrs, off);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // issue the loads here, ahead of the math
-    };
-    auto consume = [&](int64_t j0, const uint4 *kk, const uint4 *vv) {
-        float s[ROWS][G];
-#pragma unroll
-        for (int u = 0; u < ROWS; u++) {
-            const bool ok = j0 + u * RPW + r < w1;
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float t = group_sum<LPR>(dot8<DT>(qp[g], kk[u]));
-                s[u][g] = ok ? t * qscale : -INFINITY;
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float mn = mx[g];
-#pragma unroll
-            for (int u = 0; u < ROWS; u++) mn = fmaxf(mn, s[u][g]);
-            // with nothing visible yet (mn = -inf) every factor below is exp2(-inf) = 0
-            const float ref = mn == -INFINITY ? 0.f : mn;
-            const float alpha = __builtin_amdgcn_exp2f(mx[g] - ref);
-            l[g] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] *= alpha;
-#pragma unroll
-            for (int u = 0; u < ROWS; u++) {
-                float vf[8];
-                unpack8<DT>(vv[u], vf);
-                const float p = __builtin_amdgcn_exp2f(s[u][g] - ref);
-                l[g] += p;
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] += p * vf[e];
-            }
-            mx[g] = mn;
-        }
-    };
-    // two register sets in turn, so no copies wait on loads still in flight
-    constexpr int STEP = RPW * ROWS;
-    if (w0 < w1) load(w0, kr, vr);
-    for (int64_t j0 = w0; j0 < w1; j0 += 2 * STEP) {
-        load(j0 + STEP, kn, vn);
-        consume(j0, kr, vr);
-        if (j0 + STEP >= w1) break;
-        load(j0 + 2 * STEP, kr, vr);
-        consume(j0 + STEP, kn, vn);
-    }
-
-    // Combine the RPW lane groups of each wavefront by shuffles, then the NW wavefronts through
-    // LDS: [NW][G] (m, l), [NW][G][D] acc.
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-#pragma unroll
-        for (int o = LPR; o < 64; o <<= 1) {
-            const float mo = __shfl_xor(mx[g], o, 64);
-            const float M = fmaxf(mx[g], mo);
-            const float wa = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx[g] - M);
-            const float wb = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - M);
-            l[g] = l[g] * wa + __shfl_xor(l[g], o, 64) * wb;
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] * wa + __shfl_xor(acc[g][e], o, 64) * wb;
-            mx[g] = M;
-        }
-    }
-    __shared__ float sm_m[NW][G], sm_l[NW][G];
-    __shared__ float sm_acc[NW][G][D];
-    if (r == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            if (seg == 0) {
-                sm_m[wave][g] = mx[g];
-                sm_l[wave][g] = l[g];
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) sm_acc[wave][g][seg * 8 + e] = acc[g][e];
-        }
-    }
-    __syncthreads();
-    for (int x = threadIdx.x; x < G * D; x += 256) {
-        const int g = x / D, d = x % D;
-        float M = -INFINITY;
-        for (int t = 0; t < NW; t++) M = fmaxf(M, sm_m[t][g]);
-        float L = 0.f, A = 0.f;
-        if (M != -INFINITY) {
-            for (int t = 0; t < NW; t++) {
-                const float w = __builtin_amdgcn_exp2f(sm_m[t][g] - M);
-                L += sm_l[t][g] * w;
-                A += sm_acc[t][g][d] * w;
-            }
-        }
-        const int64_t h = kh * G + g;
-        const int64_t pr = (b * Hq + h) * nsplit + split;
-        part_o[pr * D + d] = L > 0.f ? A / L : 0.f;
-        // natural-log lse of the split from the base-2 running maximum
-        if (d == 0) part_lse[pr] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
-    }
-}
-
-// The split pass for D = 128 on MFMA. Each wavefront sweeps its quarter of the split in blocks
-// of 32 keys: the block's K and V rows arrive by coalesced 16-byte loads (4 rows per load), go to
-// the wavefront's own LDS tiles, and the next block's loads are in flight while this block is
+// The split pass on MFMA (D = 64, 128 or 256). Each wavefront sweeps its quarter of the split in
+// blocks of 32 keys: the block's K and V rows arrive by coalesced 16-byte loads (64 / (D / 8) rows
+// per load), go to the wavefront's own LDS tiles, and the next block's loads are in flight while this block is
 // used. Per block, S^T = K q^T (32 keys x the group's heads, padded to 32 columns) and
 // O^T += V^T P^T (4 tiles of 32 columns x the heads) run as 32x32x16 products: the scores'
 // output layout (lane = head, rows = keys) is the B operand of the second product as it stands,
@@ -302,14 +81,18 @@ __global__ __launch_bounds__(256) void decode_split(int64_t S, int64_t Hq, int64
 // table gives the page, and the half's buffer resource starts at the half's first visible key
 // and spans only its visible keys: keys before the wavefront's range (negative offsets wrap past
 // the end), past it, or on a page index out of range read as zeros, and their scores are -inf.
-template <int DT, int G, bool PAGED>
-__global__ __launch_bounds__(256, 2) void decode_split_mfma(
+// At D = 256 a wavefront's staged block (64 registers per tensor), the queries' fragments and
+// O^T need one wavefront per SIMD.
+template <int DT, int G, bool PAGED, int D>
+__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_mfma(
     int64_t S, int64_t Hq, int64_t Hkv, int64_t left, float scale, int nsplit, int span,
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     const int32_t *__restrict__ lengths, KvMap map, float *__restrict__ part_o,
     float *__restrict__ part_lse) {
-    constexpr int D = 128, NW = 4, BK = 32;
+    constexpr int NW = 4, BK = 32;
     constexpr int KS = D + 8, VS = D + 32;  // row strides (elements) of the row and transposed reads
+    constexpr int LPR = D / 8, RPL = 64 / LPR, NLD = BK / RPL;  // lanes per row, rows per load, loads
+    constexpr int KST = D / 16, DTN = D / 32;  // k-steps of the scores, 32-column tiles of O^T
     struct Tiles {
         uint16_t k[BK * KS];
         uint16_t v[BK * VS];
@@ -332,9 +115,9 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
 
     // the queries as B operands: column = head col (zero past the group), k slots
     // d = 16 st + 4 h + e and 16 st + 8 + 4 h + e (the order of the key rows' A fragments)
-    Frag8 qf[8];
+    Frag8 qf[KST];
 #pragma unroll
-    for (int st = 0; st < 8; st++) {
+    for (int st = 0; st < KST; st++) {
         if (col < G) {
             const uint16_t *qp = (const uint16_t *)q + b * map.qb + (kh * G + col) * map.qh +
                                  st * 16 + half * 4;
@@ -359,7 +142,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     // one register set: a block's loads are issued as soon as the previous block is staged, and
     // are in flight while that block's products run
     struct Stage {
-        uint4 k[8], v[8];
+        uint4 k[NLD], v[NLD];
     };
     Stage sts;
     // block rows past the wavefront's range load row w1 - 1 again (their scores are -inf)
@@ -377,18 +160,18 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
                 const __amdgpu_buffer_rsrc_t kh_rs = make_rsrc(kb + kofs, bytes);
                 const __amdgpu_buffer_rsrc_t vh_rs = make_rsrc(vb + vofs, bytes);
 #pragma unroll
-                for (int u = 4 * h; u < 4 * h + 4; u++) {
-                    const int64_t key = j0 + 4 * u + (lane >> 4);
-                    const uint32_t off = (uint32_t)(int32_t)((key - first) * row_stride) + (lane & 15) * 16;
+                for (int u = h * NLD / 2; u < (h + 1) * NLD / 2; u++) {
+                    const int64_t key = j0 + RPL * u + lane / LPR;
+                    const uint32_t off = (uint32_t)(int32_t)((key - first) * row_stride) + (lane % LPR) * 16;
                     x.k[u] = buf_load16_nt(kh_rs, off);
                     x.v[u] = buf_load16_nt(vh_rs, off);
                 }
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int64_t key = min(j0 + 4 * u + (lane >> 4), w1 - 1);
-                const uint32_t off = (uint32_t)((key - w0) * row_stride) + (lane & 15) * 16;
+            for (int u = 0; u < NLD; u++) {
+                const int64_t key = min(j0 + RPL * u + lane / LPR, w1 - 1);
+                const uint32_t off = (uint32_t)((key - w0) * row_stride) + (lane % LPR) * 16;
                 x.k[u] = buf_load16_nt(krs, off);
                 x.v[u] = buf_load16_nt(vrs, off);
             }
@@ -396,20 +179,20 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     };
     auto stage = [&](const Stage &x) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int r = 4 * u + (lane >> 4), c = (lane & 15) * 8;
+        for (int u = 0; u < NLD; u++) {
+            const int r = RPL * u + lane / LPR, c = (lane % LPR) * 8;
             *(uint4 *)(t.k + r * KS + c) = x.k[u];
             *(uint4 *)(t.v + r * VS + c) = x.v[u];
         }
     };
     float m = -INFINITY, l = 0.f;
-    f32x16_t acc[4];
+    f32x16_t acc[DTN];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) acc[dt] = zero16();
+    for (int dt = 0; dt < DTN; dt++) acc[dt] = zero16();
     auto block = [&](int64_t j0) __attribute__((always_inline)) {
         f32x16_t sc = zero16();
 #pragma unroll
-        for (int st = 0; st < 8; st++) sc = mfma32<DT>(row_frag(t.k, KS, 0, st * 16, lane), qf[st], sc);
+        for (int st = 0; st < KST; st++) sc = mfma32<DT>(row_frag(t.k, KS, 0, st * 16, lane), qf[st], sc);
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -418,39 +201,48 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
             mx = fmaxf(mx, sc[i]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx);
-        // with nothing visible yet (mn = -inf) every factor below is exp2(-inf) = 0
-        const float ref = mn == -INFINITY ? 0.f : mn;
-        const float alpha = __builtin_amdgcn_exp2f(m - ref);
-        m = mn;
+        // lazy rescale: the reference m moves (and O^T, l are rescaled) only when a head's
+        // maximum grows past it by more than 2^8 (exponentials stay below 256); from -inf any
+        // visible key moves it, and with nothing visible yet (m = -inf) every factor is 0
+        const bool grow = mx > m + 8.f;
+        if (__any(grow)) {
+            const float mn = grow ? mx : m;
+            const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DTN; dt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[dt][i] *= alpha;
+        }
+        const float ref = m == -INFINITY ? 0.f : m;
         float ps = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             sc[i] = __builtin_amdgcn_exp2f(sc[i] - ref);
             ps += sc[i];
         }
-        l = l * alpha + ps;
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) acc[dt][i] *= alpha;
+        l += ps;
         const Frag8 p0 = c_frag<DT>(sc, 0), p1 = c_frag<DT>(sc, 1);
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
+        for (int dt = 0; dt < DTN; dt++) {
             acc[dt] = mfma32<DT>(lds_tr_frag(t.v, VS, 0, dt * 32, lane), p0, acc[dt]);
             acc[dt] = mfma32<DT>(lds_tr_frag(t.v, VS, 16, dt * 32, lane), p1, acc[dt]);
         }
     };
     // (the loop is a single block: with the last block peeled off, as a separate copy after the
     // loop, the kernel measured 15% slower)
+    // (a counted loop: with the exit test as a break the compiler kept O^T in vector registers
+    // across it at D = 256 and spilled)
     if (w0 < w1) {
         const int64_t a0 = PAGED ? (w0 & ~(int64_t)15) : w0;
+        const int nblk = (int)((w1 - a0 + BK - 1) / BK);
         load(sts, a0);
-        for (int64_t j0 = a0;; j0 += BK) {
+        for (int n = 0; n < nblk; n++) {
+            const int64_t j0 = a0 + (int64_t)n * BK;
             stage(sts);
             load(sts, j0 + BK);
             block(j0);
-            if (j0 + BK >= w1) break;
         }
     }
     l += __shfl_xor(l, 32, 64);
@@ -461,7 +253,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_mfma(
     float *sm_acc = (float *)tiles, *sm_m = sm_acc + NW * G * D, *sm_l = sm_m + NW * G;
     if (col < G) {
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++)
+        for (int dt = 0; dt < DTN; dt++)
 #pragma unroll
             for (int i = 0; i < 16; i++) sm_acc[(wave * G + col) * D + dt * 32 + crow(i, lane)] = acc[dt][i];
         if (half == 0) {
@@ -607,16 +399,19 @@ static bool split_takes(const dm_attention_desc *d, int64_t page_size = 0) {
            rows;
 }
 
-// A paged cache runs the split pass on MFMA for D = 128 and pages of a multiple of 16 keys; every
-// other paged call takes the generic kernel.
+// A paged cache runs the split pass on MFMA for D = 64 and 128 and pages of a multiple of 16
+// keys (at D = 256 the page lookups' registers spill); every other paged call takes the generic
+// kernel.
 static bool paged_split_takes(const dm_attention_desc *d, int64_t page_size) {
-    return split_takes(d, page_size) && d->d == 128 && page_size % 16 == 0;
+    return split_takes(d, page_size) && d->d <= 128 && page_size % 16 == 0;
 }
 
 static int span_of(const dm_attention_desc *d) {
     int64_t span = kDecodeMinSpan;
     const int64_t heads = d->b * d->hkv;
-    const int64_t target = d->d == 128 ? kDecodeWorkgroupsMfma : kDecodeWorkgroups;
+    // (at D = 256 one workgroup fills a compute unit, and its wavefronts' sweeps need length:
+    // about one workgroup per compute unit measured best)
+    const int64_t target = d->d == 256 ? kDecodeWorkgroupsMfma / 16 : kDecodeWorkgroupsMfma;
     while (span < d->tk && heads * ((d->tk + span - 1) / span) > target) span *= 2;
     return (int)span;
 }
@@ -684,39 +479,30 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
     const size_t parts = (size_t)rows * nsplit;
     float *part_o = (float *)workspace;
     float *part_lse = (float *)((char *)workspace + align_up(parts * d->d * sizeof(float)));
-    dim3 grid(nsplit, (unsigned)d->hkv, (unsigned)d->b);
     // the MFMA kernel's grid: key-value heads fastest (the heads of a split read neighbouring
     // bytes of the same cache rows at about the same time)
     dim3 grid_hf((unsigned)d->hkv, nsplit, (unsigned)d->b);
     const int g = (int)(d->hq / d->hkv);
-#define DEC_SPLIT(DT, DD, GG)                                                               \
-    decode_split<DT, DD, GG><<<grid, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, nsplit, span, \
-                                                   q, k, v, lengths, map, part_o, part_lse)
-#define DEC_G(DT, DD)                                \
+    // (a paged call reaches here at D <= 128 only: paged_split_takes)
+    if (paged && d->d > 128) return refuse(opn + ": internal: paged split at D > 128");
+#define DEC_MFMA2(DT, GG, PG, DD)                                                           \
+    decode_split_mfma<DT, GG, PG, DD><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, \
+                                                               nsplit, span, q, k, v, lengths, \
+                                                               map, part_o, part_lse)
+#define DEC_MFMA(DT, GG, DD)                         \
+    if (paged) DEC_MFMA2(DT, GG, true, (DD == 256 ? 128 : DD)); else DEC_MFMA2(DT, GG, false, DD)
+#define DEC_GM(DT, DD)                               \
     switch (g) {                                     \
-        case 1: DEC_SPLIT(DT, DD, 1); break;         \
-        case 2: DEC_SPLIT(DT, DD, 2); break;         \
-        case 4: DEC_SPLIT(DT, DD, 4); break;         \
-        default: DEC_SPLIT(DT, DD, 8); break;        \
-    }
-#define DEC_MFMA2(DT, GG, PG)                                                               \
-    decode_split_mfma<DT, GG, PG><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale,  \
-                                                           nsplit, span, q, k, v, lengths, map, \
-                                                           part_o, part_lse)
-#define DEC_MFMA(DT, GG)                             \
-    if (paged) DEC_MFMA2(DT, GG, true); else DEC_MFMA2(DT, GG, false)
-#define DEC_G128(DT)                                 \
-    switch (g) {                                     \
-        case 1: DEC_MFMA(DT, 1); break;              \
-        case 2: DEC_MFMA(DT, 2); break;              \
-        case 4: DEC_MFMA(DT, 4); break;              \
-        default: DEC_MFMA(DT, 8); break;             \
+        case 1: DEC_MFMA(DT, 1, DD); break;          \
+        case 2: DEC_MFMA(DT, 2, DD); break;          \
+        case 4: DEC_MFMA(DT, 4, DD); break;          \
+        default: DEC_MFMA(DT, 8, DD); break;         \
     }
 #define DEC_D(DT)                                    \
     switch (d->d) {                                  \
-        case 64: DEC_G(DT, 64); break;               \
-        case 128: DEC_G128(DT); break;               \
-        default: DEC_G(DT, 256); break;              \
+        case 64: DEC_GM(DT, 64); break;              \
+        case 128: DEC_GM(DT, 128); break;            \
+        default: DEC_GM(DT, 256); break;             \
     }
     {
         KernelTimer timer(DM_KERNEL_DECODE_SPLIT, st);
@@ -728,11 +514,9 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
         decode_merge<DM_F16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
     }
 #undef DEC_D
-#undef DEC_G128
+#undef DEC_GM
 #undef DEC_MFMA
 #undef DEC_MFMA2
-#undef DEC_G
-#undef DEC_SPLIT
     probe_add(DM_PROBE_DECODE_SPLIT);
     probe_add(DM_PROBE_DECODE_MERGE);
     DM_LAUNCH_CHECK((opn + ": launch").c_str());

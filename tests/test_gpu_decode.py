@@ -1,5 +1,5 @@
 """Attention decode (attention.rs:732, reference.rs:433-467) over the shapes the split kernel
-takes (head dimensions 64/128/256, query groups 1/2/4/8, bf16/f16) and the generic one (f32, a
+takes on MFMA (head dimensions 64/128/256, query groups 1/2/4/8, bf16/f16; a probe shows it ran) and the generic one (f32, a
 group of 3), with cache lengths at the split boundaries (0, 1, a split less one, a split, a split
 plus one, a ragged tail) and left windows, against the f64 oracle on the same rounded inputs.
 
@@ -12,6 +12,7 @@ import torch
 
 import dashmag_amd as dm
 import oracle
+from dashmag_amd import _lib
 from fixtures import errors
 
 pytestmark = pytest.mark.gpu
@@ -37,10 +38,13 @@ def _case(dtype, d, hkv, g, window, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d,hkv,g", [(64, 2, 1), (128, 2, 4), (128, 1, 8), (256, 2, 2)])
+@pytest.mark.parametrize("d,hkv,g", [(64, 2, 1), (128, 2, 4), (128, 1, 8), (256, 2, 2), (256, 1, 8),
+                                     (64, 1, 8)])
 @pytest.mark.parametrize("window", [None, 700])
 def test_split_decode(dtype, d, hkv, g, window):
+    _lib.probe_reset()
     a, e = _case(dtype, d, hkv, g, window, seed=d * 100 + g * 10 + (window is None))
+    assert _lib.probe_counts()["decode_split"] > 0, "the MFMA split pass did not run"
     assert np.all(a[0] == 0.0), "an empty cache gives zeros"
     r = errors(a, e)[1]
     print(f"rel {r:.2e}")

@@ -57,7 +57,7 @@ def _bound(dtype):
 
 
 @pytest.mark.parametrize("dtype,d,hkv,g", [(torch.bfloat16, 128, 2, 4), (torch.float16, 64, 2, 2),
-                                           (torch.float32, 128, 1, 4)])
+                                           (torch.bfloat16, 256, 2, 8), (torch.float32, 128, 1, 4)])
 @pytest.mark.parametrize("window", [None, 700])
 def test_packed_cache(dtype, d, hkv, g, window):
     s = max(LENGTHS) + 7
@@ -122,6 +122,7 @@ def _paged(k, v, lengths, page_size, rng, extra=3):
     (torch.bfloat16, 128, 2, 4, 16), (torch.bfloat16, 128, 1, 8, 64),
     (torch.float16, 128, 2, 2, 32), (torch.bfloat16, 128, 2, 4, 5),
     (torch.bfloat16, 64, 2, 2, 16), (torch.float32, 128, 1, 4, 16),
+    (torch.bfloat16, 256, 2, 4, 16),
 ])
 @pytest.mark.parametrize("window", [None, 700])
 def test_paged_cache(dtype, d, hkv, g, page_size, window):
