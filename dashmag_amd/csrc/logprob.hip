@@ -770,20 +770,18 @@ int dm_linear_cross_entropy_bwd(const dm_lce_desc *d, const void *hidden, const 
     char *ws = (char *)workspace;
     float *gh = grad_hidden ? (f32 ? (float *)grad_hidden : (float *)(ws + p.off_gh)) : nullptr;
     float *gw = grad_weight ? (f32 ? (float *)grad_weight : (float *)(ws + p.off_gw)) : nullptr;
-    if (gw) {
-        lp_zero<<<1024, 256, 0, st>>>(lp->v * lp->d, gw);
-        DM_LAUNCH_CHECK("linear_cross_entropy: zero");
-    }
+    // (the accumulators need no clearing: the first row block's products write grad_weight and
+    // each row block's first chunk writes its rows of grad_hidden, with beta = 0)
     if (lp->n == 0) {
+        if (gw) {
+            lp_zero<<<1024, 256, 0, st>>>(lp->v * lp->d, gw);
+            DM_LAUNCH_CHECK("linear_cross_entropy: zero");
+        }
         if (grad_weight && !f32) {
             lp_cast<<<1024, 256, 0, st>>>(lp->v * lp->d, gw, grad_weight, lp->weight_dtype);
             DM_LAUNCH_CHECK("linear_cross_entropy: cast");
         }
         return DM_OK;
-    }
-    if (gh) {
-        lp_zero<<<1024, 256, 0, st>>>(lp->n * lp->d, gh);
-        DM_LAUNCH_CHECK("linear_cross_entropy: zero");
     }
     if (int rc = lp_upload_bits(bits, ws, p, st)) return rc;
     const void *H, *W;
@@ -815,15 +813,15 @@ int dm_linear_cross_entropy_bwd(const dm_lce_desc *d, const void *hidden, const 
             const char *Wc = (const char *)W + (size_t)c0 * lp->d * esz;
             // grad_hidden (column-major D x rows) += W_c as stored (D x cw) G^T (cw x rows)
             if (gh)
-                if (int rc = lt_gemm(st, false, false, lp->d, rows_b, cw, Wc, G, op_t, 1.f,
-                                     gh + r0 * lp->d, lt_ws))
+                if (int rc = lt_gemm(st, false, false, lp->d, rows_b, cw, Wc, G, op_t,
+                                     c0 == 0 ? 0.f : 1.f, gh + r0 * lp->d, lt_ws))
                     return rc;
             // grad_weight_c (column-major D x cw) += H_b as stored (D x rows) G (rows x cw; G
             // is stored cw x rows, so op(B) = T)
             if (gw)
                 if (int rc = lt_gemm(st, false, true, lp->d, cw, rows_b,
-                                     (const char *)H + (size_t)r0 * lp->d * esz, G, op_t, 1.f,
-                                     gw + c0 * lp->d, lt_ws))
+                                     (const char *)H + (size_t)r0 * lp->d * esz, G, op_t,
+                                     r0 == 0 ? 0.f : 1.f, gw + c0 * lp->d, lt_ws))
                     return rc;
         }
     }
