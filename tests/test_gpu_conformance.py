@@ -3,6 +3,7 @@ dashmag_amd's operations), with the conformance bodies and bounds of crates/dash
 import pytest
 
 import conformance as cf
+from dashmag_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
@@ -38,7 +39,12 @@ def test_chunk_f32_cases(adapter):
 
 
 def test_chunk_bf16_case(adapter):
+    """Dk = Dv = 32 in bf16: the MFMA kernels run it (a probe shows it), within the reference's
+    tensor-core bound."""
+    _lib.probe_reset()
     cf.check_chunk_bf16_case(adapter, "hip", cf.CHUNK_BF16_TC_TOL)
+    pc = _lib.probe_counts()
+    assert pc["gdr_chunk_fwd_mfma"] > 0 and pc["gdr_chunk_bwd_mfma"] > 0, pc
 
 
 def test_chunk_packed_f32(adapter):
@@ -46,7 +52,10 @@ def test_chunk_packed_f32(adapter):
 
 
 def test_chunk_packed_bf16(adapter):
+    _lib.probe_reset()
     cf.check_chunk_packed_bf16(adapter, "hip", cf.BF16_TC_VS_F64)
+    pc = _lib.probe_counts()
+    assert pc["gdr_chunk_fwd_mfma"] > 0 and pc["gdr_chunk_bwd_mfma"] > 0, pc
 
 
 @pytest.mark.parametrize("name", cf.CHUNK_PACKED_F32)
