@@ -26,13 +26,20 @@ FLAGS = [
 ]
 
 
+# Per-source flags. The gated-delta-rule state passes are chains of dependent steps run by one
+# wavefront per SIMD: with the products' accumulators in ordinary vector registers, the state's
+# decay and conversions work on them in place instead of moving every value out of and back into
+# the accumulator registers at each step.
+EXTRA = {"gdr_chunk_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
 
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(os.path.basename(src), []), "-x", "hip", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

@@ -30,7 +30,8 @@ __global__ __launch_bounds__(1024) void gdr_plan(int64_t nseq, int64_t T, int64_
                                                  int32_t *__restrict__ seq_chunk0,
                                                  int32_t *__restrict__ chunk_seq,
                                                  int32_t *__restrict__ chunk_tok0,
-                                                 int32_t *__restrict__ chunk_len) {
+                                                 int32_t *__restrict__ chunk_len,
+                                                 int32_t *__restrict__ seq_order) {
     __shared__ int32_t part[1024];
     const int tid = threadIdx.x;
     const int64_t per = (nseq + 1023) / 1024;
@@ -72,6 +73,23 @@ __global__ __launch_bounds__(1024) void gdr_plan(int64_t nseq, int64_t T, int64_
     const int32_t used = part[1023] < n_max ? part[1023] : (int32_t)n_max;
     if (tid == 0) seq_chunk0[nseq] = used;
     __syncthreads();  // (orders the global writes above for the whole workgroup)
+    // optionally the sequences by chunk count, the most first (ties by index): the state
+    // passes start the longest chains first. Past kOrderMax sequences, the identity.
+    if (seq_order) {
+        for (int64_t s = tid; s < nseq; s += 1024) {
+            if (nseq > kOrderMax) {
+                seq_order[s] = (int32_t)s;
+                continue;
+            }
+            const int32_t n = seq_chunk0[s + 1] - seq_chunk0[s];
+            int32_t rank = 0;
+            for (int64_t u = 0; u < nseq; u++) {
+                const int32_t m = seq_chunk0[u + 1] - seq_chunk0[u];
+                rank += (m > n) | ((m == n) & (u < s));
+            }
+            seq_order[rank] = (int32_t)s;
+        }
+    }
     // every chunk in parallel: its sequence is the last whose first chunk is at or before it
     for (int64_t x = tid; x < n_max; x += 1024) {
         if (x >= used) {
@@ -757,10 +775,10 @@ GdrArgs gdr_args(const dm_gdr_desc *d, const void *q, const void *k, const void 
 }
 
 int launch_plan(const dm_gdr_desc *d, int32_t *seq_chunk0, int32_t *chunk_seq,
-                int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st) {
+                int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st, int32_t *seq_order) {
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
     gdr_plan<<<1, 1024, 0, st>>>(S, d->t, nc, d->cu_seqlens, seq_chunk0, chunk_seq, chunk_tok0,
-                                chunk_len);
+                                chunk_len, seq_order);
     DM_LAUNCH_CHECK("chunk_gated_delta_rule: plan");
     return DM_OK;
 }

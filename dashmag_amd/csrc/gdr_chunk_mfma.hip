@@ -36,6 +36,7 @@ constexpr int kTrS = kD + 32;   // row stride read by ds_read_b64_tr_b16
 struct MfmaWs {
     int64_t nsh;       // sequences x heads
     int32_t *seq_chunk0, *chunk_seq, *chunk_tok0, *chunk_len;
+    int32_t *seq_order;  // [S]: the sequences by chunk count, the most first
     float *G;          // [ch][64]
     uint16_t *Wf;      // [ch][2 token tiles][8 dk steps][64 lanes][8]: W as A fragments of V' = W S
     uint16_t *Uc;      // [ch][4 dv tiles][2 token tiles][2][64 lanes][8]: U in the product layout
@@ -66,6 +67,7 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd 
     x.chunk_seq = (int32_t *)take(nc * 4);
     x.chunk_tok0 = (int32_t *)take(nc * 4);
     x.chunk_len = (int32_t *)take(nc * 4);
+    x.seq_order = (int32_t *)take(S * 4);
     x.G = (float *)take(ch * kC * 4);
     x.Wf = (uint16_t *)take(ch * kC * kD * 2);
     x.Uc = (uint16_t *)take(ch * kC * kD * 2);
@@ -469,14 +471,18 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 
 // The state passes' workgroup -> (sequence x head, column block): workgroup x goes to XCD x % 8,
 // and the four column blocks of a (sequence, head) take workgroups 8 apart, so they share one
-// XCD's L2 (the operands are read from HBM once). Grid: state_grid(nsh) workgroups.
+// XCD's L2 (the operands are read from HBM once). The (sequence, head) items are taken in the
+// plan's sequence order, the longest chains first, so they are dispatched first. Grid:
+// state_grid(nsh) workgroups.
 __host__ __device__ inline int64_t state_grid(int64_t nsh) { return (nsh + 7) / 8 * 32; }
-__device__ __forceinline__ bool state_item(int64_t x, int64_t grid, int64_t nsh, int64_t *sh,
-                                           int *wave) {
+__device__ __forceinline__ bool state_item(int64_t x, int64_t nsh, const int32_t *order,
+                                           int64_t H, int64_t *sh, int *wave) {
     const int64_t xcd = x % 8, y = x / 8;
     *wave = (int)(y % 4);
-    *sh = (y / 4) * 8 + xcd;
-    return *sh < nsh;
+    const int64_t idx = (y / 4) * 8 + xcd;
+    if (idx >= nsh) return false;
+    *sh = (int64_t)order[idx / H] * H + idx % H;
+    return true;
 }
 
 // The state pass with the rows of S split over a pair of wavefronts (one workgroup per column
@@ -488,11 +494,26 @@ __device__ __forceinline__ bool state_item(int64_t x, int64_t grid, int64_t nsh,
 // block, on the chain every chunk waits for.
 constexpr int kStateParts = 2;  // wavefronts sharing a column block's state rows (4 measured slower)
 
+#ifdef DM_TRACE_STATE
+// profiling aid (built only with -DDM_TRACE_STATE=<sequence x head>): per-chunk clock stamps of
+// wavefront 0 of that item's first column block, and the 100 MHz clock at its start and end
+__device__ uint64_t dm_trace_state[256][6];
+#define DM_SSTAMP(c, k)                                                                          \
+    do {                                                                                        \
+        if (sh == (DM_TRACE_STATE) && blk == 0 && p == 0 && lane == 0 && (c) - c0 < 254)        \
+            dm_trace_state[(c) - c0][k] = __builtin_readcyclecounter();                         \
+    } while (0)
+#else
+#define DM_SSTAMP(c, k) \
+    do {                \
+    } while (0)
+#endif
+
 template <int NP>
 struct PartOps {
     static constexpr int RT = 4 / NP, KS = 8 / NP;  // state tiles and dk steps per wavefront
     Frag8 wf[2][KS];  // W: token tile t, dk step KS p + st
-    uint4 uc[2][2];   // U: token tile t, two 8-value halves of the lane's 16
+    Frag8 uc[2];      // U: token tile t, the 8-value half p of the lane's 16 (NP = 2)
     Frag8 kf[RT][4];  // (lam K)^T: dk tile RT p + r, token step st
     float glast;
 };
@@ -501,11 +522,12 @@ template <int DT, int NP>
 __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, const float *h0,
                                                              float *final_state) {
     constexpr int RT = 4 / NP, KS = 8 / NP;
+    static_assert(NP == 2, "U's rows are split over two wavefronts");
     using HalfOps = PartOps<NP>;
     __shared__ __align__(16) float4 xch[2][NP][2][4][64];  // [parity][wavefront][token tile][i / 4][lane]
     int64_t sh;
     int blk;
-    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
+    if (!state_item(blockIdx.x, w.nsh, w.seq_order, a.H, &sh, &blk)) return;
     const int64_t s = sh / a.H, h = sh % a.H;
     const int lane = threadIdx.x & 63;
     const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row part
@@ -525,10 +547,25 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
                 S[r][i] = src && row < a.Dk && dv < a.Dv ? src[row * a.Dv + dv] : 0.f;
             }
     }
-    auto load = [&](int c, HalfOps &x) __attribute__((always_inline)) {
+    // -I's rows 16 p + [0, 16) as the A operand against U's half p as the B operand: lane l's B
+    // slot j is token row crow(8 p + j, l) = 16 p + 8 (j / 4) + 4 (l / 32) + j % 4 at hardware
+    // k = 8 (l / 32) + j, so A(row, k) = -1 exactly where that row is the lane's row l % 32.
+    Frag8 negid;
+    {
+        const uint16_t m1 = DT == DM_BF16 ? 0xBF80 : 0xBC00;  // -1 in bf16 / f16
+        uint16_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            e[j] = (lane & 31) == 16 * p + 8 * (j / 4) + 4 * (lane >> 5) + (j % 4) ? m1 : 0;
+        negid.u = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                             e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+    }
+    // a chunk's operands in two parts: W and U (free once W S is issued) and (lam K)^T with
+    // G_last (free once the update is issued)
+    auto load_wu = [&](int c, HalfOps &x) __attribute__((always_inline)) {
         c = c < c1 ? c : c1 - 1;
         const int64_t ch = (int64_t)c * a.H + h;
-        const uint16_t *wf = w.Wf + ch * kC * kD, *kf = w.Kf + ch * kC * kD;
+        const uint16_t *wf = w.Wf + ch * kC * kD;
         const uint16_t *uc = w.Uc + ch * kC * kD + (size_t)blk * 2 * 2 * 64 * 8;
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -536,10 +573,12 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
             for (int st = 0; st < KS; st++)
                 x.wf[t][st].u = *(const uint4 *)(wf + ((t * 8 + p * KS + st) * 64 + lane) * 8);
 #pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++)
-                x.uc[t][qq] = *(const uint4 *)(uc + ((t * 2 + qq) * 64 + lane) * 8);
+        for (int t = 0; t < 2; t++) x.uc[t].u = *(const uint4 *)(uc + ((t * 2 + p) * 64 + lane) * 8);
+    };
+    auto load_k = [&](int c, HalfOps &x) __attribute__((always_inline)) {
+        c = c < c1 ? c : c1 - 1;
+        const int64_t ch = (int64_t)c * a.H + h;
+        const uint16_t *kf = w.Kf + ch * kC * kD;
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
@@ -547,8 +586,11 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
                 x.kf[r][st].u = *(const uint4 *)(kf + (((p * RT + r) * 4 + st) * 64 + lane) * 8);
         x.glast = w.G[ch * kC + kC - 1];
     };
-    auto step = [&](int c, const HalfOps &x) __attribute__((always_inline)) {
+    // chunk c's step on the operands in x, which then load chunk cn's (each part as soon as the
+    // step's products have taken it, so the loads issue while the products run)
+    auto step = [&](int c, HalfOps &x, int cn) __attribute__((always_inline)) {
         const int64_t ch = (int64_t)c * a.H + h;
+        DM_SSTAMP(c, 0);
         // this part of S as operand fragments (dk steps KS p + st), also stored for the output
         Frag8 sf[KS];
         uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)blk * 8 * 64 * 8;
@@ -557,84 +599,92 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
             sf[st] = c_frag<DT>(S[st / 2], st % 2);
             *(uint4 *)(sfo + ((p * KS + st) * 64 + lane) * 8) = sf[st].u;
         }
-        // this part's share of W S
+        // this part's share of W S - U: the products start from -U's rows 16 p + [0, 16) of each
+        // token tile (U as a B operand times -I, exact in f32), so the pair's sum is W S - U
         f32x16_t vp[2];
 #pragma unroll
-        for (int t = 0; t < 2; t++) vp[t] = zero16();
+        for (int t = 0; t < 2; t++) vp[t] = mfma32<DT>(negid, x.uc[t], zero16());
 #pragma unroll
         for (int st = 0; st < KS; st++)
 #pragma unroll
             for (int t = 0; t < 2; t++) vp[t] = mfma32<DT>(x.wf[t][st], sf[st], vp[t]);
-        // swap the shares (summed in the same order in every wavefront)
+        // the decay of this part of S, on the vector unit while the products run
+        const float gl = __expf(x.glast);
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) S[r][i] *= gl;
+        load_wu(cn, x);
+        // swap the shares: each wavefront reads the other's (x + y = y + x exactly, so both
+        // wavefronts form the same V')
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
                 xch[c & 1][p][t][g][lane] =
                     make_float4(vp[t][4 * g], vp[t][4 * g + 1], vp[t][4 * g + 2], vp[t][4 * g + 3]);
+        DM_SSTAMP(c, 1);
         __syncthreads();
+        DM_SSTAMP(c, 2);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                float4 acc = xch[c & 1][0][t][g][lane];
-#pragma unroll
-                for (int q = 1; q < NP; q++) {
-                    const float4 y = xch[c & 1][q][t][g][lane];
-                    acc.x += y.x;
-                    acc.y += y.y;
-                    acc.z += y.z;
-                    acc.w += y.w;
-                }
-                vp[t][4 * g] = acc.x;
-                vp[t][4 * g + 1] = acc.y;
-                vp[t][4 * g + 2] = acc.z;
-                vp[t][4 * g + 3] = acc.w;
+                // V' = -(W S - U) = -(own part) - (other part)
+                const float4 y = xch[c & 1][p ^ 1][t][g][lane];
+                vp[t][4 * g] = -vp[t][4 * g] - y.x;
+                vp[t][4 * g + 1] = -vp[t][4 * g + 1] - y.y;
+                vp[t][4 * g + 2] = -vp[t][4 * g + 2] - y.z;
+                vp[t][4 * g + 3] = -vp[t][4 * g + 3] - y.w;
             }
-        // V' = U - W S (the same in every wavefront; wavefront p stores the steps st = p mod NP)
+        // V' (the same in every wavefront; wavefront p stores the steps st = p mod NP)
         Frag8 vlf[4];
         uint16_t *vfo = w.Vf ? w.Vf + ch * kC * kD + (size_t)blk * 4 * 64 * 8 : nullptr;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t uw[4] = {x.uc[t][u].x, x.uc[t][u].y, x.uc[t][u].z, x.uc[t][u].w};
-                float v8[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float uu = (e & 1) ? unpack_hi<DT>(uw[e / 2]) : unpack_lo<DT>(uw[e / 2]);
-                    v8[e] = uu - vp[t][8 * u + e];
-                }
                 const int st = t * 2 + u;
-                vlf[st].u = make_uint4(pack2<DT>(v8[0], v8[1]), pack2<DT>(v8[2], v8[3]),
-                                       pack2<DT>(v8[4], v8[5]), pack2<DT>(v8[6], v8[7]));
+                vlf[st] = c_frag<DT>(vp[t], u);
                 if (vfo && st % NP == p) *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
             }
-        // S_p <- exp(G_last) S_p + (lam K)_p^T V'
-        const float gl = __expf(x.glast);
-#pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) S[r][i] *= gl;
+        DM_SSTAMP(c, 3);
+        // S_p <- exp(G_last) S_p + (lam K)_p^T V' (the decay applied above)
 #pragma unroll
         for (int st = 0; st < 4; st++)
 #pragma unroll
             for (int r = 0; r < RT; r++) S[r] = mfma32<DT>(x.kf[r][st], vlf[st], S[r]);
+        load_k(cn, x);
+        DM_SSTAMP(c, 4);
     };
+#ifdef DM_TRACE_STATE
+    if (sh == (DM_TRACE_STATE) && blk == 0 && p == 0 && lane == 0) {
+        dm_trace_state[255][0] = __builtin_readcyclecounter();
+        dm_trace_state[255][1] = __builtin_amdgcn_s_memrealtime();
+    }
+#endif
     HalfOps oa, ob;
     if (c0 < c1) {
-        load(c0, oa);
-        load(c0 + 1, ob);
+        load_wu(c0, oa);
+        load_k(c0, oa);
+        load_wu(c0 + 1, ob);
+        load_k(c0 + 1, ob);
     }
-    // (both halves issue their loads on every pass, the second step's products conditional: on
-    // every path through the loop the second set's loads are then the most recent, and the
-    // compiler's wait counts keep them in flight across a step)
-    for (int c = c0; c < c1; c += 2) {
-        step(c, oa);
-        load(c + 2, oa);
-        if (c + 1 < c1) step(c + 1, ob);
-        load(c + 3, ob);
+    // two chunks a pass, each register set loading the chunk two ahead; an odd last chunk after
+    // the loop (every pass through the loop then issues the same loads, so the compiler's wait
+    // counts keep the next chunks' loads in flight across a step)
+    int c = c0;
+    for (; c + 1 < c1; c += 2) {
+        step(c, oa, c + 2);
+        step(c + 1, ob, c + 3);
     }
+    if (c < c1) step(c, oa, c + 2);
+#ifdef DM_TRACE_STATE
+    if (sh == (DM_TRACE_STATE) && blk == 0 && p == 0 && lane == 0) {
+        dm_trace_state[254][0] = __builtin_readcyclecounter();
+        dm_trace_state[254][1] = __builtin_amdgcn_s_memrealtime();
+    }
+#endif
     if (final_state) {
         float *dst = final_state + sh * a.Dk * a.Dv;
 #pragma unroll
@@ -896,7 +946,7 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
     __shared__ __align__(16) float4 xch[2][2][2][4][64];  // [parity][wavefront][token tile][i / 4][lane]
     int64_t sh;
     int blk;
-    if (!state_item(blockIdx.x, (int64_t)gridDim.x, w.nsh, &sh, &blk)) return;
+    if (!state_item(blockIdx.x, w.nsh, w.seq_order, a.H, &sh, &blk)) return;
     const int64_t s = sh / a.H, h = sh % a.H;
     const int lane = threadIdx.x & 63;
     const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row half
@@ -1585,6 +1635,24 @@ bool gdr_mfma_takes(const dm_gdr_desc *d) {
 
 size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { return mfma_layout(d, nullptr, nullptr); }
 
+#ifdef DM_TRACE_STATE
+extern "C" int dm_debug_trace_state(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(dm_trace_state), bytes) == hipSuccess ? 0 : 1;
+}
+#endif
+
+// LDS the state passes' launches reserve beyond their own, so that one workgroup takes a
+// compute unit: a chain step whose wavefronts share the compute unit's load, LDS and issue with
+// another workgroup's took 4,000-6,500 cycles against 2,600 alone, and the longest chains, taken
+// first, decide the pass's time (config 4: 265 -> 227 us).
+static unsigned state_lds_extra() { return 80 * 1024; }
+template <typename K>
+static void allow_lds(K kernel, unsigned bytes) {
+    if (bytes > 64 * 1024)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
 int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
                         const void *g, const void *beta, const float *h0, void *out,
                         float *final_state, void *workspace, hipStream_t st) {
@@ -1592,7 +1660,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
     mfma_layout(d, (char *)workspace, &w);
     const GdrArgs a = gdr_args(d, q, k, v, g, beta);
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
-    int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st);
+    int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st, w.seq_order);
     if (rc) return rc;
     const unsigned chunks = (unsigned)(nc * d->h), seqs = (unsigned)(S * d->h);
     if (d->dtype == DM_BF16) {
@@ -1602,7 +1670,8 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state2<DM_BF16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, 0, st>>>(a, w, h0, final_state);
+            allow_lds(gdr_mfma_state2<DM_BF16, kStateParts>, state_lds_extra());
+            gdr_mfma_state2<DM_BF16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds_extra(), st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1615,7 +1684,8 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            gdr_mfma_state2<DM_F16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, 0, st>>>(a, w, h0, final_state);
+            allow_lds(gdr_mfma_state2<DM_F16, kStateParts>, state_lds_extra());
+            gdr_mfma_state2<DM_F16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds_extra(), st>>>(a, w, h0, final_state);
         }
         {
             KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
@@ -1645,7 +1715,8 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_STATE, st);
-        gdr_mfma_state2<DT, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, 0, st>>>(a, w, h0, nullptr);
+        allow_lds(gdr_mfma_state2<DT, kStateParts>, state_lds_extra());
+            gdr_mfma_state2<DT, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds_extra(), st>>>(a, w, h0, nullptr);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_PRE, st);
@@ -1653,7 +1724,8 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_STATE, st);
-        gdr_bwd_state2<DT><<<(unsigned)state_grid(seqs), 128, 0, st>>>(a, w, d_final, dh0);
+        allow_lds(gdr_bwd_state2<DT>, state_lds_extra());
+        gdr_bwd_state2<DT><<<(unsigned)state_grid(seqs), 128, state_lds_extra(), st>>>(a, w, d_final, dh0);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_GRADS, st);
@@ -1670,7 +1742,7 @@ int launch_gdr_mfma_bwd(const dm_gdr_desc *d, const void *q, const void *k, cons
     mfma_layout(d, (char *)workspace, &w, true);
     const GdrArgs a = gdr_args(d, q, k, v, g, beta);
     const int64_t nc = gdr_chunk_bound(d), S = gdr_nseq(d);
-    int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st);
+    int rc = launch_plan(d, w.seq_chunk0, w.chunk_seq, w.chunk_tok0, w.chunk_len, st, w.seq_order);
     if (rc) return rc;
     const unsigned chunks = (unsigned)(nc * d->h), seqs = (unsigned)(S * d->h);
     if (d->dtype == DM_BF16)

@@ -52,8 +52,12 @@ struct GdrWs {
 
 int check_gdr(const dm_gdr_desc *d, const char *op, bool step);
 // The chunk plan over the call's sequences (gdr_chunk.hip).
+// seq_order (optional, [nseq]): the sequences by chunk count, the most first (ties by index),
+// for at most kOrderMax sequences; the identity beyond.
+constexpr int64_t kOrderMax = 4096;
 int launch_plan(const dm_gdr_desc *d, int32_t *seq_chunk0, int32_t *chunk_seq,
-                int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st);
+                int32_t *chunk_tok0, int32_t *chunk_len, hipStream_t st,
+                int32_t *seq_order = nullptr);
 int64_t gdr_nseq(const dm_gdr_desc *d);
 int64_t gdr_chunk_bound(const dm_gdr_desc *d);
 
