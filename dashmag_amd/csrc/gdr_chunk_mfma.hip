@@ -936,7 +936,7 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
 struct BwdHalfOps {
     Frag8 kr[2][4];  // lam K: token tile t, dk step 4 p + st
     Frag8 wt[2][4];  // W^T: dk tile 2 p + r, token step st
-    uint4 f[2][2];   // F: dk tile 2 p + r, the lane's 16 values as two 16-byte halves
+    Frag8 f[2][2];   // F: dk tile 2 p + r, the lane's 16 values as two 8-value halves
     float glast;
 };
 
@@ -964,11 +964,27 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
                 D[r][i] = d_final && row < a.Dk && dv < a.Dv
                               ? d_final[sh * a.Dk * a.Dv + row * a.Dv + dv] : 0.f;
             }
-    // a chunk before the sequence's first loads the first again (every call the same loads)
-    auto load = [&](int c, BwdHalfOps &x) __attribute__((always_inline)) {
+    // I's rows 16 u + [0, 16) as the A operand against an output-layout tile's 8-value half u
+    // as the B operand (lane l's B slot j is row crow(8 u + j, l) at hardware k = 8 (l / 32) + j):
+    // the product adds the tile, exactly in f32
+    Frag8 ident[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const uint16_t one = DT == DM_BF16 ? 0x3F80 : 0x3C00;
+        uint16_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            e[j] = (lane & 31) == 16 * u + 8 * (j / 4) + 4 * (lane >> 5) + (j % 4) ? one : 0;
+        ident[u].u = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                                e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+    }
+    // a chunk's operands in two parts: lam K and F with G_last (free once X and F's products
+    // are issued) and W^T (free once the update is issued); a chunk before the sequence's first
+    // loads the first again (every call the same loads)
+    auto load_kf = [&](int c, BwdHalfOps &x) __attribute__((always_inline)) {
         c = c >= c0 ? c : c0;
         const int64_t ch = (int64_t)c * a.H + h;
-        const uint16_t *kr = w.Krf + ch * kC * kD, *wt = w.WTf + ch * kC * kD;
+        const uint16_t *kr = w.Krf + ch * kC * kD;
         const uint16_t *f = w.F + ch * kD * kD + (size_t)blk * 4 * 64 * 16;
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -976,18 +992,24 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
             for (int st = 0; st < 4; st++)
                 x.kr[t][st].u = *(const uint4 *)(kr + ((t * 8 + p * 4 + st) * 64 + lane) * 8);
 #pragma unroll
+        for (int r = 0; r < 2; r++) {
+            x.f[r][0].u = *(const uint4 *)(f + ((size_t)(p * 2 + r) * 64 + lane) * 16);
+            x.f[r][1].u = *(const uint4 *)(f + ((size_t)(p * 2 + r) * 64 + lane) * 16 + 8);
+        }
+        x.glast = w.G[ch * kC + kC - 1];
+    };
+    auto load_w = [&](int c, BwdHalfOps &x) __attribute__((always_inline)) {
+        c = c >= c0 ? c : c0;
+        const int64_t ch = (int64_t)c * a.H + h;
+        const uint16_t *wt = w.WTf + ch * kC * kD;
+#pragma unroll
         for (int r = 0; r < 2; r++)
 #pragma unroll
             for (int st = 0; st < 4; st++)
                 x.wt[r][st].u = *(const uint4 *)(wt + (((p * 2 + r) * 4 + st) * 64 + lane) * 8);
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            x.f[r][0] = *(const uint4 *)(f + ((size_t)(p * 2 + r) * 64 + lane) * 16);
-            x.f[r][1] = *(const uint4 *)(f + ((size_t)(p * 2 + r) * 64 + lane) * 16 + 8);
-        }
-        x.glast = w.G[ch * kC + kC - 1];
     };
-    auto step = [&](int c, const BwdHalfOps &x) __attribute__((always_inline)) {
+    // chunk c's step on the operands in x, which then load chunk cn's
+    auto step = [&](int c, BwdHalfOps &x, int cn) __attribute__((always_inline)) {
         const int64_t ch = (int64_t)c * a.H + h;
         // this half of dS after the chunk, kept for the gradients as S is in Sf
         Frag8 df[4];
@@ -1005,6 +1027,18 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
         for (int st = 0; st < 4; st++)
 #pragma unroll
             for (int t = 0; t < 2; t++) X[t] = mfma32<DT>(x.kr[t][st], df[st], X[t]);
+        // dS_c = exp(G_last) dS_{c+1} + F - W^T X on this half's rows: the decay on the vector
+        // unit and F by identity products while X's products run
+        const float gl = __expf(x.glast);
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) D[r][i] *= gl;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) D[r] = mfma32<DT>(ident[u], x.f[r][u], D[r]);
+        load_kf(cn, x);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -1012,52 +1046,45 @@ __global__ __launch_bounds__(128, 1) void gdr_bwd_state2(GdrArgs a, MfmaWs w, co
                 xch[c & 1][p][t][g][lane] =
                     make_float4(X[t][4 * g], X[t][4 * g + 1], X[t][4 * g + 2], X[t][4 * g + 3]);
         __syncthreads();
-        // the two shares summed in the same order in both wavefronts
+        // -X from the two shares: each wavefront reads the other's (x + y = y + x exactly, so
+        // both wavefronts form the same values)
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const float4 x0 = xch[c & 1][0][t][g][lane], x1 = xch[c & 1][1][t][g][lane];
-                X[t][4 * g] = x0.x + x1.x;
-                X[t][4 * g + 1] = x0.y + x1.y;
-                X[t][4 * g + 2] = x0.z + x1.z;
-                X[t][4 * g + 3] = x0.w + x1.w;
+                const float4 y = xch[c & 1][p ^ 1][t][g][lane];
+                X[t][4 * g] = -X[t][4 * g] - y.x;
+                X[t][4 * g + 1] = -X[t][4 * g + 1] - y.y;
+                X[t][4 * g + 2] = -X[t][4 * g + 2] - y.z;
+                X[t][4 * g + 3] = -X[t][4 * g + 3] - y.w;
             }
         Frag8 nx[4];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            nx[2 * t] = c_frag<DT>(X[t], 0, -1.f);
-            nx[2 * t + 1] = c_frag<DT>(X[t], 1, -1.f);
-        }
-        // dS_c = exp(G_last) dS_{c+1} + F - W^T X on this half's rows
-        const float gl = __expf(x.glast);
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const uint32_t fw[8] = {x.f[r][0].x, x.f[r][0].y, x.f[r][0].z, x.f[r][0].w,
-                                    x.f[r][1].x, x.f[r][1].y, x.f[r][1].z, x.f[r][1].w};
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float fv = (i & 1) ? unpack_hi<DT>(fw[i / 2]) : unpack_lo<DT>(fw[i / 2]);
-                D[r][i] = D[r][i] * gl + fv;
-            }
+            nx[2 * t] = c_frag<DT>(X[t], 0);
+            nx[2 * t + 1] = c_frag<DT>(X[t], 1);
         }
 #pragma unroll
         for (int st = 0; st < 4; st++)
 #pragma unroll
             for (int r = 0; r < 2; r++) D[r] = mfma32<DT>(x.wt[r][st], nx[st], D[r]);
+        load_w(cn, x);
     };
     BwdHalfOps oa, ob;
     if (c0 < c1) {
-        load(c1 - 1, oa);
-        load(c1 - 2, ob);
+        load_kf(c1 - 1, oa);
+        load_w(c1 - 1, oa);
+        load_kf(c1 - 2, ob);
+        load_w(c1 - 2, ob);
     }
-    for (int c = c1 - 1; c >= c0; c -= 2) {
-        step(c, oa);
-        load(c - 2, oa);
-        if (c - 1 < c0) break;
-        step(c - 1, ob);
-        load(c - 3, ob);
+    // two chunks a pass, backwards, each register set loading the chunk two before; an odd
+    // first chunk after the loop (every pass through the loop issues the same loads)
+    int c = c1 - 1;
+    for (; c - 1 >= c0; c -= 2) {
+        step(c, oa, c - 2);
+        step(c - 1, ob, c - 3);
     }
+    if (c >= c0) step(c, oa, c - 2);
     if (dh0) {
 #pragma unroll
         for (int r = 0; r < 2; r++)
