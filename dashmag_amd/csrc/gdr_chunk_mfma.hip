@@ -9,14 +9,16 @@
 //   gdr_mfma_prep    per (chunk, head), parallel: G = cumsum g; K K^T and Q K^T (MFMA); A and
 //                    T = (I + A)^-1 in f32 by 16 x 16 blocks (each diagonal block by column
 //                    forward substitution, the rest by block forward substitution); W = T (beta
-//                    gamma K), U = T (beta V) (MFMA); Aqk = scale (Q K^T o decay).
+//                    gamma K), U = T (beta V) (MFMA); Aqk = scale (Q K^T o decay) (the forward
+//                    stores it transposed, with Q, as the output products' B fragments).
 //   gdr_mfma_state2  per (sequence, head, 32 state columns), serial over the sequence's chunks:
 //                    the state S lives in registers in the 32x32 products' output layout, which
 //                    is also the operand layout of the next product, its rows split over a
 //                    pair of wavefronts; V' = U - W S; S <- exp(G_last) S + (lam K)^T V'; the
 //                    operands come from the prep kernel as ready-made fragments straight into
-//                    registers; S and V' are stored as operand fragments for the output kernel.
-//   gdr_mfma_output  per (chunk, head), parallel: O^T = scale gamma (S^T Q^T) + V'^T Aqk^T.
+//                    registers. In the forward two more wavefronts of the workgroup form the
+//                    output O^T = scale gamma (S^T Q^T) + V'^T Aqk^T from S and V' handed over
+//                    in LDS; the backward's run stores S and V' as operand fragments instead.
 // Notation as chunk/reference.rs:11-18 (Q scaled, G_last the chunk's last cumulative gate).
 #include <string>
 #include <type_traits>
@@ -44,7 +46,10 @@ struct MfmaWs {
     uint16_t *Aqk;     // [ch][64][64] row-major, scale included
     uint16_t *Sf;      // [ch][4 dv tiles][8 dk steps][64 lanes][8]: S entering the chunk
     uint16_t *Vf;      // [ch][4 dv tiles][4 token steps][64 lanes][8]: V'
-    uint16_t *Qn;      // [ch][64][128] normalised queries (with the l2 normalisation)
+    uint16_t *Qn;      // [ch][64][128] normalised queries (backward, with the l2 normalisation)
+    // the forward's, instead of Aqk, Sf, Vf and Qn: what its output wavefronts load
+    uint16_t *Qf;      // [ch][2 token tiles][8 dk steps][64 lanes][8]: Q (normalised) as B fragments
+    uint16_t *Af;      // [ch][2 token tiles][4 key steps][64 lanes][8]: Aqk^T as B fragments
     // the backward's, besides
     uint16_t *Tm;      // [ch][64][64] T = (I + A)^-1, row-major
     uint16_t *Krf;     // [ch][2 token tiles][8 dk steps][64][8]: lam K as A fragments (rows tokens)
@@ -72,10 +77,15 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd 
     x.Wf = (uint16_t *)take(ch * kC * kD * 2);
     x.Uc = (uint16_t *)take(ch * kC * kD * 2);
     x.Kf = (uint16_t *)take(ch * kC * kD * 2);
-    x.Aqk = (uint16_t *)take(ch * kC * kC * 2);
-    x.Sf = (uint16_t *)take(ch * kD * kD * 2);
-    x.Vf = (uint16_t *)take(ch * kC * kD * 2);
-    if (d->qk_l2norm) x.Qn = (uint16_t *)take(ch * kC * kD * 2);
+    if (bwd) {
+        x.Aqk = (uint16_t *)take(ch * kC * kC * 2);
+        x.Sf = (uint16_t *)take(ch * kD * kD * 2);
+        x.Vf = (uint16_t *)take(ch * kC * kD * 2);
+        if (d->qk_l2norm) x.Qn = (uint16_t *)take(ch * kC * kD * 2);
+    } else {
+        x.Qf = (uint16_t *)take(ch * kC * kD * 2);
+        x.Af = (uint16_t *)take(ch * kC * kC * 2);
+    }
     if (bwd) {
         x.Tm = (uint16_t *)take(ch * kC * kC * 2);
         x.Krf = (uint16_t *)take(ch * kC * kD * 2);
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
                             pack2<DT>(qf[4] * qi, qf[5] * qi), pack2<DT>(qf[6] * qi, qf[7] * qi));
             kv = make_uint4(pack2<DT>(kf[0] * ki, kf[1] * ki), pack2<DT>(kf[2] * ki, kf[3] * ki),
                             pack2<DT>(kf[4] * ki, kf[5] * ki), pack2<DT>(kf[6] * ki, kf[7] * ki));
-            *(uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8) = qv;
+            if (w.Qn) *(uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8) = qv;
         }
         sm.q[r * (kRowS / 8) + c] = qv;
         sm.k[r * (kRowS / 8) + c] = kv;
@@ -244,7 +254,11 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
     // K K^T and Q K^T on the lower tiles (0,0), (1,0), (1,1) (waves 0-2); A = beta (K K^T) o
     // decay strictly below the diagonal, Aqk = scale (Q K^T) o decay on and below it. Output
     // element i of tile (ti, tj): row 32 ti + 8 (i / 4) + 4 h + i % 4, column 32 tj + col.
-    uint16_t *aq_out = w.Aqk + ch * kC * kC;
+    // The forward instead forms K Q^T o decay (key rows, query columns: Aqk^T), whose output
+    // fragments are the B operands of its output products as they stand (lane = query, k =
+    // key in the chain's fragment order); it also stores Q as B fragments.
+    const bool fwd = w.Af != nullptr;
+    uint16_t *aq_out = fwd ? nullptr : w.Aqk + ch * kC * kC;
     if (wave < 3) {
         const int ti = wave == 0 ? 0 : 1, tj = wave == 2 ? 1 : 0;
         f32x16_t kk, qk;
@@ -257,7 +271,9 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             aq.u = *(const uint4 *)(qs + (ti * 32 + col) * kRowS + half * 8 + st * 16);
             bk.u = *(const uint4 *)(ks + (tj * 32 + col) * kRowS + half * 8 + st * 16);
             kk = mfma32<DT>(ak, bk, kk);
-            qk = mfma32<DT>(aq, bk, qk);
+            // (A and B fragments share a layout: K(tj) rows as A and Q(ti) rows as B give
+            // element (key 32 tj + crow(i), query 32 ti + col))
+            qk = fwd ? mfma32<DT>(bk, aq, qk) : mfma32<DT>(aq, bk, qk);
         }
         const int j = tj * 32 + col;
 #pragma unroll
@@ -266,13 +282,46 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             // masked before the exponential (above the diagonal G_i - G_j > 0)
             const float dec = r >= j ? __expf(sm.g[r] - sm.g[j]) : 0.f;
             if ((r >> 4) >= (j >> 4)) a_at(sm, r, j) = r > j ? sm.bet[r] * kk[i] * dec : 0.f;
-            const uint32_t p2 = pack2<DT>(r >= j ? qk[i] * dec * a.scale : 0.f, 0.f);
-            aq_out[r * kC + j] = (uint16_t)(p2 & 0xffffu);
+            if (!fwd) {
+                const uint32_t p2 = pack2<DT>(r >= j ? qk[i] * dec * a.scale : 0.f, 0.f);
+                aq_out[r * kC + j] = (uint16_t)(p2 & 0xffffu);
+            }
         }
+        if (fwd) {
+            // element i: key kr = 32 tj + crow(i), query qj = 32 ti + col
+            const int qj = ti * 32 + col;
+            f32x16_t v;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int kr = tj * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+                v[i] = kr <= qj ? qk[i] * __expf(sm.g[qj] - sm.g[kr]) * a.scale : 0.f;
+            }
+            uint16_t *af = w.Af + ch * kC * kC;
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+                *(uint4 *)(af + ((ti * 4 + 2 * tj + u) * 64 + lane) * 8) = c_frag<DT>(v, u).u;
+        }
+    } else if (fwd) {
+        // query tile 0 sees no key of tile 1
+        uint16_t *af = w.Af + ch * kC * kC;
+#pragma unroll
+        for (int u = 0; u < 2; u++) *(uint4 *)(af + ((2 + u) * 64 + lane) * 8) = zero4();
     } else {
         for (int xx = lane; xx < 32 * 32; xx += 64) {
             const int r = xx / 32, j = 32 + xx % 32;
             aq_out[r * kC + j] = 0;
+        }
+    }
+    if (fwd) {
+        // Q as B fragments: fragment (token tile t, dk step st), lane l: token 32 t + l % 32,
+        // dk 16 st + 4 (l / 32) + [0, 4) and 16 st + 8 + 4 (l / 32) + [0, 4); four a wavefront
+        uint16_t *qf = w.Qf + ch * kC * kD;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int f = wave * 4 + i, t = f / 8, st = f % 8;
+            const uint16_t *src = qs + (t * 32 + col) * kRowS + st * 16 + half * 4;
+            const uint2 lo = *(const uint2 *)src, hi = *(const uint2 *)(src + 8);
+            *(uint4 *)(qf + (f * 64 + lane) * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
     }
     __syncthreads();  // the query tile is dead from here; the key tile lives until W
@@ -498,13 +547,22 @@ constexpr int kStateParts = 2;  // wavefronts sharing a column block's state row
 // profiling aid (built only with -DDM_TRACE_STATE=<sequence x head>): per-chunk clock stamps of
 // wavefront 0 of that item's first column block, and the 100 MHz clock at its start and end
 __device__ uint64_t dm_trace_state[256][6];
+__device__ uint64_t dm_trace_out[256][6];
 #define DM_SSTAMP(c, k)                                                                          \
     do {                                                                                        \
         if (sh == (DM_TRACE_STATE) && blk == 0 && p == 0 && lane == 0 && (c) - c0 < 254)        \
             dm_trace_state[(c) - c0][k] = __builtin_readcyclecounter();                         \
     } while (0)
+#define DM_OSTAMP(c, k)                                                                          \
+    do {                                                                                        \
+        if (traced && t == 0 && lane == 0 && (c) - c0 < 254)                                    \
+            dm_trace_out[(c) - c0][k] = __builtin_readcyclecounter();                           \
+    } while (0)
 #else
 #define DM_SSTAMP(c, k) \
+    do {                \
+    } while (0)
+#define DM_OSTAMP(c, k) \
     do {                \
     } while (0)
 #endif
@@ -518,22 +576,134 @@ struct PartOps {
     float glast;
 };
 
-template <int DT, int NP>
-__global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs w, const float *h0,
-                                                             float *final_state) {
+// OUT: the workgroup also computes the chunks' outputs, on two more wavefronts (one per token
+// tile, on SIMDs the chain leaves idle): the chain hands each chunk's S and V' over in LDS
+// instead of storing them, and the output wavefronts form O^T = scale gamma (S^T Q^T) +
+// V'^T Aqk^T for the block's 32 columns one chunk behind, in the barriers' rhythm.
+// The output wavefronts of the fused state pass: token tile t of each chunk, the block's 32
+// columns. Q^T and Aqk^T come as the B fragments the prep kernel stored (lane = token, k slots
+// 16 st + 8 (j / 4) + 4 (l / 32) + j % 4, the order of the chain's fragments), loaded two
+// chunks ahead; S^T and V'^T are the chain's fragments as A operands.
+struct OutOps {
+    Frag8 q[8], aq[4];
+    float gam;
+    int len;
+    int64_t tok0;
+};
+template <int DT, int NP, int KS>
+__device__ __forceinline__ void state_output(const GdrArgs &a, const MfmaWs &w, void *out,
+                                             const uint4 (*sbuf)[NP][KS][64],
+                                             const uint4 (*vbuf)[4][64], int64_t h, int blk,
+                                             int c0, int c1, int t, int lane, bool traced) {
+    const int col = lane & 31, half = lane >> 5;
+    const int r = t * 32 + col;  // this lane's token within the chunk (column of O^T)
+    // the sequence's tokens, read once: chunk c starts 64 (c - c0) tokens into them (no load
+    // in the chunk loop waits on another)
+    int64_t first = 0, end = 0;
+    if (c0 < c1) {
+        first = w.chunk_tok0[c0];
+        end = (int64_t)w.chunk_tok0[c1 - 1] + w.chunk_len[c1 - 1];
+    }
+    // the lane's output columns: blk * 32 + 8 g + 4 (l / 32) + [0, 4), g < 4
+    uint16_t *obase = (uint16_t *)out + h * a.Dv + blk * 32 + half * 4;
+    const int64_t orow_stride = a.H * a.Dv;
+    const int ocols = (int)a.Dv - blk * 32 - half * 4;  // columns left in the row from there
+    auto load = [&](int c, OutOps &x) __attribute__((always_inline)) {
+        c = c < c1 ? c : c1 - 1;
+        const int64_t ch = (int64_t)c * a.H + h;
+        const int64_t tok0 = first + (int64_t)(c - c0) * kC;
+        const uint16_t *qf = w.Qf + ch * kC * kD + (size_t)t * 8 * 64 * 8 + lane * 8;
+        const uint16_t *af = w.Af + ch * kC * kC + (size_t)t * 4 * 64 * 8 + lane * 8;
+#pragma unroll
+        for (int st = 0; st < 8; st++) x.q[st].u = *(const uint4 *)(qf + st * 64 * 8);
+#pragma unroll
+        for (int st = 0; st < 4; st++) x.aq[st].u = *(const uint4 *)(af + st * 64 * 8);
+        x.gam = w.G[ch * kC + r];
+        x.len = (int)(end - tok0 < kC ? end - tok0 : kC);
+        x.tok0 = tok0;
+    };
+    auto emit = [&](int c, const OutOps &x) __attribute__((always_inline)) {
+        DM_OSTAMP(c, 0);
+        Frag8 sa[8], va[4];
+#pragma unroll
+        for (int st = 0; st < 8; st++) sa[st].u = sbuf[c % 3][st / KS][st % KS][lane];
+#pragma unroll
+        for (int st = 0; st < 4; st++) va[st].u = vbuf[c & 1][st][lane];
+        DM_OSTAMP(c, 1);
+        f32x16_t inter = zero16(), intra = zero16();
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            inter = mfma32<DT>(sa[st], x.q[st], inter);
+            if (st < 4) intra = mfma32<DT>(va[st], x.aq[st], intra);
+        }
+        DM_OSTAMP(c, 2);
+        const float f = a.scale * __expf(x.gam);
+        if (r < x.len) {
+            uint16_t *orow = obase + (x.tok0 + r) * orow_stride;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++)
+                if (g4 * 8 < ocols)
+                    *(uint2 *)(orow + g4 * 8) = make_uint2(
+                        pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]),
+                        pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]));
+        }
+        DM_OSTAMP(c, 3);
+    };
+    // one barrier per chunk of the chain plus its last one; after barrier b the chunk b - 1
+    // has its S and V' in LDS
+    OutOps oa, ob;
+    if (c0 < c1) {
+        load(c0, oa);
+        load(c0 + 1, ob);
+    }
+    __syncthreads();  // barrier c0
+    int b = c0 + 1;
+    for (; b + 1 <= c1; b += 2) {
+        __syncthreads();  // barrier b
+        emit(b - 1, oa);
+        load(b + 1, oa);
+        DM_OSTAMP(b - 1, 4);
+        __syncthreads();  // barrier b + 1
+        emit(b, ob);
+        load(b + 2, ob);
+        DM_OSTAMP(b, 4);
+    }
+    if (b <= c1) {
+        __syncthreads();
+        emit(b - 1, oa);
+    }
+}
+
+template <int DT, int NP, bool OUT>
+__global__ __launch_bounds__(64 * NP + (OUT ? 128 : 0), 1) void gdr_mfma_state2(
+    GdrArgs a, MfmaWs w, const float *h0, float *final_state, void *out) {
     constexpr int RT = 4 / NP, KS = 8 / NP;
     static_assert(NP == 2, "U's rows are split over two wavefronts");
     using HalfOps = PartOps<NP>;
     __shared__ __align__(16) float4 xch[2][NP][2][4][64];  // [parity][wavefront][token tile][i / 4][lane]
+    // OUT: S by chunk mod 3 (written before a step's barrier, read after the next one, while
+    // the chain writes the chunk after next) and V' by chunk parity (written after a step's
+    // barrier), both as the fragments the chain formed
+    __shared__ __align__(16) uint4 sbuf[OUT ? 3 : 1][NP][KS][64];
+    __shared__ __align__(16) uint4 vbuf[OUT ? 2 : 1][4][64];
     int64_t sh;
     int blk;
     if (!state_item(blockIdx.x, w.nsh, w.seq_order, a.H, &sh, &blk)) return;
     const int64_t s = sh / a.H, h = sh % a.H;
     const int lane = threadIdx.x & 63;
-    const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row part
+    const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row part (>= NP: output)
     const int col = lane & 31;
     const int c0 = w.seq_chunk0[s], c1 = w.seq_chunk0[s + 1];
     const int dv = blk * 32 + col;
+    if (OUT && p >= NP) {
+#ifdef DM_TRACE_STATE
+        const bool traced = sh == (DM_TRACE_STATE) && blk == 0;
+#else
+        const bool traced = false;
+#endif
+        state_output<DT, NP, KS>(a, w, out, sbuf, vbuf, h, blk, c0, c1, p - NP, lane, traced);
+        return;
+    }
 
     // S_p: tile r holds rows 32 (RT p + r) + crow(i) of column dv
     f32x16_t S[RT];
@@ -597,7 +767,10 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
 #pragma unroll
         for (int st = 0; st < KS; st++) {
             sf[st] = c_frag<DT>(S[st / 2], st % 2);
-            *(uint4 *)(sfo + ((p * KS + st) * 64 + lane) * 8) = sf[st].u;
+            if (OUT)
+                sbuf[OUT ? c % 3 : 0][p][st][lane] = sf[st].u;
+            else
+                *(uint4 *)(sfo + ((p * KS + st) * 64 + lane) * 8) = sf[st].u;
         }
         // this part's share of W S - U: the products start from -U's rows 16 p + [0, 16) of each
         // token tile (U as a B operand times -I, exact in f32), so the pair's sum is W S - U
@@ -646,7 +819,12 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
             for (int u = 0; u < 2; u++) {
                 const int st = t * 2 + u;
                 vlf[st] = c_frag<DT>(vp[t], u);
-                if (vfo && st % NP == p) *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
+                if (st % NP == p) {
+                    if (OUT)
+                        vbuf[c & 1][st][lane] = vlf[st].u;
+                    else if (vfo)
+                        *(uint4 *)(vfo + (st * 64 + lane) * 8) = vlf[st].u;
+                }
             }
         DM_SSTAMP(c, 3);
         // S_p <- exp(G_last) S_p + (lam K)_p^T V' (the decay applied above)
@@ -679,6 +857,7 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
         step(c + 1, ob, c + 3);
     }
     if (c < c1) step(c, oa, c + 2);
+    if (OUT) __syncthreads();  // the last chunk's V' to the output wavefronts
 #ifdef DM_TRACE_STATE
     if (sh == (DM_TRACE_STATE) && blk == 0 && p == 0 && lane == 0) {
         dm_trace_state[254][0] = __builtin_readcyclecounter();
@@ -694,114 +873,6 @@ __global__ __launch_bounds__(64 * NP, 1) void gdr_mfma_state2(GdrArgs a, MfmaWs 
                 const int row = (RT * p + r) * 32 + crow(i, lane);
                 if (row < a.Dk && dv < a.Dv) dst[row * a.Dv + dv] = S[r][i];
             }
-    }
-}
-
-// ------------------------------------------------------------------------------------------
-// Output
-// ------------------------------------------------------------------------------------------
-
-// O^T = scale gamma (S^T Q^T) + V'^T Aqk^T per (chunk, head): 8 output tiles (4 of 32 state
-// columns x 2 of 32 tokens); wave w takes column tile w for both token tiles. A = S^T and V'^T
-// fragments as the state pass stored them (the operand layouts of A and B are the same); B = Q^T
-// and Aqk^T from rows (k slots 16 st + 8 j + 4 h + e). Each lane then holds one token's 4
-// consecutive columns per group: 8-byte stores along the output row.
-struct OutSmem {
-    uint4 q[kC * kRowB / 8 + 1];      // queries, rows (8-byte reads)
-    uint4 aq[kC * (kC + 4) / 8 + 1];  // Aqk, rows (8-byte reads)
-    float g[kC];
-};
-
-template <int DT>
-__global__ __launch_bounds__(256) void gdr_mfma_output(GdrArgs a, MfmaWs w, void *out) {
-    __shared__ OutSmem sm;
-    const int64_t ch = blockIdx.x, n = ch / a.H, h = ch % a.H;
-    const int len = w.chunk_len[n];
-    if (len == 0) return;
-    const int64_t tok0 = w.chunk_tok0[n];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int col = lane & 31, half = lane >> 5;
-    const uint16_t *sfo = w.Sf + ch * kD * kD + (size_t)wave * 8 * 64 * 8;
-    const uint16_t *vfo = w.Vf + ch * kC * kD + (size_t)wave * 4 * 64 * 8;
-    const uint16_t *aqg = w.Aqk + ch * kC * kC;
-    uint16_t *qs = (uint16_t *)sm.q, *as = (uint16_t *)sm.aq;
-    constexpr int AS = kC + 4;
-    // the chunk's queries (the normalised chunk-major copy, or the inputs' rows) and Aqk
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int x = tid + 256 * u, r = x / 16, c = x % 16;
-        uint4 qv;
-        if (a.l2norm)
-            qv = *(const uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8);
-        else
-            qv = r < len && c * 8 < a.Dk
-                     ? *(const uint4 *)((const uint16_t *)a.q + q_at(a, tok0 + r, h) + c * 8)
-                     : zero4();
-        uint2 *qp = (uint2 *)(qs + r * kRowB + c * 8);
-        qp[0] = make_uint2(qv.x, qv.y);
-        qp[1] = make_uint2(qv.z, qv.w);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int x = tid + 256 * u, r = x / 8, c = x % 8;
-        const uint4 av = *(const uint4 *)(aqg + r * kC + c * 8);
-        uint2 *ap = (uint2 *)(as + r * AS + c * 8);
-        ap[0] = make_uint2(av.x, av.y);
-        ap[1] = make_uint2(av.z, av.w);
-    }
-    if (tid < kC) sm.g[tid] = w.G[ch * kC + tid];
-    Frag8 sf[8], vf[4];
-#pragma unroll
-    for (int st = 0; st < 8; st++) sf[st].u = *(const uint4 *)(sfo + (st * 64 + lane) * 8);
-#pragma unroll
-    for (int st = 0; st < 4; st++) vf[st].u = *(const uint4 *)(vfo + (st * 64 + lane) * 8);
-    __syncthreads();
-    uint2 res[2][4];  // O, packed: token tile tt, the lane's 4 groups of 4 columns
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        const int tok = tt * 32 + col;  // this lane's token (column of O^T)
-        f32x16_t inter, intra;
-#pragma unroll
-        for (int i = 0; i < 16; i++) inter[i] = intra[i] = 0.f;
-        const uint16_t *qr = qs + tok * kRowB + half * 4;
-        const uint16_t *ar = as + tok * AS + half * 4;
-#pragma unroll
-        for (int st = 0; st < 8; st++) {
-            Frag8 bq;
-            const uint2 lo4 = *(const uint2 *)(qr + st * 16), hi4 = *(const uint2 *)(qr + st * 16 + 8);
-            bq.u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
-            inter = mfma32<DT>(sf[st], bq, inter);
-            if (st < 4) {
-                Frag8 ba;
-                const uint2 l2 = *(const uint2 *)(ar + st * 16), h2 = *(const uint2 *)(ar + st * 16 + 8);
-                ba.u = make_uint4(l2.x, l2.y, h2.x, h2.y);
-                intra = mfma32<DT>(vf[st], ba, intra);
-            }
-        }
-        const float f = a.scale * __expf(sm.g[tok]);
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            res[tt][g4].x = pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]);
-            res[tt][g4].y = pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]);
-        }
-    }
-    // O as rows through LDS (the queries' space, dead now), then 16-byte stores along the rows
-    __syncthreads();
-    uint16_t *orow = qs;
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++)
-            *(uint2 *)(orow + (tt * 32 + col) * kRowB + wave * 32 + g4 * 8 + half * 4) = res[tt][g4];
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int x = tid + 256 * u, r = x / 16, c = x % 16;
-        if (r < len && c * 8 < a.Dv) {
-            const uint2 *src = (const uint2 *)(orow + r * kRowB + c * 8);
-            *(uint4 *)((uint16_t *)out + ((tok0 + r) * a.H + h) * a.Dv + c * 8) =
-                make_uint4(src[0].x, src[0].y, src[1].x, src[1].y);
-        }
     }
 }
 
@@ -1116,6 +1187,24 @@ static_assert(kC * kR * 2 <= bl::TOKF - bl::M2T && kC * kR * 2 <= bl::DTT + kC *
                   kC * kR * 2 <= bl::TB - bl::DWT,
               "output rows in dead regions");
 
+#ifdef DM_TRACE_GRADS
+// profiling aid (built only with -DDM_TRACE_GRADS=<chunk x head>): clock stamps of thread 0 of
+// that item at the kernel's barriers
+__device__ uint64_t dm_trace_grads[32];
+#define DM_GSTAMP(k)                                                     \
+    do {                                                                \
+        if (ch == (DM_TRACE_GRADS) && threadIdx.x == 0)                 \
+            dm_trace_grads[k] = __builtin_readcyclecounter();           \
+    } while (0)
+extern "C" int dm_debug_trace_grads(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(dm_trace_grads), bytes) == hipSuccess ? 0 : 1;
+}
+#else
+#define DM_GSTAMP(k) \
+    do {             \
+    } while (0)
+#endif
+
 template <int DT>
 __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
                                                         void *dq, void *dk, void *dv, void *dg,
@@ -1126,6 +1215,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     if (len == 0) return;
     const int64_t tok0 = w.chunk_tok0[n];
     const int tid = threadIdx.x, lane = tid & 63;
+    DM_GSTAMP(0);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
     // wavefront w: columns 32 (w % 4) + [0, 32) of dq, dk, dv at tokens 32 (w / 4) + [0, 32);
@@ -1199,6 +1289,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         for (int x = tid; x < 8 * 256; x += 512) pGam[x] = 0.f;
     }
     __syncthreads();
+    DM_GSTAMP(1);
     // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns and 32 tokens, stored as dV'^T
     {
         const uint16_t *kr = w.Krf + ch * kC * kD;
@@ -1225,6 +1316,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
     }
     __syncthreads();
+    DM_GSTAMP(2);
     // (a) d(gamma q) = dO S^T, (e) dkt = V' dS_{c+1}^T, (f) dw = -dV' S^T: the wave's token tile
     // of its 32 dk columns; (b) d attn = dO V'^T on the wave's tile, zero above the diagonal
     f32x16_t dqg, dkt, dw, datt = zero16();
@@ -1262,6 +1354,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         if (lane == 0) F32(bl::RED)[wave] = acc;
     }
     __syncthreads();  // phase 1 done: S^T, dS^T, V'^T and dO are dead
+    DM_GSTAMP(3);
 
     // ---- phase 2: Q, K (normalised as the forward did, with the inverse norms), V, T ----
     uint4 q2[2], k2[2], v2[2], t2;
@@ -1347,6 +1440,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         store_ct<DT>(sM1T, kT, ti * 32, tj * 32, m, lane);
     }
     __syncthreads();  // Q, K, V, T, dw^T, m1^T in place
+    DM_GSTAMP(4);
     const float scale = a.scale;
     // (d) d attn o attn: + row sums, - column sums into dG
     if (tilew && !(ti == 0 && tj == 1)) {
@@ -1458,6 +1552,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
     }
     __syncthreads();  // dT^T complete
+    DM_GSTAMP(5);
     // (i) m2 = T^T dT on the wave's tile (a, b) = (ti, tj), stored as m2^T
     if (tilew) {
         f32x16_t m2 = zero16();
@@ -1468,6 +1563,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m2, lane);
     }
     __syncthreads();
+    DM_GSTAMP(6);
     // dA = -(m2 T^T) strictly below the diagonal on tile (a, c) = (ti, tj); the recomputed
     // A = beta (K K^T) o decay for the gate's sums; m3 = dA o decay
     f32x16_t m3 = zero16(), m3b = zero16();
@@ -1501,11 +1597,13 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         if (half == 0) pGc[wave * 64 + j] += cs;
     }
     __syncthreads();  // m2^T dead: m3^T takes its place
+    DM_GSTAMP(7);
     if (tilew) {
         store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m3, lane);
         store_ct<DT>(sM3BT, kT, ti * 32, tj * 32, m3b, lane);
     }
     __syncthreads();
+    DM_GSTAMP(8);
     // (j) dkbeta = m3 K: dk += beta dkbeta; d beta sums; dk += m3^T (beta K)
     {
         const int t = tw;
@@ -1560,6 +1658,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
     }
     __syncthreads();
+    DM_GSTAMP(9);
     // per token: dG, then dg = its reverse cumulative sum; d beta
     if (wave == 0) {
         const int i = lane;
@@ -1606,6 +1705,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
     }
     __syncthreads();
+    DM_GSTAMP(10);
     // dq, dk (the scale and the l2 normalisation undone), dv: staged as rows in LDS (regions
     // dead by now), then stored 16 bytes per lane
     uint16_t *oq = U16(bl::DWT), *ok_ = U16(bl::M2T), *ov = U16(bl::TB);
@@ -1631,6 +1731,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         }
     }
     __syncthreads();
+    DM_GSTAMP(11);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int x = tid + 512 * u, r = x / 16, c = x % 16;
@@ -1644,6 +1745,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             if (c * 8 < a.Dv) *(uint4 *)((uint16_t *)dv + ov_) = *(const uint4 *)(ov + r * kR + c * 8);
         }
     }
+    DM_GSTAMP(12);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1666,18 +1768,27 @@ size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { return mfma_layout(d, null
 extern "C" int dm_debug_trace_state(void *host, size_t bytes) {
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(dm_trace_state), bytes) == hipSuccess ? 0 : 1;
 }
+extern "C" int dm_debug_trace_out(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(dm_trace_out), bytes) == hipSuccess ? 0 : 1;
+}
 #endif
 
-// LDS the state passes' launches reserve beyond their own, so that one workgroup takes a
-// compute unit: a chain step whose wavefronts share the compute unit's load, LDS and issue with
-// another workgroup's took 4,000-6,500 cycles against 2,600 alone, and the longest chains, taken
-// first, decide the pass's time (config 4: 265 -> 227 us).
-static unsigned state_lds_extra() { return 80 * 1024; }
+// LDS the state passes' launches take in all (their own plus a dynamic reservation), so that one
+// workgroup takes a compute unit: a chain step whose wavefronts share the compute unit's load,
+// LDS and issue with another workgroup's took 4,000-6,500 cycles against 2,600 alone, and the
+// longest chains, taken first, decide the pass's time (config 4: 265 -> 227 us).
+constexpr unsigned kStateLds = 82 * 1024;
+// the dynamic LDS a launch of `kernel` adds to its own to take kStateLds
 template <typename K>
-static void allow_lds(K kernel, unsigned bytes) {
-    if (bytes > 64 * 1024)
+static unsigned state_lds(K kernel) {
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kernel)) != hipSuccess) return 0;
+    const unsigned own = (unsigned)fa.sharedSizeBytes;
+    const unsigned extra = own >= kStateLds ? 0u : kStateLds - own;
+    if (extra > 64 * 1024)
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)extra);
+    return extra;
 }
 
 int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
@@ -1697,12 +1808,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            allow_lds(gdr_mfma_state2<DM_BF16, kStateParts>, state_lds_extra());
-            gdr_mfma_state2<DM_BF16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds_extra(), st>>>(a, w, h0, final_state);
-        }
-        {
-            KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
-            if (chunks) gdr_mfma_output<DM_BF16><<<chunks, 256, 0, st>>>(a, w, out);
+            gdr_mfma_state2<DM_BF16, kStateParts, true><<<(unsigned)state_grid(seqs), 64 * kStateParts + 128, state_lds(gdr_mfma_state2<DM_BF16, kStateParts, true>), st>>>(a, w, h0, final_state, out);
         }
     } else {
         {
@@ -1711,12 +1817,7 @@ int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, cons
         }
         {
             KernelTimer t(DM_KERNEL_GDR_STATE, st);
-            allow_lds(gdr_mfma_state2<DM_F16, kStateParts>, state_lds_extra());
-            gdr_mfma_state2<DM_F16, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds_extra(), st>>>(a, w, h0, final_state);
-        }
-        {
-            KernelTimer t(DM_KERNEL_GDR_OUTPUT, st);
-            if (chunks) gdr_mfma_output<DM_F16><<<chunks, 256, 0, st>>>(a, w, out);
+            gdr_mfma_state2<DM_F16, kStateParts, true><<<(unsigned)state_grid(seqs), 64 * kStateParts + 128, state_lds(gdr_mfma_state2<DM_F16, kStateParts, true>), st>>>(a, w, h0, final_state, out);
         }
     }
     probe_add(DM_PROBE_GDR_CHUNK_FWD, 4);
@@ -1742,8 +1843,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_STATE, st);
-        allow_lds(gdr_mfma_state2<DT, kStateParts>, state_lds_extra());
-            gdr_mfma_state2<DT, kStateParts><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds_extra(), st>>>(a, w, h0, nullptr);
+        gdr_mfma_state2<DT, kStateParts, false><<<(unsigned)state_grid(seqs), 64 * kStateParts, state_lds(gdr_mfma_state2<DT, kStateParts, false>), st>>>(a, w, h0, nullptr, nullptr);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_PRE, st);
@@ -1751,8 +1851,7 @@ static void gdr_mfma_bwd_kernels(const GdrArgs &a, const MfmaWs &w, unsigned chu
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_STATE, st);
-        allow_lds(gdr_bwd_state2<DT>, state_lds_extra());
-        gdr_bwd_state2<DT><<<(unsigned)state_grid(seqs), 128, state_lds_extra(), st>>>(a, w, d_final, dh0);
+        gdr_bwd_state2<DT><<<(unsigned)state_grid(seqs), 128, state_lds(gdr_bwd_state2<DT>), st>>>(a, w, d_final, dh0);
     }
     {
         KernelTimer t(DM_KERNEL_GDR_BWD_GRADS, st);
