@@ -903,6 +903,34 @@ __device__ __forceinline__ void store_ct(uint16_t *t, int stride, int r0, int c0
 // Sum over the 32 lanes that share lane / 32 (the columns of a product tile).
 __device__ __forceinline__ float sum32(float x) { return group_sum<32>(x); }
 
+// Row sums of a 32x32 product tile held as its output fragment (v[i]: row crow(i, lane), column
+// lane % 32), by a reduce-scatter over the 32 lanes of each half: at each stage a lane keeps half
+// of its values and adds its partner's copy of them, the partners pairing by lane bit 4 (a
+// swizzle), 3 (row_ror 8), 2 (row_half_mirror), 1 and 0 (quad swaps), each pairing lanes that
+// agree on the bits already used. Lane l ends with the sum of value 8 b4 + 4 b3 + 2 b2 + b1
+// (b_k = bit k of l), as do lanes l ^ 1; returns it and that value's row in *row. 31 moves and
+// adds in place of 16 reductions of 5 each.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float tile_rowsum(const float (&v)[16], int lane, int *row) {
+    const bool b4 = lane & 16, b3 = lane & 8, b2 = lane & 4, b1 = lane & 2;
+    float a8[8], a4[4], a2[2];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        a8[k] = (b4 ? v[8 + k] : v[k]) + __shfl_xor(b4 ? v[k] : v[8 + k], 16, 64);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        a4[k] = (b3 ? a8[4 + k] : a8[k]) + dpp_f<0x128>(b3 ? a8[k] : a8[4 + k]);  // row_ror:8
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+        a2[k] = (b2 ? a4[2 + k] : a4[k]) + dpp_f<0x141>(b2 ? a4[k] : a4[2 + k]);  // half mirror
+    const float a1 = (b1 ? a2[1] : a2[0]) + dpp_f<0x4E>(b1 ? a2[0] : a2[1]);  // quad [2,3,0,1]
+    *row = crow(8 * b4 + 4 * b3 + 2 * b2 + b1, lane);
+    return a1 + dpp_f<0xB1>(a1);  // quad [1,0,3,2]
+}
+
 constexpr int kR = kD + 8;  // 128-column tiles (row and transposed reads)
 constexpr int kT = kC + 8;  // 64-column tiles
 
@@ -1445,18 +1473,19 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     // (d) d attn o attn: + row sums, - column sums into dG
     if (tilew && !(ti == 0 && tj == 1)) {
         const int j = tj * 32 + col;
-        float cs = 0.f;
+        float cs = 0.f, p[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = ti * 32 + crow(i, lane);
             const uint16_t ab = sAQ[r * kT + j];
             const float av = (DT == DM_BF16) ? __uint_as_float((uint32_t)ab << 16)
                                              : (float)__builtin_bit_cast(_Float16, ab);
-            const float p = datt[i] * av;
-            cs += p;
-            const float rs = sum32(p);
-            if (col == 0) pGr[wave * 64 + r] += rs;
+            p[i] = datt[i] * av;
+            cs += p[i];
         }
+        int rr;
+        const float rs = tile_rowsum(p, lane, &rr);
+        if (!(lane & 1)) pGr[wave * 64 + ti * 32 + rr] += rs;
         cs += __shfl_xor(cs, 32, 64);
         if (half == 0) pGc[wave * 64 + j] += cs;
     }
@@ -1478,13 +1507,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             dqa[i] = tGam[r] * dqg[i];
             dka[i] = tLam[r] * dkt[i];
         }
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float g1 = sum32(gsum[i]), s1 = sum32(ssum[i]);
-            if (col == 0) {
-                const int r = t * 32 + crow(i, lane);
-                pGam[cw * 64 + r] += g1;
-                pS[cw * 64 + r] += s1;
+        {
+            int rr;
+            const float g1 = tile_rowsum(gsum, lane, &rr), s1 = tile_rowsum(ssum, lane, &rr);
+            if (!(lane & 1)) {
+                pGam[cw * 64 + t * 32 + rr] += g1;
+                pS[cw * 64 + t * 32 + rr] += s1;
             }
         }
         f32x16_t x = zero16();
@@ -1541,13 +1569,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             bs[i] = xb[i] * vv;
             us[i] = xk[i] * kv;
         }
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float b1 = sum32(bs[i]), u1 = sum32(us[i]);
-            if (col == 0) {
-                const int r = t * 32 + crow(i, lane);
-                pBet[cw * 64 + r] += b1;
-                pU[cw * 64 + r] += u1;
+        {
+            int rr;
+            const float b1 = tile_rowsum(bs, lane, &rr), u1 = tile_rowsum(us, lane, &rr);
+            if (!(lane & 1)) {
+                pBet[cw * 64 + t * 32 + rr] += b1;
+                pU[cw * 64 + t * 32 + rr] += u1;
             }
         }
     }
@@ -1578,7 +1605,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             kk = mfma32<DT>(row_frag(sKB, kR, ti * 32, st * 16, lane),
                             row_frag(sKB, kR, tj * 32, st * 16, lane), kk);
         const int j = tj * 32 + col;
-        float cs = 0.f;
+        float cs = 0.f, p[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = ti * 32 + crow(i, lane);
@@ -1586,12 +1613,15 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             const float d = lower ? -da[i] : 0.f;
             const float dec = lower ? __expf(tG[r] - tG[j]) : 0.f;
             const float am = tBet[r] * kk[i] * dec;
-            const float p = d * am;
-            cs += p;
-            const float rs = sum32(p);
-            if (col == 0) pGr[wave * 64 + r] += rs;
+            p[i] = d * am;
+            cs += p[i];
             m3[i] = d * dec;
             m3b[i] = m3[i] * tBet[r];
+        }
+        {
+            int rr;
+            const float rs = tile_rowsum(p, lane, &rr);
+            if (!(lane & 1)) pGr[wave * 64 + ti * 32 + rr] += rs;
         }
         cs += __shfl_xor(cs, 32, 64);
         if (half == 0) pGc[wave * 64 + j] += cs;
@@ -1624,10 +1654,10 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             dka[i] += tBet[r] * xb[i] + xt[i];
             bs[i] = xb[i] * kv;
         }
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float b1 = sum32(bs[i]);
-            if (col == 0) pBet[cw * 64 + crow(i, lane) + t * 32] += b1;
+        {
+            int rr;
+            const float b1 = tile_rowsum(bs, lane, &rr);
+            if (!(lane & 1)) pBet[cw * 64 + t * 32 + rr] += b1;
         }
     }
     // (m) the l2 normalisation's sums: <qn, scale dq>, <kn, dk> per token
@@ -1646,13 +1676,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
                 qs[i] = qv * dqa[i] * scale;
                 ks[i] = kv * dka[i];
             }
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float q1 = sum32(qs[i]), k1 = sum32(ks[i]);
-                if (col == 0) {
-                    const int r = t * 32 + crow(i, lane);
-                    pSq[cw * 64 + r] = q1;
-                    pSk[cw * 64 + r] = k1;
+            {
+                int rr;
+                const float q1 = tile_rowsum(qs, lane, &rr), k1 = tile_rowsum(ks, lane, &rr);
+                if (!(lane & 1)) {
+                    pSq[cw * 64 + t * 32 + rr] = q1;
+                    pSk[cw * 64 + t * 32 + rr] = k1;
                 }
             }
         }
