@@ -39,7 +39,8 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list: attn,attn4096,attn256,decode,gdr,step,conv1d,logprob")
+    p.add_argument("--only", default="",
+                   help="comma list: attn,attn4096,attn256,decode,gdr,step,conv1d,logprob,refshapes")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (torch copy_), 5 times: the known-size "
                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
@@ -102,12 +103,12 @@ def check(rc, lib):
         raise RuntimeError(lib.dm_last_error().decode())
 
 
-def bench_attention(torch, dm, ops, lib, data, steps, warmup, cu=None):
+def bench_attention(torch, dm, ops, lib, data, steps, warmup, cu=None, opts=None):
     """Forward + backward of one batch; returns (ms_step, ms_fwd, ms_bwd)."""
     from dashmag_amd import _lib
     q, k, v, do = data["q"], data["k"], data["v"], data["do"]
     mask = dm.AttentionMask.none() if cu is None else dm.AttentionMask.packed(cu, cu)
-    opts = dm.AttentionOptions(causal=True)
+    opts = opts or dm.AttentionOptions(causal=True)
     keep = []
     desc = ops._attention_desc("attention", q, k, v, mask, opts, keep)
     o = torch.empty_like(q)
@@ -137,6 +138,153 @@ def bench_attention(torch, dm, ops, lib, data, steps, warmup, cu=None):
     ms_step = t.run(steps, warmup)
     bench_attention.ms_plain = t.ms_plain
     return ms_step, ms_fwd, ms_bwd, _lib.probe_counts(), t.kernel_ms
+
+
+def ref_shapes(torch, dm, ops, lib, syn, dev, args):
+    """dash-ops' published device times (crates/dash-ops/README.md:72-88, RTX 5070 Ti, bf16) and
+    this build's for the same work on one MI355X, in ms per call (back-to-back calls between
+    HIP events; inputs from the synthetic generator at those shapes)."""
+    from dashmag_amd import _lib
+    out = {}
+    steps = max(3, args.steps // 2)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def note(name, ms, ref_ms, shape, tm=None, n=None):
+        # short calls: the device's time (the library's kernel timers, summed per call) beside
+        # the back-to-back call time, which the host's dispatch bounds at these sizes; dash-ops'
+        # figures are device times too (sums over nsys's kernels)
+        dev_ms = None
+        if tm is not None:
+            dev_ms = sum(v[0] * v[1] for v in tm.kernel_ms.values()) / n
+        t = dev_ms if dev_ms is not None else ms
+        out[name] = dict(ms=round(t, 4), reference_ms=ref_ms,
+                         reference_over_this=round(ref_ms / t, 2), shape=shape)
+        if dev_ms is not None:
+            out[name]["call_ms_back_to_back"] = round(ms, 4)
+            out[name]["timing"] = "device time (kernel timers)"
+        print(f"reference shape {name}: {t:.4f} ms (dash-ops on an RTX 5070 Ti: {ref_ms} ms)",
+              file=sys.stderr, flush=True)
+
+    # attention forward + backward, T=6144, Hq=8, Hkv=2, D=256 (README.md:83): causal; no mask;
+    # 4 packed sequences of 1536 (causal within each); causal within a window of 1024
+    c = syn.config2_single(dev, t=6144, hq=8, hkv=2, d=256)
+    cu4 = torch.tensor([0, 1536, 3072, 4608, 6144], dtype=torch.int32, device=dev)
+    for name, cu, opts, ref in [
+            ("attention_fwd_bwd_D256_causal", None, dm.AttentionOptions(causal=True), 9.17),
+            ("attention_fwd_bwd_D256_no_mask", None, dm.AttentionOptions(), 17.6),
+            ("attention_fwd_bwd_D256_packed_4x1536", cu4, dm.AttentionOptions(causal=True), 2.59),
+            ("attention_fwd_bwd_D256_window_1024", None,
+             dm.AttentionOptions(causal=True, window=dm.Window(1024, 0)), 3.07)]:
+        ms, _, _, _, _ = bench_attention(torch, dm, ops, lib, c, steps, 1, cu, opts)
+        note(name, ms, ref, "T=6144, Hq=8, Hkv=2, D=256, bf16, deterministic backward")
+    del c
+    # attention forward, T=6144, Hq=8, Hkv=2, D=64 (README.md:84)
+    c = syn.config2_single(dev, t=6144, hq=8, hkv=2, d=64)
+    for name, cu, opts, ref in [
+            ("attention_fwd_D64_causal", None, dm.AttentionOptions(causal=True), 0.528),
+            ("attention_fwd_D64_no_mask", None, dm.AttentionOptions(), 0.902),
+            ("attention_fwd_D64_packed_4x1536", cu4, dm.AttentionOptions(causal=True), 0.145),
+            ("attention_fwd_D64_window_1024", None,
+             dm.AttentionOptions(causal=True, window=dm.Window(1024, 0)), 0.163)]:
+        _, mf, _, _, _ = bench_attention(torch, dm, ops, lib, c, steps, 1, cu, opts)
+        note(name, mf, ref, "T=6144, Hq=8, Hkv=2, D=64, bf16, forward only")
+    del c
+    # attention decoding, batch 8, 6144 cached keys, Hq=8, Hkv=2, D=256 (README.md:85): the
+    # whole cache; lengths from 100 to 6144; a window of 1024
+    c = syn.config3(dev, b=8, hq=8, hkv=2, d=256, s=6144, lo=6144)
+    q, k, v = c["q"], c["k"], c["v"]
+    o = torch.empty_like(q)
+    for name, lens, opts, ref in [
+            ("decode_D256_whole_cache", [6144] * 8, dm.AttentionOptions(), 0.131),
+            ("decode_D256_lengths_100_to_6144", [100 + (6044 * i) // 7 for i in range(8)],
+             dm.AttentionOptions(), 0.036),
+            ("decode_D256_window_1024", [6144] * 8, dm.AttentionOptions(window=dm.Window(1024, 0)),
+             0.015)]:
+        lt = torch.tensor(lens, dtype=torch.int32, device=dev)
+        keep = []
+        desc = ops._attention_desc("attention_decode", q.unsqueeze(1), k, v,
+                                   dm.AttentionMask.none(), opts, keep)
+        nb = lib.dm_attention_decode_workspace(ctypes.byref(desc))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        ptrs = [ctypes.c_void_p(t_.data_ptr()) for t_ in (q, k, v, lt, o, ws)]
+        fn = lambda: check(lib.dm_attention_decode(ctypes.byref(desc), *ptrs[:5], ptrs[5], nb,  # noqa
+                                                   st), lib)
+        n_ = max(args.steps, 50)
+        tm = Timed(torch, fn)
+        ms = tm.run(n_, args.warmup)
+        note(name, ms, ref, "B=8, S=6144, Hq=8, Hkv=2, D=256, bf16", tm, n_)
+    del c, q, k, v, o
+    # chunked gated delta rule forward, and forward + backward, 6144 tokens, 16 heads of 128
+    # (README.md:80): one sequence; four packed sequences of 1536
+    for label, cuts, ref_f, ref_fb in [("1x6144", [0, 6144], 0.81, 2.57),
+                                       ("4x1536", [0, 1536, 3072, 4608, 6144], 0.79, 2.44)]:
+        c = syn.config4(dev, total=6144, nseq=len(cuts) - 1)
+        c["cu_seqlens"] = torch.tensor(cuts, dtype=torch.int32, device=dev)
+        c["h0"] = c["h0"][:len(cuts) - 1].contiguous()
+        keep = []
+        args_t = [c[x] for x in ("q", "k", "v", "g", "beta")]
+        desc, _, _ = ops._gdr_desc("chunk_gated_delta_rule", *args_t, c["cu_seqlens"], False,
+                                   None, False, keep)
+        outg, fin = torch.empty_like(c["v"]), torch.empty_like(c["h0"])
+        nb = lib.dm_gdr_chunk_fwd_workspace(ctypes.byref(desc))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [c["h0"], outg, fin, ws]]
+        fwd = lambda: check(lib.dm_gdr_chunk_fwd(ctypes.byref(desc), *p[:8], p[8], nb, st), lib)  # noqa
+        dq, dk_, dv_ = (torch.empty_like(x) for x in args_t[:3])
+        dg, db, dh0 = torch.empty_like(c["g"]), torch.empty_like(c["beta"]), torch.empty_like(c["h0"])
+        nbb = lib.dm_gdr_chunk_bwd_workspace(ctypes.byref(desc))
+        wsb = torch.empty(max(nbb, 1), dtype=torch.uint8, device=dev)
+        pb = [ctypes.c_void_p(x.data_ptr()) for x in
+              args_t + [c["h0"], c["do"], fin, dq, dk_, dv_, dg, db, dh0, wsb]]
+        bwd = lambda: check(lib.dm_gdr_chunk_bwd(ctypes.byref(desc), *pb[:14], pb[14], nbb, st),  # noqa
+                            lib)
+
+        def both():
+            fwd()
+            bwd()
+
+        ms_f = Timed(torch, fwd).run(steps, 1)
+        ms_fb = Timed(torch, both).run(steps, 1)
+        note(f"gdr_chunk_fwd_{label}", ms_f, ref_f, "6144 tokens, H=16, Dk=Dv=128, bf16")
+        note(f"gdr_chunk_fwd_bwd_{label}", ms_fb, ref_fb, "6144 tokens, H=16, Dk=Dv=128, bf16")
+        del c, ws, wsb
+    # the recurrent decoding step, batch 8, 16 heads of 128 (README.md:82)
+    c = syn.config5(dev, b=8)
+    keep = []
+    args_t = [c[x] for x in ("q", "k", "v", "g", "beta")]
+    desc, _, _ = ops._gdr_desc("gated_delta_step", *args_t, None, False, None, True, keep)
+    outs = torch.empty_like(c["v"])
+    p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [c["state"], c["state"], outs]]
+    fn = lambda: check(lib.dm_gdr_step(ctypes.byref(desc), *p, st), lib)  # noqa
+    n_ = max(args.steps, 100)
+    tm = Timed(torch, fn)
+    ms = tm.run(n_, args.warmup)
+    note("gdr_step_B8", ms, 0.0217, "B=8, H=16, Dk=Dv=128, f32 state, bf16 inputs", tm, n_)
+    del c
+    # causal conv1d forward + backward, 6144 steps, 6144 channels, width 4, SiLU (README.md:88)
+    c = syn.conv1d_config(dev)
+    x = c["x"][:, :6144].contiguous()
+    wt, go = c["weight"], c["go"][:, :6144].contiguous()
+    _, t, ch = x.shape
+    kw = wt.shape[1]
+    desc = _lib.Conv1dDesc(b=1, t=t, c=ch, k=kw, dtype=_lib.DM_BF16, has_bias=0,
+                           activation=_lib.DM_ACT_SILU)
+    outc, gx, gw = torch.empty_like(x), torch.empty_like(x), torch.empty_like(wt)
+    ws = torch.empty(max(lib.dm_causal_conv1d_bwd_workspace(ctypes.byref(desc)), 1),
+                     dtype=torch.uint8, device=dev)
+    P = lambda tt: None if tt is None else ctypes.c_void_p(tt.data_ptr())  # noqa: E731
+
+    def conv():
+        check(lib.dm_causal_conv1d_fwd(ctypes.byref(desc), P(x), P(wt), None, None, P(outc), None,
+                                       st), lib)
+        check(lib.dm_causal_conv1d_bwd(ctypes.byref(desc), P(x), P(wt), None, None, P(go),
+                                       _lib.DM_BF16, None, P(gx), P(gw), None, None, P(ws),
+                                       ws.numel(), st), lib)
+
+    ms = Timed(torch, conv).run(max(args.steps, 50), args.warmup)
+    note("conv1d_fwd_bwd", ms, 0.56, "T=6144, C=6144, K=4, SiLU, bf16")
+    del c, x, go
+    return out
 
 
 def main():
@@ -453,6 +601,11 @@ def main():
               f"{ms_b * 1e3:.1f} us ({bwd_bytes / ms_b / 1e6:.0f} GB/s), step {ms_u * 1e3:.1f} us",
               file=sys.stderr, flush=True)
         del c, x, go, out, gx
+
+    # ---- the shapes dash-ops publishes its own device times for (crates/dash-ops/README.md:72-88,
+    #      one RTX 5070 Ti; context, not a target): the same work here, per call ----
+    if want("refshapes"):
+        secondary["reference_shapes"] = ref_shapes(torch, dm, ops, lib, syn, dev, args)
 
     # ---- chosen-token log-probability, config 7 (after the model: the next row) ----
     if want("logprob"):

@@ -162,7 +162,7 @@ def probe_reset() -> None:
 
 KERNELS = ["attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "decode_split", "gdr_prep", "gdr_state",
            "gdr_output", "gdr_step", "gdr_bwd_pre", "gdr_bwd_state", "gdr_bwd_grads",
-           "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob_stats"]
+           "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob_stats", "decode_merge"]
 
 
 def kernel_timing(enable: bool) -> None:

@@ -17,7 +17,7 @@
 
 namespace dm {
 
-constexpr int kDecodeMinSpan = 512;          // fewest keys a workgroup takes
+constexpr int kDecodeMinSpan = 128;          // fewest keys a workgroup takes (one block a wavefront)
 constexpr int kDecodeWorkgroupsMfma = 4096;  // the split count aims at about this many workgroups
 
 // Where the cache keeps sequence b's keys. Dense: rows b * S .. b * S + S - 1 of k, v
@@ -406,25 +406,32 @@ static bool paged_split_takes(const dm_attention_desc *d, int64_t page_size) {
     return split_takes(d, page_size) && d->d <= 128 && page_size % 16 == 0;
 }
 
-static int span_of(const dm_attention_desc *d) {
-    int64_t span = kDecodeMinSpan;
-    const int64_t heads = d->b * d->hkv;
-    // (at D = 256 one workgroup fills a compute unit, and its wavefronts' sweeps need length:
-    // about one workgroup per compute unit measured best)
-    const int64_t target = d->d == 256 ? kDecodeWorkgroupsMfma / 16 : kDecodeWorkgroupsMfma;
-    while (span < d->tk && heads * ((d->tk + span - 1) / span) > target) span *= 2;
-    return (int)span;
-}
-
-static int nsplit_of(const dm_attention_desc *d) {
-    const int64_t span = span_of(d);
-    return (int)((d->tk + span - 1) / span);
-}
-
 static int64_t left_of(const dm_attention_desc *d) {
     const uint64_t span = (uint64_t)d->tk + 1;  // `bound(left, s + 1)`, reference.rs:449
     const uint64_t left = d->options.has_window ? d->options.window_left : DM_UNBOUNDED;
     return left < span ? (int64_t)left : -1;
+}
+
+// The most keys a sequence's query sees: the cache, or the window's left + 1 (the splits cover
+// the visible keys only; they start at the window's first key).
+static int64_t visible_of(const dm_attention_desc *d) {
+    const int64_t left = left_of(d);
+    return left >= 0 && left + 1 < d->tk ? left + 1 : d->tk;
+}
+
+static int span_of(const dm_attention_desc *d) {
+    int64_t span = kDecodeMinSpan;
+    const int64_t heads = d->b * d->hkv, keys = visible_of(d);
+    // (at D = 256 one workgroup fills a compute unit, and its wavefronts' sweeps need length:
+    // about one workgroup per compute unit measured best)
+    const int64_t target = d->d == 256 ? kDecodeWorkgroupsMfma / 16 : kDecodeWorkgroupsMfma;
+    while (span < keys && heads * ((keys + span - 1) / span) > target) span *= 2;
+    return (int)span;
+}
+
+static int nsplit_of(const dm_attention_desc *d) {
+    const int64_t span = span_of(d), keys = visible_of(d);
+    return (int)((keys + span - 1) / span);
 }
 
 // The checks both entry points share; returns DM_OK or the refusal.
@@ -508,10 +515,13 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
         KernelTimer timer(DM_KERNEL_DECODE_SPLIT, st);
         if (d->dtype == DM_BF16) { DEC_D(DM_BF16); } else { DEC_D(DM_F16); }
     }
-    if (d->dtype == DM_BF16) {
-        decode_merge<DM_BF16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
-    } else {
-        decode_merge<DM_F16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
+    {
+        KernelTimer timer(DM_KERNEL_DECODE_MERGE, st);
+        if (d->dtype == DM_BF16) {
+            decode_merge<DM_BF16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
+        } else {
+            decode_merge<DM_F16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
+        }
     }
 #undef DEC_D
 #undef DEC_GM

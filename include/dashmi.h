@@ -209,7 +209,7 @@ typedef enum {
     DM_KERNEL_DECODE_SPLIT,   /* decode, pass 1 */
     DM_KERNEL_GDR_PREP,       /* chunked gated delta rule: per-chunk preparation */
     DM_KERNEL_GDR_STATE,      /* chunked gated delta rule: the state pass */
-    DM_KERNEL_GDR_OUTPUT,     /* chunked gated delta rule: the output */
+    DM_KERNEL_GDR_OUTPUT,     /* chunked gated delta rule: the output (generic f32 kernels) */
     DM_KERNEL_GDR_STEP,       /* gated delta rule step */
     DM_KERNEL_GDR_BWD_PRE,    /* chunked gated delta rule backward: per-chunk state-gradient terms */
     DM_KERNEL_GDR_BWD_STATE,  /* chunked gated delta rule backward: the state-gradient pass */
@@ -218,6 +218,7 @@ typedef enum {
     DM_KERNEL_CONV1D_BWD,     /* causal conv1d backward: the input gradient and the partial sums */
     DM_KERNEL_CONV1D_UPDATE,  /* causal conv1d decoding step */
     DM_KERNEL_LOGPROB_STATS,  /* chosen-token log-probability: the per-chunk statistics */
+    DM_KERNEL_DECODE_MERGE,   /* decode, pass 2: the splits merged by log-sum-exp */
     DM_KERNEL_COUNT
 } dm_kernel;
 int dm_kernel_timing(int enable);
