@@ -276,25 +276,43 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             qk = fwd ? mfma32<DT>(bk, aq, qk) : mfma32<DT>(aq, bk, qk);
         }
         const int j = tj * 32 + col;
+        // The gates read up front (broadcast reads), then the masked exponentials without
+        // branches: where the mask drops a term its exponent is zeroed (above the diagonal
+        // G_i - G_j > 0) and the result selected away, so no lane waits on another's reads.
+        float gr[16], br[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-            // masked before the exponential (above the diagonal G_i - G_j > 0)
-            const float dec = r >= j ? __expf(sm.g[r] - sm.g[j]) : 0.f;
-            if ((r >> 4) >= (j >> 4)) a_at(sm, r, j) = r > j ? sm.bet[r] * kk[i] * dec : 0.f;
+            gr[i] = sm.g[r];
+            br[i] = sm.bet[r];
+        }
+        const float gj = sm.g[j];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
+            const bool on = r >= j;
+            const float ex = __expf(on ? gr[i] - gj : 0.f);
+            const float dec = on ? ex : 0.f;
+            if ((r >> 4) >= (j >> 4)) a_at(sm, r, j) = r > j ? br[i] * kk[i] * dec : 0.f;
             if (!fwd) {
-                const uint32_t p2 = pack2<DT>(r >= j ? qk[i] * dec * a.scale : 0.f, 0.f);
+                const uint32_t p2 = pack2<DT>(on ? qk[i] * dec * a.scale : 0.f, 0.f);
                 aq_out[r * kC + j] = (uint16_t)(p2 & 0xffffu);
             }
         }
         if (fwd) {
             // element i: key kr = 32 tj + crow(i), query qj = 32 ti + col
             const int qj = ti * 32 + col;
+            float gk[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) gk[i] = sm.g[tj * 32 + (i / 4) * 8 + half * 4 + (i % 4)];
+            const float gq = sm.g[qj];
             f32x16_t v;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int kr = tj * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                v[i] = kr <= qj ? qk[i] * __expf(sm.g[qj] - sm.g[kr]) * a.scale : 0.f;
+                const bool on = kr <= qj;
+                const float ex = __expf(on ? gq - gk[i] : 0.f);
+                v[i] = on ? qk[i] * ex * a.scale : 0.f;
             }
             uint16_t *af = w.Af + ch * kC * kC;
 #pragma unroll
