@@ -1251,6 +1251,25 @@ extern "C" int dm_debug_trace_grads(void *host, size_t bytes) {
     } while (0)
 #endif
 
+// A 16-bit tile's values at a product output's positions (rows r0 + crow(i, lane), column
+// c0 + lane % 32), as f32: two transposed reads (ds_read_b64_tr_b16 hands lane l the rows
+// r0 + 8 j + 4 (l / 32) + e of its column in slot 4 j + e, i.e. rows crow(i) for i < 8) in place
+// of 16 two-byte reads.
+template <int DT>
+__device__ __forceinline__ void tile_at_out(const uint16_t *t, int stride, int r0, int c0, int lane,
+                                            float (&v)[16]) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const Frag8 f = lds_tr_frag(t, stride, r0 + 16 * hh, c0, lane);
+        const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[8 * hh + 2 * e] = unpack_lo<DT>(w4[e]);
+            v[8 * hh + 2 * e + 1] = unpack_hi<DT>(w4[e]);
+        }
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
                                                         void *dq, void *dk, void *dv, void *dg,
@@ -1491,13 +1510,11 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     // (d) d attn o attn: + row sums, - column sums into dG
     if (tilew && !(ti == 0 && tj == 1)) {
         const int j = tj * 32 + col;
-        float cs = 0.f, p[16];
+        float cs = 0.f, p[16], avs[16];
+        tile_at_out<DT>(sAQ, kT, ti * 32, tj * 32, lane, avs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = ti * 32 + crow(i, lane);
-            const uint16_t ab = sAQ[r * kT + j];
-            const float av = (DT == DM_BF16) ? __uint_as_float((uint32_t)ab << 16)
-                                             : (float)__builtin_bit_cast(_Float16, ab);
+            const float av = avs[i];
             p[i] = datt[i] * av;
             cs += p[i];
         }
@@ -1511,15 +1528,13 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     f32x16_t dqa, dka, dva;
     {
         const int t = tw;
-        float gsum[16], ssum[16];
+        float gsum[16], ssum[16], qvs[16], kvs[16];
+        tile_at_out<DT>(sQB, kR, t * 32, cw * 32, lane, qvs);
+        tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
-            const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
-            const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
-                                             : (float)__builtin_bit_cast(_Float16, qb);
-            const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
-                                             : (float)__builtin_bit_cast(_Float16, kb);
+            const int r = t * 32 + crow(i, lane);
+            const float qv = qvs[i], kv = kvs[i];
             gsum[i] = dqg[i] * qv * scale;
             ssum[i] = dkt[i] * kv;
             dqa[i] = tGam[r] * dqg[i];
@@ -1573,15 +1588,13 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             xb = mfma32<DT>(ta, row_frag(sDVLO, kT, cw * 32, st * 16, lane), xb);
             xk = mfma32<DT>(ta, row_frag(sDWT, kT, cw * 32, st * 16, lane), xk);
         }
-        float bs[16], us[16];
+        float bs[16], us[16], vvs[16], kvs[16];
+        tile_at_out<DT>(sVB, kR, t * 32, cw * 32, lane, vvs);
+        tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
-            const uint16_t vb = sVB[r * kR + c], kb = sKB[r * kR + c];
-            const float vv = (DT == DM_BF16) ? __uint_as_float((uint32_t)vb << 16)
-                                             : (float)__builtin_bit_cast(_Float16, vb);
-            const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
-                                             : (float)__builtin_bit_cast(_Float16, kb);
+            const int r = t * 32 + crow(i, lane);
+            const float vv = vvs[i], kv = kvs[i];
             dva[i] = tBet[r] * xb[i];
             dka[i] += tBet[r] * tGam[r] * xk[i];
             bs[i] = xb[i] * vv;
@@ -1662,13 +1675,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             xb = mfma32<DT>(lds_tr_frag(sM2T, kT, st * 16, t * 32, lane), kb, xb);
             xt = mfma32<DT>(row_frag(sM3BT, kT, t * 32, st * 16, lane), kb, xt);
         }
-        float bs[16];
+        float bs[16], kvs[16];
+        tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
-            const uint16_t kb = sKB[r * kR + c];
-            const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
-                                             : (float)__builtin_bit_cast(_Float16, kb);
+            const int r = t * 32 + crow(i, lane);
+            const float kv = kvs[i];
             dka[i] += tBet[r] * xb[i] + xt[i];
             bs[i] = xb[i] * kv;
         }
@@ -1682,15 +1694,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     if (a.l2norm) {
         {
             const int t = tw;
-            float qs[16], ks[16];
+            float qs[16], ks[16], qvs[16], kvs[16];
+            tile_at_out<DT>(sQB, kR, t * 32, cw * 32, lane, qvs);
+            tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const int r = t * 32 + crow(i, lane), c = cw * 32 + col;
-                const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
-                const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
-                                                 : (float)__builtin_bit_cast(_Float16, qb);
-                const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
-                                                 : (float)__builtin_bit_cast(_Float16, kb);
+                const float qv = qvs[i], kv = kvs[i];
                 qs[i] = qv * dqa[i] * scale;
                 ks[i] = kv * dka[i];
             }
