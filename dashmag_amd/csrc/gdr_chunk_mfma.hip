@@ -20,8 +20,11 @@
 //                    output O^T = scale gamma (S^T Q^T) + V'^T Aqk^T from S and V' handed over
 //                    in LDS; the backward's run stores S and V' as operand fragments instead.
 // Notation as chunk/reference.rs:11-18 (Q scaled, G_last the chunk's last cumulative gate).
+#include <mutex>
 #include <string>
+#include <tuple>
 #include <type_traits>
+#include <vector>
 
 #include "attention_kernels.h"
 #include "gdr_common.h"
@@ -1834,17 +1837,30 @@ extern "C" int dm_debug_trace_out(void *host, size_t bytes) {
 // LDS and issue with another workgroup's took 4,000-6,500 cycles against 2,600 alone, and the
 // longest chains, taken first, decide the pass's time (config 4: 265 -> 227 us).
 constexpr unsigned kStateLds = 82 * 1024;
-// the dynamic LDS a launch of `kernel` adds to its own to take kStateLds
+// the dynamic LDS a launch of `kernel` adds to its own to take kStateLds (worked out, and the
+// kernel's dynamic-LDS limit raised, once per device and kernel)
+static unsigned state_lds_of(const void *kernel) {
+    static std::mutex mu;
+    static std::vector<std::tuple<int, const void *, unsigned>> known;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto &e : known)
+        if (std::get<0>(e) == dev && std::get<1>(e) == kernel) return std::get<2>(e);
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return 0;
+    const unsigned own = (unsigned)fa.sharedSizeBytes;
+    unsigned extra = own >= kStateLds ? 0u : kStateLds - own;
+    if (extra > 64 * 1024 &&
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)extra) !=
+            hipSuccess)
+        extra = 0;  // (then workgroups may share a compute unit: slower, still correct)
+    known.emplace_back(dev, kernel, extra);
+    return extra;
+}
 template <typename K>
 static unsigned state_lds(K kernel) {
-    hipFuncAttributes fa{};
-    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kernel)) != hipSuccess) return 0;
-    const unsigned own = (unsigned)fa.sharedSizeBytes;
-    const unsigned extra = own >= kStateLds ? 0u : kStateLds - own;
-    if (extra > 64 * 1024)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)extra);
-    return extra;
+    return state_lds_of(reinterpret_cast<const void *>(kernel));
 }
 
 int launch_gdr_mfma_fwd(const dm_gdr_desc *d, const void *q, const void *k, const void *v,
