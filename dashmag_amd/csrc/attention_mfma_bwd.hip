@@ -223,13 +223,25 @@ __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t
     };
     for (int64_t x = tid; x < nwork; x += 1024) atomicAdd(&hist[bucket(x)], 1);
     __syncthreads();
-    if (tid == 0) {  // exclusive offsets, the largest bucket first
-        int32_t run = 0;
-        for (int x = kOrderBuckets - 1; x >= 0; x--) {
-            const int32_t c = hist[x];
-            hist[x] = run;
-            run += c;
+    {
+        // exclusive offsets, the largest bucket first: thread t takes bucket 1023 - t, a scan
+        // within each wavefront, then over the wavefronts' totals
+        static_assert(kOrderBuckets == 1024, "one bucket per thread");
+        __shared__ int32_t wtot[16];
+        const int lane = tid & 63, wv = tid >> 6;
+        const int x = kOrderBuckets - 1 - tid;
+        const int32_t c = hist[x];
+        int32_t incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
         }
+        if (lane == 63) wtot[wv] = incl;
+        __syncthreads();
+        int32_t before = 0;
+        for (int u = 0; u < wv; u++) before += wtot[u];
+        hist[x] = before + incl - c;
     }
     __syncthreads();
     for (int64_t x = tid; x < nwork; x += 1024) w.order[atomicAdd(&hist[bucket(x)], 1)] = (int32_t)x;
