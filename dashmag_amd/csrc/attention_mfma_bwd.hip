@@ -105,21 +105,35 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
         w.rlo[row] = (int32_t)lo;
         w.rhi[row] = (int32_t)hi;
     }
-    constexpr int CH = D / 8;  // 16-byte chunks per head row
-    for (int64_t h = lane / CH; h < Hq; h += 64 / CH) {
-        const int c = lane % CH;
-        const uint4 a = *(const uint4 *)(o + b * sd.o.b + i * sd.o.t + h * sd.o.h + c * 8);
-        const uint4 g = *(const uint4 *)(d_o + b * sd.g.b + i * sd.g.t + h * sd.g.h + c * 8);
-        float s = unpack_lo<DT>(a.x) * unpack_lo<DT>(g.x) + unpack_hi<DT>(a.x) * unpack_hi<DT>(g.x) +
-                  unpack_lo<DT>(a.y) * unpack_lo<DT>(g.y) + unpack_hi<DT>(a.y) * unpack_hi<DT>(g.y) +
-                  unpack_lo<DT>(a.z) * unpack_lo<DT>(g.z) + unpack_hi<DT>(a.z) * unpack_hi<DT>(g.z) +
-                  unpack_lo<DT>(a.w) * unpack_lo<DT>(g.w) + unpack_hi<DT>(a.w) * unpack_hi<DT>(g.w);
+    constexpr int CH = D / 8;       // 16-byte chunks per head row
+    constexpr int HPI = 64 / CH;    // heads a wavefront covers at once
+    constexpr int U = 8;            // rounds whose loads are issued together
+    const int c = lane % CH;
+    for (int64_t h0 = lane / CH; h0 < Hq; h0 += HPI * U) {
+        uint4 a[U], g[U];
+        float l[U];
 #pragma unroll
-        for (int off = CH / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-        if (c == 0) {
-            delta[row * Hq + h] = s;
-            const float l = lse[row * Hq + h];
-            w.lse2[row * Hq + h] = l == -INFINITY ? INFINITY : l * 1.4426950408889634f;
+        for (int u = 0; u < U; u++) {
+            const int64_t h = h0 + u * HPI;
+            const bool ok = h < Hq;
+            const int64_t hh = ok ? h : h0;
+            a[u] = *(const uint4 *)(o + b * sd.o.b + i * sd.o.t + hh * sd.o.h + c * 8);
+            g[u] = *(const uint4 *)(d_o + b * sd.g.b + i * sd.g.t + hh * sd.g.h + c * 8);
+            l[u] = lse[row * Hq + hh];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t h = h0 + u * HPI;
+            float s = unpack_lo<DT>(a[u].x) * unpack_lo<DT>(g[u].x) + unpack_hi<DT>(a[u].x) * unpack_hi<DT>(g[u].x) +
+                      unpack_lo<DT>(a[u].y) * unpack_lo<DT>(g[u].y) + unpack_hi<DT>(a[u].y) * unpack_hi<DT>(g[u].y) +
+                      unpack_lo<DT>(a[u].z) * unpack_lo<DT>(g[u].z) + unpack_hi<DT>(a[u].z) * unpack_hi<DT>(g[u].z) +
+                      unpack_lo<DT>(a[u].w) * unpack_lo<DT>(g[u].w) + unpack_hi<DT>(a[u].w) * unpack_hi<DT>(g[u].w);
+#pragma unroll
+            for (int off = CH / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+            if (c == 0 && h < Hq) {
+                delta[row * Hq + h] = s;
+                w.lse2[row * Hq + h] = l[u] == -INFINITY ? INFINITY : l[u] * 1.4426950408889634f;
+            }
         }
     }
 }
