@@ -111,7 +111,7 @@ struct PrepSmem {
     uint4 k[kC * kRowS / 8];  // keys, rows; later beta V rows; later W rows
     uint4 q[kC * kRowS / 8];  // queries, rows; later T (f32)
     float a[10][16][20];      // A's blocks (bi, bj), bi >= bj, at bi (bi + 1) / 2 + bj; f32
-    float mm[3][16][20];      // T's off-diagonal block products
+    float mm[4][16][20];      // T's off-diagonal block products
     float g[kC], gam[kC], bet[kC], lam[kC];
 };
 static_assert(sizeof(float) * kC * (kC + 4) <= sizeof(uint4) * kC * kRowS / 8, "T in q");
@@ -377,56 +377,74 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         }
     }
     __syncthreads();
-    // Off-diagonal blocks, one block diagonal (lev = i - j) at a time, wave j taking block
-    // (j + lev, j): M = sum_{k = j}^{i - 1} A_ik T_kj, then T_ij = -T_ii M. Lane: column
-    // cc = lane % 16 and rows 4 (lane / 16) + e.
+    // Off-diagonal blocks by doubling (T of a block-lower-triangular matrix from its diagonal
+    // blocks' inverses). Step 1, the 32 x 32 diagonal halves: waves 0 and 1 form
+    // M = A_{b+1,b} T_bb, then T_{b+1,b} = -T_{b+1,b+1} M (b = 0, 2). Step 2, the lower-left 32 x 32
+    // quarter: wave w forms block (i, j) = (2 + w / 2, w % 2) of X = A[2:4, 0:2] T[0:2, 0:2],
+    // then of T[2:4, 0:2] = -T[2:4, 2:4] X. Lane: column cc = lane % 16, rows 4 (lane / 16) + e.
     {
         const int cc = lane & 15, r0 = 4 * (lane >> 4);
-        auto level = [&](auto levc) {
-            constexpr int lev = decltype(levc)::value;
-            const int bj = wave, bi = wave + lev;
-            if (wave < 4 - lev) {
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        // acc[e] += sum_y A(16 bi + r0 + e, 16 kb + y) T(16 kb + y, 16 bj + cc)
+        auto a_times_t = [&](float (&acc)[4], int bi, int kb, int bj) {
+            float tcol[16];
 #pragma unroll
-                for (int kk = 0; kk < lev; kk++) {
-                    const int kb_ = bj + kk;
-                    float tcol[16];
+            for (int y = 0; y < 16; y++) tcol[y] = tt[16 * kb + y][16 * bj + cc];
 #pragma unroll
-                    for (int y = 0; y < 16; y++) tcol[y] = tt[16 * kb_ + y][16 * bj + cc];
+            for (int e = 0; e < 4; e++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-#pragma unroll
-                        for (int y4 = 0; y4 < 16; y4 += 4) {
-                            const float4 a4 = *(const float4 *)&a_at(sm, 16 * bi + r0 + e, 16 * kb_ + y4);
-                            acc[e] += a4.x * tcol[y4] + a4.y * tcol[y4 + 1] + a4.z * tcol[y4 + 2] +
-                                      a4.w * tcol[y4 + 3];
-                        }
+                for (int y4 = 0; y4 < 16; y4 += 4) {
+                    const float4 a4 = *(const float4 *)&a_at(sm, 16 * bi + r0 + e, 16 * kb + y4);
+                    acc[e] += a4.x * tcol[y4] + a4.y * tcol[y4 + 1] + a4.z * tcol[y4 + 2] +
+                              a4.w * tcol[y4 + 3];
                 }
-#pragma unroll
-                for (int e = 0; e < 4; e++) mm[wave][r0 + e][cc] = acc[e];
-            }
-            __syncthreads();
-            if (wave < 4 - lev) {
-                float mcol[16];
-#pragma unroll
-                for (int y = 0; y < 16; y++) mcol[y] = mm[wave][y][cc];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float s = 0.f;
-#pragma unroll
-                    for (int y4 = 0; y4 < 16; y4 += 4) {
-                        const float4 t4 = *(const float4 *)&tt[16 * bi + r0 + e][16 * bi + y4];
-                        s += t4.x * mcol[y4] + t4.y * mcol[y4 + 1] + t4.z * mcol[y4 + 2] +
-                             t4.w * mcol[y4 + 3];
-                    }
-                    tt[16 * bi + r0 + e][16 * bj + cc] = -s;
-                }
-            }
-            __syncthreads();
         };
-        level(std::integral_constant<int, 1>{});
-        level(std::integral_constant<int, 2>{});
-        level(std::integral_constant<int, 3>{});
+        // acc[e] += sum_y T(16 bi + r0 + e, 16 kb + y) X_m(y, cc)
+        auto t_times_m = [&](float (&acc)[4], int bi, int kb, int m) {
+            float mcol[16];
+#pragma unroll
+            for (int y = 0; y < 16; y++) mcol[y] = mm[m][y][cc];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int y4 = 0; y4 < 16; y4 += 4) {
+                    const float4 t4 = *(const float4 *)&tt[16 * bi + r0 + e][16 * kb + y4];
+                    acc[e] += t4.x * mcol[y4] + t4.y * mcol[y4 + 1] + t4.z * mcol[y4 + 2] +
+                              t4.w * mcol[y4 + 3];
+                }
+        };
+        if (wave < 2) {
+            const int bj = 2 * wave, bi = bj + 1;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            a_times_t(acc, bi, bj, bj);
+#pragma unroll
+            for (int e = 0; e < 4; e++) mm[wave][r0 + e][cc] = acc[e];
+        }
+        __syncthreads();
+        if (wave < 2) {
+            const int bj = 2 * wave, bi = bj + 1;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            t_times_m(acc, bi, bi, wave);
+#pragma unroll
+            for (int e = 0; e < 4; e++) tt[16 * bi + r0 + e][16 * bj + cc] = -acc[e];
+        }
+        __syncthreads();
+        const int bi = 2 + (wave >> 1), bj = wave & 1;
+        {
+            // X_{bi,bj} = sum over k = bj .. 1 of A_{bi,k} T_{k,bj} (T_{0,1} = 0)
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = bj; kb < 2; kb++) a_times_t(acc, bi, kb, bj);
+#pragma unroll
+            for (int e = 0; e < 4; e++) mm[wave][r0 + e][cc] = acc[e];
+        }
+        __syncthreads();
+        {
+            // T_{bi,bj} = -(sum over k = 2 .. bi of T_{bi,k} X_{k,bj}); X_{k,bj} is wave 2 (k - 2) + bj's
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = 2; kb <= bi; kb++) t_times_m(acc, bi, kb, 2 * (kb - 2) + bj);
+#pragma unroll
+            for (int e = 0; e < 4; e++) tt[16 * bi + r0 + e][16 * bj + cc] = -acc[e];
+        }
+        __syncthreads();
     }
 
     // W = (T diag(beta gamma)) K, then U = T (beta V): 8 output tiles each (2 token rows x 4
