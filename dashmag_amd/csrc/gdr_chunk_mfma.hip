@@ -355,16 +355,17 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         float tc[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            float s = 0.f;
+            // four partial sums (by x mod 4), so a row waits on about i / 4 dependent products
+            float sp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int x4 = 0; x4 < i; x4 += 4) {
                 const float4 a4 = *(const float4 *)&a_at(sm, 16 * b + i, 16 * b + x4);
                 const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    if (x4 + e < i) s += av[e] * tc[x4 + e];
+                    if (x4 + e < i) sp[e] += av[e] * tc[x4 + e];
             }
-            tc[i] = (i == c ? 1.f : 0.f) - s;
+            tc[i] = (i == c ? 1.f : 0.f) - ((sp[0] + sp[1]) + (sp[2] + sp[3]));
         }
         if (lane < 16) {
 #pragma unroll
