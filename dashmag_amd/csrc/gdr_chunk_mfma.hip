@@ -1320,6 +1320,18 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     float *pGam = F32(bl::PART), *pU = pGam + 256, *pS = pGam + 512, *pBet = pGam + 768,
           *pGr = pGam + 1024, *pGc = pGam + 1280, *pSq = pGam + 1536, *pSk = pGam + 1792;
 
+    // dV''s first products' operands, (lam K) and dS_{c+1} fragments, loaded with phase 1's rows
+    // (they are used straight from registers after its barrier)
+    Frag8 dv_ka[8], dv_db[8];
+    {
+        const uint16_t *kr = w.Krf + ch * kC * kD;
+        const uint16_t *dsf = w.dSf + ch * kD * kD + (size_t)cw * 8 * 64 * 8;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            dv_ka[st].u = *(const uint4 *)(kr + ((tw * 8 + st) * 64 + lane) * 8);
+            dv_db[st].u = *(const uint4 *)(dsf + (st * 64 + lane) * 8);
+        }
+    }
     // ---- phase 1: per-token values; S^T, dS^T, V'^T from their fragments; dO, Aqk rows ----
     {
         const uint16_t *sf = w.Sf + ch * kD * kD, *dsf = w.dSf + ch * kD * kD;
@@ -1379,18 +1391,11 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     DM_GSTAMP(1);
     // dV' = (lam K) dS_{c+1} + Aqk^T dO for the wave's 32 columns and 32 tokens, stored as dV'^T
     {
-        const uint16_t *kr = w.Krf + ch * kC * kD;
-        const uint16_t *dsf = w.dSf + ch * kD * kD + (size_t)cw * 8 * 64 * 8;
         const int t = tw;
         {
             f32x16_t x = zero16();
 #pragma unroll
-            for (int st = 0; st < 8; st++) {
-                Frag8 ka, db;
-                ka.u = *(const uint4 *)(kr + ((t * 8 + st) * 64 + lane) * 8);
-                db.u = *(const uint4 *)(dsf + (st * 64 + lane) * 8);
-                x = mfma32<DT>(ka, db, x);
-            }
+            for (int st = 0; st < 8; st++) x = mfma32<DT>(dv_ka[st], dv_db[st], x);
 #pragma unroll
             for (int st = 0; st < 4; st++)
                 x = mfma32<DT>(lds_tr_frag(sAQ, kT, st * 16, t * 32, lane),
