@@ -1,0 +1,116 @@
+"""The hot path under HIP graph capture: callers that replay a captured step (serving loops,
+training steps under torch.cuda.graphs) call the C ABI with descriptors and workspaces prepared
+beforehand, on the capturing stream. Each op is run eagerly once (the library's one-time set-up:
+kernel attributes), captured, then the graph is replayed several times with other device work and
+synchronisations between the replays; every replay must equal the eager call to the bit (the
+kernels are deterministic and none of them records a memset)."""
+import ctypes
+
+import pytest
+import torch
+
+import dashmag_amd as dm
+from dashmag_amd import _lib, ops, synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(rc, lib):
+    assert rc == 0, lib.dm_last_error().decode()
+
+
+def _replays(fn, outs, n=3):
+    """Eager outputs, then n graph replays of fn compared with them bit for bit."""
+    fn()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    for o in outs:
+        o.fill_(float("nan")) if o.is_floating_point() else o.zero_()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    torch.cuda.synchronize()
+    for r in range(n):
+        for o in outs:
+            o.fill_(float("nan")) if o.is_floating_point() else o.zero_()
+        junk = torch.randn(1 << 20, device="cuda") * (r + 1)  # other device work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for a, e in zip(outs, eager):
+            assert torch.equal(a, e), f"replay {r} differs"
+        del junk
+
+
+def test_attention_fwd_bwd_packed_graph():
+    lib = _lib.lib()
+    c = syn.config2("cuda", total=2048)
+    q, k, v, do, cu = c["q"], c["k"], c["v"], c["do"], c["cu_seqlens"]
+    keep = []
+    mask = dm.AttentionMask.packed(cu, cu)
+    desc = ops._attention_desc("attention", q, k, v, mask, dm.AttentionOptions(causal=True), keep)
+    o, lse = torch.empty_like(q), torch.empty(q.shape[:3], dtype=torch.float32, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    nb = max(lib.dm_attention_fwd_workspace(ctypes.byref(desc)),
+             lib.dm_attention_bwd_workspace(ctypes.byref(desc)), 1)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    P = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o, lse, do, dq, dk, dv, ws)]
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _check(lib.dm_attention_fwd(ctypes.byref(desc), P[0], P[1], P[2], P[3], P[4], P[9], nb, st), lib)
+        _check(lib.dm_attention_bwd(ctypes.byref(desc), P[0], P[1], P[2], P[3], P[4], P[5], P[6],
+                                    P[7], P[8], P[9], nb, st), lib)
+
+    _replays(fn, [o, lse, dq, dk, dv])
+
+
+def test_gdr_chunk_fwd_bwd_graph():
+    lib = _lib.lib()
+    c = syn.config4("cuda", total=3000, nseq=3)
+    keep = []
+    args_t = [c[x] for x in ("q", "k", "v", "g", "beta")]
+    desc, _, _ = ops._gdr_desc("chunk_gated_delta_rule", *args_t, c["cu_seqlens"], False, None,
+                               False, keep)
+    out, fin = torch.empty_like(c["v"]), torch.empty_like(c["h0"])
+    dq, dk, dv = (torch.empty_like(x) for x in args_t[:3])
+    dg, db, dh0 = torch.empty_like(c["g"]), torch.empty_like(c["beta"]), torch.empty_like(c["h0"])
+    nf = max(lib.dm_gdr_chunk_fwd_workspace(ctypes.byref(desc)), 1)
+    nbw = max(lib.dm_gdr_chunk_bwd_workspace(ctypes.byref(desc)), 1)
+    wf = torch.empty(nf, dtype=torch.uint8, device="cuda")
+    wb = torch.empty(nbw, dtype=torch.uint8, device="cuda")
+    p = [ctypes.c_void_p(x.data_ptr()) for x in args_t + [c["h0"], out, fin, wf]]
+    pb = [ctypes.c_void_p(x.data_ptr()) for x in
+          args_t + [c["h0"], c["do"], fin, dq, dk, dv, dg, db, dh0, wb]]
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _check(lib.dm_gdr_chunk_fwd(ctypes.byref(desc), *p[:8], p[8], nf, st), lib)
+        _check(lib.dm_gdr_chunk_bwd(ctypes.byref(desc), *pb[:14], pb[14], nbw, st), lib)
+
+    _lib.probe_reset()
+    _replays(fn, [out, fin, dq, dk, dv, dg, db, dh0])
+    pc = _lib.probe_counts()
+    assert pc["gdr_chunk_fwd_mfma"] > 0 and pc["gdr_chunk_bwd_mfma"] > 0, pc
+
+
+def test_decode_graph():
+    lib = _lib.lib()
+    c = syn.config3("cuda", b=8, s=2048, lo=100)
+    q, k, v, lens = c["q"], c["k"], c["v"], c["lengths"]
+    keep = []
+    desc = ops._attention_desc("attention_decode", q.unsqueeze(1), k, v, dm.AttentionMask.none(),
+                               dm.AttentionOptions(), keep)
+    o = torch.empty_like(q)
+    nb = max(lib.dm_attention_decode_workspace(ctypes.byref(desc)), 1)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    P = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, lens, o, ws)]
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _check(lib.dm_attention_decode(ctypes.byref(desc), *P[:5], P[5], nb, st), lib)
+
+    _replays(fn, [o])
