@@ -613,6 +613,20 @@ static int cv1_check(const dm_conv1d_desc *d, const char *op, bool step) {
     return DM_OK;
 }
 
+// compute units of the current device (256 on MI355X), read once
+static int cv1_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        cus = hipGetDevice(&dev) == hipSuccess &&
+                      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                      n > 0
+                  ? n
+                  : 256;
+    }
+    return cus;
+}
+
 static int64_t cv1_nseq(const dm_conv1d_desc *d) { return d->cu_seqlens ? d->nseq : d->b; }
 
 // the vector width (channels per thread) a call takes: 16 bytes of channels when C divides
@@ -638,9 +652,13 @@ static Cv1Args cv1_args(const dm_conv1d_desc *d, bool bwd = false) {
     a.silu = d->activation == DM_ACT_SILU ? 1 : 0;
     const int vec = cv1_vec(d, bwd);
     a.cv = (d->c + vec - 1) / vec;
-    // segments: about 256K threads in all, at most 256 segments of at least 16 steps
-    int64_t nseg = (256 * 1024 + a.cv - 1) / std::max<int64_t>(a.cv, 1);
-    nseg = std::min<int64_t>(nseg, 256);
+    // segments: three workgroups of 256 threads per compute unit in all (measured on config 6's
+    // shape over 1.3-6 workgroups per compute unit, both directions: the backward 331 us at 4.0
+    // and 268 us at 3, the forward 193 us at 4 and 182-186 us at 3; at 3.3-3.5 both slow by 7%, as
+    // some compute units then hold a fourth), at most 512 segments of at least 16 steps
+    const int64_t gx = (a.cv + kCv1Threads - 1) / kCv1Threads;
+    int64_t nseg = 3 * cv1_cus() / std::max<int64_t>(gx, 1);
+    nseg = std::min<int64_t>(nseg, 512);
     nseg = std::min<int64_t>(nseg, (a.rows + 15) / 16);
     nseg = std::max<int64_t>(nseg, 1);
     a.seg_len = (a.rows + nseg - 1) / nseg;
