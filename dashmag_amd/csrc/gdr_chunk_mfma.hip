@@ -1292,6 +1292,61 @@ __device__ __forceinline__ void tile_at_out(const uint16_t *t, int stride, int r
     }
 }
 
+// Unpadded 16-bit tiles of W = 128 or 64 columns with their 16-byte column chunks permuted by
+// row (chunk m of row r at m ^ f(r)): the transposed fragment reads (4 rows x 64 bytes a pass of
+// 32 lanes), 16-byte reads and writes of 16 consecutive rows at one column, and 16-byte row
+// writes are all free of bank conflicts at 64 banks of 4 bytes; 8-byte accesses of 32 rows at one
+// column are 2-way, as with padded rows. (Rows padded to 272 or 144 bytes had made every
+// transposed read of the 128-column tiles a 4-way conflict and of the 64-column tiles 2-way.)
+template <int W>
+__device__ __forceinline__ int sw(int r, int c) {
+    const int f = W == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    return r * W + ((((c >> 3) ^ f)) << 3) + (c & 7);
+}
+template <int W>
+__device__ __forceinline__ Frag8 lds_tr_sw(const uint16_t *tile, int k0, int c0, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int row = k0 + 4 * (g >> 1) + (i >> 2);
+    const int colx = c0 + 16 * (g & 1) + 4 * (i & 3);
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row, colx)));
+    s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row + 8, colx)));
+    Frag8 f;
+    __builtin_memcpy(&f.u.x, &a, 8);
+    __builtin_memcpy(&f.u.z, &b, 8);
+    return f;
+}
+template <int W>
+__device__ __forceinline__ Frag8 row_frag_sw(const uint16_t *t, int r0, int k0, int lane) {
+    const int r = r0 + (lane & 31), c = k0 + (lane >> 5) * 4;
+    const uint2 lo = *(const uint2 *)(t + sw<W>(r, c)), hi = *(const uint2 *)(t + sw<W>(r, c + 8));
+    Frag8 f;
+    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    return f;
+}
+template <int DT, int W>
+__device__ __forceinline__ void store_ct_sw(uint16_t *t, int r0, int c0, const f32x16_t &v, int lane,
+                                            float f = 1.f) {
+    const int r = c0 + (lane & 31), c = r0 + (lane >> 5) * 4;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        *(uint2 *)(t + sw<W>(r, c + g * 8)) = make_uint2(pack2<DT>(v[4 * g] * f, v[4 * g + 1] * f),
+                                                        pack2<DT>(v[4 * g + 2] * f, v[4 * g + 3] * f));
+}
+template <int DT, int W>
+__device__ __forceinline__ void tile_at_out_sw(const uint16_t *t, int r0, int c0, int lane, float (&v)[16]) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const Frag8 f = lds_tr_sw<W>(t, r0 + 16 * hh, c0, lane);
+        const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[8 * hh + 2 * e] = unpack_lo<DT>(w4[e]);
+            v[8 * hh + 2 * e + 1] = unpack_hi<DT>(w4[e]);
+        }
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, const void *d_out,
                                                         void *dq, void *dk, void *dv, void *dg,
@@ -1367,24 +1422,24 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         for (int i = 0; i < 4; i++) {
             const int x = tid + 512 * i, f = x / 64, l = x % 64, p = f / 8, st = f % 8;
             const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
-            *(uint2 *)(sST + r * kR + c) = make_uint2(s1[i].x, s1[i].y);
-            *(uint2 *)(sST + r * kR + c + 8) = make_uint2(s1[i].z, s1[i].w);
-            *(uint2 *)(sDST + r * kR + c) = make_uint2(s2[i].x, s2[i].y);
-            *(uint2 *)(sDST + r * kR + c + 8) = make_uint2(s2[i].z, s2[i].w);
+            *(uint2 *)(sST + sw<128>(r, c)) = make_uint2(s1[i].x, s1[i].y);
+            *(uint2 *)(sST + sw<128>(r, c + 8)) = make_uint2(s1[i].z, s1[i].w);
+            *(uint2 *)(sDST + sw<128>(r, c)) = make_uint2(s2[i].x, s2[i].y);
+            *(uint2 *)(sDST + sw<128>(r, c + 8)) = make_uint2(s2[i].z, s2[i].w);
         }
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int x = tid + 512 * i, f = x / 64, l = x % 64, p = f / 4, st = f % 4;
             const int r = p * 32 + (l & 31), c = st * 16 + (l >> 5) * 4;
-            *(uint2 *)(sVPT + r * kT + c) = make_uint2(s3[i].x, s3[i].y);
-            *(uint2 *)(sVPT + r * kT + c + 8) = make_uint2(s3[i].z, s3[i].w);
+            *(uint2 *)(sVPT + sw<64>(r, c)) = make_uint2(s3[i].x, s3[i].y);
+            *(uint2 *)(sVPT + sw<64>(r, c + 8)) = make_uint2(s3[i].z, s3[i].w);
         }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int x = tid + 512 * u, r = x / 16, c = x % 16;
-            *(uint4 *)(sDOB + r * kR + c * 8) = r < len ? s4[u] : make_uint4(0, 0, 0, 0);
+            *(uint4 *)(sDOB + sw<128>(r, c * 8)) = r < len ? s4[u] : make_uint4(0, 0, 0, 0);
         }
-        *(uint4 *)(sAQ + (tid / 8) * kT + (tid % 8) * 8) = s5;
+        *(uint4 *)(sAQ + sw<64>(tid / 8, (tid % 8) * 8)) = s5;
         for (int x = tid; x < 8 * 256; x += 512) pGam[x] = 0.f;
     }
     __syncthreads();
@@ -1398,13 +1453,13 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             for (int st = 0; st < 8; st++) x = mfma32<DT>(dv_ka[st], dv_db[st], x);
 #pragma unroll
             for (int st = 0; st < 4; st++)
-                x = mfma32<DT>(lds_tr_frag(sAQ, kT, st * 16, t * 32, lane),
-                               lds_tr_frag(sDOB, kR, st * 16, cw * 32, lane), x);
-            store_ct<DT>(sDVPT, kT, t * 32, cw * 32, x, lane);
+                x = mfma32<DT>(lds_tr_sw<64>(sAQ, st * 16, t * 32, lane),
+                               lds_tr_sw<128>(sDOB, st * 16, cw * 32, lane), x);
+            store_ct_sw<DT, 64>(sDVPT, t * 32, cw * 32, x, lane);
             // and what the rounding left, for T^T dV' (d beta's largest term)
 #pragma unroll
             for (int i = 0; i < 16; i++) x[i] -= round_to<DT>(x[i]);
-            store_ct<DT>(sDVLO, kT, t * 32, cw * 32, x, lane);
+            store_ct_sw<DT, 64>(sDVLO, t * 32, cw * 32, x, lane);
         }
     }
     __syncthreads();
@@ -1417,25 +1472,25 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         dqg = dkt = dw = zero16();
 #pragma unroll
         for (int st = 0; st < 8; st++) {
-            const Frag8 bs = lds_tr_frag(sST, kR, st * 16, cw * 32, lane);
-            dqg = mfma32<DT>(row_frag(sDOB, kR, t * 32, st * 16, lane), bs, dqg);
-            dw = mfma32<DT>(lds_tr_frag(sDVPT, kT, st * 16, t * 32, lane), bs, dw);
-            dkt = mfma32<DT>(lds_tr_frag(sVPT, kT, st * 16, t * 32, lane),
-                             lds_tr_frag(sDST, kR, st * 16, cw * 32, lane), dkt);
+            const Frag8 bs = lds_tr_sw<128>(sST, st * 16, cw * 32, lane);
+            dqg = mfma32<DT>(row_frag_sw<128>(sDOB, t * 32, st * 16, lane), bs, dqg);
+            dw = mfma32<DT>(lds_tr_sw<64>(sDVPT, st * 16, t * 32, lane), bs, dw);
+            dkt = mfma32<DT>(lds_tr_sw<64>(sVPT, st * 16, t * 32, lane),
+                             lds_tr_sw<128>(sDST, st * 16, cw * 32, lane), dkt);
         }
     }
     if (tilew && !(ti == 0 && tj == 1)) {
 #pragma unroll
         for (int st = 0; st < 8; st++)
-            datt = mfma32<DT>(row_frag(sDOB, kR, ti * 32, st * 16, lane),
-                              lds_tr_frag(sVPT, kT, st * 16, tj * 32, lane), datt);
+            datt = mfma32<DT>(row_frag_sw<128>(sDOB, ti * 32, st * 16, lane),
+                              lds_tr_sw<64>(sVPT, st * 16, tj * 32, lane), datt);
     }
     // <S, dS_{c+1}> over the chunk
     {
         float acc = 0.f;
         for (int x = tid; x < kD * 16; x += 512) {
             const int r = x / 16, c = (x % 16) * 8;
-            const uint4 s1 = *(const uint4 *)(sST + r * kR + c), s2 = *(const uint4 *)(sDST + r * kR + c);
+            const uint4 s1 = *(const uint4 *)(sST + sw<128>(r, c)), s2 = *(const uint4 *)(sDST + sw<128>(r, c));
             const uint32_t a1[4] = {s1.x, s1.y, s1.z, s1.w}, a2[4] = {s2.x, s2.y, s2.z, s2.w};
 #pragma unroll
             for (int e = 0; e < 4; e++)
@@ -1500,24 +1555,24 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             // rows past the chunk's tokens are zero (component-wise selects: a select of whole
             // vectors goes through private memory)
             const uint32_t keep = ok ? 0xffffffffu : 0u;
-            *(uint4 *)(U16(bl::QB) + r * kR + c * 8) =
+            *(uint4 *)(U16(bl::QB) + sw<128>(r, c * 8)) =
                 make_uint4(qv.x & keep, qv.y & keep, qv.z & keep, qv.w & keep);
-            *(uint4 *)(U16(bl::KB) + r * kR + c * 8) =
+            *(uint4 *)(U16(bl::KB) + sw<128>(r, c * 8)) =
                 make_uint4(kv.x & keep, kv.y & keep, kv.z & keep, kv.w & keep);
-            *(uint4 *)(U16(bl::VB) + r * kR + c * 8) =
+            *(uint4 *)(U16(bl::VB) + sw<128>(r, c * 8)) =
                 make_uint4(vv.x & keep, vv.y & keep, vv.z & keep, vv.w & keep);
             if (c == 0) {
                 tQi[r] = qi;
                 tKi[r] = ki;
             }
         }
-        *(uint4 *)(U16(bl::TB) + (tid / 8) * kT + (tid % 8) * 8) = t2;
+        *(uint4 *)(U16(bl::TB) + sw<64>(tid / 8, (tid % 8) * 8)) = t2;
     }
     uint16_t *sQB = U16(bl::QB), *sKB = U16(bl::KB), *sVB = U16(bl::VB), *sDWT = U16(bl::DWT);
     uint16_t *sTB = U16(bl::TB), *sM1T = U16(bl::M1T), *sDTT = U16(bl::DTT);
     uint16_t *sM2T = U16(bl::M2T), *sM3BT = U16(bl::M3BT);
     // dw^T (negated: dw = -dV' S^T) and m1^T = (d attn o decay)^T
-    store_ct<DT>(sDWT, kT, tw * 32, cw * 32, dw, lane, -1.f);
+    store_ct_sw<DT, 64>(sDWT, tw * 32, cw * 32, dw, lane, -1.f);
     if (tilew) {
         f32x16_t m = zero16();
         if (!(ti == 0 && tj == 1)) {
@@ -1529,7 +1584,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
                 m[i] = datt[i] * (r >= j ? __expf(tG[r] - tG[j]) : 0.f);
             }
         }
-        store_ct<DT>(sM1T, kT, ti * 32, tj * 32, m, lane);
+        store_ct_sw<DT, 64>(sM1T, ti * 32, tj * 32, m, lane);
     }
     __syncthreads();  // Q, K, V, T, dw^T, m1^T in place
     DM_GSTAMP(4);
@@ -1538,7 +1593,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     if (tilew && !(ti == 0 && tj == 1)) {
         const int j = tj * 32 + col;
         float cs = 0.f, p[16], avs[16];
-        tile_at_out<DT>(sAQ, kT, ti * 32, tj * 32, lane, avs);
+        tile_at_out_sw<DT, 64>(sAQ, ti * 32, tj * 32, lane, avs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float av = avs[i];
@@ -1556,8 +1611,8 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     {
         const int t = tw;
         float gsum[16], ssum[16], qvs[16], kvs[16];
-        tile_at_out<DT>(sQB, kR, t * 32, cw * 32, lane, qvs);
-        tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
+        tile_at_out_sw<DT, 128>(sQB, t * 32, cw * 32, lane, qvs);
+        tile_at_out_sw<DT, 128>(sKB, t * 32, cw * 32, lane, kvs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = t * 32 + crow(i, lane);
@@ -1578,10 +1633,10 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         f32x16_t x = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            dqa = mfma32<DT>(lds_tr_frag(sM1T, kT, st * 16, t * 32, lane),
-                             lds_tr_frag(sKB, kR, st * 16, cw * 32, lane), dqa);
-            x = mfma32<DT>(row_frag(sM1T, kT, t * 32, st * 16, lane),
-                           lds_tr_frag(sQB, kR, st * 16, cw * 32, lane), x);
+            dqa = mfma32<DT>(lds_tr_sw<64>(sM1T, st * 16, t * 32, lane),
+                             lds_tr_sw<128>(sKB, st * 16, cw * 32, lane), dqa);
+            x = mfma32<DT>(row_frag_sw<64>(sM1T, t * 32, st * 16, lane),
+                           lds_tr_sw<128>(sQB, st * 16, cw * 32, lane), x);
         }
 #pragma unroll
         for (int i = 0; i < 16; i++) dka[i] += scale * x[i];
@@ -1592,16 +1647,16 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         f32x16_t c1 = zero16(), c2 = zero16();
 #pragma unroll
         for (int st = 0; st < 8; st++) {
-            c1 = mfma32<DT>(lds_tr_frag(sDVPT, kT, st * 16, ti * 32, lane),
-                            row_frag(sVB, kR, tj * 32, st * 16, lane), c1);
-            c2 = mfma32<DT>(lds_tr_frag(sDWT, kT, st * 16, ti * 32, lane),
-                            row_frag(sKB, kR, tj * 32, st * 16, lane), c2);
+            c1 = mfma32<DT>(lds_tr_sw<64>(sDVPT, st * 16, ti * 32, lane),
+                            row_frag_sw<128>(sVB, tj * 32, st * 16, lane), c1);
+            c2 = mfma32<DT>(lds_tr_sw<64>(sDWT, st * 16, ti * 32, lane),
+                            row_frag_sw<128>(sKB, tj * 32, st * 16, lane), c2);
         }
         const int j = tj * 32 + col;
         const float bj = tBet[j], bgj = tBet[j] * tGam[j];
 #pragma unroll
         for (int i = 0; i < 16; i++) c1[i] = c1[i] * bj + c2[i] * bgj;
-        store_ct<DT>(sDTT, kT, ti * 32, tj * 32, c1, lane);
+        store_ct_sw<DT, 64>(sDTT, ti * 32, tj * 32, c1, lane);
     }
     // (h) dvb = T^T dV', dkbg = T^T dw: dv = beta dvb; dk += beta gamma dkbg; sums for d beta,
     // d gamma
@@ -1610,14 +1665,14 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         f32x16_t xb = zero16(), xk = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            const Frag8 ta = lds_tr_frag(sTB, kT, st * 16, t * 32, lane);
-            xb = mfma32<DT>(ta, row_frag(sDVPT, kT, cw * 32, st * 16, lane), xb);
-            xb = mfma32<DT>(ta, row_frag(sDVLO, kT, cw * 32, st * 16, lane), xb);
-            xk = mfma32<DT>(ta, row_frag(sDWT, kT, cw * 32, st * 16, lane), xk);
+            const Frag8 ta = lds_tr_sw<64>(sTB, st * 16, t * 32, lane);
+            xb = mfma32<DT>(ta, row_frag_sw<64>(sDVPT, cw * 32, st * 16, lane), xb);
+            xb = mfma32<DT>(ta, row_frag_sw<64>(sDVLO, cw * 32, st * 16, lane), xb);
+            xk = mfma32<DT>(ta, row_frag_sw<64>(sDWT, cw * 32, st * 16, lane), xk);
         }
         float bs[16], us[16], vvs[16], kvs[16];
-        tile_at_out<DT>(sVB, kR, t * 32, cw * 32, lane, vvs);
-        tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
+        tile_at_out_sw<DT, 128>(sVB, t * 32, cw * 32, lane, vvs);
+        tile_at_out_sw<DT, 128>(sKB, t * 32, cw * 32, lane, kvs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = t * 32 + crow(i, lane);
@@ -1643,9 +1698,9 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         f32x16_t m2 = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++)
-            m2 = mfma32<DT>(lds_tr_frag(sTB, kT, st * 16, ti * 32, lane),
-                            row_frag(sDTT, kT, tj * 32, st * 16, lane), m2);
-        store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m2, lane);
+            m2 = mfma32<DT>(lds_tr_sw<64>(sTB, st * 16, ti * 32, lane),
+                            row_frag_sw<64>(sDTT, tj * 32, st * 16, lane), m2);
+        store_ct_sw<DT, 64>(sM2T, ti * 32, tj * 32, m2, lane);
     }
     __syncthreads();
     DM_GSTAMP(6);
@@ -1656,12 +1711,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         f32x16_t da = zero16(), kk = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++)
-            da = mfma32<DT>(lds_tr_frag(sM2T, kT, st * 16, ti * 32, lane),
-                            row_frag(sTB, kT, tj * 32, st * 16, lane), da);
+            da = mfma32<DT>(lds_tr_sw<64>(sM2T, st * 16, ti * 32, lane),
+                            row_frag_sw<64>(sTB, tj * 32, st * 16, lane), da);
 #pragma unroll
         for (int st = 0; st < 8; st++)
-            kk = mfma32<DT>(row_frag(sKB, kR, ti * 32, st * 16, lane),
-                            row_frag(sKB, kR, tj * 32, st * 16, lane), kk);
+            kk = mfma32<DT>(row_frag_sw<128>(sKB, ti * 32, st * 16, lane),
+                            row_frag_sw<128>(sKB, tj * 32, st * 16, lane), kk);
         const int j = tj * 32 + col;
         float cs = 0.f, p[16];
 #pragma unroll
@@ -1687,8 +1742,8 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
     __syncthreads();  // m2^T dead: m3^T takes its place
     DM_GSTAMP(7);
     if (tilew) {
-        store_ct<DT>(sM2T, kT, ti * 32, tj * 32, m3, lane);
-        store_ct<DT>(sM3BT, kT, ti * 32, tj * 32, m3b, lane);
+        store_ct_sw<DT, 64>(sM2T, ti * 32, tj * 32, m3, lane);
+        store_ct_sw<DT, 64>(sM3BT, ti * 32, tj * 32, m3b, lane);
     }
     __syncthreads();
     DM_GSTAMP(8);
@@ -1698,12 +1753,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         f32x16_t xb = zero16(), xt = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            const Frag8 kb = lds_tr_frag(sKB, kR, st * 16, cw * 32, lane);
-            xb = mfma32<DT>(lds_tr_frag(sM2T, kT, st * 16, t * 32, lane), kb, xb);
-            xt = mfma32<DT>(row_frag(sM3BT, kT, t * 32, st * 16, lane), kb, xt);
+            const Frag8 kb = lds_tr_sw<128>(sKB, st * 16, cw * 32, lane);
+            xb = mfma32<DT>(lds_tr_sw<64>(sM2T, st * 16, t * 32, lane), kb, xb);
+            xt = mfma32<DT>(row_frag_sw<64>(sM3BT, t * 32, st * 16, lane), kb, xt);
         }
         float bs[16], kvs[16];
-        tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
+        tile_at_out_sw<DT, 128>(sKB, t * 32, cw * 32, lane, kvs);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = t * 32 + crow(i, lane);
@@ -1722,8 +1777,8 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
         {
             const int t = tw;
             float qs[16], ks[16], qvs[16], kvs[16];
-            tile_at_out<DT>(sQB, kR, t * 32, cw * 32, lane, qvs);
-            tile_at_out<DT>(sKB, kR, t * 32, cw * 32, lane, kvs);
+            tile_at_out_sw<DT, 128>(sQB, t * 32, cw * 32, lane, qvs);
+            tile_at_out_sw<DT, 128>(sKB, t * 32, cw * 32, lane, kvs);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float qv = qvs[i], kv = kvs[i];
@@ -1800,7 +1855,7 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
             const int c = cw * 32 + col;
             float qo = dqa[i] * scale, ko = dka[i];
             if (a.l2norm) {
-                const uint16_t qb = sQB[r * kR + c], kb = sKB[r * kR + c];
+                const uint16_t qb = sQB[sw<128>(r, c)], kb = sKB[sw<128>(r, c)];
                 const float qv = (DT == DM_BF16) ? __uint_as_float((uint32_t)qb << 16)
                                                  : (float)__builtin_bit_cast(_Float16, qb);
                 const float kv = (DT == DM_BF16) ? __uint_as_float((uint32_t)kb << 16)
