@@ -975,6 +975,61 @@ constexpr int kR = kD + 8;  // 128-column tiles (row and transposed reads)
 constexpr int kT = kC + 8;  // 64-column tiles
 
 // F per (chunk, head): wave w takes state columns 32 w + [0, 32).
+// Unpadded 16-bit tiles of W = 128 or 64 columns with their 16-byte column chunks permuted by
+// row (chunk m of row r at m ^ f(r)): the transposed fragment reads (4 rows x 64 bytes a pass of
+// 32 lanes), 16-byte reads and writes of 16 consecutive rows at one column, and 16-byte row
+// writes are all free of bank conflicts at 64 banks of 4 bytes; 8-byte accesses of 32 rows at one
+// column are 2-way, as with padded rows. (Rows padded to 272 or 144 bytes had made every
+// transposed read of the 128-column tiles a 4-way conflict and of the 64-column tiles 2-way.)
+template <int W>
+__device__ __forceinline__ int sw(int r, int c) {
+    const int f = W == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    return r * W + ((((c >> 3) ^ f)) << 3) + (c & 7);
+}
+template <int W>
+__device__ __forceinline__ Frag8 lds_tr_sw(const uint16_t *tile, int k0, int c0, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int row = k0 + 4 * (g >> 1) + (i >> 2);
+    const int colx = c0 + 16 * (g & 1) + 4 * (i & 3);
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row, colx)));
+    s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row + 8, colx)));
+    Frag8 f;
+    __builtin_memcpy(&f.u.x, &a, 8);
+    __builtin_memcpy(&f.u.z, &b, 8);
+    return f;
+}
+template <int W>
+__device__ __forceinline__ Frag8 row_frag_sw(const uint16_t *t, int r0, int k0, int lane) {
+    const int r = r0 + (lane & 31), c = k0 + (lane >> 5) * 4;
+    const uint2 lo = *(const uint2 *)(t + sw<W>(r, c)), hi = *(const uint2 *)(t + sw<W>(r, c + 8));
+    Frag8 f;
+    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    return f;
+}
+template <int DT, int W>
+__device__ __forceinline__ void store_ct_sw(uint16_t *t, int r0, int c0, const f32x16_t &v, int lane,
+                                            float f = 1.f) {
+    const int r = c0 + (lane & 31), c = r0 + (lane >> 5) * 4;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        *(uint2 *)(t + sw<W>(r, c + g * 8)) = make_uint2(pack2<DT>(v[4 * g] * f, v[4 * g + 1] * f),
+                                                        pack2<DT>(v[4 * g + 2] * f, v[4 * g + 3] * f));
+}
+template <int DT, int W>
+__device__ __forceinline__ void tile_at_out_sw(const uint16_t *t, int r0, int c0, int lane, float (&v)[16]) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const Frag8 f = lds_tr_sw<W>(t, r0 + 16 * hh, c0, lane);
+        const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[8 * hh + 2 * e] = unpack_lo<DT>(w4[e]);
+            v[8 * hh + 2 * e + 1] = unpack_hi<DT>(w4[e]);
+        }
+    }
+}
+
 struct BwdPreSmem {
     uint16_t dO[kC * kR];   // dO rows
     uint16_t qg[kC * kR];   // gamma scale Q rows
@@ -1028,19 +1083,19 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
         uint32_t qo[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) qo[e] = pack2<DT>(unpack_lo<DT>(qw[e]) * f, unpack_hi<DT>(qw[e]) * f);
-        *(uint4 *)(sm.qg + r * kR + c * 8) = make_uint4(qo[0], qo[1], qo[2], qo[3]);
-        *(uint4 *)(sm.dO + r * kR + c * 8) = ok ? dv[u] : make_uint4(0, 0, 0, 0);
+        *(uint4 *)(sm.qg + sw<128>(r, c * 8)) = make_uint4(qo[0], qo[1], qo[2], qo[3]);
+        *(uint4 *)(sm.dO + sw<128>(r, c * 8)) = ok ? dv[u] : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int x = tid + 256 * u, r = x / 8, c = x % 8;
-        *(uint4 *)(sm.aq + r * kT + c * 8) = av[u];
+        *(uint4 *)(sm.aq + sw<64>(r, c * 8)) = av[u];
     }
     __syncthreads();
     // dO as B fragments (k = token, col = state column)
     Frag8 bo[4];
 #pragma unroll
-    for (int st = 0; st < 4; st++) bo[st] = lds_tr_frag(sm.dO, kR, st * 16, wave * 32, lane);
+    for (int st = 0; st < 4; st++) bo[st] = lds_tr_sw<128>(sm.dO, st * 16, wave * 32, lane);
     // Aqk^T dO (rows = tokens j), then as B fragments of W^T (.), negated
     Frag8 nd[4];
 #pragma unroll
@@ -1048,7 +1103,7 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
         f32x16_t x = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++)
-            x = mfma32<DT>(lds_tr_frag(sm.aq, kT, st * 16, t * 32, lane), bo[st], x);
+            x = mfma32<DT>(lds_tr_sw<64>(sm.aq, st * 16, t * 32, lane), bo[st], x);
         nd[2 * t] = c_frag<DT>(x, 0, -1.f);
         nd[2 * t + 1] = c_frag<DT>(x, 1, -1.f);
     }
@@ -1060,7 +1115,7 @@ __global__ __launch_bounds__(256) void gdr_bwd_pre(GdrArgs a, MfmaWs w, const vo
         f32x16_t x = zero16();
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            x = mfma32<DT>(lds_tr_frag(sm.qg, kR, st * 16, r * 32, lane), bo[st], x);
+            x = mfma32<DT>(lds_tr_sw<128>(sm.qg, st * 16, r * 32, lane), bo[st], x);
             x = mfma32<DT>(wa[r][st], nd[st], x);
         }
         uint4 *o = (uint4 *)(fo + ((size_t)r * 64 + lane) * 16);
@@ -1283,61 +1338,6 @@ __device__ __forceinline__ void tile_at_out(const uint16_t *t, int stride, int r
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         const Frag8 f = lds_tr_frag(t, stride, r0 + 16 * hh, c0, lane);
-        const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            v[8 * hh + 2 * e] = unpack_lo<DT>(w4[e]);
-            v[8 * hh + 2 * e + 1] = unpack_hi<DT>(w4[e]);
-        }
-    }
-}
-
-// Unpadded 16-bit tiles of W = 128 or 64 columns with their 16-byte column chunks permuted by
-// row (chunk m of row r at m ^ f(r)): the transposed fragment reads (4 rows x 64 bytes a pass of
-// 32 lanes), 16-byte reads and writes of 16 consecutive rows at one column, and 16-byte row
-// writes are all free of bank conflicts at 64 banks of 4 bytes; 8-byte accesses of 32 rows at one
-// column are 2-way, as with padded rows. (Rows padded to 272 or 144 bytes had made every
-// transposed read of the 128-column tiles a 4-way conflict and of the 64-column tiles 2-way.)
-template <int W>
-__device__ __forceinline__ int sw(int r, int c) {
-    const int f = W == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-    return r * W + ((((c >> 3) ^ f)) << 3) + (c & 7);
-}
-template <int W>
-__device__ __forceinline__ Frag8 lds_tr_sw(const uint16_t *tile, int k0, int c0, int lane) {
-    const int g = lane >> 4, i = lane & 15;
-    const int row = k0 + 4 * (g >> 1) + (i >> 2);
-    const int colx = c0 + 16 * (g & 1) + 4 * (i & 3);
-    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
-    s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row, colx)));
-    s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row + 8, colx)));
-    Frag8 f;
-    __builtin_memcpy(&f.u.x, &a, 8);
-    __builtin_memcpy(&f.u.z, &b, 8);
-    return f;
-}
-template <int W>
-__device__ __forceinline__ Frag8 row_frag_sw(const uint16_t *t, int r0, int k0, int lane) {
-    const int r = r0 + (lane & 31), c = k0 + (lane >> 5) * 4;
-    const uint2 lo = *(const uint2 *)(t + sw<W>(r, c)), hi = *(const uint2 *)(t + sw<W>(r, c + 8));
-    Frag8 f;
-    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    return f;
-}
-template <int DT, int W>
-__device__ __forceinline__ void store_ct_sw(uint16_t *t, int r0, int c0, const f32x16_t &v, int lane,
-                                            float f = 1.f) {
-    const int r = c0 + (lane & 31), c = r0 + (lane >> 5) * 4;
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-        *(uint2 *)(t + sw<W>(r, c + g * 8)) = make_uint2(pack2<DT>(v[4 * g] * f, v[4 * g + 1] * f),
-                                                        pack2<DT>(v[4 * g + 2] * f, v[4 * g + 3] * f));
-}
-template <int DT, int W>
-__device__ __forceinline__ void tile_at_out_sw(const uint16_t *t, int r0, int c0, int lane, float (&v)[16]) {
-#pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const Frag8 f = lds_tr_sw<W>(t, r0 + 16 * hh, c0, lane);
         const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
