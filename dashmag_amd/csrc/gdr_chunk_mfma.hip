@@ -104,6 +104,61 @@ static size_t mfma_layout(const dm_gdr_desc *d, char *base, MfmaWs *w, bool bwd 
 // Prep
 // ------------------------------------------------------------------------------------------
 
+// Unpadded 16-bit tiles of W = 128 or 64 columns with their 16-byte column chunks permuted by
+// row (chunk m of row r at m ^ f(r)): the transposed fragment reads (4 rows x 64 bytes a pass of
+// 32 lanes), 16-byte reads and writes of 16 consecutive rows at one column, and 16-byte row
+// writes are all free of bank conflicts at 64 banks of 4 bytes; 8-byte accesses of 32 rows at one
+// column are 2-way, as with padded rows. (Rows padded to 272 or 144 bytes had made every
+// transposed read of the 128-column tiles a 4-way conflict and of the 64-column tiles 2-way.)
+template <int W>
+__device__ __forceinline__ int sw(int r, int c) {
+    const int f = W == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    return r * W + ((((c >> 3) ^ f)) << 3) + (c & 7);
+}
+template <int W>
+__device__ __forceinline__ Frag8 lds_tr_sw(const uint16_t *tile, int k0, int c0, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int row = k0 + 4 * (g >> 1) + (i >> 2);
+    const int colx = c0 + 16 * (g & 1) + 4 * (i & 3);
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row, colx)));
+    s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row + 8, colx)));
+    Frag8 f;
+    __builtin_memcpy(&f.u.x, &a, 8);
+    __builtin_memcpy(&f.u.z, &b, 8);
+    return f;
+}
+template <int W>
+__device__ __forceinline__ Frag8 row_frag_sw(const uint16_t *t, int r0, int k0, int lane) {
+    const int r = r0 + (lane & 31), c = k0 + (lane >> 5) * 4;
+    const uint2 lo = *(const uint2 *)(t + sw<W>(r, c)), hi = *(const uint2 *)(t + sw<W>(r, c + 8));
+    Frag8 f;
+    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    return f;
+}
+template <int DT, int W>
+__device__ __forceinline__ void store_ct_sw(uint16_t *t, int r0, int c0, const f32x16_t &v, int lane,
+                                            float f = 1.f) {
+    const int r = c0 + (lane & 31), c = r0 + (lane >> 5) * 4;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        *(uint2 *)(t + sw<W>(r, c + g * 8)) = make_uint2(pack2<DT>(v[4 * g] * f, v[4 * g + 1] * f),
+                                                        pack2<DT>(v[4 * g + 2] * f, v[4 * g + 3] * f));
+}
+template <int DT, int W>
+__device__ __forceinline__ void tile_at_out_sw(const uint16_t *t, int r0, int c0, int lane, float (&v)[16]) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const Frag8 f = lds_tr_sw<W>(t, r0 + 16 * hh, c0, lane);
+        const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[8 * hh + 2 * e] = unpack_lo<DT>(w4[e]);
+            v[8 * hh + 2 * e + 1] = unpack_hi<DT>(w4[e]);
+        }
+    }
+}
+
 // 52 KB: three workgroups per CU. The query tile's space later holds T (f32); the key tile's
 // space keeps the keys until W = (T diag(beta gamma)) K, then holds beta V for U = T (beta V),
 // then stages the W rows for the fragment stores. A is kept as its ten lower 16 x 16 blocks.
@@ -195,8 +250,8 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
                             pack2<DT>(kf[4] * ki, kf[5] * ki), pack2<DT>(kf[6] * ki, kf[7] * ki));
             if (w.Qn) *(uint4 *)(w.Qn + (ch * kC + r) * kD + c * 8) = qv;
         }
-        sm.q[r * (kRowS / 8) + c] = qv;
-        sm.k[r * (kRowS / 8) + c] = kv;
+        sm.q[sw<128>(r, c * 8) / 8] = qv;
+        sm.k[sw<128>(r, c * 8) / 8] = kv;
     }
     __syncthreads();
     if (wave == 0) {
@@ -220,7 +275,7 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         uint16_t *kf_out = w.Kf + ch * kC * kD;
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            const Frag8 kt = lds_tr_frag(ks, kRowS, st * 16, wave * 32, lane);
+            const Frag8 kt = lds_tr_sw<128>(ks, st * 16, wave * 32, lane);
             const uint32_t kw[4] = {kt.u.x, kt.u.y, kt.u.z, kt.u.w};
             uint32_t o[4];
 #pragma unroll
@@ -241,8 +296,8 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int f = wave * 4 + j, t = f / 8, st = f % 8, row = t * 32 + col;
-                const uint16_t *rp = ks + row * kRowS + st * 16 + half * 4;
-                const uint2 lo4 = *(const uint2 *)rp, hi4 = *(const uint2 *)(rp + 8);
+                const uint2 lo4 = *(const uint2 *)(ks + sw<128>(row, st * 16 + half * 4)),
+                            hi4 = *(const uint2 *)(ks + sw<128>(row, st * 16 + 8 + half * 4));
                 const uint32_t kw[4] = {lo4.x, lo4.y, hi4.x, hi4.y};
                 const float lm = sm.lam[row];
                 uint32_t o[4];
@@ -270,9 +325,9 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 #pragma unroll
         for (int st = 0; st < kD / 16; st++) {
             Frag8 ak, aq, bk;
-            ak.u = *(const uint4 *)(ks + (ti * 32 + col) * kRowS + half * 8 + st * 16);
-            aq.u = *(const uint4 *)(qs + (ti * 32 + col) * kRowS + half * 8 + st * 16);
-            bk.u = *(const uint4 *)(ks + (tj * 32 + col) * kRowS + half * 8 + st * 16);
+            ak.u = *(const uint4 *)(ks + sw<128>(ti * 32 + col, half * 8 + st * 16));
+            aq.u = *(const uint4 *)(qs + sw<128>(ti * 32 + col, half * 8 + st * 16));
+            bk.u = *(const uint4 *)(ks + sw<128>(tj * 32 + col, half * 8 + st * 16));
             kk = mfma32<DT>(ak, bk, kk);
             // (A and B fragments share a layout: K(tj) rows as A and Q(ti) rows as B give
             // element (key 32 tj + crow(i), query 32 ti + col))
@@ -340,8 +395,8 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int f = wave * 4 + i, t = f / 8, st = f % 8;
-            const uint16_t *src = qs + (t * 32 + col) * kRowS + st * 16 + half * 4;
-            const uint2 lo = *(const uint2 *)src, hi = *(const uint2 *)(src + 8);
+            const uint2 lo = *(const uint2 *)(qs + sw<128>(t * 32 + col, st * 16 + half * 4)),
+                        hi = *(const uint2 *)(qs + sw<128>(t * 32 + col, st * 16 + 8 + half * 4));
             *(uint4 *)(qf + (f * 64 + lane) * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
     }
@@ -474,7 +529,7 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         wt[ti] = zero16();
 #pragma unroll
         for (int st = 0; st < kC / 16; st++)
-            wt[ti] = mfma32<DT>(tfrag(ti, st, true), lds_tr_frag(ks, kRowS, st * 16, wave * 32, lane), wt[ti]);
+            wt[ti] = mfma32<DT>(tfrag(ti, st, true), lds_tr_sw<128>(ks, st * 16, wave * 32, lane), wt[ti]);
     }
     __syncthreads();  // the key tile is dead from here
     // beta V rows for U's product, in the key tile's space
@@ -488,7 +543,7 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 #pragma unroll
         for (int e = 0; e < 4; e++)
             vo[e] = pack2<DT>(unpack_lo<DT>(vw[e]) * fv, unpack_hi<DT>(vw[e]) * fv);
-        *(uint4 *)(vs + r * kRowS + c * 8) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+        *(uint4 *)(vs + sw<128>(r, c * 8)) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
     }
     __syncthreads();
 #pragma unroll
@@ -496,7 +551,7 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
         ut[ti] = zero16();
 #pragma unroll
         for (int st = 0; st < kC / 16; st++)
-            ut[ti] = mfma32<DT>(tfrag(ti, st, false), lds_tr_frag(vs, kRowS, st * 16, wave * 32, lane), ut[ti]);
+            ut[ti] = mfma32<DT>(tfrag(ti, st, false), lds_tr_sw<128>(vs, st * 16, wave * 32, lane), ut[ti]);
     }
     __syncthreads();
     // for the backward: T, row-major in the dtype
@@ -532,14 +587,15 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int r = ti * 32 + (i / 4) * 8 + half * 4 + (i % 4);
-                wrows[r * kRowS + wave * 32 + col] = (uint16_t)(pack2<DT>(wt[ti][i], 0.f) & 0xffffu);
+                wrows[sw<128>(r, wave * 32 + col)] = (uint16_t)(pack2<DT>(wt[ti][i], 0.f) & 0xffffu);
             }
         __syncthreads();
         uint16_t *wf = w.Wf + ch * kC * kD;
         for (int xx = tid; xx < 16 * 64; xx += 256) {
             const int f = xx / 64, l = xx % 64, t = f / 8, st = f % 8;
-            const uint16_t *row = wrows + (t * 32 + (l & 31)) * kRowS + st * 16 + (l >> 5) * 4;
-            const uint2 lo4 = *(const uint2 *)row, hi4 = *(const uint2 *)(row + 8);
+            const int wr = t * 32 + (l & 31), wc = st * 16 + (l >> 5) * 4;
+            const uint2 lo4 = *(const uint2 *)(wrows + sw<128>(wr, wc)),
+                        hi4 = *(const uint2 *)(wrows + sw<128>(wr, wc + 8));
             *(uint4 *)(wf + (size_t)xx * 8) = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
         }
         // for the backward, W^T as A fragments (rows dk, k = tokens), as (lam K)^T in Kf
@@ -547,7 +603,7 @@ __global__ __launch_bounds__(256, 3) void gdr_mfma_prep(GdrArgs a, MfmaWs w) {
             uint16_t *wt_out = w.WTf + ch * kC * kD;
 #pragma unroll
             for (int st = 0; st < 4; st++) {
-                const Frag8 x = lds_tr_frag(wrows, kRowS, st * 16, wave * 32, lane);
+                const Frag8 x = lds_tr_sw<128>(wrows, st * 16, wave * 32, lane);
                 *(uint4 *)(wt_out + (size_t)((wave * 4 + st) * 64 + lane) * 8) = x.u;
             }
         }
@@ -975,61 +1031,6 @@ constexpr int kR = kD + 8;  // 128-column tiles (row and transposed reads)
 constexpr int kT = kC + 8;  // 64-column tiles
 
 // F per (chunk, head): wave w takes state columns 32 w + [0, 32).
-// Unpadded 16-bit tiles of W = 128 or 64 columns with their 16-byte column chunks permuted by
-// row (chunk m of row r at m ^ f(r)): the transposed fragment reads (4 rows x 64 bytes a pass of
-// 32 lanes), 16-byte reads and writes of 16 consecutive rows at one column, and 16-byte row
-// writes are all free of bank conflicts at 64 banks of 4 bytes; 8-byte accesses of 32 rows at one
-// column are 2-way, as with padded rows. (Rows padded to 272 or 144 bytes had made every
-// transposed read of the 128-column tiles a 4-way conflict and of the 64-column tiles 2-way.)
-template <int W>
-__device__ __forceinline__ int sw(int r, int c) {
-    const int f = W == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-    return r * W + ((((c >> 3) ^ f)) << 3) + (c & 7);
-}
-template <int W>
-__device__ __forceinline__ Frag8 lds_tr_sw(const uint16_t *tile, int k0, int c0, int lane) {
-    const int g = lane >> 4, i = lane & 15;
-    const int row = k0 + 4 * (g >> 1) + (i >> 2);
-    const int colx = c0 + 16 * (g & 1) + 4 * (i & 3);
-    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
-    s16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row, colx)));
-    s16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + sw<W>(row + 8, colx)));
-    Frag8 f;
-    __builtin_memcpy(&f.u.x, &a, 8);
-    __builtin_memcpy(&f.u.z, &b, 8);
-    return f;
-}
-template <int W>
-__device__ __forceinline__ Frag8 row_frag_sw(const uint16_t *t, int r0, int k0, int lane) {
-    const int r = r0 + (lane & 31), c = k0 + (lane >> 5) * 4;
-    const uint2 lo = *(const uint2 *)(t + sw<W>(r, c)), hi = *(const uint2 *)(t + sw<W>(r, c + 8));
-    Frag8 f;
-    f.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    return f;
-}
-template <int DT, int W>
-__device__ __forceinline__ void store_ct_sw(uint16_t *t, int r0, int c0, const f32x16_t &v, int lane,
-                                            float f = 1.f) {
-    const int r = c0 + (lane & 31), c = r0 + (lane >> 5) * 4;
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-        *(uint2 *)(t + sw<W>(r, c + g * 8)) = make_uint2(pack2<DT>(v[4 * g] * f, v[4 * g + 1] * f),
-                                                        pack2<DT>(v[4 * g + 2] * f, v[4 * g + 3] * f));
-}
-template <int DT, int W>
-__device__ __forceinline__ void tile_at_out_sw(const uint16_t *t, int r0, int c0, int lane, float (&v)[16]) {
-#pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const Frag8 f = lds_tr_sw<W>(t, r0 + 16 * hh, c0, lane);
-        const uint32_t w4[4] = {f.u.x, f.u.y, f.u.z, f.u.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            v[8 * hh + 2 * e] = unpack_lo<DT>(w4[e]);
-            v[8 * hh + 2 * e + 1] = unpack_hi<DT>(w4[e]);
-        }
-    }
-}
-
 struct BwdPreSmem {
     uint16_t dO[kC * kR];   // dO rows
     uint16_t qg[kC * kR];   // gamma scale Q rows
