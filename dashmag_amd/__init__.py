@@ -14,7 +14,8 @@ from .ops import (attention, attention_backward, attention_decode, attention_dec
                   causal_conv1d, causal_conv1d_backward, causal_conv1d_update, chosen_logprob,
                   chosen_logprob_with_grad, linear_cross_entropy,
                   linear_cross_entropy_backward,
-                  chunk_gated_delta_rule, chunk_gated_delta_rule_backward, gated_delta_step)
+                  chunk_gated_delta_rule, chunk_gated_delta_rule_backward, gated_delta_step,
+                  gated_delta_step_backward)
 
 __all__ = [
     "Activation", "AttentionMask", "AttentionOptions", "CausalConv1dOptions",
@@ -26,4 +27,5 @@ __all__ = [
     "chosen_logprob_with_grad", "linear_cross_entropy", "linear_cross_entropy_backward",
     "CrossEntropyOptions", "Reduction",
     "chunk_gated_delta_rule", "chunk_gated_delta_rule_backward", "gated_delta_step",
+    "gated_delta_step_backward",
 ]

@@ -17,7 +17,7 @@ DM_UNBOUNDED = (1 << 64) - 1
 PROBES = ["attn_fwd_mfma", "attn_fwd_generic", "attn_bwd_mfma", "attn_bwd_generic",
           "decode_split", "decode_merge", "gdr_chunk_fwd", "gdr_chunk_bwd", "gdr_step",
           "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob", "lce_fwd", "lce_bwd",
-          "gdr_chunk_fwd_mfma", "gdr_chunk_bwd_mfma"]
+          "gdr_chunk_fwd_mfma", "gdr_chunk_bwd_mfma", "gdr_step_bwd"]
 DM_ACT_NONE, DM_ACT_SILU = 0, 1
 
 
@@ -117,6 +117,8 @@ SIGNATURES = {
     "dm_gdr_chunk_bwd_workspace": (_SZ, [_GD]),
     "dm_gdr_chunk_bwd": (ctypes.c_int, [_GD] + [_VP] * 15 + [_SZ, _VP]),
     "dm_gdr_step": (ctypes.c_int, [_GD] + [_VP] * 9),
+    "dm_gdr_step_bwd_workspace": (_SZ, [_GD]),
+    "dm_gdr_step_bwd": (ctypes.c_int, [_GD] + [_VP] * 15 + [_SZ, _VP]),
     "dm_causal_conv1d_fwd": (ctypes.c_int, [_CD] + [_VP] * 7),
     "dm_causal_conv1d_bwd_workspace": (_SZ, [_CD]),
     "dm_causal_conv1d_bwd": (ctypes.c_int, [_CD] + [_VP] * 5 + [ctypes.c_int] + [_VP] * 6
@@ -162,7 +164,8 @@ def probe_reset() -> None:
 
 KERNELS = ["attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "decode_split", "gdr_prep", "gdr_state",
            "gdr_output", "gdr_step", "gdr_bwd_pre", "gdr_bwd_state", "gdr_bwd_grads",
-           "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob_stats", "decode_merge"]
+           "conv1d_fwd", "conv1d_bwd", "conv1d_update", "logprob_stats", "decode_merge",
+           "gdr_step_bwd"]
 
 
 def kernel_timing(enable: bool) -> None:

@@ -544,6 +544,50 @@ def gated_delta_step(q, k, v, g, beta, state, cu_seqlens=None,
     return out, st_out
 
 
+def gated_delta_step_backward(q, k, v, g, beta, state, cu_seqlens, d_out, d_state=None,
+                              options: Optional[GatedDeltaStepOptions] = None):
+    """The gradients of :func:`gated_delta_step` (what the reference's tracked step gets from
+    autodiff over its reference, gated_delta/recurrent.rs:89-130): from the output's gradient
+    ``d_out`` ``[B, H, Dv]`` (``None``: zeros; rounded to q's dtype, as the output is) and the new
+    states' ``d_state`` (``None``: zeros), ``(dq, dk, dv, dg, dbeta, d_state_in)``, each in its
+    input's dtype, ``d_state_in`` f32."""
+    op = "gated_delta_step_backward"
+    options = options or GatedDeltaStepOptions()
+    _device(op, q, k, v, g, beta, state, d_out, d_state)
+    keep = []
+    desc, nseq, (b, _, h, dk, dv) = _gdr_desc(op, q, k, v, g, beta, cu_seqlens,
+                                              options.qk_l2norm, options.scale, True, keep)
+    if tuple(state.shape) != (nseq, h, dk, dv):
+        raise Unsupported(f"{op}: state must be [S, H, Dk, Dv], one per sequence")
+    if state.dtype != torch.float32:
+        raise Unsupported(f"{op}: the state is f32")
+    if d_out is not None and tuple(d_out.shape) != (b, h, dv):
+        raise Unsupported(f"{op}: the output's gradient is [B, H, Dv]")
+    if d_state is not None and tuple(d_state.shape) != (nseq, h, dk, dv):
+        raise Unsupported(f"{op}: the new states' gradient is [S, H, Dk, Dv]")
+    qc, kc, vc = (_gdr_view(x, False, True) for x in (q, k, v))
+    do = None if d_out is None else _gdr_view(d_out.to(q.dtype), False, True)
+    views = dict(sq=qc, sk=kc, sv=vc, sg=g, sbeta=beta)
+    if do is not None:
+        views["sdo"] = do
+    _gdr_strides(desc, True, **views)
+    st_in = state.contiguous()
+    dst = None if d_state is None else d_state.to(torch.float32).contiguous()
+    dq = torch.empty((b, h, dk), dtype=q.dtype, device=q.device)
+    dk_ = torch.empty((b, h, dk), dtype=q.dtype, device=q.device)
+    dv_ = torch.empty((b, h, dv), dtype=q.dtype, device=q.device)
+    dg = torch.empty((b, h), dtype=g.dtype, device=q.device)
+    db = torch.empty((b, h), dtype=beta.dtype, device=q.device)
+    dst_in = torch.empty_like(st_in)
+    nbytes = _lib.lib().dm_gdr_step_bwd_workspace(ctypes.byref(desc))
+    ws = _workspace(nbytes, q.device)
+    _check(op, _lib.lib().dm_gdr_step_bwd(
+        ctypes.byref(desc), _ptr(qc), _ptr(kc), _ptr(vc), _ptr(g), _ptr(beta), _ptr(st_in),
+        _ptr(do), _ptr(dst), _ptr(dq), _ptr(dk_), _ptr(dv_), _ptr(dg), _ptr(db), _ptr(dst_in),
+        _ptr(ws), nbytes, _stream()))
+    return dq, dk_, dv_, dg, db, dst_in
+
+
 # ------------------------------------------------------------------------------------------
 # Causal conv1d
 # ------------------------------------------------------------------------------------------

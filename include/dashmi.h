@@ -13,6 +13,8 @@
  *   dm_gdr_chunk_bwd     ChunkGatedDeltaBackend::chunk_gated_delta_backward (the Autodiff node's
  *                        backward, chunk.rs:542-767, as an explicit entry point)
  *   dm_gdr_step          GatedDeltaStepBackend::gated_delta_step crates/dash-ops/src/gated_delta/recurrent.rs:52-81, :158
+ *   dm_gdr_step_bwd      the tracked step's gradients (recurrent.rs:89-130: the reference under
+ *                        autodiff), as an explicit entry point
  *   dm_causal_conv1d_fwd     CausalConv1dBackend::causal_conv1d  crates/dash-ops/src/conv1d.rs:198-300, :690
  *   dm_causal_conv1d_bwd     CausalConv1dBackend::causal_conv1d_backward
  *                                                               crates/dash-ops/src/conv1d.rs:300-329
@@ -193,6 +195,7 @@ typedef enum {
     DM_PROBE_LCE_BWD,
     DM_PROBE_GDR_CHUNK_FWD_MFMA, /* the MFMA kernels of the chunked forward (a subset of the above) */
     DM_PROBE_GDR_CHUNK_BWD_MFMA, /* the MFMA kernels of the chunked backward */
+    DM_PROBE_GDR_STEP_BWD,       /* the recurrent step's backward */
     DM_PROBE_COUNT
 } dm_probe;
 uint64_t dm_probe_count(int probe);
@@ -219,6 +222,7 @@ typedef enum {
     DM_KERNEL_CONV1D_UPDATE,  /* causal conv1d decoding step */
     DM_KERNEL_LOGPROB_STATS,  /* chosen-token log-probability: the per-chunk statistics */
     DM_KERNEL_DECODE_MERGE,   /* decode, pass 2: the splits merged by log-sum-exp */
+    DM_KERNEL_GDR_STEP_BWD,   /* gated delta rule step backward (both of its kernels) */
     DM_KERNEL_COUNT
 } dm_kernel;
 int dm_kernel_timing(int enable);
@@ -312,6 +316,20 @@ int dm_gdr_chunk_bwd(const dm_gdr_desc *desc, const void *q, const void *k, cons
 int dm_gdr_step(const dm_gdr_desc *desc, const void *q, const void *k, const void *v,
                 const void *g, const void *beta, const float *state_in, float *state_out,
                 void *out, void *stream);
+
+/* The step's backward: from d_out [B, H, Dv] (dtype; NULL: zeros) and d_state, the new states'
+ * gradient [S, H, Dk, Dv] f32 (NULL: zeros), the gradients dq, dk [B, H, Dk], dv [B, H, Dv]
+ * (dtype), dg (g_dtype), dbeta (beta_dtype) [B, H] and d_state_in [S, H, Dk, Dv] f32 (NULL: not
+ * wanted), all contiguous. The reference's tracked step runs its reference under autodiff
+ * (recurrent.rs:89-130, the operations of :362-404); dash-conformance holds the gradients to
+ * torch's (crates/dash-conformance/src/gated_delta_recurrent.rs:229-269,
+ * gated_delta_packed.rs:419-517). The workspace holds, with cu_seqlens, the state before every
+ * token ([B, H, Dk, Dv] f32: packed tokens are walked in reverse), plus per-token partial sums. */
+size_t dm_gdr_step_bwd_workspace(const dm_gdr_desc *desc);
+int dm_gdr_step_bwd(const dm_gdr_desc *desc, const void *q, const void *k, const void *v,
+                    const void *g, const void *beta, const float *state_in, const void *d_out,
+                    const float *d_state, void *dq, void *dk, void *dv, void *dg, void *dbeta,
+                    float *d_state_in, void *workspace, size_t workspace_bytes, void *stream);
 
 /* The causal depthwise conv1d over sequences: out [B, T, C] in dtype and, with has_final, each
  * sequence's final state (the last w_out steps of its history) [S, w_out, C] f32; with

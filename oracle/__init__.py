@@ -220,6 +220,27 @@ def gdr_step(q, k, v, g, beta, state, cu=None, l2norm=False, scale=None, precisi
     return out, st
 
 
+def gdr_step_bwd(q, k, v, g, beta, state, d_out, d_state, cu=None, l2norm=False, scale=None,
+                 precision="f32"):
+    """The step's gradients (reverse-mode through recurrent.rs:362-404, as the reference's
+    tracked step gets them, :89-130): ``(dq, dk, dv, dg, dbeta, d_state_in)``; ``d_out`` or
+    ``d_state`` may be ``None`` (zeros)."""
+    q, k, v, g, beta = map(_f32, (q, k, v, g, beta))
+    st = _f32(state)
+    s, cu = _gdr(q[None], v[None], cu, l2norm, scale)
+    s.b = q.shape[0]
+    d_out = None if d_out is None else _f32(d_out)
+    d_state = None if d_state is None else _f32(d_state)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    dg, db = np.zeros_like(g), np.zeros_like(beta)
+    dst = np.zeros_like(st)
+    rc = getattr(lib(), f"dmo_gdr_step_bwd_{precision}")(
+        ctypes.byref(s), _p(q), _p(k), _p(v), _p(g), _p(beta), _p(st), _p(d_out), _p(d_state),
+        _p(dq), _p(dk), _p(dv), _p(dg), _p(db), _p(dst))
+    assert rc == 0
+    return dq, dk, dv, dg, db, dst
+
+
 class _Conv1d(ctypes.Structure):
     _fields_ = [
         ("b", ctypes.c_int64), ("t", ctypes.c_int64), ("c", ctypes.c_int64), ("k", ctypes.c_int64),

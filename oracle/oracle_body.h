@@ -714,3 +714,136 @@ int FN(dmo_gdr_step)(const dmo_gdr *p, const float *q, const float *k, const flo
     }
     return 0;
 }
+
+/* The step's gradients: reverse-mode differentiation of `step` (recurrent.rs:362-396) and of
+ * `l2norm` (:400-404), as the reference's tracked step gets them from Burn's autodiff over the
+ * same operations (:89-130), packed sequences token by token (:318-358). Each sequence's
+ * per-token states are kept from a forward sweep, then the tokens are walked in reverse:
+ *   S' = a P (a = exp g), kv = S'^T k, delta = beta (v - kv), S = S' + k delta^T, o = S^T qs;
+ *   dS += qs dO^T;  dqs = S dO;  ddelta = dS^T k;  dkv = -beta ddelta;
+ *   dk = dS delta + S' dkv;  dv = beta ddelta;  dbeta = ddelta . (v - kv);
+ *   dS' = dS + k dkv^T;  dg = sum(dS' o S');  dP = a dS'.
+ * d_out [T, H, Dv] and d_state [S, H, Dk, Dv] (NULL: zeros); d_state_in may be NULL. */
+int FN(dmo_gdr_step_bwd)(const dmo_gdr *p, const float *q, const float *k, const float *v,
+                         const float *g, const float *beta, const float *state,
+                         const float *d_out, const float *d_state, float *dq, float *dk,
+                         float *dv, float *dg, float *dbeta, float *d_state_in) {
+    const int64_t S = p->cu ? p->nseq : p->b, H = p->h, dk_ = p->dk, dv_ = p->dv;
+    const int64_t DD = dk_ * dv_;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t r = 0; r < S * H; r++) {
+        int64_t s = r / H, h = r % H;
+        int64_t t0 = p->cu ? p->cu[s] : s, t1 = p->cu ? p->cu[s + 1] : s + 1;
+        int64_t len = t1 - t0;
+        /* pre[i]: the state before token t0 + i */
+        R *pre = (R *)malloc(sizeof(R) * DD * (len > 0 ? len : 1));
+        R *ds = (R *)malloc(sizeof(R) * DD), *sp = (R *)malloc(sizeof(R) * DD);
+        R *qn = (R *)malloc(sizeof(R) * dk_), *kn = (R *)malloc(sizeof(R) * dk_);
+        R *qi = (R *)malloc(sizeof(R) * (len > 0 ? len : 1)), *ki = (R *)malloc(sizeof(R) * (len > 0 ? len : 1));
+        R *kv = (R *)malloc(sizeof(R) * dv_), *delta = (R *)malloc(sizeof(R) * dv_);
+        R *ddelta = (R *)malloc(sizeof(R) * dv_), *dkv = (R *)malloc(sizeof(R) * dv_);
+        R *dqs = (R *)malloc(sizeof(R) * dk_), *dkn = (R *)malloc(sizeof(R) * dk_);
+        for (int64_t x = 0; x < DD; x++) {
+            ds[x] = d_state ? (R)d_state[r * DD + x] : 0;
+            if (len > 0) pre[x] = state[r * DD + x];
+        }
+        /* forward sweep: the normalised rows and the state before each token */
+        for (int64_t i = 0; i < len; i++) {
+            int64_t t = t0 + i;
+            const float *qt = q + (t * H + h) * dk_, *kt = k + (t * H + h) * dk_;
+            R qs = 0, ks = 0;
+            for (int64_t x = 0; x < dk_; x++) {
+                qs += (R)qt[x] * (R)qt[x];
+                ks += (R)kt[x] * (R)kt[x];
+            }
+            qi[i] = p->qk_l2norm ? (R)1 / SQRT(qs + (R)DMO_L2NORM_EPS) : (R)1;
+            ki[i] = p->qk_l2norm ? (R)1 / SQRT(ks + (R)DMO_L2NORM_EPS) : (R)1;
+            if (i + 1 == len) break;
+            R a = EXP((R)g[t * H + h]), bt = beta[t * H + h];
+            const R *P = pre + i * DD;
+            R *N = pre + (i + 1) * DD;
+            for (int64_t x = 0; x < dk_; x++) kn[x] = (R)kt[x] * ki[i];
+            for (int64_t y = 0; y < dv_; y++) {
+                R acc = 0;
+                for (int64_t x = 0; x < dk_; x++) acc += a * P[x * dv_ + y] * kn[x];
+                delta[y] = ((R)v[(t * H + h) * dv_ + y] - acc) * bt;
+            }
+            for (int64_t x = 0; x < dk_; x++)
+                for (int64_t y = 0; y < dv_; y++)
+                    N[x * dv_ + y] = a * P[x * dv_ + y] + kn[x] * delta[y];
+        }
+        /* reverse sweep */
+        for (int64_t i = len - 1; i >= 0; i--) {
+            int64_t t = t0 + i;
+            const float *qt = q + (t * H + h) * dk_, *kt = k + (t * H + h) * dk_;
+            const float *vt = v + (t * H + h) * dv_;
+            const float *dot = d_out ? d_out + (t * H + h) * dv_ : NULL;
+            R a = EXP((R)g[t * H + h]), bt = beta[t * H + h];
+            const R *P = pre + i * DD;
+            for (int64_t x = 0; x < dk_; x++) {
+                qn[x] = (R)qt[x] * qi[i] * (R)p->scale;
+                kn[x] = (R)kt[x] * ki[i];
+            }
+            for (int64_t x = 0; x < DD; x++) sp[x] = a * P[x];
+            for (int64_t y = 0; y < dv_; y++) {
+                R acc = 0;
+                for (int64_t x = 0; x < dk_; x++) acc += sp[x * dv_ + y] * kn[x];
+                kv[y] = acc;
+                delta[y] = ((R)vt[y] - acc) * bt;
+            }
+            /* o = S^T qs with S = S' + k delta^T */
+            for (int64_t x = 0; x < dk_; x++) {
+                R acc = 0;
+                for (int64_t y = 0; y < dv_; y++) {
+                    R o = dot ? (R)dot[y] : 0;
+                    acc += (sp[x * dv_ + y] + kn[x] * delta[y]) * o;
+                    ds[x * dv_ + y] += qn[x] * o;
+                }
+                dqs[x] = acc;
+            }
+            R db = 0;
+            for (int64_t y = 0; y < dv_; y++) {
+                R acc = 0;
+                for (int64_t x = 0; x < dk_; x++) acc += ds[x * dv_ + y] * kn[x];
+                ddelta[y] = acc;
+                dkv[y] = -bt * acc;
+                db += acc * ((R)vt[y] - kv[y]);
+                dv[(t * H + h) * dv_ + y] = (float)(bt * acc);
+            }
+            R dgs = 0;
+            for (int64_t x = 0; x < dk_; x++) {
+                R acc = 0;
+                for (int64_t y = 0; y < dv_; y++) {
+                    acc += ds[x * dv_ + y] * delta[y] + sp[x * dv_ + y] * dkv[y];
+                    R d1 = ds[x * dv_ + y] + kn[x] * dkv[y];
+                    dgs += d1 * sp[x * dv_ + y];
+                    ds[x * dv_ + y] = a * d1;
+                }
+                dkn[x] = acc;
+            }
+            dg[t * H + h] = (float)dgs;
+            dbeta[t * H + h] = (float)db;
+            /* through the scale and the l2 normalisation: d x = (d xn - xn (xn . d xn)) / n */
+            R sq = 0, sk = 0;
+            for (int64_t x = 0; x < dk_; x++) {
+                dqs[x] *= (R)p->scale;
+                sq += (R)qt[x] * qi[i] * dqs[x];
+                sk += (R)kt[x] * ki[i] * dkn[x];
+            }
+            for (int64_t x = 0; x < dk_; x++) {
+                if (p->qk_l2norm) {
+                    dq[(t * H + h) * dk_ + x] = (float)(qi[i] * (dqs[x] - (R)qt[x] * qi[i] * sq));
+                    dk[(t * H + h) * dk_ + x] = (float)(ki[i] * (dkn[x] - (R)kt[x] * ki[i] * sk));
+                } else {
+                    dq[(t * H + h) * dk_ + x] = (float)dqs[x];
+                    dk[(t * H + h) * dk_ + x] = (float)dkn[x];
+                }
+            }
+        }
+        if (d_state_in)
+            for (int64_t x = 0; x < DD; x++) d_state_in[r * DD + x] = (float)ds[x];
+        free(pre); free(ds); free(sp); free(qn); free(kn); free(qi); free(ki); free(kv);
+        free(delta); free(ddelta); free(dkv); free(dqs); free(dkn);
+    }
+    return 0;
+}

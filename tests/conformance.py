@@ -106,12 +106,14 @@ class GatedDeltaStep:
     state: HostTensor
     cu_seqlens: Optional[np.ndarray]
     options: GatedDeltaStepOptions
+    grad: Optional[tuple] = None  # (d_out HostTensor, d_state HostTensor), lib.rs:378-385
 
 
 @dataclasses.dataclass
 class GatedDeltaStepOut:
     out: HostTensor
     state: HostTensor
+    grads: Optional[dict] = None  # q, k, v, g, beta, state (lib.rs:398-413)
 
 
 def ran(label, thunk):
@@ -338,6 +340,10 @@ STEPS = ["step_f32", "step_f32_scale"]
 # gated_delta_recurrent.rs:34-45
 STEP_F32_OUT = 8e-7
 STEP_F32_STATE = 4e-7
+# gated_delta_recurrent.rs:44: the step's gradients against torch autograd
+STEP_GRAD_VS_TORCH = 2e-6
+# gated_delta_packed.rs:57-59: the packed step's gradients against float64
+STEP_GRAD = 4e-7
 STEP_BF16_VS_TORCH_BF16 = (8e-3, 4e-3)
 STEP_BF16_VS_UPCAST = (4e-3, 4e-7)
 
@@ -577,3 +583,79 @@ def check_bf16_step(adapter, label):
         ab, rel = errors(data, n(what))
         print(f"{label} step_bf16 against {what}: abs {ab:.3e} rel {rel:.3e} (tol {tol:.0e})")
         assert rel <= tol, (what, rel)
+
+
+def check_gradients(adapter, label):
+    """gated_delta_recurrent.rs:229-269: one step's output, new state and the gradients of every
+    input against torch autograd through the same step."""
+    f = File("gated_delta_recurrent/step_grad.safetensors")
+    n = lambda k: f[f"step_grad.{k}"]  # noqa: E731
+    call = GatedDeltaStep(*(HostTensor("f32", n(k)) for k in ["q", "k", "v", "g", "beta", "state"]),
+                          cu_seqlens=None, options=GatedDeltaStepOptions(qk_l2norm=True),
+                          grad=(HostTensor("f32", n("w_out")), HostTensor("f32", n("w_state"))))
+    r = ran("step_grad", lambda: adapter.gated_delta_step(call))
+    if r is None:
+        return False
+    checks = [("out", r.out.values, n("out"), STEP_F32_OUT),
+              ("new_state", r.state.values, n("new_state"), STEP_F32_STATE)]
+    assert r.grads is not None, "step_grad: the gradients asked for"
+    for name in ["q", "k", "v", "g", "beta", "state"]:
+        checks.append((f"grad_{name}", r.grads[name].values, n(f"grad_{name}"),
+                       STEP_GRAD_VS_TORCH))
+    for what, act, exp, tol in checks:
+        ab, rel = errors(act, exp)
+        print(f"{label} step_grad {what}: max abs {ab:.3e}, relative {rel:.3e} (tol {tol:.0e})")
+        assert rel <= tol, (what, rel)
+    return True
+
+
+def check_step_gradients(adapter, label):
+    """gated_delta_packed.rs:419-443, :504-517: the packed step's gradients (cotangents of the
+    output and of the final states) against transformers in float64, sequences of 1, 3, 0 and 2
+    tokens (an empty one passes the state's gradient through) and of 2, 1 and 4."""
+    import json
+    ran_cases = 0
+    for name in STEPS:
+        f = File(f"gated_delta_packed/{name}.safetensors")
+        scale = json.loads(f.meta("scale", "null"))
+        opts = GatedDeltaStepOptions(_flag(f, "l2norm"), None if scale is None else float(scale))
+        call = GatedDeltaStep(*(HostTensor("f32", f[k]) for k in ["q", "k", "v", "g", "beta",
+                                                                   "h0"]),
+                              cu_seqlens=f["cu_seqlens"], options=opts,
+                              grad=(HostTensor("f32", f["d_out"]), HostTensor("f32", f["d_state"])))
+        r = ran(name, lambda: adapter.gated_delta_step(call))
+        if r is None:
+            continue
+        assert r.grads is not None, f"{name}: the gradients asked for"
+        res = {"dq": r.grads["q"].values, "dk": r.grads["k"].values, "dv": r.grads["v"].values,
+               "dg": r.grads["g"].values, "dbeta": r.grads["beta"].values,
+               "dh0": r.grads["state"].values}
+        check_results(name, label, res, f, "_f64", STEP_GRAD)
+        ran_cases += 1
+    return ran_cases
+
+
+def the_default_scale_is_one_over_the_root_of_dk(adapter, label):
+    """gated_delta_packed.rs:519-548: giving the scale 1 / sqrt(Dk) explicitly changes nothing,
+    to the bit (chunk_f32, normalised queries and keys, final states)."""
+    f = File("gated_delta_packed/chunk_f32.safetensors")
+    dk = f["q"].shape[3]
+
+    def run(scale):
+        options = ChunkGatedDeltaOptions(qk_l2norm=True, scale=scale, output_final_state=True)
+        call = ChunkGatedDelta(
+            q=HostTensor("f32", f["q"]), k=HostTensor("f32", f["k"]), v=HostTensor("f32", f["v"]),
+            g=HostTensor("f32", f["g"]), beta=HostTensor("f32", f["beta"]),
+            initial_state=HostTensor("f32", f["h0"]), cu_seqlens=f["cu_seqlens"], options=options)
+        r = ran("chunk_f32", lambda: adapter.chunk_gated_delta_rule(call))
+        return None if r is None else (r.out.values, r.final_state.values)
+
+    by_default = run(None)
+    # the scale as the contract computes it in f32: 1 / sqrt(Dk) (dash-contract lib.rs query_scale)
+    given = run(float(np.float32(1.0) / np.sqrt(np.float32(dk))))
+    if by_default is None or given is None:
+        return False
+    for a, b in zip(by_default, given):
+        assert np.array_equal(a, b), f"{label}: an explicit 1/sqrt(Dk) changed the result"
+    print(f"{label} default scale: out and final states identical to the bit")
+    return True

@@ -76,4 +76,11 @@ class GpuAdapter:
                                                  call.state))
         cu = None if call.cu_seqlens is None else torch.as_tensor(call.cu_seqlens).cuda()
         out, ns = dm.gated_delta_step(q, k, v, g, beta, st, cu, call.options)
-        return GatedDeltaStepOut(host(out), host(ns))
+        grads = None
+        if call.grad is not None:
+            d_out, d_state = call.grad
+            r = dm.gated_delta_step_backward(q, k, v, g, beta, st, cu, dev(d_out).to(q.dtype),
+                                             dev(d_state), call.options)
+            grads = {"q": host(r[0]), "k": host(r[1]), "v": host(r[2]), "g": host(r[3]),
+                     "beta": host(r[4]), "state": host(r[5])}
+        return GatedDeltaStepOut(host(out), host(ns), grads)

@@ -84,7 +84,17 @@ class OracleAdapter:
     def gated_delta_step(self, call):
         o = call.options
         scale = query_scale(o.scale, call.q.shape[2])
-        out, st = oracle.gdr_step(call.q.values, call.k.values, call.v.values, call.g.values,
-                                  call.beta.values, call.state.values, cu=call.cu_seqlens,
-                                  l2norm=o.qk_l2norm, scale=scale, precision=self.precision)
-        return GatedDeltaStepOut(as_dtype(out, call.q.dtype), HostTensor("f32", st))
+        args = [call.q.values, call.k.values, call.v.values, call.g.values, call.beta.values,
+                call.state.values]
+        out, st = oracle.gdr_step(*args, cu=call.cu_seqlens, l2norm=o.qk_l2norm, scale=scale,
+                                  precision=self.precision)
+        grads = None
+        if call.grad is not None:
+            # the output's cotangent meets the output in its dtype (the reference's cast back)
+            d_out = as_dtype(call.grad[0].values, call.q.dtype).values
+            r = oracle.gdr_step_bwd(*args, d_out, call.grad[1].values, cu=call.cu_seqlens,
+                                    l2norm=o.qk_l2norm, scale=scale, precision=self.precision)
+            grads = {"q": as_dtype(r[0], call.q.dtype), "k": as_dtype(r[1], call.k.dtype),
+                     "v": as_dtype(r[2], call.v.dtype), "g": as_dtype(r[3], call.g.dtype),
+                     "beta": as_dtype(r[4], call.beta.dtype), "state": HostTensor("f32", r[5])}
+        return GatedDeltaStepOut(as_dtype(out, call.q.dtype), HostTensor("f32", st), grads)

@@ -77,3 +77,20 @@ def test_prefill_then_decode(adapter):
 
 def test_bf16_step(adapter):
     cf.check_bf16_step(adapter, "hip")
+
+
+def test_step_gradients(adapter):
+    """gated_delta_recurrent.rs:229-269: one step's gradients against torch autograd."""
+    _lib.probe_reset()
+    assert cf.check_gradients(adapter, "hip")
+    assert _lib.probe_counts()["gdr_step_bwd"] > 0
+
+
+def test_packed_step_gradients(adapter):
+    """gated_delta_packed.rs:504-517: the packed step's gradients against float64."""
+    assert cf.check_step_gradients(adapter, "hip") == 2
+
+
+def test_default_scale(adapter):
+    """gated_delta_packed.rs:519-548."""
+    assert cf.the_default_scale_is_one_over_the_root_of_dk(adapter, "hip")

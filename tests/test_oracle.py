@@ -150,3 +150,60 @@ def test_chunk_continues_into_step():
     np.testing.assert_allclose(out[:, :-1], out1, rtol=0, atol=1e-5)
     np.testing.assert_allclose(out[:, -1], o2, rtol=0, atol=1e-5)
     np.testing.assert_allclose(fin, st, rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("precision", ["f32", "f64"])
+def test_step_gradients(precision):
+    """dash-conformance's check_gradients (torch autograd through one step) and
+    check_step_gradients (packed steps against float64) on the oracle's step backward."""
+    assert cf.check_gradients(OracleAdapter(precision), f"oracle-{precision}")
+    assert cf.check_step_gradients(OracleAdapter(precision), f"oracle-{precision}") == 2
+
+
+def test_default_scale():
+    assert cf.the_default_scale_is_one_over_the_root_of_dk(OracleAdapter("f32"), "oracle")
+
+
+@pytest.mark.parametrize("l2norm", [False, True])
+def test_step_gradients_finite_differences(l2norm):
+    """The step backward in f64 against central differences of the f64 step: the loss
+    sum(out * d_out) + sum(new_state * d_state) over packed sequences of 3, 0, 1 and 4 tokens,
+    each input perturbed one element at a time. Independent of the fixtures: a dropped term, a
+    wrong sign or a transposed product shows here."""
+    rng = np.random.default_rng(11)
+    cu = np.array([0, 3, 3, 4, 8], np.int64)
+    t, s, h, dk, dv = 8, 4, 2, 5, 3
+    q, k = rng.standard_normal((2, t, h, dk))
+    v = rng.standard_normal((t, h, dv))
+    g = -np.log1p(np.exp(rng.standard_normal((t, h))))
+    beta = 1 / (1 + np.exp(-rng.standard_normal((t, h))))
+    st = 0.3 * rng.standard_normal((s, h, dk, dv))
+    d_out = rng.standard_normal((t, h, dv))
+    d_st = rng.standard_normal((s, h, dk, dv))
+    scale = 0.7
+    inputs = [q, k, v, g, beta, st]
+
+    def loss(xs):
+        # the f64 oracle takes f32 arrays: keep the perturbation exact in f32 by scaling the
+        # inputs to values f32 holds exactly is not needed, the tolerance covers it
+        out, ns = oracle.gdr_step(*xs, cu=cu, l2norm=l2norm, scale=scale, precision="f64")
+        return float(np.sum(out.astype(np.float64) * d_out) + np.sum(ns.astype(np.float64) * d_st))
+
+    grads = oracle.gdr_step_bwd(*inputs, d_out, d_st, cu=cu, l2norm=l2norm, scale=scale,
+                                precision="f64")
+    eps = 1e-3
+    for which, (x, gx) in enumerate(zip(inputs, grads)):
+        flat = x.reshape(-1)
+        num = np.zeros(flat.size)
+        for i in range(flat.size):
+            keep = flat[i]
+            flat[i] = keep + eps
+            lp = loss(inputs)
+            flat[i] = keep - eps
+            lm = loss(inputs)
+            flat[i] = keep
+            num[i] = (lp - lm) / (2 * eps)
+        np.testing.assert_allclose(gx.reshape(-1), num, rtol=2e-3, atol=2e-3,
+                                   err_msg=f"input {which}")
+    # the empty sequence passes the state's gradient through
+    np.testing.assert_array_equal(grads[5][1], d_st[1].astype(np.float32))
