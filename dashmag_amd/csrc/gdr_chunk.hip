@@ -810,8 +810,14 @@ int dm_gdr_chunk_fwd(const dm_gdr_desc *d, const void *q, const void *k, const v
     hipStream_t st = (hipStream_t)stream;
     const int64_t S = gdr_nseq(d), nc = gdr_chunk_bound(d);
     if (S * d->h == 0) return DM_OK;
-    if (gdr_mfma_takes(d))
+    if (gdr_mfma_takes(d)) {
+        for (const void *p : {q, k, v, (const void *)out})
+            if (!aligned_16b(p))
+                return refuse("chunk_gated_delta_rule: q, k, v and out must be 16-byte aligned "
+                              "(16-bit heads that are multiples of 8 wide read and write whole "
+                              "rows; the host copies other views)");
         return launch_gdr_mfma_fwd(d, q, k, v, g, beta, h0, out, final_state, workspace, st);
+    }
     GdrWs w;
     gdr_ws_layout(d, false, (char *)workspace, &w);
     GdrArgs a = gdr_args(d, q, k, v, g, beta);
@@ -852,9 +858,15 @@ int dm_gdr_chunk_bwd(const dm_gdr_desc *d, const void *q, const void *k, const v
     hipStream_t st = (hipStream_t)stream;
     const int64_t S = gdr_nseq(d), nc = gdr_chunk_bound(d);
     if (S * d->h == 0) return DM_OK;
-    if (gdr_mfma_takes(d))
+    if (gdr_mfma_takes(d)) {
+        for (const void *p : {q, k, v, d_out, (const void *)dq, (const void *)dk, (const void *)dv})
+            if (!aligned_16b(p))
+                return refuse("chunk_gated_delta_rule_backward: q, k, v, d_out, dq, dk and dv "
+                              "must be 16-byte aligned (16-bit heads that are multiples of 8 "
+                              "wide read and write whole rows; the host copies other views)");
         return launch_gdr_mfma_bwd(d, q, k, v, g, beta, h0, d_out, d_final, dq, dk, dv, dg,
                                    dbeta, dh0, workspace, st);
+    }
     GdrWs w;
     gdr_ws_layout(d, true, (char *)workspace, &w);
     GdrArgs a = gdr_args(d, q, k, v, g, beta);

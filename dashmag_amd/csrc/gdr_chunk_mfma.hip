@@ -1892,13 +1892,12 @@ __global__ __launch_bounds__(512, 1) void gdr_bwd_grads(GdrArgs a, MfmaWs w, con
 // ------------------------------------------------------------------------------------------
 
 bool gdr_mfma_takes(const dm_gdr_desc *d) {
-    // (the state pass addresses the keys through a 32-bit buffer range; 16-byte row loads)
-    // head widths below 128 run the same products with the columns past the width held at
+    // (16-byte row loads and stores; the base pointers' alignment is checked by the entry
+    // points, which refuse misaligned ones) head widths below 128 run the same products with the columns past the width held at
     // zero (loaded as zeros, never stored): a zero key or query column adds nothing to any
     // product or norm, and the state's rows and columns past the widths stay zero
     return (d->dtype == DM_BF16 || d->dtype == DM_F16) && d->dk % 8 == 0 && d->dv % 8 == 0 &&
-           d->dk >= 8 && d->dv >= 8 && d->dk <= kD && d->dv <= kD &&
-           d->b * d->t * d->h * kD * 2 < (1ll << 32) && gdr_strides_16b(d);
+           d->dk >= 8 && d->dv >= 8 && d->dk <= kD && d->dv <= kD && gdr_strides_16b(d);
 }
 
 size_t gdr_mfma_fwd_workspace(const dm_gdr_desc *d) { return mfma_layout(d, nullptr, nullptr); }

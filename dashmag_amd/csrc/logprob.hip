@@ -345,7 +345,9 @@ __global__ __launch_bounds__(kLpThreads) void lce_dz(int64_t rows, int64_t cw, i
 // 16-bit dtype); the tail past a multiple of 8 element by element.
 __global__ void lp_cast(int64_t count, const float *__restrict__ x, void *__restrict__ y, int dt) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t n8 = count / 8;
+    // whole 16-byte stores only into a 16-byte aligned destination (a caller's output may be
+    // an offset view); element by element otherwise
+    const int64_t n8 = ((uintptr_t)y & 15) ? 0 : count / 8;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
         const f32x4_t av = __builtin_nontemporal_load((const f32x4_t *)x + 2 * i);
         const f32x4_t bv = __builtin_nontemporal_load((const f32x4_t *)x + 2 * i + 1);
@@ -811,7 +813,10 @@ int dm_linear_cross_entropy_bwd(const dm_lce_desc *d, const void *hidden, const 
                     rows_b, cw, c0, Z, targets + r0, dbits, rows + r0, coef + r0, lp->n, G);
             DM_LAUNCH_CHECK("linear_cross_entropy: logits gradient");
             const char *Wc = (const char *)W + (size_t)c0 * lp->d * esz;
-            // grad_hidden (column-major D x rows) += W_c as stored (D x cw) G^T (cw x rows)
+            // grad_hidden (column-major D x rows) += W_c as stored (D x cw) G^T (cw x rows).
+            // The first product of each accumulator runs with beta = 0, which hipBLASLt takes
+            // as "C is not read" (the accumulators are never cleared; a workspace poisoned with
+            // NaN gives the same bits as a zeroed one, a property the GPU tests hold it to)
             if (gh)
                 if (int rc = lt_gemm(st, false, false, lp->d, rows_b, cw, Wc, G, op_t,
                                      c0 == 0 ? 0.f : 1.f, gh + r0 * lp->d, lt_ws))

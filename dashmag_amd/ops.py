@@ -64,7 +64,9 @@ def _readable(t):
     if st[-1] != 1 and t.shape[-1] > 1:
         return t.contiguous()
     if t.element_size() == 2 and (any(x % 8 for x in st[:-1]) or t.data_ptr() % 16):
-        return t.contiguous()
+        c = t.contiguous()
+        # a contiguous view at an offset is its own contiguous(): copy it to a fresh allocation
+        return c.clone() if c.data_ptr() % 16 else c
     return t
 
 

@@ -37,7 +37,9 @@
  *     elements are given and its last dimension is contiguous; the kernels read it in place
  *     (crates/dash-ops/src/attention.rs:85-93, attention/cube.rs:428-461). The fast kernels
  *     take strides that are multiples of 16 bytes and 16-byte aligned bases (other calls run
- *     the generic kernels, which take any). Without `strided`, every input is contiguous.
+ *     the generic kernels, which take any), except the chunked gated delta rule: a bf16/f16
+ *     call whose heads are multiples of 8 wide (up to 128) is refused unless q, k, v, d_out
+ *     and its 16-bit outputs are 16-byte aligned. Without `strided`, every input is contiguous.
  *   - Floating inputs of a call share one dtype (dm_dtype); lse and states are f32; g and beta
  *     of the gated delta rule may each be f32 or the inputs' dtype.
  *   - Sequence boundaries (cu_seqlens) and cache lengths are int32 device arrays.
@@ -271,8 +273,10 @@ int dm_attention_decode(const dm_attention_desc *desc, const void *q, const void
  * static device array of 16 MiB per GPU, held until the process ends; a call whose
  * dm_attention_decode_workspace exceeds 16 MiB is refused (about 64 sequences x 32 query heads
  * x 16 splits at D = 128). Every call on one GPU shares that array: calls that overlap on one GPU
- * (concurrent streams or threads) race. Same arguments, results and refusals as
- * dm_attention_decode otherwise (dense or packed cache). */
+ * (concurrent streams or threads) race, and so do replays of graphs that captured it. The
+ * first call on a device looks up that device's array (hipGetSymbolAddress): make it outside
+ * graph capture. Same arguments, results and refusals as dm_attention_decode otherwise (dense
+ * or packed cache). */
 int dm_attention_decode_noalloc(const dm_attention_desc *desc, const void *q, const void *k,
                                 const void *v, const int32_t *lengths, void *o, void *stream);
 

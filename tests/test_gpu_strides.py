@@ -176,3 +176,46 @@ def test_gdr_step_views():
                                  beta.contiguous(), st, None, opts)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_gdr_chunk_refuses_misaligned_bases():
+    """Through the C ABI: bf16 heads that the MFMA kernels take (multiples of 8 wide) with q's
+    base 2 elements (4 bytes) past a 16-byte boundary are refused with the op's name, forward and
+    backward, before any launch; the aligned call on the same data runs."""
+    import ctypes
+    from dashmag_amd import ops
+    lib = _lib.lib()
+    t, h, dk = 128, 2, 64
+    buf = syn.normal(40, (t * h * dk + 8,), "cuda").bfloat16()
+    q_bad = buf[2:2 + t * h * dk].view(1, t, h, dk)
+    k = syn.normal(41, (1, t, h, dk), "cuda").bfloat16()
+    v = syn.normal(42, (1, t, h, dk), "cuda").bfloat16()
+    g = -torch.nn.functional.softplus(syn.normal(43, (1, t, h), "cuda"))
+    beta = torch.sigmoid(syn.normal(44, (1, t, h), "cuda"))
+    desc, _, _ = ops._gdr_desc("chunk_gated_delta_rule", q_bad, k, v, g, beta, None, True, None,
+                               False, [])
+    out = torch.empty_like(v)
+    dq, dk_, dv = torch.empty_like(k), torch.empty_like(k), torch.empty_like(v)
+    dg, db = torch.empty_like(g), torch.empty_like(beta)
+    nf = lib.dm_gdr_chunk_fwd_workspace(ctypes.byref(desc))
+    nb = lib.dm_gdr_chunk_bwd_workspace(ctypes.byref(desc))
+    ws = torch.empty(max(nf, nb, 1), dtype=torch.uint8, device="cuda")
+    p = lambda x: ctypes.c_void_p(None if x is None else x.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.probe_reset()
+    rc = lib.dm_gdr_chunk_fwd(ctypes.byref(desc), p(q_bad), p(k), p(v), p(g), p(beta), p(None),
+                              p(out), p(None), p(ws), ws.numel(), st)
+    assert rc == _lib.DM_ERR_REFUSED
+    assert _lib.last_error().startswith("chunk_gated_delta_rule: "), _lib.last_error()
+    rc = lib.dm_gdr_chunk_bwd(ctypes.byref(desc), p(q_bad), p(k), p(v), p(g), p(beta), p(None),
+                              p(out), p(None), p(dq), p(dk_), p(dv), p(dg), p(db), p(None), p(ws),
+                              ws.numel(), st)
+    assert rc == _lib.DM_ERR_REFUSED
+    assert _lib.last_error().startswith("chunk_gated_delta_rule_backward: "), _lib.last_error()
+    assert _lib.probe_counts()["gdr_chunk_fwd"] == 0
+    # the operations copy such a view and run
+    o, _ = dm.chunk_gated_delta_rule(q_bad, k, v, g, beta, None, None,
+                                     dm.ChunkGatedDeltaOptions(qk_l2norm=True))
+    o2, _ = dm.chunk_gated_delta_rule(q_bad.contiguous(), k, v, g, beta, None, None,
+                                      dm.ChunkGatedDeltaOptions(qk_l2norm=True))
+    assert torch.equal(o, o2)

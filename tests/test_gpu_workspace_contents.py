@@ -114,3 +114,19 @@ def test_gated_delta_rule_and_conv1d():
     copts = dm.CausalConv1dOptions(activation=dm.Activation.SILU)
     a, b = _twice(lambda: dm.causal_conv1d_backward(x, wc, None, None, cu, gy, None, copts))
     _equal(a, b)
+
+
+def test_gated_delta_step_backward():
+    """The step backward's kept states and per-slice partial sums."""
+    cu = torch.tensor([0, 3, 3, 4, 9], dtype=torch.int32, device="cuda")
+    q = syn.normal(22, (9, 2, 128), "cuda").bfloat16()
+    k = syn.normal(23, (9, 2, 128), "cuda").bfloat16()
+    v = syn.normal(24, (9, 2, 128), "cuda").bfloat16()
+    g = -torch.nn.functional.softplus(syn.normal(25, (9, 2), "cuda"))
+    beta = torch.sigmoid(syn.normal(26, (9, 2), "cuda"))
+    st = syn.normal(27, (4, 2, 128, 128), "cuda", std=0.1)
+    do = syn.normal(28, (9, 2, 128), "cuda").bfloat16()
+    dst = syn.normal(29, (4, 2, 128, 128), "cuda")
+    opts = dm.GatedDeltaStepOptions(qk_l2norm=True)
+    a, b = _twice(lambda: dm.gated_delta_step_backward(q, k, v, g, beta, st, cu, do, dst, opts))
+    _equal(a, b)

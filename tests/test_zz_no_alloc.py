@@ -65,3 +65,40 @@ def test_noalloc_decode_packed_cache():
     # and the dense cache's own result, to the bit
     o3, _, _ = _both(q, k, v, lens, _desc(q, k, v))
     assert torch.equal(o1, o3)
+
+
+def test_noalloc_decode_under_graph_capture():
+    """An eager call first (the device's array looked up outside capture), then the call captured
+    in a HIP graph and replayed three times, other device work between the replays: every replay
+    equals the eager output to the bit."""
+    lib = _lib.lib()
+    b, s, hq, hkv, d = 8, 2048, 8, 2, 128
+    q, k, v, lens = _inputs(b, s, hq, hkv, d, 31)
+    desc = _desc(q, k, v)
+    o = torch.empty_like(q)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.dm_attention_decode_noalloc(ctypes.byref(desc), p(q), p(k), p(v), p(lens), p(o),
+                                             st)
+        assert rc == 0, _lib.last_error()
+
+    fn()
+    torch.cuda.synchronize()
+    eager = o.clone()
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(g, stream=cs):
+            fn()
+    torch.cuda.synchronize()
+    for r in range(3):
+        o.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device="cuda") * (r + 1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, eager), f"replay {r} differs"
+        del junk
