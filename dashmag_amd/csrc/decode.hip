@@ -68,6 +68,88 @@ __device__ __forceinline__ int64_t kv_page(const KvMap &m, int64_t b, int64_t j)
     return pg >= 0 && pg < m.num_pages ? pg : -1;
 }
 
+// The splits of one (sequence, query head) merged by their log-sum-exp, by the 256 threads of a
+// workgroup. The row's log-sum-exps go to LDS once (one load a thread) and become the splits'
+// weights; then thread t sums, for the 4 columns of its 16-byte piece d4 = t % (D / 4), the
+// splits s = t / (D / 4) + k * (1024 / D), four loads in flight at a time, and the split groups'
+// sums are added in a fixed order through LDS. (A thread walking every split of its columns one
+// dependent load after another took 6-8 us for a handful of rows.)
+struct MergeLds {
+    float w[4096];      // the splits' weights (nsplit <= 4096, span_of)
+    float4 red[256];    // the split groups' partial sums
+};
+template <int DT>
+__device__ __forceinline__ void merge_row(int64_t row, int64_t D, int nsplit,
+                                          const float *__restrict__ part_o,
+                                          const float *__restrict__ part_lse,
+                                          void *__restrict__ o, MergeLds &ml) {
+    float *wsm = ml.w;
+    float4 *red = ml.red;
+    const int tid = threadIdx.x;
+    const float *pl = part_lse + row * nsplit;
+    float mx = -INFINITY;
+    for (int sp = tid; sp < nsplit; sp += 256) {
+        const float x = pl[sp];
+        wsm[sp] = x;
+        mx = fmaxf(mx, x);
+    }
+    mx = wave_max(mx);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6].x = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0].x, red[1].x), fmaxf(red[2].x, red[3].x));
+    float lsum = 0.f;
+    for (int sp = tid; sp < nsplit; sp += 256) {
+        const float w = M == -INFINITY ? 0.f : __expf(wsm[sp] - M);
+        wsm[sp] = w;
+        lsum += w;
+    }
+    lsum = wave_sum(lsum);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6].y = lsum;
+    __syncthreads();
+    const float L = (red[0].y + red[1].y) + (red[2].y + red[3].y);
+    __syncthreads();
+    const int nd4 = (int)(D / 4), groups = 256 / nd4;
+    const int d4 = tid % nd4, grp = tid / nd4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (grp < groups) {
+        const float4 *po = (const float4 *)(part_o + row * nsplit * D) + d4;
+        int sp = grp;
+        for (; sp + 3 * groups < nsplit; sp += 4 * groups) {
+            float4 x[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) x[u] = po[(int64_t)(sp + u * groups) * nd4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float w = wsm[sp + u * groups];
+                acc.x += w * x[u].x, acc.y += w * x[u].y, acc.z += w * x[u].z, acc.w += w * x[u].w;
+            }
+        }
+        for (; sp < nsplit; sp += groups) {
+            const float4 x = po[(int64_t)sp * nd4];
+            const float w = wsm[sp];
+            acc.x += w * x.x, acc.y += w * x.y, acc.z += w * x.z, acc.w += w * x.w;
+        }
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < nd4) {
+        float4 a = red[tid];
+        for (int g = 1; g < groups; g++) {
+            const float4 b = red[g * nd4 + tid];
+            a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const int64_t ob = row * D + tid * 4;
+        st<DT>(o, ob, a.x * inv);
+        st<DT>(o, ob + 1, a.y * inv);
+        st<DT>(o, ob + 2, a.z * inv);
+        st<DT>(o, ob + 3, a.w * inv);
+    }
+    __syncthreads();
+}
+
 // The split pass on MFMA (D = 64, 128 or 256). Each wavefront sweeps its quarter of the split in
 // blocks of 32 keys: the block's K and V rows arrive by coalesced 16-byte loads (64 / (D / 8) rows
 // per load), go to the wavefront's own LDS tiles, and the next block's loads are in flight while this block is
@@ -88,7 +170,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_mfma(
     int64_t S, int64_t Hq, int64_t Hkv, int64_t left, float scale, int nsplit, int span,
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     const int32_t *__restrict__ lengths, KvMap map, float *__restrict__ part_o,
-    float *__restrict__ part_lse) {
+    float *__restrict__ part_lse, void *__restrict__ out) {
     constexpr int NW = 4, BK = 32;
     constexpr int KS = D + 8, VS = D + 32;  // row strides (elements) of the row and transposed reads
     constexpr int LPR = D / 8, RPL = 64 / LPR, NLD = BK / RPL;  // lanes per row, rows per load, loads
@@ -275,12 +357,21 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_mfma(
             }
         }
         const int64_t pr = (b * Hq + kh * G + g) * nsplit + split;
+        if (nsplit == 1) {
+            // one split: its normalised partial is the output
+            st<DT>(out, (b * Hq + kh * G + g) * D + d, L > 0.f ? A / L : 0.f);
+            continue;
+        }
         part_o[pr * D + d] = L > 0.f ? A / L : 0.f;
         if (d == 0) part_lse[pr] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
     }
 }
 
-// Pass 2: merges the splits of one (sequence, query head) by their log-sum-exp.
+// Pass 2: merges the splits of one (sequence, query head) by their log-sum-exp, one workgroup a
+// row. (Merging in the split kernel instead, by the last of a key-value head's splits to finish,
+// measured slower: with release/acquire fences every workgroup wrote back and invalidated its
+// L2, 5x the split pass's time; with write-through partial stores and a relaxed counter each
+// workgroup waited on its stores' acknowledgement, 237 against 215 us on config 3.)
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge(int64_t rows, int64_t D, int nsplit,
                                                     const float *__restrict__ part_o,
@@ -288,20 +379,8 @@ __global__ __launch_bounds__(256) void decode_merge(int64_t rows, int64_t D, int
                                                     void *__restrict__ o) {
     const int64_t row = blockIdx.x;
     if (row >= rows) return;
-    const float *pl = part_lse + row * nsplit;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pl[s]);
-    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-        float L = 0.f, A = 0.f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < nsplit; s++) {
-                const float w = __expf(pl[s] - M);
-                L += w;
-                A += w * part_o[(row * nsplit + s) * D + d];
-            }
-        }
-        st<DT>(o, row * D + d, L > 0.f ? A / L : 0.f);
-    }
+    __shared__ MergeLds ml;
+    merge_row<DT>(row, D, nsplit, part_o, part_lse, o, ml);
 }
 
 // The generic decode: the generic attention forward's arithmetic, one wavefront per
@@ -483,6 +562,7 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
         return DM_OK;
     }
     const int nsplit = nsplit_of(d), span = span_of(d);
+    if (nsplit > 4096) return refuse(opn + ": internal: more than 4096 splits");
     const size_t parts = (size_t)rows * nsplit;
     float *part_o = (float *)workspace;
     float *part_lse = (float *)((char *)workspace + align_up(parts * d->d * sizeof(float)));
@@ -495,7 +575,7 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
 #define DEC_MFMA2(DT, GG, PG, DD)                                                           \
     decode_split_mfma<DT, GG, PG, DD><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, \
                                                                nsplit, span, q, k, v, lengths, \
-                                                               map, part_o, part_lse)
+                                                               map, part_o, part_lse, o)
 #define DEC_MFMA(DT, GG, DD)                         \
     if (paged) DEC_MFMA2(DT, GG, true, (DD == 256 ? 128 : DD)); else DEC_MFMA2(DT, GG, false, DD)
 #define DEC_GM(DT, DD)                               \
@@ -515,12 +595,12 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
         KernelTimer timer(DM_KERNEL_DECODE_SPLIT, st);
         if (d->dtype == DM_BF16) { DEC_D(DM_BF16); } else { DEC_D(DM_F16); }
     }
-    {
+    if (nsplit > 1) {  // (one split: the split kernel wrote the output itself)
         KernelTimer timer(DM_KERNEL_DECODE_MERGE, st);
         if (d->dtype == DM_BF16) {
-            decode_merge<DM_BF16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
+            decode_merge<DM_BF16><<<(unsigned)rows, 256, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
         } else {
-            decode_merge<DM_F16><<<(unsigned)rows, 128, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
+            decode_merge<DM_F16><<<(unsigned)rows, 256, 0, st>>>(rows, d->d, nsplit, part_o, part_lse, o);
         }
     }
 #undef DEC_D
@@ -528,11 +608,13 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
 #undef DEC_MFMA
 #undef DEC_MFMA2
     probe_add(DM_PROBE_DECODE_SPLIT);
-    probe_add(DM_PROBE_DECODE_MERGE);
+    if (nsplit > 1) probe_add(DM_PROBE_DECODE_MERGE);
     DM_LAUNCH_CHECK((opn + ": launch").c_str());
     return DM_OK;
 }
 
+// The split pass's workspace: partial outputs [B, Hq, nsplit, D] f32 and their log-sum-exps
+// [B, Hq, nsplit].
 static size_t decode_workspace(const dm_attention_desc *d, bool split) {
     if (!d || !split) return 0;
     const size_t parts = (size_t)(d->b * d->hq) * nsplit_of(d);

@@ -57,3 +57,25 @@ def test_generic_decode(dtype, d, hkv, g):
     r = errors(a, e)[1]
     print(f"rel {r:.2e}")
     assert r <= (1e-5 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("d,g", [(64, 4), (128, 4), (256, 2)])
+def test_single_split_writes_the_output(d, g):
+    """A cache of at most one split's keys (128): the split kernel writes the output itself and no
+    merge runs."""
+    gen = torch.Generator().manual_seed(d + g)
+    lengths = torch.tensor([0, 1, 77, 128], dtype=torch.int32)
+    b, s, hkv = 4, 128, 2
+    q = torch.randn(b, hkv * g, d, generator=gen).bfloat16()
+    k = torch.randn(b, s, hkv, d, generator=gen).bfloat16()
+    v = torch.randn(b, s, hkv, d, generator=gen).bfloat16()
+    _lib.probe_reset()
+    out = dm.attention_decode(q.cuda(), k.cuda(), v.cuda(), lengths.cuda())
+    torch.cuda.synchronize()
+    pc = _lib.probe_counts()
+    assert pc["decode_split"] == 1 and pc["decode_merge"] == 0, pc
+    e = oracle.attention_decode(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                lengths.numpy(), precision="f64")
+    a = out.float().cpu().numpy()
+    assert np.all(a[0] == 0.0)
+    assert errors(a, e)[1] <= 1e-2
