@@ -680,6 +680,7 @@ struct PartOps {
 // columns. Q^T and Aqk^T come as the B fragments the prep kernel stored (lane = token, k slots
 // 16 st + 8 (j / 4) + 4 (l / 32) + j % 4, the order of the chain's fragments), loaded two
 // chunks ahead; S^T and V'^T are the chain's fragments as A operands.
+constexpr int kOutRow = 40;  // 16-bit elements a row of an output tile in LDS (32 + 8)
 struct OutOps {
     Frag8 q[8], aq[4];
     float gam;
@@ -689,8 +690,9 @@ struct OutOps {
 template <int DT, int NP, int KS>
 __device__ __forceinline__ void state_output(const GdrArgs &a, const MfmaWs &w, void *out,
                                              const uint4 (*sbuf)[NP][KS][64],
-                                             const uint4 (*vbuf)[4][64], int64_t h, int blk,
-                                             int c0, int c1, int t, int lane, bool traced) {
+                                             const uint4 (*vbuf)[4][64], uint16_t *otiles,
+                                             int64_t h, int blk, int c0, int c1, int t, int lane,
+                                             bool traced) {
     const int col = lane & 31, half = lane >> 5;
     const int r = t * 32 + col;  // this lane's token within the chunk (column of O^T)
     // the sequence's tokens, read once: chunk c starts 64 (c - c0) tokens into them (no load
@@ -700,10 +702,11 @@ __device__ __forceinline__ void state_output(const GdrArgs &a, const MfmaWs &w, 
         first = w.chunk_tok0[c0];
         end = (int64_t)w.chunk_tok0[c1 - 1] + w.chunk_len[c1 - 1];
     }
-    // the lane's output columns: blk * 32 + 8 g + 4 (l / 32) + [0, 4), g < 4
-    uint16_t *obase = (uint16_t *)out + h * a.Dv + blk * 32 + half * 4;
+    // the block's output columns blk * 32 + [0, 32) of the rows
+    uint16_t *obase0 = (uint16_t *)out + h * a.Dv + blk * 32;
     const int64_t orow_stride = a.H * a.Dv;
-    const int ocols = (int)a.Dv - blk * 32 - half * 4;  // columns left in the row from there
+    const int ocols0 = (int)a.Dv - blk * 32;  // columns of the block within the head
+    uint16_t *otile = otiles + t * 32 * kOutRow;
     auto load = [&](int c, OutOps &x) __attribute__((always_inline)) {
         c = c < c1 ? c : c1 - 1;
         const int64_t ch = (int64_t)c * a.H + h;
@@ -734,15 +737,24 @@ __device__ __forceinline__ void state_output(const GdrArgs &a, const MfmaWs &w, 
         }
         DM_OSTAMP(c, 2);
         const float f = a.scale * __expf(x.gam);
-        if (r < x.len) {
-            uint16_t *orow = obase + (x.tok0 + r) * orow_stride;
+        // the tile through LDS, token rows of the block's 32 columns: lane (token r) writes its
+        // 16 values as 8-byte pieces, then each lane stores 16 bytes of a row (4 lanes a row, 16
+        // rows an instruction). 8-byte stores straight from the products' layout touched 32 rows
+        // an instruction, and cost the pass about 45 us on config 4 (316 -> 272 us).
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++)
-                if (g4 * 8 < ocols)
-                    *(uint2 *)(orow + g4 * 8) = make_uint2(
-                        pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]),
-                        pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]));
+        for (int g4 = 0; g4 < 4; g4++)
+            *(uint2 *)(otile + col * kOutRow + g4 * 8 + half * 4) = make_uint2(
+                pack2<DT>(inter[4 * g4] * f + intra[4 * g4], inter[4 * g4 + 1] * f + intra[4 * g4 + 1]),
+                pack2<DT>(inter[4 * g4 + 2] * f + intra[4 * g4 + 2], inter[4 * g4 + 3] * f + intra[4 * g4 + 3]));
+        __builtin_amdgcn_wave_barrier();  // (a wavefront's LDS accesses complete in order)
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int rr = k * 16 + (lane >> 2), piece = lane & 3;
+            const uint4 v = *(const uint4 *)(otile + rr * kOutRow + piece * 8);
+            if (t * 32 + rr < x.len && piece * 8 < ocols0)
+                *(uint4 *)(obase0 + (x.tok0 + t * 32 + rr) * orow_stride + piece * 8) = v;
         }
+        __builtin_amdgcn_wave_barrier();
         DM_OSTAMP(c, 3);
     };
     // one barrier per chunk of the chain plus its last one; after barrier b the chunk b - 1
@@ -782,6 +794,8 @@ __global__ __launch_bounds__(64 * NP + (OUT ? 128 : 0), 1) void gdr_mfma_state2(
     // barrier), both as the fragments the chain formed
     __shared__ __align__(16) uint4 sbuf[OUT ? 3 : 1][NP][KS][64];
     __shared__ __align__(16) uint4 vbuf[OUT ? 2 : 1][4][64];
+    // OUT: an output tile (32 tokens x 32 columns) a output wavefront, for its stores
+    __shared__ __align__(16) uint16_t otiles[OUT ? 2 * 32 * kOutRow : 8];
     int64_t sh;
     int blk;
     if (!state_item(blockIdx.x, w.nsh, w.seq_order, a.H, &sh, &blk)) return;
@@ -797,7 +811,8 @@ __global__ __launch_bounds__(64 * NP + (OUT ? 128 : 0), 1) void gdr_mfma_state2(
 #else
         const bool traced = false;
 #endif
-        state_output<DT, NP, KS>(a, w, out, sbuf, vbuf, h, blk, c0, c1, p - NP, lane, traced);
+        state_output<DT, NP, KS>(a, w, out, sbuf, vbuf, otiles, h, blk, c0, c1, p - NP, lane,
+                                 traced);
         return;
     }
 
