@@ -28,6 +28,8 @@ constexpr int kDqM = 128;      // queries per dQ workgroup
 
 struct BwdWs {
     float *lse2;      // [B, Tq, Hq]
+    int4 *rec;        // [B, Tq, Hq]: {lse2, delta (f32 bits), lo, hi - lo (>= 0)} per query row
+                      // and head, what the dK/dV kernel stages for a row in one 16-byte load
     int32_t *rlo;     // [B, Tq]
     int32_t *rhi;     // [B, Tq]
     int32_t *trange;  // [B, ntiles, 4]: union lo, union hi, full lo, full hi
@@ -70,6 +72,7 @@ static size_t bwd_layout(const dm_attention_desc *d, char *base, BwdWs *w) {
     };
     BwdWs x;
     x.lse2 = (float *)take(rows * 4);
+    x.rec = (int4 *)take(rows * 16);
     x.rlo = (int32_t *)take(qrows * 4);
     x.rhi = (int32_t *)take(qrows * 4);
     x.trange = (int32_t *)take(d->b * ntiles * 4 * 4);
@@ -131,8 +134,11 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
 #pragma unroll
             for (int off = CH / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
             if (c == 0 && h < Hq) {
+                const float l2 = l[u] == -INFINITY ? INFINITY : l[u] * 1.4426950408889634f;
                 delta[row * Hq + h] = s;
-                w.lse2[row * Hq + h] = l[u] == -INFINITY ? INFINITY : l[u] * 1.4426950408889634f;
+                w.lse2[row * Hq + h] = l2;
+                w.rec[row * Hq + h] = make_int4(__float_as_int(l2), __float_as_int(s), (int32_t)lo,
+                                                (int32_t)(hi > lo ? hi - lo : 0));
             }
         }
     }
@@ -295,7 +301,7 @@ struct DkdvSlot {
 
 #ifdef DM_TRACE_DKDV
 // profiling aid (built only with -DDM_TRACE_DKDV): per-step clock stamps of one workgroup
-__device__ uint64_t dm_trace[2][256][4];
+__device__ uint64_t dm_trace[2][256][8];
 #define DM_STAMP(role, step, k)                                                                  \
     do {                                                                                        \
         if (work == DM_TRACE_DKDV && kw == 0 && lane == 0 && (step) < 256)                      \
@@ -436,17 +442,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
     const uint32_t gbytes = (uint32_t)(((Tq - 1) * sd.g.t + D) * 2);
     struct Stage {
         uint4 q[NCH], g[NCH];
-        float lse, delta;
-        int32_t lo, hi;
+        uint4 rec;  // the row's lse2, delta, lo, hi - lo
     };
     Stage stg0, stg1;
     // Every call issues the same loads (so the compiler's count of loads in flight is exact and
     // a store waits only for its own set): rows past the tile's last valid row read zeros or a
     // repeated row, and every thread reads a row's lse / delta / interval (only 32 store them).
     // Zeros are harmless: a row whose interval is empty gets P = 0.
-    const uint32_t mbytes = (uint32_t)(((Tq - 1) * Hq + 1) * 4);
-    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(w.rlo + b * Tq, (uint32_t)(Tq * 4));
-    const __amdgpu_buffer_rsrc_t hrs = make_rsrc(w.rhi + b * Tq, (uint32_t)(Tq * 4));
+    const uint32_t rbytes = (uint32_t)(((Tq - 1) * Hq + 1) * 16);
     // each chunk's byte offset within a step's rows (loop-invariant)
     uint32_t qoff[NCH], goff[NCH];
 #pragma unroll
@@ -466,12 +469,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
             x.g[u] = buf_load16(grs, gb + goff[u]);
         }
         const uint32_t i = (uint32_t)(t * kDkdvStep) + (tid & (kDkdvStep - 1));
-        const __amdgpu_buffer_rsrc_t srs = make_rsrc(w.lse2 + b * Tq * Hq + h, mbytes);
-        const __amdgpu_buffer_rsrc_t drs = make_rsrc(delta + b * Tq * Hq + h, mbytes);
-        x.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, i * (uint32_t)Hq * 4, 0, 0));
-        x.delta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drs, i * (uint32_t)Hq * 4, 0, 0));
-        x.lo = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(lrs, i * 4, 0, 0);
-        x.hi = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(hrs, i * 4, 0, 0);
+        const __amdgpu_buffer_rsrc_t rrs = make_rsrc(w.rec + b * Tq * Hq + h, rbytes);
+        x.rec = buf_load16(rrs, i * (uint32_t)Hq * 16);
     };
     auto store = [&](const Stage &x, DkdvSlot<D> &sl) {
 #pragma unroll
@@ -484,10 +483,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
             sl.gt[r * (TS / 8) + ccol] = x.g[u];
         }
         if (tid < kDkdvStep) {
-            sl.lse2[tid] = x.lse;
-            sl.delta[tid] = x.delta;
-            sl.rlo[tid] = x.lo;
-            sl.rhi[tid] = max(x.hi - x.lo, 0);  // stored as the span hi - lo
+            sl.lse2[tid] = __uint_as_float(x.rec.x);
+            sl.delta[tid] = __uint_as_float(x.rec.y);
+            sl.rlo[tid] = (int32_t)x.rec.z;
+            sl.rhi[tid] = (int32_t)x.rec.w;  // the span hi - lo
         }
     };
 
@@ -530,9 +529,19 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
 
     // stage step n + 1 (held by this step's register set) into slot `nslot`; the set then
     // loads step n + 3
-    auto restage = [&](const int n, const int nslot, Stage &x) __attribute__((always_inline)) {
-        if (entry(n + 1).valid) store(x, sm.slot[nslot]);
-        const Entry e = entry(n + 3);
+    // (r1, r3: the schedule entries of steps n + 1 and n + 3, read by the caller before the
+    // previous step's barrier, so their LDS latency hides behind it)
+    auto restage = [&](const int n, const int nslot, Stage &x, const int4 r1, const int4 r3)
+                       __attribute__((always_inline)) {
+        const bool v1 = __builtin_amdgcn_readfirstlane(r1.w) != 0;
+        Entry e;
+        e.h = __builtin_amdgcn_readfirstlane(r3.x);
+        e.t = __builtin_amdgcn_readfirstlane(r3.y);
+        e.valid = __builtin_amdgcn_readfirstlane(r3.w) != 0;
+        DM_STAMP(pwave ? 0 : 1, n, 4);
+        if (v1) store(x, sm.slot[nslot]);
+        DM_STAMP(pwave ? 0 : 1, n, 5);
+        DM_STAMP(pwave ? 0 : 1, n, 6);
         // a step past the last loads the group's first tile again (the same loads every call)
         load(x, e.valid ? e.h : h_first, e.valid ? e.t : 0);
     };
@@ -662,45 +671,57 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv(MaskInfo m, int64_t B, int64_
         cs = ns;
         ns = t;
     };
+    // The schedule entries a step needs (its own, and steps n + 1 and n + 3 for the staging)
+    // are read at the end of the step before, ahead of its barrier: entry n + 4 was published
+    // one step earlier, and the slots read are never the one wavefront 0 writes in that step.
+    auto valid_of = [](const int4 e) { return __builtin_amdgcn_readfirstlane(e.w) != 0; };
     if (pwave) {
         int n = 0;
+        int4 e0 = sm.sched[0], r1 = sm.sched[1], r3 = sm.sched[3];
         auto one = [&](Stage &x) __attribute__((always_inline)) {
             DM_STAMP(0, n, 0);
-            restage(n, ns, x);
+            restage(n, ns, x, r1, r3);
             DM_STAMP(0, n, 1);
-            pstep(n, cs, entry(n).masked);
+            pstep(n, cs, __builtin_amdgcn_readfirstlane(e0.z) != 0);
             DM_STAMP(0, n, 3);
             if (wave == 0) publish(n + 5);
+            e0 = r1;
+            r1 = sm.sched[(n + 2) % kDkdvRing];
+            r3 = sm.sched[(n + 4) % kDkdvRing];
             __syncthreads();
             n++;
             rotate();
         };
         for (;;) {
-            if (!entry(n).valid) break;
+            if (!valid_of(e0)) break;
             one(stg0);
-            if (!entry(n).valid) break;
+            if (!valid_of(e0)) break;
             one(stg1);
         }
         __syncthreads();  // iteration N
     } else {
-        restage(0, ns, stg0);
+        restage(0, ns, stg0, sm.sched[1], sm.sched[3]);
         __syncthreads();
         int n = 1;
         rotate();
+        int4 em = sm.sched[0], r1 = sm.sched[2], r3 = sm.sched[4];
         auto one = [&](Stage &x) __attribute__((always_inline)) {
             DM_STAMP(1, n, 0);
-            restage(n, ns, x);
+            restage(n, ns, x, r1, r3);
             DM_STAMP(1, n, 1);
             dsstep(n - 1, ps);
             DM_STAMP(1, n, 3);
+            em = sm.sched[n % kDkdvRing];
+            r1 = sm.sched[(n + 2) % kDkdvRing];
+            r3 = sm.sched[(n + 4) % kDkdvRing];
             __syncthreads();
             n++;
             rotate();
         };
         for (;;) {
-            if (!entry(n - 1).valid) break;
+            if (!valid_of(em)) break;
             one(stg1);
-            if (!entry(n - 1).valid) break;
+            if (!valid_of(em)) break;
             one(stg0);
         }
     }
@@ -1564,7 +1585,7 @@ static bool mfma_bwd_shape_takes(const dm_attention_desc *d) {
            (d->d == 64 || d->d == 128 || d->d == 256) && d->tq < (1ll << 30) && d->tk < (1ll << 30) && scale_of(d) > 0.f &&
            rows_fit_32bit(s.k, d->tk, d->d) && rows_fit_32bit(s.v, d->tk, d->d) &&
            rows_fit_32bit(s.q, d->tq, d->d) && rows_fit_32bit(s.g, d->tq, d->d) &&
-           d->tq * d->hq < (1ll << 29) && strides_16b(s.q) && strides_16b(s.k) &&
+           d->tq * d->hq < (1ll << 28) && strides_16b(s.q) && strides_16b(s.k) &&
            strides_16b(s.v) && strides_16b(s.o) && strides_16b(s.g);
 }
 
