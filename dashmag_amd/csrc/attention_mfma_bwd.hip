@@ -780,6 +780,24 @@ __global__ __launch_bounds__(256) void bwd_kv_reduce(int64_t n, int hs, const fl
 // dQ
 // ------------------------------------------------------------------------------------------
 
+#ifdef DM_TRACE_DQ
+// profiling aid (built only with -DDM_TRACE_DQ=<workgroup>): per-step clock stamps of
+// wavefronts 0 and 4 of one workgroup
+__device__ uint64_t dm_trace_dq[2][256][4];
+#define DM_QSTAMP(role, step, k)                                                                 \
+    do {                                                                                        \
+        if (blockIdx.x == (DM_TRACE_DQ) && (threadIdx.x & 255) == 0 && (step) < 256)            \
+            dm_trace_dq[role][step][k] = __builtin_readcyclecounter();                          \
+    } while (0)
+extern "C" int dm_debug_trace_dq(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(dm_trace_dq), bytes) == hipSuccess ? 0 : 1;
+}
+#else
+#define DM_QSTAMP(role, step, k) \
+    do {                         \
+    } while (0)
+#endif
+
 // Wave pairs, as the dK/dV kernel: a workgroup of 8 wavefronts takes 128 queries of one query
 // head; wavefronts w and w + 4 (one SIMD) share the queries 32 w + [0, 32). Per 32-key step,
 // wavefront w holds Q and computes S^T = K Q^T and P (masked), handing P (f32) over through LDS;
@@ -1020,8 +1038,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         // every path through the loop the second register set's loads are then the most recent,
         // and the compiler's wait counts keep them in flight across a step)
         auto one = [&](KvStage &x) __attribute__((always_inline)) {
+            DM_QSTAMP(0, n, 0);
             restage(n, x);
+            DM_QSTAMP(0, n, 1);
             if (n < nsteps) pstep(n, cs);
+            DM_QSTAMP(0, n, 2);
             __syncthreads();
             n++;
             rotate();
@@ -1037,8 +1058,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         int n = 1;
         rotate();
         auto one = [&](KvStage &x) __attribute__((always_inline)) {
+            DM_QSTAMP(1, n, 0);
             restage(n, x);
+            DM_QSTAMP(1, n, 1);
             if (n <= nsteps) dsstep(n - 1, ps);
+            DM_QSTAMP(1, n, 2);
             __syncthreads();
             n++;
             rotate();
