@@ -13,7 +13,8 @@
 //              dK += dS^T Q, whose B operands come from transposed LDS copies of the tile.
 //   bwd_dq     per (tile of 128 queries, query head): sweeps the key tiles as the forward does,
 //              recomputing S^T and dP^T, dQ^T += K^T dS^T.
-//   bwd_dkdv_w4, bwd_dq_w4   head width 256: one wavefront per SIMD, dV and dK in two passes.
+//   bwd_dkdv_w4, bwd_dq_w4   head width 256: one wavefront per SIMD, dV and dK in two passes
+//              (work items of one launch).
 #include <string>
 #include <type_traits>
 
@@ -81,7 +82,7 @@ static size_t bwd_layout(const dm_attention_desc *d, char *base, BwdWs *w) {
                             : nullptr;
     const int64_t nkb = (d->tk + kKvBlock - 1) / kKvBlock;
     x.kbsteps = (int32_t *)take(d->b * (nkb + 1) * 4);
-    x.order = (int32_t *)take(nkb * d->hkv * d->b * x.hsplit * 4);
+    x.order = (int32_t *)take(nkb * d->hkv * d->b * x.hsplit * (d->d == 256 ? 2 : 1) * 4);
     if (w) *w = x;
     return off;
 }
@@ -190,8 +191,12 @@ __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) 
 constexpr int kOrderBuckets = 1024;
 constexpr int kOrderLds = 8192;  // per-block counts held in LDS up to this many
 
+// passes = 1: one work item per (key block, key-value head, query-head part), its steps the
+// query tiles that see the block times the part's query heads. passes = 2 (the head width 256
+// kernel): each of those twice, the dV pass first, then the dK pass, weighted by their products
+// per step (2 : 3), and sorted together.
 __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t Tk, int64_t Hkv,
-                                                  int64_t group, BwdWs w) {
+                                                  int64_t group, int passes, BwdWs w) {
     __shared__ int32_t hist[kOrderBuckets];
     const int tid = threadIdx.x;
     const int64_t ntiles = (Tq + kRowTile - 1) / kRowTile;
@@ -237,11 +242,14 @@ __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t
     __syncthreads();
     const int64_t nwork = nkb * Hkv * B * hs;
     auto bucket = [&](int64_t item) {
+        const int64_t weight = passes == 1 ? 1 : (item >= nwork ? 3 : 2);
+        item = item % nwork;
         const int64_t kb = (item / (Hkv * hs)) % nkb, b = item / (Hkv * hs * nkb);
-        const int64_t steps = (int64_t)cnt[b * (nkb + 1) + kb] * per;
+        const int64_t steps = (int64_t)cnt[b * (nkb + 1) + kb] * per * weight;
         return (int)(steps < kOrderBuckets - 1 ? steps : kOrderBuckets - 1);
     };
-    for (int64_t x = tid; x < nwork; x += 1024) atomicAdd(&hist[bucket(x)], 1);
+    const int64_t nitems = nwork * passes;
+    for (int64_t x = tid; x < nitems; x += 1024) atomicAdd(&hist[bucket(x)], 1);
     __syncthreads();
     {
         // exclusive offsets, the largest bucket first: thread t takes bucket 1023 - t, a scan
@@ -264,7 +272,7 @@ __global__ __launch_bounds__(1024) void bwd_order(int64_t B, int64_t Tq, int64_t
         hist[x] = before + incl - c;
     }
     __syncthreads();
-    for (int64_t x = tid; x < nwork; x += 1024) w.order[atomicAdd(&hist[bucket(x)], 1)] = (int32_t)x;
+    for (int64_t x = tid; x < nitems; x += 1024) w.order[atomicAdd(&hist[bucket(x)], 1)] = (int32_t)x;
 
 }
 
@@ -1093,7 +1101,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 //
 // At D = 256 a wavefront's 32 keys need dK and dV accumulators of 128 registers each, and the
 // products' outputs share the accumulator registers with them: both gradients at once do not
-// fit beside the S and dP outputs. The gradients are then two launches of one kernel, each
+// fit beside the S and dP outputs. The gradients are then two passes of one kernel body, each
 // workgroup 4 wavefronts (one per SIMD) taking 32 keys each through every step:
 //   dV pass: S = Q K^T, P, dV += P^T dO                      (32 products of 32x32x16 a step)
 //   dK pass: S = Q K^T, P, dP = dO V^T, dS = P (dP - delta), dK += dS^T Q     (48 a step)
@@ -1109,24 +1117,20 @@ struct Dkdv4Smem {
 };
 
 template <int DT, int D, bool PAD, int MODE>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv_w4(MaskInfo m, int64_t B, int64_t Hq,
-                                                      int64_t Hkv, float scale, AttnStrides sd,
-                                                      const uint16_t *__restrict__ q,
-                                                      const uint16_t *__restrict__ k,
-                                                      const uint16_t *__restrict__ v,
-                                                      const uint16_t *__restrict__ d_o,
-                                                      const float *__restrict__ delta,
-                                                      BwdWs w, uint16_t *__restrict__ out) {
+__device__ __forceinline__ void dkdv_w4_pass(Dkdv4Smem<D> &sm, const int64_t work, MaskInfo m,
+                                             int64_t B, int64_t Hq, int64_t Hkv, float scale,
+                                             AttnStrides sd, const uint16_t *__restrict__ q,
+                                             const uint16_t *__restrict__ k,
+                                             const uint16_t *__restrict__ v,
+                                             const uint16_t *__restrict__ d_o,
+                                             const float *__restrict__ delta, BwdWs w,
+                                             uint16_t *__restrict__ out) {
     constexpr bool DK = MODE == kDkdvDK;
     constexpr int RS = BwdStrides<D>::ROW, TS = BwdStrides<D>::TR;
-    __shared__ Dkdv4Smem<D> sm;
     constexpr int KSTEPS = D / 16, DT32 = D / 32;
     const int64_t Tq = m.tq, Tk = m.tk;
     const int64_t nkb = (Tk + kKvBlock - 1) / kKvBlock;
     const int hs = w.hsplit;
-    const int64_t nwork = nkb * Hkv * B * hs;
-    if ((int64_t)blockIdx.x >= nwork) return;
-    const int64_t work = w.order[blockIdx.x];
     const int64_t kh = work % Hkv, part = (work / Hkv) % hs;
     const int64_t kb = (work / (Hkv * hs)) % nkb, b = work / (Hkv * hs * nkb);
     const int64_t group = Hq / Hkv;
@@ -1414,6 +1418,32 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_w4(MaskInfo m, int64_t B, int
     }
 }
 
+// Both passes in one launch: work items [0, nwork) are dV passes and [nwork, 2 nwork) dK passes
+// of the same (key block, key-value head, query-head part), taken in the order bwd_order makes
+// over both, weighted by their products per step (32 and 48), so the dV passes fill in beside
+// the longest dK passes instead of each launch ending on its own tail.
+template <int DT, int D, bool PAD>
+__global__ __launch_bounds__(256, 1) void bwd_dkdv_w4(MaskInfo m, int64_t B, int64_t Hq,
+                                                      int64_t Hkv, float scale, AttnStrides sd,
+                                                      const uint16_t *__restrict__ q,
+                                                      const uint16_t *__restrict__ k,
+                                                      const uint16_t *__restrict__ v,
+                                                      const uint16_t *__restrict__ d_o,
+                                                      const float *__restrict__ delta, BwdWs w,
+                                                      uint16_t *__restrict__ dk,
+                                                      uint16_t *__restrict__ dv) {
+    __shared__ Dkdv4Smem<D> sm;
+    const int64_t nwork = (m.tk + kKvBlock - 1) / kKvBlock * Hkv * B * w.hsplit;
+    if ((int64_t)blockIdx.x >= 2 * nwork) return;
+    const int64_t item = w.order[blockIdx.x];
+    if (item >= nwork)
+        dkdv_w4_pass<DT, D, PAD, kDkdvDK>(sm, item - nwork, m, B, Hq, Hkv, scale, sd, q, k, v, d_o,
+                                          delta, w, dk);
+    else
+        dkdv_w4_pass<DT, D, PAD, kDkdvDV>(sm, item, m, B, Hq, Hkv, scale, sd, q, k, v, d_o, delta,
+                                          w, dv);
+}
+
 // dQ at D = 256: 4 wavefronts of 32 queries (128 per workgroup), each holding its queries' Q
 // and dO fragments and dQ^T (256 x 32) over the key steps: S^T = K Q^T, dP^T = V dO^T,
 // dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T (48 products per 32-key step). Key and value tiles
@@ -1641,7 +1671,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     const int64_t nq = (d->tq + kDqM - 1) / kDqM;
     const int64_t nb_kv = nkb * d->hkv * d->b * w.hsplit;
     const int64_t nb_q = nq * d->hq * d->b;
-    if (nb_kv >= (1ll << 31) || nb_q >= (1ll << 31)) return refuse("attention_backward: too large");
+    if (2 * nb_kv >= (1ll << 31) || nb_q >= (1ll << 31)) return refuse("attention_backward: too large");
     const uint16_t *qq = (const uint16_t *)q, *kk = (const uint16_t *)k, *vv = (const uint16_t *)v;
     const uint16_t *oo = (const uint16_t *)o, *gg = (const uint16_t *)d_o;
     const AttnStrides sd = attn_strides(d);
@@ -1649,7 +1679,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, sd, oo, gg,  \
                                                                    lse, delta, w);             \
     bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
-    bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, w);              \
+    bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, 1, w);           \
     if (m.pad) {                                                                               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
@@ -1669,25 +1699,24 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
                                                               qq, kk, vv, gg, delta, w,            \
                                                               (uint16_t *)dq); }               \
     }
-#define DKDV4(DT, P, MODE, OUT)                                                                \
-    bwd_dkdv_w4<DT, 256, P, MODE><<<(unsigned)nb_kv, 256, 0, st>>>(                            \
-        m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)(OUT))
+#define DKDV4(DT, P)                                                                           \
+    bwd_dkdv_w4<DT, 256, P><<<(unsigned)(2 * nb_kv), 256, 0, st>>>(                            \
+        m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)dk,           \
+        (uint16_t *)dv)
 #define BWD4(DT)                                                                               \
     bwd_prep<DT, 256><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, sd, oo, gg, \
                                                                     lse, delta, w);            \
     bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
-    bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, w);              \
+    bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, 2, w);           \
     if (m.pad) {                                                                               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
-          DKDV4(DT, true, kDkdvDV, dv);                                                        \
-          DKDV4(DT, true, kDkdvDK, dk); }                                                      \
+          DKDV4(DT, true); }                                                                   \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
         bwd_dq_w4<DT, 256, true><<<(unsigned)nb_q, 256, 0, st>>>(                             \
             m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)dq); }    \
     } else {                                                                                   \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
-          DKDV4(DT, false, kDkdvDV, dv);                                                       \
-          DKDV4(DT, false, kDkdvDK, dk); }                                                     \
+          DKDV4(DT, false); }                                                                  \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
         bwd_dq_w4<DT, 256, false><<<(unsigned)nb_q, 256, 0, st>>>(                            \
             m, d->b, d->hq, d->hkv, scale, sd, qq, kk, vv, gg, delta, w, (uint16_t *)dq); }    \
