@@ -245,6 +245,44 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_fwd_kernel(Cv1Args a, cons
 #pragma unroll
                 for (int e = 0; e < VEC; e++) win[j][e] = win[j + 1][e];
         };
+        if constexpr (DT != DM_F32 && VEC == 8) {
+            // 16-bit rows of 8 channels: two register sets of kCv1Batch raw 16-byte loads, the
+            // next batch's loads issued before this batch's steps, so a thread always has a
+            // batch in flight while it computes
+            u32x4_t ra[kCv1Batch], rb[kCv1Batch];
+            auto issue = [&](u32x4_t (&buf)[kCv1Batch], int64_t rr) __attribute__((always_inline)) {
+#pragma unroll
+                for (int u = 0; u < kCv1Batch; u++)
+                    buf[u] = __builtin_nontemporal_load(
+                        (const u32x4_t *)((const uint16_t *)x + (rr + u) * a.c + c0));
+            };
+            auto consume = [&](const u32x4_t (&buf)[kCv1Batch], int64_t rr) __attribute__((always_inline)) {
+#pragma unroll
+                for (int u = 0; u < kCv1Batch; u++) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        win[KT - 1][2 * e] = unpack_lo<DT>(buf[u][e]);
+                        win[KT - 1][2 * e + 1] = unpack_hi<DT>(buf[u][e]);
+                    }
+                    step(rr + u);
+                }
+            };
+            if (r + kCv1Batch <= pend) {
+                issue(ra, r);
+                while (true) {
+                    const bool more = r + 2 * kCv1Batch <= pend;
+                    if (more) issue(rb, r + kCv1Batch);
+                    consume(ra, r);
+                    r += kCv1Batch;
+                    if (!more) break;
+                    const bool more2 = r + 2 * kCv1Batch <= pend;
+                    if (more2) issue(ra, r + kCv1Batch);
+                    consume(rb, r);
+                    r += kCv1Batch;
+                    if (!more2) break;
+                }
+            }
+        }
         // kCv1Batch steps at a time: their rows' loads all issued before the first is used
         for (; r + kCv1Batch <= pend; r += kCv1Batch) {
             float xb[kCv1Batch][VEC];
@@ -655,7 +693,9 @@ static Cv1Args cv1_args(const dm_conv1d_desc *d, bool bwd = false) {
     // segments: three workgroups of 256 threads per compute unit in all (measured on config 6's
     // shape over 1.3-6 workgroups per compute unit, both directions: the backward 331 us at 4.0
     // and 268 us at 3, the forward 193 us at 4 and 182-186 us at 3; at 3.3-3.5 both slow by 7%, as
-    // some compute units then hold a fourth), at most 512 segments of at least 16 steps
+    // some compute units then hold a fourth; with the forward's two register sets of loads, at
+    // 248 registers, the forward measured 167 us at 3, 204 at 2, 191 at 4 and 168 at 6), at most
+    // 512 segments of at least 16 steps
     const int64_t gx = (a.cv + kCv1Threads - 1) / kCv1Threads;
     int64_t nseg = 3 * cv1_cus() / std::max<int64_t>(gx, 1);
     nseg = std::min<int64_t>(nseg, 512);
