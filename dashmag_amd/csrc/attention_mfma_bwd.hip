@@ -3,18 +3,20 @@
 // reference's default does (crates/dash-ops/src/attention/kernels.rs:999-2058; the contract's
 // `deterministic`, crates/dash-contract/src/attention.rs:100-105).
 //
-//   bwd_prep   per query row: delta = rowsum(dO o O), lse in log2 units (+inf for a row that
-//              sees no key, so its probabilities are 0), the row's visibility interval; per tile
-//              of 64 rows the union of the intervals and the keys every row sees.
+//   bwd_rows   per query row: the row's visibility interval; bwd_tiles, per tile of 32 rows, the
+//              union of the intervals and the keys every row sees.
+//   bwd_dq     (head widths 64 and 128, first) per (tile of 128 queries, query head): delta =
+//              rowsum(dO o O) from the dO it holds and each row's record (lse in log2 units, +inf
+//              for a row that sees no key, delta, the interval) for the dK/dV kernel; then the
+//              key tiles swept as the forward does, recomputing S^T and dP^T, dQ^T += K^T dS^T.
 //   bwd_dkdv   per (tile of 128 keys, key-value head): sweeps the query heads of the group and
 //              the 64-query tiles that see the keys. The keys and values stay in registers as the
 //              B operands of S = Q K^T and dP = dO V^T (v_mfma_f32_32x32x16); P and dS go from the
 //              products' output layout straight into the A operands of dV += P^T dO and
 //              dK += dS^T Q, whose B operands come from transposed LDS copies of the tile.
-//   bwd_dq     per (tile of 128 queries, query head): sweeps the key tiles as the forward does,
-//              recomputing S^T and dP^T, dQ^T += K^T dS^T.
 //   bwd_dkdv_w4, bwd_dq_w4   head width 256: one wavefront per SIMD, dV and dK in two passes
-//              (work items of one launch).
+//              (work items of one launch), after bwd_prep (per query row: the interval, delta and
+//              lse in log2 units).
 #include <string>
 #include <type_traits>
 
@@ -143,6 +145,17 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
             }
         }
     }
+}
+
+// Head widths 64 and 128: only the rows' visibility intervals here (the dQ kernel forms delta and
+// the rows' records from the dO it holds, before the dK/dV kernel runs). One thread per row.
+__global__ __launch_bounds__(256) void bwd_rows(MaskInfo m, int64_t B, BwdWs w) {
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B * Tq
+    if (row >= B * m.tq) return;
+    int64_t lo = 0, hi = 0;
+    row_bounds(m, row % m.tq, &lo, &hi);
+    w.rlo[row] = (int32_t)lo;
+    w.rhi[row] = (int32_t)hi;
 }
 
 // Per tile of kRowTile rows: [union lo, union hi) of the rows' intervals, and [full lo, full hi), the
@@ -835,7 +848,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
                                                  const uint16_t *__restrict__ k,
                                                  const uint16_t *__restrict__ v,
                                                  const uint16_t *__restrict__ d_o,
-                                                 const float *__restrict__ delta, BwdWs w,
+                                                 const uint16_t *__restrict__ o,
+                                                 const float *__restrict__ lse,
+                                                 float *__restrict__ delta, BwdWs w,
                                                  uint16_t *__restrict__ dq) {
     using Sm = DqSmem<D>;
     constexpr int RS = BwdStrides<D>::ROW, TS = BwdStrides<D>::TR;
@@ -861,13 +876,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     const int64_t qi = tile * kDqM + qw * 32 + col;
     const bool qvalid = qi < Tq;
     int32_t lo = 0, hi = 0;
-    float lse2 = INFINITY, dl = 0.f;
+    float lse2 = INFINITY;
     if (qvalid) {
         lo = w.rlo[b * Tq + qi];
         hi = w.rhi[b * Tq + qi];
-        lse2 = w.lse2[(b * Tq + qi) * Hq + h];
-        dl = delta[(b * Tq + qi) * Hq + h];
+        // lse in log2 units, +inf for a row that sees no key (its probabilities are then 0)
+        const float l = lse[(b * Tq + qi) * Hq + h];
+        lse2 = l == -INFINITY ? INFINITY : l * 1.4426950408889634f;
     }
+    const int32_t hi_row = hi;      // the row's interval, for its record
     if (lse2 == INFINITY) hi = lo;  // a query that sees no key: dq = 0
     if (pwave) {
         int32_t wl = lo < hi ? lo : INT32_MAX, wh = lo < hi ? hi : INT32_MIN;
@@ -901,6 +918,18 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++)
             bf[s].u = qvalid ? *(const uint4 *)(src + s * 16) : make_uint4(0, 0, 0, 0);
+    }
+    // delta = rowsum(dO o O) for this query and head, by the dS wavefronts from the dO fragments
+    // they hold (lane halves hold alternate 8-column pieces of the row); the O loads issue here,
+    // beside dO's and the first tiles', and the sums are formed after the prologue. (Every lane
+    // loads, a row past the end reading row 0, so the loads issue together without a branch
+    // each; those lanes' sums are unused.)
+    float dl = 0.f;
+    uint4 ov[KSTEPS];
+    if (!pwave) {
+        const uint16_t *op = o + b * sd.o.b + (qvalid ? qi : 0) * sd.o.t + h * sd.o.h + half * 8;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++) ov[s] = *(const uint4 *)(op + s * 16);
     }
     f32x16_t acc[DT32];
 #pragma unroll
@@ -1026,6 +1055,22 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
     if (nsteps > 0) store(st0, sm.slot[0]);
     load(st0, 1);
     load(st1, 2);
+    if (!pwave) {
+        // delta (the row's record for the dK/dV kernel, which runs after this one, is stored at
+        // the end)
+        float acc_d = 0.f;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++) {
+            const uint32_t ow[4] = {ov[s].x, ov[s].y, ov[s].z, ov[s].w};
+            const uint32_t gw[4] = {bf[s].u.x, bf[s].u.y, bf[s].u.z, bf[s].u.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                acc_d = fmaf(unpack_lo<DT>(ow[e]), unpack_lo<DT>(gw[e]), acc_d);
+                acc_d = fmaf(unpack_hi<DT>(ow[e]), unpack_hi<DT>(gw[e]), acc_d);
+            }
+        }
+        dl = acc_d + __shfl_xor(acc_d, 32, 64);
+    }
     __syncthreads();
     // iterations n = 0 .. nsteps: the P waves compute step n (n < nsteps), the dS waves step
     // n - 1 (n >= 1); each iteration stores step n + 1 from its set and loads step n + 3
@@ -1078,6 +1123,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dq(MaskInfo m, int64_t B, int64_t 
         while (n <= nsteps) {
             one(st1);
             one(st0);
+        }
+        // the row's record for the dK/dV kernel, stored at the end so that the loop's waits for
+        // its loads do not also wait for these stores
+        if (qvalid && half == 0) {
+            const int64_t r = (b * Tq + qi) * Hq + h;
+            w.rec[r] = make_int4(__float_as_int(lse2), __float_as_int(dl), lo, hi_row > lo ? hi_row - lo : 0);
         }
         if (qvalid) {
             uint16_t *op = dq + ((b * Tq + qi) * Hq + h) * D;
@@ -1676,28 +1727,27 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     const uint16_t *oo = (const uint16_t *)o, *gg = (const uint16_t *)d_o;
     const AttnStrides sd = attn_strides(d);
 #define BWD(DT, DD)                                                                            \
-    bwd_prep<DT, DD><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, sd, oo, gg,  \
-                                                                   lse, delta, w);             \
+    bwd_rows<<<(unsigned)((qrows + 255) / 256), 256, 0, st>>>(m, d->b, w);                     \
     bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
     bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, 1, w);           \
     if (m.pad) {                                                                               \
+        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
+        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
+                                                             qq, kk, vv, gg, oo, lse, delta, w, \
+                                                             (uint16_t *)dq); }                \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, true><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
                                                                 sd, qq, kk, vv, gg, delta, w,      \
                                                                 (uint16_t *)dk, (uint16_t *)dv); } \
-        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
-        bwd_dq<DT, DD, true><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
-                                                             qq, kk, vv, gg, delta, w,             \
-                                                             (uint16_t *)dq); }                \
     } else {                                                                                   \
+        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
+        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
+                                                              qq, kk, vv, gg, oo, lse, delta, w, \
+                                                              (uint16_t *)dq); }               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
         bwd_dkdv<DT, DD, false><<<(unsigned)nb_kv, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, \
                                                                  sd, qq, kk, vv, gg, delta, w,     \
                                                                  (uint16_t *)dk, (uint16_t *)dv); } \
-        { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
-        bwd_dq<DT, DD, false><<<(unsigned)nb_q, 512, 0, st>>>(m, d->b, d->hq, d->hkv, scale, sd, \
-                                                              qq, kk, vv, gg, delta, w,            \
-                                                              (uint16_t *)dq); }               \
     }
 #define DKDV4(DT, P)                                                                           \
     bwd_dkdv_w4<DT, 256, P><<<(unsigned)(2 * nb_kv), 256, 0, st>>>(                            \
