@@ -227,24 +227,43 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_mfma(
         uint4 k[NLD], v[NLD];
     };
     Stage sts;
+    // PAGED: the pages of a block's two 16-key halves (-1: no visible key, or an index out of
+    // range), looked up one block ahead of the block's loads
+    struct Pages {
+        int64_t pg[2];
+    };
+    auto pages_of = [&](int64_t j0) __attribute__((always_inline)) {
+        Pages p;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t h0 = j0 + 16 * h;
+            const int64_t first = max(h0, w0), last = min(h0 + 16, w1);
+            p.pg[h] = PAGED && first < last ? kv_page(map, b, first) : -1;
+        }
+        return p;
+    };
     // block rows past the wavefront's range load row w1 - 1 again (their scores are -inf)
-    auto load = [&](Stage &x, int64_t j0) __attribute__((always_inline)) {
+    auto load = [&](Stage &x, int64_t j0, const Pages &pages) __attribute__((always_inline)) {
         if constexpr (PAGED) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int64_t h0 = j0 + 16 * h;
                 const int64_t first = max(h0, w0), last = min(h0 + 16, w1);
-                const int64_t pg = first < last ? kv_page(map, b, first) : -1;
+                const int64_t pg = pages.pg[h];
                 const uint32_t bytes = pg >= 0 ? (uint32_t)((last - first) * row_stride) : 0u;
                 // the half's first visible key within its page
                 const int64_t kofs = pg >= 0 ? (pg * map.kb + first % map.page_size * map.kt) * 2 : 0;
                 const int64_t vofs = pg >= 0 ? (pg * map.vb + first % map.page_size * map.vt) * 2 : 0;
                 const __amdgpu_buffer_rsrc_t kh_rs = make_rsrc(kb + kofs, bytes);
                 const __amdgpu_buffer_rsrc_t vh_rs = make_rsrc(vb + vofs, bytes);
+                // the offset of key j0 + RPL u + lane / LPR from the half's first visible key: a
+                // lane part and a wavefront-uniform part per load (negative before that key: it
+                // wraps past the resource's range and reads zeros)
+                const uint32_t lane_off = (uint32_t)((lane / LPR) * row_stride) + (lane % LPR) * 16;
+                const int32_t ubase = __builtin_amdgcn_readfirstlane((int32_t)((j0 - first) * row_stride));
 #pragma unroll
                 for (int u = h * NLD / 2; u < (h + 1) * NLD / 2; u++) {
-                    const int64_t key = j0 + RPL * u + lane / LPR;
-                    const uint32_t off = (uint32_t)(int32_t)((key - first) * row_stride) + (lane % LPR) * 16;
+                    const uint32_t off = lane_off + (uint32_t)(ubase + (int32_t)(RPL * u * row_stride));
                     x.k[u] = buf_load16_nt(kh_rs, off);
                     x.v[u] = buf_load16_nt(vh_rs, off);
                 }
@@ -319,11 +338,14 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_mfma(
     if (w0 < w1) {
         const int64_t a0 = PAGED ? (w0 & ~(int64_t)15) : w0;
         const int nblk = (int)((w1 - a0 + BK - 1) / BK);
-        load(sts, a0);
+        Pages pn = pages_of(a0);
+        load(sts, a0, pn);
+        pn = pages_of(a0 + BK);
         for (int n = 0; n < nblk; n++) {
             const int64_t j0 = a0 + (int64_t)n * BK;
             stage(sts);
-            load(sts, j0 + BK);
+            load(sts, j0 + BK, pn);
+            pn = pages_of(j0 + 2 * BK);
             block(j0);
         }
     }
@@ -478,11 +500,10 @@ static bool split_takes(const dm_attention_desc *d, int64_t page_size = 0) {
            rows;
 }
 
-// A paged cache runs the split pass on MFMA for D = 64 and 128 and pages of a multiple of 16
-// keys (at D = 256 the page lookups' registers spill); every other paged call takes the generic
-// kernel.
+// A paged cache runs the split pass on MFMA for pages of a multiple of 16 keys; other page sizes
+// take the generic kernel.
 static bool paged_split_takes(const dm_attention_desc *d, int64_t page_size) {
-    return split_takes(d, page_size) && d->d <= 128 && page_size % 16 == 0;
+    return split_takes(d, page_size) && page_size % 16 == 0;
 }
 
 static int64_t left_of(const dm_attention_desc *d) {
@@ -570,14 +591,12 @@ static int run_decode(const char *op, const dm_attention_desc *d, bool split, bo
     // bytes of the same cache rows at about the same time)
     dim3 grid_hf((unsigned)d->hkv, nsplit, (unsigned)d->b);
     const int g = (int)(d->hq / d->hkv);
-    // (a paged call reaches here at D <= 128 only: paged_split_takes)
-    if (paged && d->d > 128) return refuse(opn + ": internal: paged split at D > 128");
 #define DEC_MFMA2(DT, GG, PG, DD)                                                           \
     decode_split_mfma<DT, GG, PG, DD><<<grid_hf, 256, 0, st>>>(d->tk, d->hq, d->hkv, left, scale, \
                                                                nsplit, span, q, k, v, lengths, \
                                                                map, part_o, part_lse, o)
 #define DEC_MFMA(DT, GG, DD)                         \
-    if (paged) DEC_MFMA2(DT, GG, true, (DD == 256 ? 128 : DD)); else DEC_MFMA2(DT, GG, false, DD)
+    if (paged) DEC_MFMA2(DT, GG, true, DD); else DEC_MFMA2(DT, GG, false, DD)
 #define DEC_GM(DT, DD)                               \
     switch (g) {                                     \
         case 1: DEC_MFMA(DT, 1, DD); break;          \

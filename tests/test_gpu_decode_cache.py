@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import dashmag_amd as dm
+from dashmag_amd import _lib
 import oracle
 from fixtures import errors
 
@@ -135,9 +136,14 @@ def test_paged_cache(dtype, d, hkv, g, page_size, window):
     lengths = torch.tensor(LENGTHS, dtype=torch.int32)
     rng = np.random.default_rng(page_size)
     kp, vp, table = _paged(k, v, LENGTHS, page_size, rng)
+    _lib.probe_reset()
     out = dm.attention_decode_paged(q.cuda(), kp.cuda(), vp.cuda(), torch.from_numpy(table),
                                     lengths.cuda(), opts)
     torch.cuda.synchronize()
+    # the MFMA split pass for 16-bit pages of a multiple of 16 keys, the generic kernel otherwise
+    split = dtype != torch.float32 and page_size % 16 == 0
+    pc = _lib.probe_counts()
+    assert (pc["decode_split"] > 0) == split and (pc["attn_fwd_generic"] > 0) != split, pc
     a = out.float().cpu().numpy()
     e = _expect(q, k, v, LENGTHS, window)
     assert np.all(a[0] == 0.0), "an empty cache gives zeros"
@@ -153,12 +159,12 @@ def test_paged_cache(dtype, d, hkv, g, page_size, window):
     assert torch.equal(out.cpu(), out2.cpu())
 
 
-@pytest.mark.parametrize("page_size", [16, 5])
-def test_paged_bad_page_reads_zeros(page_size):
-    dtype, d, hkv, g = torch.bfloat16, 128, 2, 4
+@pytest.mark.parametrize("page_size,d", [(16, 128), (5, 128), (16, 256)])
+def test_paged_bad_page_reads_zeros(page_size, d):
+    dtype, hkv, g = torch.bfloat16, 2, 4
     s = max(LENGTHS) + 7
     q, k, v = _qkv(dtype, d, hkv, g, s, seed=3)
-    print(f"paged decode, page index out of range, page_size={page_size}", flush=True)
+    print(f"paged decode, page index out of range, page_size={page_size} d={d}", flush=True)
     lengths = torch.tensor(LENGTHS, dtype=torch.int32)
     kp, vp, table = _paged(k, v, LENGTHS, page_size, np.random.default_rng(1))
     # the last sequence's third page: below zero; the one before's second: past the pages
