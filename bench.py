@@ -551,6 +551,30 @@ def main():
                                                 for k, v in tm.kernel_ms.items()})
         print(f"gdr step: {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s", file=sys.stderr,
               flush=True)
+        # the step's backward on the same inputs, N(0, 1) cotangents of the output and the new
+        # states: the state and its gradient read, the state's gradient written, plus the tokens'
+        # inputs and gradients
+        gen = torch.Generator().manual_seed(55)
+        d_out = torch.randn(c["v"].shape, generator=gen).to(c["v"].dtype).to(dev)
+        d_st = torch.randn(st_in.shape, generator=gen).to(dev)
+        gq, gk, gv = torch.empty_like(c["q"]), torch.empty_like(c["k"]), torch.empty_like(c["v"])
+        gg, gb = torch.empty_like(c["g"]), torch.empty_like(c["beta"])
+        gst = torch.empty_like(st_in)
+        wsb = lib.dm_gdr_step_bwd_workspace(ctypes.byref(desc))
+        wst = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        pb = [ctypes.c_void_p(x.data_ptr())
+              for x in args_t + [st_in, d_out, d_st, gq, gk, gv, gg, gb, gst, wst]]
+        fnb = lambda: check(lib.dm_gdr_step_bwd(ctypes.byref(desc), *pb, wsb, st), lib)  # noqa
+        tmb = Timed(torch, fnb)
+        msb = tmb.run(max(args.steps, 100), args.warmup)
+        nb_b = 3 * 4 * b * h * dk * dv + (8 * 2 * h * 128 + 4 * 4 * h) * b
+        secondary["gdr_step_bwd"] = dict(unit="GB/s", value=nb_b / msb / 1e6,
+                                         us_per_call=msb * 1e3, bytes=nb_b,
+                                         frac_of_hbm_peak=nb_b / msb / 1e6 / HBM_PEAK_GBS,
+                                         kernel_us={k: round(v[0] * 1e3, 2)
+                                                    for k, v in tmb.kernel_ms.items()})
+        print(f"gdr step backward: {msb * 1e3:.1f} us, {nb_b / msb / 1e6:.0f} GB/s",
+              file=sys.stderr, flush=True)
         del c
 
     # ---- causal conv1d, config 6 (beside config 4: a Gated DeltaNet layer's conv) ----
