@@ -155,7 +155,11 @@ def test_mfma_attention_nondeterministic_flag_matches():
 
 D256_CASES = [c for c in CASES if c[0] in (
     "none_129", "causal_1", "causal_31", "causal_127_scale", "causal_tq127_tk33_empty_rows",
-    "window_both_300", "key_padding_160", "packed_cross", "packed_no_causal")]
+    "window_both_300", "key_padding_160", "packed_cross", "packed_no_causal")] + [
+    # the reference's head shape (Hq = 8, Hkv = 2) over a longer causal sequence: dK/dV work
+    # items of both passes in one launch, split over the query heads
+    ("causal_1024_gqa4", 1, 1024, 1024, 8, 2, None, True, None, None),
+]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -164,7 +168,7 @@ def test_mfma_attention_d256_matches_oracle(case, dtype):
     """Head width 256 (the reference's published attention shapes): forward and backward on the
     MFMA kernels (4-wavefront forms; probes show them), against the f64 oracle."""
     print(f"case {case[0]} {dtype} D=256", flush=True)
-    seed = 3000 + 17 * CASES.index(case)
+    seed = 3000 + 17 * (CASES.index(case) if case in CASES else len(CASES) + D256_CASES.index(case))
     (q, k, v, do), mask, opts, mk = _build(case, dtype, 256, seed)
     _lib.probe_reset()
     o, lse = dm.attention_with_lse(q, k, v, mask, opts)
