@@ -84,6 +84,11 @@ _XD = ctypes.POINTER(LceDesc)
 SIGNATURES = {
     "dm_last_error": (ctypes.c_char_p, []),
     "dm_describe": (ctypes.c_int, [ctypes.c_char_p, _SZ]),
+    "dm_device_alloc": (ctypes.c_int, [_SZ, ctypes.POINTER(ctypes.c_void_p)]),
+    "dm_device_free": (ctypes.c_int, [_VP]),
+    "dm_copy_to_device": (ctypes.c_int, [_VP, _VP, _SZ, _VP]),
+    "dm_copy_to_host": (ctypes.c_int, [_VP, _VP, _SZ, _VP]),
+    "dm_stream_synchronize": (ctypes.c_int, [_VP]),
     "dm_probe_count": (ctypes.c_uint64, [ctypes.c_int]),
     "dm_probe_reset": (None, []),
     "dm_kernel_timing": (ctypes.c_int, [ctypes.c_int]),

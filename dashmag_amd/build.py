@@ -69,5 +69,23 @@ def build(verbose=False, jobs=8) -> str:
     return LIB
 
 
+HOST_CHECK_SRC = os.path.join(os.path.dirname(HERE), "tests", "host", "dm_host_check.cpp")
+HOST_CHECK = os.path.splitext(HOST_CHECK_SRC)[0]
+
+
+def build_host_check() -> str:
+    """Compiles tests/host/dm_host_check.cpp, a caller that binds only include/dashmi.h and links
+    libdashmi.so (no HIP headers), with the host compiler."""
+    cxx = os.environ.get("CXX", "g++")
+    inc = os.path.join(os.path.dirname(HERE), "include")
+    cmd = [cxx, "-O2", "-std=c++17", "-Wall", f"-I{inc}", HOST_CHECK_SRC, f"-L{HERE}", "-ldashmi",
+           "-Wl,-rpath,$ORIGIN/../../dashmag_amd", "-o", HOST_CHECK]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{cxx} failed on {HOST_CHECK_SRC}:\n{r.stderr}")
+    return HOST_CHECK
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_host_check())

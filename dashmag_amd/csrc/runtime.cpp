@@ -164,6 +164,48 @@ int dm_describe(char *buf, size_t len) {
     return dm::device_ok(&why) ? DM_OK : dm::refuse("dm_describe: " + why);
 }
 
+int dm_device_alloc(size_t bytes, void **ptr) {
+    if (!ptr) return dm::refuse("device_alloc: null result pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return DM_OK;
+    const hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        return dm::hip_status(e, ("device_alloc: " + std::to_string(bytes) + " bytes").c_str());
+    }
+    return DM_OK;
+}
+
+int dm_device_free(void *ptr) {
+    if (!ptr) return DM_OK;
+    const hipError_t e = hipFree(ptr);
+    return e == hipSuccess ? DM_OK : dm::hip_status(e, "device_free");
+}
+
+// (the copies wait for their own completion: a host source or destination may be pageable)
+static int dm_copy(void *dst, const void *src, size_t bytes, hipMemcpyKind kind, void *stream,
+                   const char *what) {
+    if (bytes == 0) return DM_OK;
+    if (!dst || !src) return dm::refuse(std::string(what) + ": null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? DM_OK : dm::hip_status(e, what);
+}
+
+int dm_copy_to_device(void *dst, const void *src, size_t bytes, void *stream) {
+    return dm_copy(dst, src, bytes, hipMemcpyHostToDevice, stream, "copy_to_device");
+}
+
+int dm_copy_to_host(void *dst, const void *src, size_t bytes, void *stream) {
+    return dm_copy(dst, src, bytes, hipMemcpyDeviceToHost, stream, "copy_to_host");
+}
+
+int dm_stream_synchronize(void *stream) {
+    const hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? DM_OK : dm::hip_status(e, "stream_synchronize");
+}
+
 int dm_attention_row_bounds(const dm_attention_desc *desc, int64_t b, int64_t i, int64_t *lo,
                             int64_t *hi) {
     (void)b;

@@ -172,6 +172,18 @@ typedef struct {
 /* The message of this thread's last refusal or error. */
 const char *dm_last_error(void);
 
+/* Device buffers and copies, for a caller that binds no HIP API of its own (the uploads and
+ * read-backs of the reference's adapter, crates/dash-ops/tests/common/adapter.rs:140-154, which a
+ * Rust -sys crate would otherwise take from a HIP binding). dm_device_alloc returns 256-byte
+ * aligned device memory (*ptr = NULL for bytes = 0); the copies are enqueued on `stream` (NULL:
+ * the default stream) and have completed when they return; dm_stream_synchronize waits for
+ * every launch enqueued on `stream`. */
+int dm_device_alloc(size_t bytes, void **ptr);
+int dm_device_free(void *ptr);
+int dm_copy_to_device(void *dst, const void *src, size_t bytes, void *stream);
+int dm_copy_to_host(void *dst, const void *src, size_t bytes, void *stream);
+int dm_stream_synchronize(void *stream);
+
 /* Library and device facts: "gfx950, 256 CUs, ..." (the capability probe of
  * crates/dash-ops/src/cube.rs:27-151). Returns DM_OK, or DM_ERR_REFUSED on a device the kernels
  * are not built for. */
