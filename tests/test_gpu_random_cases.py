@@ -1,7 +1,7 @@
 """Seeded random shapes, masks and packings for the hot path's operations on the GPU, each
 against the f64 oracle with the bounds of its dedicated tests: attention forward and backward
-(test_gpu_attention_sweep.py), the chunked gated delta rule forward (test_gpu_gdr_mfma.py),
-decode (test_gpu_decode.py). Each case prints its draw before the GPU call, so a failure names
+(test_gpu_attention_sweep.py), the chunked gated delta rule forward and backward
+(test_gpu_gdr_mfma.py), decode (test_gpu_decode.py) and the causal conv1d (test_gpu_conv1d.py). Each case prints its draw before the GPU call, so a failure names
 its shape."""
 import numpy as np
 import pytest
@@ -156,3 +156,99 @@ def test_random_decode(seed):
     r = errors(a, e)[1]
     print(f"  rel {r:.2e}")
     assert r <= 1e-2
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_chunk_gated_delta_rule_backward(seed):
+    """Bounds of test_gpu_gdr_mfma.py's backward (the reference's own for its tensor-core kernels
+    at [1, 200, 2, 128, 128]: 7.5e-3 with the l2 normalisation, 1.2e-2 without), taken 1.5 times
+    for packings of up to four sequences of up to 300 tokens."""
+    rng = np.random.default_rng(7500 + seed)
+    n = int(rng.integers(1, 5))
+    lens = [int(x) for x in rng.integers(0, 300, n)]
+    if sum(lens) == 0:
+        lens[-1] = 1
+    h = int(rng.integers(1, 3))
+    l2norm = bool(rng.random() < 0.5)
+    states = bool(rng.random() < 0.6)
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    tol = 1.5 * (7.5e-3 if l2norm else 1.2e-2)
+    print(f"random chunk GDR backward lens={lens} h={h} l2norm={l2norm} states={states} {dtype}",
+          flush=True)
+    T, D = sum(lens), 128
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    s0 = 7600 + seed * 10
+    q = syn.normal(s0, (1, T, h, D), "cuda")
+    k = syn.normal(s0 + 1, (1, T, h, D), "cuda")
+    if not l2norm:
+        q, k = syn.l2norm(q), syn.l2norm(k)
+    v = syn.normal(s0 + 2, (1, T, h, D), "cuda")
+    g = -torch.nn.functional.softplus(syn.normal(s0 + 3, (1, T, h), "cuda"))
+    beta = torch.sigmoid(syn.normal(s0 + 4, (1, T, h), "cuda"))
+    h0 = syn.normal(s0 + 5, (n, h, D, D), "cuda", std=0.1) if states else None
+    do = syn.normal(s0 + 6, (1, T, h, D), "cuda").to(dtype)
+    dfin = syn.normal(s0 + 7, (n, h, D, D), "cuda", std=0.1) if states else None
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    _lib.probe_reset()
+    opts = dm.ChunkGatedDeltaOptions(qk_l2norm=l2norm, output_final_state=True)
+    r = dm.chunk_gated_delta_rule_backward(q, k, v, g, beta, h0, cu.cuda(), do, dfin, opts)
+    torch.cuda.synchronize()
+    assert _lib.probe_counts()["gdr_chunk_bwd_mfma"] > 0
+    e = oracle.gdr_chunk_bwd(host(q), host(k), host(v), host(g), host(beta),
+                             None if h0 is None else host(h0), host(do),
+                             None if dfin is None else host(dfin), cu.numpy(), l2norm,
+                             precision="f64")
+    names = ["dq", "dk", "dv", "dg", "dbeta", "dh0"]
+    if h0 is None:
+        names, r, e = names[:5], r[:5], e[:5]
+    for name, a_, e_ in zip(names, r, e):
+        rr = errors(host(a_), e_)[1]
+        print(f"  {name}: rel {rr:.2e} (bound {tol:.1e})")
+        assert rr <= tol, (name, rr)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_conv1d(seed):
+    """The conv1d forward and backward (test_gpu_conv1d.py's bounds: 1e-2 for 16-bit inputs,
+    2e-6 for f32; the final states bit-equal)."""
+    from test_gpu_conv1d import TD, _act, _g, _n, _random_call
+    rng = np.random.default_rng(7700 + seed)
+    dtype = str(rng.choice(["bf16", "f16", "f32"]))
+    k = int(rng.integers(1, 9))
+    c = int(rng.choice([8, 40, 64, 96, 128, 264]))
+    packed = bool(rng.random() < 0.5)
+    lens = [int(x) for x in rng.integers(0, 400, int(rng.integers(1, 5)))] if packed else None
+    b = 1 if packed else int(rng.integers(1, 4))
+    t = 0 if packed else int(rng.integers(1, 600))
+    w = None if rng.random() < 0.3 else int(rng.integers(k - 1 if k > 1 else 1, k + 4))
+    w_out = None if rng.random() < 0.3 else int(rng.integers(1, k + 4))
+    bias, silu = bool(rng.random() < 0.5), bool(rng.random() < 0.6)
+    print(f"random conv1d {dtype} b={b} t={t} c={c} k={k} lens={lens} w={w} w_out={w_out} "
+          f"bias={bias} silu={silu}", flush=True)
+    x, wt, bs, h0, cu, go, gf = _random_call(7800 + seed, dtype, b, t, c, k, lens, w, w_out, bias,
+                                             silu)
+    dt = TD[dtype]
+    opts = dm.CausalConv1dOptions(activation=_act(silu))
+    if w_out is not None:
+        opts = opts.with_final_state_len(w_out)
+    cut = None if cu is None else torch.from_numpy(cu)
+    out, fin = dm.causal_conv1d(_g(x, dt), _g(wt, dt), _g(bs, dt), _g(h0), cut, opts)
+    grads = dm.causal_conv1d_backward(_g(x, dt), _g(wt, dt), _g(bs, dt), _g(h0), cut, _g(go),
+                                      _g(gf), opts)
+    torch.cuda.synchronize()
+    eo, ef = oracle.conv1d_fwd(x, wt, bs, h0, cu, silu, w_out, precision="f64")
+    eg = oracle.conv1d_bwd(x, wt, bs, h0, go, gf, cu, silu, precision="f64")
+    tol = 1e-2 if dtype != "f32" else 2e-6
+    assert errors(_n(out), eo)[1] <= tol
+    if w_out is not None:
+        np.testing.assert_array_equal(_n(fin), ef)
+    for name, a, e in zip(["grad_x", "grad_weight", "grad_bias", "grad_initial_state"], grads, eg):
+        if e is None:
+            assert a is None
+            continue
+        t_ = tol if dtype != "f32" or name == "grad_x" else 5e-6
+        if name == "grad_initial_state":
+            t_ = 2e-6
+        rel = errors(_n(a), e)[1]
+        print(f"  {name}: rel {rel:.2e} (bound {t_:.1e})")
+        assert rel <= t_, (name, rel)
