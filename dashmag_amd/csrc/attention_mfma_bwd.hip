@@ -3,8 +3,8 @@
 // reference's default does (crates/dash-ops/src/attention/kernels.rs:999-2058; the contract's
 // `deterministic`, crates/dash-contract/src/attention.rs:100-105).
 //
-//   bwd_rows   per query row: the row's visibility interval; bwd_tiles, per tile of 32 rows, the
-//              union of the intervals and the keys every row sees.
+//   bwd_tiles  per tile of 32 query rows: the rows' visibility intervals, their union and the
+//              keys every row sees.
 //   bwd_dq     (head widths 64 and 128, first) per (tile of 128 queries, query head): delta =
 //              rowsum(dO o O) from the dO it holds and each row's record (lse in log2 units, +inf
 //              for a row that sees no key, delta, the interval) for the dK/dV kernel; then the
@@ -147,20 +147,12 @@ __global__ __launch_bounds__(256) void bwd_prep(MaskInfo m, int64_t B, int64_t H
     }
 }
 
-// Head widths 64 and 128: only the rows' visibility intervals here (the dQ kernel forms delta and
-// the rows' records from the dO it holds, before the dK/dV kernel runs). One thread per row.
-__global__ __launch_bounds__(256) void bwd_rows(MaskInfo m, int64_t B, BwdWs w) {
-    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B * Tq
-    if (row >= B * m.tq) return;
-    int64_t lo = 0, hi = 0;
-    row_bounds(m, row % m.tq, &lo, &hi);
-    w.rlo[row] = (int32_t)lo;
-    w.rhi[row] = (int32_t)hi;
-}
-
 // Per tile of kRowTile rows: [union lo, union hi) of the rows' intervals, and [full lo, full hi), the
 // keys every row of the tile sees (empty when a row of the tile sees nothing).
-__global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) {
+// ROWS (head widths 64 and 128, where no prep pass runs): the tile's rows' intervals are formed
+// here and stored first (the dQ kernel forms delta and the rows' records itself).
+template <bool ROWS>
+__global__ __launch_bounds__(64) void bwd_tiles(MaskInfo m, int64_t B, int64_t Tq, BwdWs w) {
     const int64_t ntiles = (Tq + kRowTile - 1) / kRowTile;
     const int64_t t = blockIdx.x;
     if (t >= B * ntiles) return;
@@ -168,7 +160,18 @@ __global__ __launch_bounds__(64) void bwd_tiles(int64_t B, int64_t Tq, BwdWs w) 
     const int64_t i = tile * kRowTile + threadIdx.x;
     int32_t ul = INT32_MAX, uh = INT32_MIN, fl = INT32_MIN, fh = INT32_MAX;
     if (threadIdx.x < kRowTile && i < Tq) {
-        const int32_t lo = w.rlo[b * Tq + i], hi = w.rhi[b * Tq + i];
+        int32_t lo, hi;
+        if constexpr (ROWS) {
+            int64_t lo64 = 0, hi64 = 0;
+            row_bounds(m, i, &lo64, &hi64);
+            lo = (int32_t)lo64;
+            hi = (int32_t)hi64;
+            w.rlo[b * Tq + i] = lo;
+            w.rhi[b * Tq + i] = hi;
+        } else {
+            lo = w.rlo[b * Tq + i];
+            hi = w.rhi[b * Tq + i];
+        }
         if (lo < hi) {
             ul = lo;
             uh = hi;
@@ -1727,8 +1730,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
     const uint16_t *oo = (const uint16_t *)o, *gg = (const uint16_t *)d_o;
     const AttnStrides sd = attn_strides(d);
 #define BWD(DT, DD)                                                                            \
-    bwd_rows<<<(unsigned)((qrows + 255) / 256), 256, 0, st>>>(m, d->b, w);                     \
-    bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
+    bwd_tiles<true><<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(m, d->b, d->tq, w);            \
     bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, 1, w);           \
     if (m.pad) {                                                                               \
         { KernelTimer t2(DM_KERNEL_ATTN_BWD_DQ, st);                                         \
@@ -1756,7 +1758,7 @@ int launch_attn_bwd_mfma(const MaskInfo &m, const dm_attention_desc *d, float sc
 #define BWD4(DT)                                                                               \
     bwd_prep<DT, 256><<<(unsigned)((qrows + 3) / 4), 256, 0, st>>>(m, d->b, d->hq, sd, oo, gg, \
                                                                     lse, delta, w);            \
-    bwd_tiles<<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(d->b, d->tq, w);                     \
+    bwd_tiles<false><<<(unsigned)(d->b * ntiles_r), 64, 0, st>>>(m, d->b, d->tq, w);           \
     bwd_order<<<1, 1024, 0, st>>>(d->b, d->tq, d->tk, d->hkv, d->hq / d->hkv, 2, w);           \
     if (m.pad) {                                                                               \
         { KernelTimer t1(DM_KERNEL_ATTN_BWD_DKDV, st);                                       \
