@@ -296,7 +296,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (every GPU "
-              "box here has one GPU, and the hot path shards with no exchange: see DESIGN.md)",
+              "box here has one GPU; the hot path shards over sequences and heads with no exchange)",
               file=sys.stderr)
         sys.exit(2)
     import torch
@@ -756,7 +756,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (splitmix64 + Box-Muller, BASELINE.md seeds)",
+        "data": "synthetic (splitmix64 + Box-Muller, the benchmark configs' seeds)",
         "config": {"workload": "attention fwd+bwd, packed varlen causal, 16384 tokens in "
                                f"{len(syn.attention_lengths()[0])} sequences, Hq=32, Hkv=8, "
                                "D=128 (BASELINE config 2)",
