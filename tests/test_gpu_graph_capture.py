@@ -68,6 +68,36 @@ def test_attention_fwd_bwd_packed_graph():
     _replays(fn, [o, lse, dq, dk, dv])
 
 
+def test_attention_fwd_bwd_d256_graph():
+    """Head width 256 (the reference's shape, Hq = 8, Hkv = 2, causal): the backward's dV and dK
+    passes in one launch, split over the query heads, their partials added by a second kernel."""
+    lib = _lib.lib()
+    t, hq, hkv, d = 1024, 8, 2, 256
+    q = syn.normal(41, (1, t, hq, d), "cuda").to(torch.bfloat16)
+    k = syn.normal(42, (1, t, hkv, d), "cuda").to(torch.bfloat16)
+    v = syn.normal(43, (1, t, hkv, d), "cuda").to(torch.bfloat16)
+    do = syn.normal(44, (1, t, hq, d), "cuda").to(torch.bfloat16)
+    keep = []
+    desc = ops._attention_desc("attention", q, k, v, dm.AttentionMask.none(),
+                               dm.AttentionOptions(causal=True), keep)
+    o, lse = torch.empty_like(q), torch.empty(q.shape[:3], dtype=torch.float32, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    nb = max(lib.dm_attention_fwd_workspace(ctypes.byref(desc)),
+             lib.dm_attention_bwd_workspace(ctypes.byref(desc)), 1)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    P = [ctypes.c_void_p(x.data_ptr()) for x in (q, k, v, o, lse, do, dq, dk, dv, ws)]
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _check(lib.dm_attention_fwd(ctypes.byref(desc), P[0], P[1], P[2], P[3], P[4], P[9], nb, st), lib)
+        _check(lib.dm_attention_bwd(ctypes.byref(desc), P[0], P[1], P[2], P[3], P[4], P[5], P[6],
+                                    P[7], P[8], P[9], nb, st), lib)
+
+    _lib.probe_reset()
+    _replays(fn, [o, lse, dq, dk, dv])
+    assert _lib.probe_counts()["attn_bwd_mfma"] > 0
+
+
 def test_gdr_chunk_fwd_bwd_graph():
     lib = _lib.lib()
     c = syn.config4("cuda", total=3000, nseq=3)
