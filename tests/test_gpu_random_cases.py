@@ -1,7 +1,8 @@
 """Seeded random shapes, masks and packings for the hot path's operations on the GPU, each
 against the f64 oracle with the bounds of its dedicated tests: attention forward and backward
 (test_gpu_attention_sweep.py), the chunked gated delta rule forward and backward
-(test_gpu_gdr_mfma.py), decode (test_gpu_decode.py) and the causal conv1d (test_gpu_conv1d.py). Each case prints its draw before the GPU call, so a failure names
+(test_gpu_gdr_mfma.py), decode (test_gpu_decode.py), the recurrent step (test_gpu_step_grad.py)
+and the causal conv1d and its decoding step (test_gpu_conv1d.py). Each case prints its draw before the GPU call, so a failure names
 its shape."""
 import numpy as np
 import pytest
@@ -252,3 +253,69 @@ def test_random_conv1d(seed):
         rel = errors(_n(a), e)[1]
         print(f"  {name}: rel {rel:.2e} (bound {t_:.1e})")
         assert rel <= t_, (name, rel)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_gated_delta_step(seed):
+    """The recurrent step over random packings (several tokens per sequence, empty sequences),
+    widths and options, against the f64 oracle (test_gpu_step_grad.py's bounds: 1e-5 for f32
+    inputs, 1e-2 for bf16; the new states 1e-5)."""
+    rng = np.random.default_rng(7900 + seed)
+    n = int(rng.integers(1, 6))
+    lens = [int(x) for x in rng.integers(0, 6, n)]
+    if sum(lens) == 0:
+        lens[0] = 1
+    h = int(rng.integers(1, 4))
+    dk = int(rng.choice([16, 32, 64, 128]))
+    dv = int(rng.choice([8, 13, 64, 96, 128]))
+    l2norm = bool(rng.random() < 0.5)
+    dtype = torch.bfloat16 if rng.random() < 0.6 else torch.float32
+    print(f"random step lens={lens} h={h} dk={dk} dv={dv} l2norm={l2norm} {dtype}", flush=True)
+    t = sum(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    gen = torch.Generator().manual_seed(8000 + seed)
+    rn = lambda *s: torch.randn(*s, generator=gen)  # noqa: E731
+    q, k, v = rn(t, h, dk).to(dtype), rn(t, h, dk).to(dtype), rn(t, h, dv).to(dtype)
+    g = -torch.nn.functional.softplus(rn(t, h))
+    beta = torch.sigmoid(rn(t, h)).to(dtype)
+    st = 0.3 * rn(n, h, dk, dv)
+    scale = None if l2norm else 0.4
+    opts = dm.GatedDeltaStepOptions(qk_l2norm=l2norm, scale=scale)
+    args = [x.cuda() for x in (q, k, v, g, beta, st)]
+    out, ns = dm.gated_delta_step(*args, torch.as_tensor(cu, dtype=torch.int32).cuda(), opts)
+    torch.cuda.synchronize()
+    sc = scale if scale is not None else float(np.float32(1 / np.sqrt(dk)))
+    eo, es = oracle.gdr_step(*(x.float().numpy() for x in (q, k, v, g, beta, st)), cu=cu,
+                             l2norm=l2norm, scale=sc, precision="f64")
+    ro, rs = errors(host(out), eo)[1], errors(host(ns), es)[1]
+    print(f"  out {ro:.2e} state {rs:.2e}")
+    assert ro <= (1e-5 if dtype == torch.float32 else 1e-2) and rs <= 1e-5
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_conv1d_update(seed):
+    """The conv1d decoding step against the f64 oracle (1e-2 for 16-bit inputs, 2e-6 for f32;
+    the next state exact: it only shifts values)."""
+    rng = np.random.default_rng(8100 + seed)
+    dtype = str(rng.choice(["bf16", "f16", "f32"]))
+    b, c, k = int(rng.integers(1, 9)), int(rng.choice([8, 40, 128, 264])), int(rng.integers(1, 9))
+    w = int(rng.integers(max(k - 1, 1), k + 4))
+    bias, silu = bool(rng.random() < 0.5), bool(rng.random() < 0.6)
+    print(f"random conv1d update {dtype} b={b} c={c} k={k} w={w} bias={bias} silu={silu}",
+          flush=True)
+    td = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    gen = torch.Generator().manual_seed(8200 + seed)
+    x = torch.randn(b, c, generator=gen).to(td)
+    wt = (0.5 * torch.randn(c, k, generator=gen)).to(td)
+    bs = torch.randn(c, generator=gen).to(td) if bias else None
+    state = torch.randn(b, w, c, generator=gen)
+    opts = dm.CausalConv1dStepOptions(
+        activation=dm.Activation.SILU if silu else dm.Activation.NONE)
+    out, nxt = dm.causal_conv1d_update(x.cuda(), wt.cuda(), None if bs is None else bs.cuda(),
+                                       state.cuda(), opts)
+    torch.cuda.synchronize()
+    eo, en = oracle.conv1d_update(x.float().numpy(), wt.float().numpy(),
+                                  None if bs is None else bs.float().numpy(), state.numpy(),
+                                  silu, precision="f64")
+    assert errors(host(out), eo)[1] <= (2e-6 if dtype == "f32" else 1e-2)
+    np.testing.assert_array_equal(host(nxt), en)
