@@ -43,6 +43,11 @@ struct Cv1Args {
     int32_t has_h0, has_bias, silu;
     int64_t seg_len;    // steps per segment
     int64_t cv;         // channel vectors per row
+    int64_t nseg;       // segments: the launch's first grid rows
+    // the per-sequence work the launch also carries (the forward's final states, the backward's
+    // initial states' gradient): aux_blocks blocks of it in aux_rows grid rows after the
+    // segments' (a grid-stride loop over the blocks beyond aux_rows x the grid's width)
+    int64_t aux_blocks, aux_rows;
 };
 
 // The sequence holding row r: s and its rows [s0, s1) (packed: the last sequence whose start is
@@ -201,12 +206,48 @@ __device__ __forceinline__ void cv1_taps(const Cv1Args &a, const void *wt, int64
 // Forward (conv1d/reference.rs:183-268)
 // ------------------------------------------------------------------------------------------
 
+// The final states: the last W' steps of each sequence's history, zeros in front where it is
+// shorter (reference.rs:183-197). One thread per (sequence, step, channel).
+template <int DT>
+__device__ __forceinline__ void cv1_final_block(const Cv1Args &a, const void *__restrict__ x,
+                                                const float *__restrict__ h0, float *__restrict__ fin,
+                                                int64_t blk) {
+    const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
+    const int64_t item = blk / cb;
+    const int64_t c = (blk % cb) * kCv1Threads + threadIdx.x;
+    if (c >= a.c) return;
+    const int64_t s = item / a.w_out, i = item % a.w_out;
+    int64_t s0, len;
+    if (a.cu) {
+        s0 = a.cu[s];
+        len = a.cu[s + 1] - s0;
+    } else {
+        s0 = s * a.t;
+        len = a.t;
+    }
+    const int64_t wh = a.has_h0 ? a.w : 0;
+    const int64_t hstep = wh + len - a.w_out + i;  // step of the history, from its first
+    float v = 0.f;
+    if (hstep >= wh)
+        v = ld<DT>(x, (s0 + hstep - wh) * a.c + c);
+    else if (hstep >= 0)
+        v = h0[(s * a.w + hstep) * a.c + c];
+    fin[(s * a.w_out + i) * a.c + c] = v;
+}
+
 template <int DT, int VEC, int KT>
 __global__ __launch_bounds__(kCv1Threads) void conv1d_fwd_kernel(Cv1Args a, const void *__restrict__ x,
                                                                  const void *__restrict__ wt,
                                                                  const void *__restrict__ bias,
                                                                  const float *__restrict__ h0,
-                                                                 void *__restrict__ out) {
+                                                                 void *__restrict__ out,
+                                                                 float *__restrict__ fin) {
+    if ((int64_t)blockIdx.y >= a.nseg) {  // the final states' rows
+        for (int64_t b = ((int64_t)blockIdx.y - a.nseg) * gridDim.x + blockIdx.x; b < a.aux_blocks;
+             b += a.aux_rows * gridDim.x)
+            cv1_final_block<DT>(a, x, h0, fin, b);
+        return;
+    }
     const int64_t cvi = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
     if (cvi >= a.cv) return;
     const int64_t c0 = cvi * VEC;
@@ -302,35 +343,6 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_fwd_kernel(Cv1Args a, cons
     }
 }
 
-// The final states: the last W' steps of each sequence's history, zeros in front where it is
-// shorter (reference.rs:183-197). One thread per (sequence, step, channel).
-template <int DT>
-__global__ __launch_bounds__(kCv1Threads) void conv1d_final_kernel(Cv1Args a, const void *__restrict__ x,
-                                                                   const float *__restrict__ h0,
-                                                                   float *__restrict__ fin) {
-    const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
-    const int64_t item = blockIdx.x / cb;
-    const int64_t c = (blockIdx.x % cb) * kCv1Threads + threadIdx.x;
-    if (c >= a.c) return;
-    const int64_t s = item / a.w_out, i = item % a.w_out;
-    int64_t s0, len;
-    if (a.cu) {
-        s0 = a.cu[s];
-        len = a.cu[s + 1] - s0;
-    } else {
-        s0 = s * a.t;
-        len = a.t;
-    }
-    const int64_t wh = a.has_h0 ? a.w : 0;
-    const int64_t hstep = wh + len - a.w_out + i;  // step of the history, from its first
-    float v = 0.f;
-    if (hstep >= wh)
-        v = ld<DT>(x, (s0 + hstep - wh) * a.c + c);
-    else if (hstep >= 0)
-        v = h0[(s * a.w + hstep) * a.c + c];
-    fin[(s * a.w_out + i) * a.c + c] = v;
-}
-
 // ------------------------------------------------------------------------------------------
 // Backward (conv1d/reference.rs:270-482)
 // ------------------------------------------------------------------------------------------
@@ -349,11 +361,73 @@ __device__ __forceinline__ float cv1_dy(float g, float y, int silu) {
     }
 }
 
+// The initial states' gradient: per (sequence, channel), the padded steps before the first step
+// take sum_j weight[j] dy[q - j] (reference.rs:318-325), the state's earlier steps zero, then the
+// final states' gradient where the history is short enough to keep state steps (:342-373). A few
+// steps per sequence: computed in f64 and rounded once (f32 leaves it about an ulp off, the width
+// of its conformance bound).
+template <int DT, int GT>
+__device__ __forceinline__ void cv1_h0_block(const Cv1Args &a, const void *__restrict__ x,
+                                             const void *__restrict__ wt, const void *__restrict__ bias,
+                                             const float *__restrict__ h0, const void *__restrict__ go,
+                                             const float *__restrict__ gfin, float *__restrict__ gh0,
+                                             int64_t blk) {
+    const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
+    const int64_t s = blk / cb;
+    const int64_t c = (blk % cb) * kCv1Threads + threadIdx.x;
+    if (c >= a.c) return;
+    int64_t s0, len;
+    if (a.cu) {
+        s0 = a.cu[s];
+        len = a.cu[s + 1] - s0;
+    } else {
+        s0 = s * a.t;
+        len = a.t;
+    }
+    const int64_t K = a.k, W = a.w;
+    const double b = a.has_bias ? (double)ld<DT>(bias, c) : 0.0;
+    auto hist = [&](int64_t tau) -> double {
+        if (tau >= 0) return ld<DT>(x, (s0 + tau) * a.c + c);
+        if (tau >= -W) return h0[(s * W + W + tau) * a.c + c];
+        return 0.0;
+    };
+    auto dy = [&](int64_t t) -> double {
+        double y = 0.0;
+        for (int64_t j = 0; j < K; j++) y += (double)ld<DT>(wt, c * K + j) * hist(t - (K - 1) + j);
+        y += b;
+        const double g = ld<GT>(go, (s0 + t) * a.c + c);
+        if (!a.silu) return g;
+        const double sg = 1.0 / (1.0 + exp(-y));
+        return g * (sg * (y * (1.0 - sg) + 1.0));
+    };
+    const int64_t P = W + len;
+    for (int64_t i = 0; i < W; i++) {
+        double g = 0.0;
+        const int64_t q = i - (W - (K - 1));  // padded step before the first
+        if (q >= 0)
+            for (int64_t j = 0; j < K; j++) {
+                const int64_t t = q - j;
+                if (t >= 0 && t < len) g += (double)ld<DT>(wt, c * K + j) * dy(t);
+            }
+        if (gfin) {
+            const int64_t idx = i - (P - a.w_out);
+            if (idx >= 0) g += gfin[(s * a.w_out + idx) * a.c + c];
+        }
+        gh0[(s * W + i) * a.c + c] = (float)g;
+    }
+}
+
 template <int DT, int GT, int VEC, int KT>
 __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_kernel(
     Cv1Args a, const void *__restrict__ x, const void *__restrict__ wt, const void *__restrict__ bias,
     const float *__restrict__ h0, const void *__restrict__ go, const float *__restrict__ gfin,
-    void *__restrict__ gx, float *__restrict__ part) {
+    void *__restrict__ gx, float *__restrict__ part, float *__restrict__ gh0) {
+    if ((int64_t)blockIdx.y >= a.nseg) {  // the initial states' gradient's rows
+        for (int64_t b = ((int64_t)blockIdx.y - a.nseg) * gridDim.x + blockIdx.x; b < a.aux_blocks;
+             b += a.aux_rows * gridDim.x)
+            cv1_h0_block<DT, GT>(a, x, wt, bias, h0, go, gfin, gh0, b);
+        return;
+    }
     const int64_t cvi = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
     if (cvi >= a.cv) return;
     const int64_t c0 = cvi * VEC;
@@ -531,61 +605,6 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_reduce(int64_t nseg, i
         st<DT>(gb, c, acc);
 }
 
-// The initial states' gradient: per (sequence, channel), the padded steps before the first step
-// take sum_j weight[j] dy[q - j] (reference.rs:318-325), the state's earlier steps zero, then the
-// final states' gradient where the history is short enough to keep state steps (:342-373). A few
-// steps per sequence: computed in f64 and rounded once (f32 leaves it about an ulp off, the width
-// of its conformance bound).
-template <int DT, int GT>
-__global__ __launch_bounds__(kCv1Threads) void conv1d_bwd_h0_kernel(
-    Cv1Args a, const void *__restrict__ x, const void *__restrict__ wt, const void *__restrict__ bias,
-    const float *__restrict__ h0, const void *__restrict__ go, const float *__restrict__ gfin,
-    float *__restrict__ gh0) {
-    const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
-    const int64_t s = blockIdx.x / cb;
-    const int64_t c = (blockIdx.x % cb) * kCv1Threads + threadIdx.x;
-    if (c >= a.c) return;
-    int64_t s0, len;
-    if (a.cu) {
-        s0 = a.cu[s];
-        len = a.cu[s + 1] - s0;
-    } else {
-        s0 = s * a.t;
-        len = a.t;
-    }
-    const int64_t K = a.k, W = a.w;
-    const double b = a.has_bias ? (double)ld<DT>(bias, c) : 0.0;
-    auto hist = [&](int64_t tau) -> double {
-        if (tau >= 0) return ld<DT>(x, (s0 + tau) * a.c + c);
-        if (tau >= -W) return h0[(s * W + W + tau) * a.c + c];
-        return 0.0;
-    };
-    auto dy = [&](int64_t t) -> double {
-        double y = 0.0;
-        for (int64_t j = 0; j < K; j++) y += (double)ld<DT>(wt, c * K + j) * hist(t - (K - 1) + j);
-        y += b;
-        const double g = ld<GT>(go, (s0 + t) * a.c + c);
-        if (!a.silu) return g;
-        const double sg = 1.0 / (1.0 + exp(-y));
-        return g * (sg * (y * (1.0 - sg) + 1.0));
-    };
-    const int64_t P = W + len;
-    for (int64_t i = 0; i < W; i++) {
-        double g = 0.0;
-        const int64_t q = i - (W - (K - 1));  // padded step before the first
-        if (q >= 0)
-            for (int64_t j = 0; j < K; j++) {
-                const int64_t t = q - j;
-                if (t >= 0 && t < len) g += (double)ld<DT>(wt, c * K + j) * dy(t);
-            }
-        if (gfin) {
-            const int64_t idx = i - (P - a.w_out);
-            if (idx >= 0) g += gfin[(s * a.w_out + idx) * a.c + c];
-        }
-        gh0[(s * W + i) * a.c + c] = (float)g;
-    }
-}
-
 // ------------------------------------------------------------------------------------------
 // The decoding step (conv1d/reference.rs:484-520)
 // ------------------------------------------------------------------------------------------
@@ -702,10 +721,18 @@ static Cv1Args cv1_args(const dm_conv1d_desc *d, bool bwd = false) {
     nseg = std::min<int64_t>(nseg, (a.rows + 15) / 16);
     nseg = std::max<int64_t>(nseg, 1);
     a.seg_len = (a.rows + nseg - 1) / nseg;
+    a.nseg = a.rows ? (a.rows + a.seg_len - 1) / a.seg_len : 0;
     return a;
 }
 
-static int64_t cv1_nseg(const Cv1Args &a) { return a.rows ? (a.rows + a.seg_len - 1) / a.seg_len : 0; }
+static int64_t cv1_nseg(const Cv1Args &a) { return a.nseg; }
+
+// the per-sequence work's blocks, in rows of the launch's width (at most 4096 rows)
+static void cv1_aux(Cv1Args &a, int64_t blocks) {
+    const int64_t gx = (a.cv + kCv1Threads - 1) / kCv1Threads;
+    a.aux_blocks = blocks;
+    a.aux_rows = blocks > 0 ? std::min<int64_t>((blocks + gx - 1) / gx, 4096) : 0;
+}
 
 // kernel width -> template instance: 1..8 exactly, wider ones in a window of 16
 #define CV1_K_SWITCH(K, MACRO, ...)        \
@@ -723,10 +750,11 @@ static int64_t cv1_nseg(const Cv1Args &a) { return a.rows ? (a.rows + a.seg_len 
 
 template <int DT>
 static void cv1_fwd_launch(const Cv1Args &a, int vec, const void *x, const void *w, const void *bias,
-                           const float *h0, void *out, hipStream_t st) {
-    const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)cv1_nseg(a));
+                           const float *h0, void *out, float *fin, hipStream_t st) {
+    const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)(a.nseg + a.aux_rows));
     constexpr int V = DT == DM_F32 ? 4 : 8;
-#define CV1_FWD(KT, VV) conv1d_fwd_kernel<DT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, out)
+#define CV1_FWD(KT, VV) \
+    conv1d_fwd_kernel<DT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, out, fin)
     if (vec == V && a.k <= 8) {
         CV1_K_SWITCH(a.k, CV1_FWD, V)
     } else {
@@ -738,11 +766,12 @@ static void cv1_fwd_launch(const Cv1Args &a, int vec, const void *x, const void 
 template <int DT, int GT>
 static void cv1_bwd_launch(const Cv1Args &a, int vec, const void *x, const void *w, const void *bias,
                            const float *h0, const void *go, const float *gfin, void *gx, float *part,
-                           hipStream_t st) {
-    const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)cv1_nseg(a));
+                           float *gh0, hipStream_t st) {
+    const dim3 grid((unsigned)((a.cv + kCv1Threads - 1) / kCv1Threads), (unsigned)(a.nseg + a.aux_rows));
     constexpr int V = 4;
-#define CV1_BWD(KT, VV) \
-    conv1d_bwd_kernel<DT, GT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, go, gfin, gx, part)
+#define CV1_BWD(KT, VV)                                                                          \
+    conv1d_bwd_kernel<DT, GT, VV, KT><<<grid, kCv1Threads, 0, st>>>(a, x, w, bias, h0, go, gfin, gx, \
+                                                                    part, gh0)
     if (vec == V && a.k <= 8) {
         CV1_K_SWITCH(a.k, CV1_BWD, V)
     } else {
@@ -768,28 +797,21 @@ int dm_causal_conv1d_fwd(const dm_conv1d_desc *d, const void *x, const void *wei
     if (d->has_final && !final_state)
         return refuse(std::string(op) + ": has_final without a final state buffer");
     hipStream_t st = (hipStream_t)stream;
-    const Cv1Args a = cv1_args(d);
+    Cv1Args a = cv1_args(d);
     const int vec = cv1_vec(d);
+    // the final states ride in the same launch, as rows after the segments'
+    if (d->has_final && a.w_out > 0 && a.nseq > 0 && a.c > 0)
+        cv1_aux(a, a.nseq * a.w_out * ((a.c + kCv1Threads - 1) / kCv1Threads));
     {
         KernelTimer timer(DM_KERNEL_CONV1D_FWD, st);
-        if (a.rows > 0 && a.c > 0) {
+        if (a.c > 0 && a.nseg + a.aux_rows > 0) {
             if (d->dtype == DM_F32)
-                cv1_fwd_launch<DM_F32>(a, vec, x, weight, bias, initial_state, out, st);
+                cv1_fwd_launch<DM_F32>(a, vec, x, weight, bias, initial_state, out, final_state, st);
             else if (d->dtype == DM_BF16)
-                cv1_fwd_launch<DM_BF16>(a, vec, x, weight, bias, initial_state, out, st);
+                cv1_fwd_launch<DM_BF16>(a, vec, x, weight, bias, initial_state, out, final_state, st);
             else
-                cv1_fwd_launch<DM_F16>(a, vec, x, weight, bias, initial_state, out, st);
+                cv1_fwd_launch<DM_F16>(a, vec, x, weight, bias, initial_state, out, final_state, st);
         }
-    }
-    if (d->has_final && a.w_out > 0 && a.nseq > 0 && a.c > 0) {
-        const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
-        const unsigned blocks = (unsigned)(a.nseq * a.w_out * cb);
-        if (d->dtype == DM_F32)
-            conv1d_final_kernel<DM_F32><<<blocks, kCv1Threads, 0, st>>>(a, x, initial_state, final_state);
-        else if (d->dtype == DM_BF16)
-            conv1d_final_kernel<DM_BF16><<<blocks, kCv1Threads, 0, st>>>(a, x, initial_state, final_state);
-        else
-            conv1d_final_kernel<DM_F16><<<blocks, kCv1Threads, 0, st>>>(a, x, initial_state, final_state);
     }
     probe_add(DM_PROBE_CONV1D_FWD);
     DM_LAUNCH_CHECK("causal_conv1d: launch");
@@ -820,26 +842,31 @@ int dm_causal_conv1d_bwd(const dm_conv1d_desc *d, const void *x, const void *wei
         return refuse(std::string(op) +
                       ": the workspace is smaller than dm_causal_conv1d_bwd_workspace");
     hipStream_t st = (hipStream_t)stream;
-    const Cv1Args a = cv1_args(d, true);
+    Cv1Args a = cv1_args(d, true);
     const int vec = cv1_vec(d, true);
+    // the initial states' gradient rides in the same launch, as rows after the segments'
+    if (d->has_initial && a.w > 0 && a.nseq > 0 && a.c > 0)
+        cv1_aux(a, a.nseq * ((a.c + kCv1Threads - 1) / kCv1Threads));
     const float *gfin = d->has_final && a.w_out > 0 ? grad_final_state : nullptr;
     float *part = (float *)workspace;
     const int64_t nseg = cv1_nseg(a);
     {
         KernelTimer timer(DM_KERNEL_CONV1D_BWD, st);
-        if (a.c > 0 && nseg > 0) {
-#define CV1_BWD_DT(DT)                                                                               \
-    if (grad_out_dtype == DM_F32)                                                                    \
-        cv1_bwd_launch<DT, DM_F32>(a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, st); \
-    else                                                                                             \
-        cv1_bwd_launch<DT, DT>(a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, st)
+        if (a.c > 0 && nseg + a.aux_rows > 0) {
+#define CV1_BWD_ARGS a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, grad_initial_state, st
+#define CV1_BWD_DT(DT)                                   \
+    if (grad_out_dtype == DM_F32)                        \
+        cv1_bwd_launch<DT, DM_F32>(CV1_BWD_ARGS);        \
+    else                                                 \
+        cv1_bwd_launch<DT, DT>(CV1_BWD_ARGS)
             if (d->dtype == DM_F32) {
-                cv1_bwd_launch<DM_F32, DM_F32>(a, vec, x, weight, bias, initial_state, grad_out, gfin, grad_x, part, st);
+                cv1_bwd_launch<DM_F32, DM_F32>(CV1_BWD_ARGS);
             } else if (d->dtype == DM_BF16) {
                 CV1_BWD_DT(DM_BF16);
             } else {
                 CV1_BWD_DT(DM_F16);
             }
+#undef CV1_BWD_ARGS
 #undef CV1_BWD_DT
         }
     }
@@ -858,21 +885,6 @@ int dm_causal_conv1d_bwd(const dm_conv1d_desc *d, const void *x, const void *wei
         } else {
             conv1d_bwd_reduce<DM_F16><<<blocks, kCv1Threads, 0, st>>>(nseg, a.c, a.k, part, grad_weight, gb);
         }
-    }
-    if (d->has_initial && a.w > 0 && a.nseq > 0 && a.c > 0) {
-        const int64_t cb = (a.c + kCv1Threads - 1) / kCv1Threads;
-        const unsigned blocks = (unsigned)(a.nseq * cb);
-#define CV1_H0(DT, GT)                                                                             \
-    conv1d_bwd_h0_kernel<DT, GT><<<blocks, kCv1Threads, 0, st>>>(a, x, weight, bias, initial_state, \
-                                                                 grad_out, gfin, grad_initial_state)
-        if (d->dtype == DM_F32) {
-            CV1_H0(DM_F32, DM_F32);
-        } else if (d->dtype == DM_BF16) {
-            if (grad_out_dtype == DM_F32) { CV1_H0(DM_BF16, DM_F32); } else { CV1_H0(DM_BF16, DM_BF16); }
-        } else {
-            if (grad_out_dtype == DM_F32) { CV1_H0(DM_F16, DM_F32); } else { CV1_H0(DM_F16, DM_F16); }
-        }
-#undef CV1_H0
     }
     probe_add(DM_PROBE_CONV1D_BWD);
     DM_LAUNCH_CHECK("causal_conv1d_backward: launch");
