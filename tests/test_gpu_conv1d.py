@@ -117,6 +117,10 @@ BIG = [
     ("f16", 2, 517, 100, 5, None, 6, 6, True, True),           # one channel per thread
     ("bf16", 1, 0, 128, 12, [300, 0, 77, 1024], 11, 13, True, True),  # widths above 8
     ("f32", 2, 640, 40, 8, None, 7, 2, False, True),           # K = 8, f32 vectors
+    # no steps at all: only the states' rows of the launches run
+    ("bf16", 1, 0, 64, 4, [0, 0, 0], 3, 4, True, True),
+    # 2500 short sequences: more states' blocks than the launches' 4096 rows of them hold
+    ("f16", 1, 0, 16, 3, [i % 5 for i in range(2500)], 2, 3, True, False),
 ]
 
 
