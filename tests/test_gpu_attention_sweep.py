@@ -3,7 +3,8 @@ head widths they take, D = 128 and 64, in bf16 and f16, against the CPU oracle o
 kind of the contract: no mask, sliding windows (left, right, both, with and without causality),
 key padding, packed sequences with different query and key lengths (bottom-right alignment),
 Tq < Tk and Tq > Tk, an explicit scale, and lengths that cut the 32-, 64-, 128- and 256-row tiles
-(1, 31, 33, 127, 129, 4097).
+(1, 31, 33, 127, 129, 4097). One packed case has sequences longer than the query tiles, an empty one
+and query rows after the last sequence.
 
 Rows that see no key must give lse = -inf, o = 0 and dq = 0 exactly
 (crates/dash-contract/src/attention.rs:56-71); a launch probe shows that the MFMA kernels, not the
@@ -63,6 +64,9 @@ CASES = [
     ("packed_no_causal", 1, None, None, 2, 1, ("packed", [40, 1, 90], [100, 7, 90]), False, None,
      None),
     ("causal_4097", 1, 4097, 4097, 4, 2, None, True, None, None),
+    # sequences longer than the query tiles, an empty one, one row, and rows after the last
+    ("packed_tiles_tail", 1, None, None, 4, 2,
+     ("packed", [300, 700, 0, 257, 129, 1], [300, 700, 0, 257, 129, 1], 77), True, None, None),
 ]
 
 
@@ -74,6 +78,8 @@ def _build(case, dtype, d, seed):
         cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
         cu_k = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
         tq, tk = int(cu_q[-1]), int(cu_k[-1])
+        if len(mspec) > 3:
+            tq += mspec[3]  # query rows after the last sequence: they see no key
     q = syn.normal(seed, (b, tq, hq, d), "cuda").to(dtype)
     k = syn.normal(seed + 1, (b, tk, hkv, d), "cuda").to(dtype)
     v = syn.normal(seed + 2, (b, tk, hkv, d), "cuda").to(dtype)
@@ -155,7 +161,8 @@ def test_mfma_attention_nondeterministic_flag_matches():
 
 D256_CASES = [c for c in CASES if c[0] in (
     "none_129", "causal_1", "causal_31", "causal_127_scale", "causal_tq127_tk33_empty_rows",
-    "window_both_300", "key_padding_160", "packed_cross", "packed_no_causal")] + [
+    "window_both_300", "key_padding_160", "packed_cross", "packed_no_causal",
+    "packed_tiles_tail")] + [
     # the reference's head shape (Hq = 8, Hkv = 2) over a longer causal sequence: dK/dV work
     # items of both passes in one launch, split over the query heads
     ("causal_1024_gqa4", 1, 1024, 1024, 8, 2, None, True, None, None),
@@ -194,3 +201,4 @@ def test_mfma_attention_d256_matches_oracle(case, dtype):
     empty = el == -np.inf
     if empty.any():
         assert np.all(got[0][empty] == 0.0) and np.all(got[2][empty] == 0.0)
+
