@@ -144,3 +144,65 @@ def test_decode_graph():
         _check(lib.dm_attention_decode(ctypes.byref(desc), *P[:5], P[5], nb, st), lib)
 
     _replays(fn, [o])
+
+
+def _into(bufs):
+    """Copies of an op's outputs into buffers made once, so that a captured op's outputs (new
+    tensors in the graph's pool) are compared across replays through fixed tensors."""
+    def put(*outs):
+        for b, o in zip(bufs, outs):
+            if o is not None:
+                b.copy_(o)
+    return put
+
+
+def test_conv1d_fwd_bwd_update_graph():
+    """The conv1d forward (final states in its launch), backward (initial states' gradient in
+    its launch, then the segments' sums) and decoding step, batched (no offsets to check on the
+    host), with bias, SiLU and states."""
+    b, t, c, k, w = 3, 700, 256, 4, 3
+    x = syn.normal(11, (b, t, c), "cuda").to(torch.bfloat16)
+    wt = (syn.normal(12, (c, k), "cuda") * 0.5).to(torch.bfloat16)
+    bias = syn.normal(13, (c,), "cuda").to(torch.bfloat16)
+    h0 = syn.normal(14, (b, w, c), "cuda")
+    go = syn.normal(15, (b, t, c), "cuda").to(torch.bfloat16)
+    gf = syn.normal(16, (b, w, c), "cuda")
+    xs = syn.normal(17, (b, c), "cuda").to(torch.bfloat16)
+    opts = dm.CausalConv1dOptions(activation=dm.Activation.SILU).with_final_state_len(w)
+    step = dm.contract.CausalConv1dStepOptions.from_sequence(opts)
+    bufs = [torch.empty_like(x), torch.empty((b, w, c), device="cuda"), torch.empty_like(x),
+            torch.empty_like(wt), torch.empty_like(bias), torch.empty_like(h0),
+            torch.empty_like(xs), torch.empty_like(h0)]
+    put = _into(bufs)
+
+    def fn():
+        out, fin = dm.causal_conv1d(x, wt, bias, h0, None, opts)
+        grads = dm.causal_conv1d_backward(x, wt, bias, h0, None, go, gf, opts)
+        ys, hs = dm.causal_conv1d_update(xs, wt, bias, h0, step)
+        put(out, fin, *grads, ys, hs)
+
+    _lib.probe_reset()
+    _replays(fn, bufs)
+    pc = _lib.probe_counts()
+    assert pc["conv1d_fwd"] > 0 and pc["conv1d_bwd"] > 0, pc
+
+
+def test_gdr_step_fwd_bwd_graph():
+    """The recurrent step out of place and its backward (per-slice sums, then the finishing
+    pass), batched, with the l2 normalisation."""
+    c = syn.config5("cuda", b=16, h=4)
+    args = [c[x] for x in ("q", "k", "v", "g", "beta")]
+    st = c["state"]
+    do = syn.normal(21, tuple(c["v"].shape), "cuda").to(torch.bfloat16)
+    dst = syn.normal(22, tuple(st.shape), "cuda", std=0.1)
+    opts = dm.GatedDeltaStepOptions().with_qk_l2norm(True)
+    bufs = [torch.empty_like(c["v"]), torch.empty_like(st)] + \
+        [torch.empty_like(x) for x in args] + [torch.empty_like(st)]
+    put = _into(bufs)
+
+    def fn():
+        out, st_out = dm.gated_delta_step(*args, st, None, opts)
+        grads = dm.gated_delta_step_backward(*args, st, None, do, dst, opts)
+        put(out, st_out, *grads)
+
+    _replays(fn, bufs)
