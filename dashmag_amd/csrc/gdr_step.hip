@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     float *qs = sm;            // [Dk]
     float *ks = qs + Dk;       // [Dk]
     float *red = ks + Dk;      // [NKG][4 NQ] partial sums
-    __shared__ float norm2[2];
+    __shared__ float norm2[2][4];  // the wavefronts' sums of q^2 and k^2
 
     int64_t t0, t1;
     if (cu) {
@@ -103,19 +103,18 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
         if (l2norm) {
             pq = wave_sum(pq);
             pk = wave_sum(pk);
-            if (tid == 0) norm2[0] = norm2[1] = 0.f;
-            __syncthreads();
             if ((tid & 63) == 0) {
-                atomicAdd(&norm2[0], pq);
-                atomicAdd(&norm2[1], pk);
+                norm2[0][tid >> 6] = pq;
+                norm2[1][tid >> 6] = pk;
             }
         }
         __syncthreads();
         float qmul = scale, kmul = 1.f;
         if (l2norm) {
-            // x * (1 / sqrt(sum x^2 + eps)) (recurrent.rs:400-404)
-            qmul = (1.f / sqrtf(norm2[0] + 1e-6f));
-            kmul = 1.f / sqrtf(norm2[1] + 1e-6f);
+            // x * (1 / sqrt(sum x^2 + eps)) (recurrent.rs:400-404); the four wavefronts' sums
+            // added in a fixed order, so that a call's result does not depend on their timing
+            qmul = 1.f / sqrtf(((norm2[0][0] + norm2[0][1]) + (norm2[0][2] + norm2[0][3])) + 1e-6f);
+            kmul = 1.f / sqrtf(((norm2[1][0] + norm2[1][1]) + (norm2[1][2] + norm2[1][3])) + 1e-6f);
         }
         const float decay = expf(ld_any(g_dt, g, g_at(a, t, h)));
         const float bt = ld_any(beta_dt, beta, b_at(a, t, h));

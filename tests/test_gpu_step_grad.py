@@ -119,3 +119,24 @@ def test_config5_step_backward():
         rr = rel(host(a[rows]), ee)
         print(f"config 5 backward {name}: rel {rr:.2e}")
         assert rr <= (1e-5 if name == "d_state" else 2e-2), (name, rr)
+
+
+@pytest.mark.parametrize("dk", [128, 256])
+def test_wide_step_packed_equals_token_by_token(dk):
+    """With the l2 normalisation at Dk = 256 every wavefront of a workgroup holds part of q's and
+    k's squared sums: they are added in a fixed order, so a packed call equals its tokens run one
+    call at a time, and a repeated call itself, to the bit (gated_delta_packed.rs:459-502)."""
+    cu = [0, 3, 4]
+    x = inputs(91 + dk, cu, 2, dk, 64, torch.bfloat16)
+    args = [x[n] for n in ("q", "k", "v", "g", "beta")]
+    opts = dm.GatedDeltaStepOptions().with_qk_l2norm(True)
+    cut = torch.tensor(cu, dtype=torch.int32)
+    out, st = dm.gated_delta_step(*args, x["state"], cut, opts)
+    out2, st2 = dm.gated_delta_step(*args, x["state"], cut, opts)
+    assert torch.equal(out, out2) and torch.equal(st, st2)
+    for s in range(len(cu) - 1):
+        state = x["state"][s:s + 1].clone()
+        for t in range(cu[s], cu[s + 1]):
+            o1, state = dm.gated_delta_step(*(a[t:t + 1] for a in args), state, None, opts)
+            assert torch.equal(o1[0], out[t]), (s, t)
+        assert torch.equal(state[0], st[s]), s
