@@ -214,11 +214,16 @@ __device__ __forceinline__ float group_sum(float x, int P) {
 // them in `states` ([rows, H, Dk, Dv]); the first is state_in. The sums over the columns (dqs,
 // dk, dg, dbeta) are per slice, into `part` ([ncs][rows * H][2 Dk + 2]); gdr_step_bwd_finish
 // adds the slices and takes them through the scale and the l2 normalisation.
-template <int DT, bool VEC, int MAXR>
-__global__ __launch_bounds__(256) void gdr_step_bwd_kernel(
-    GdrArgs a, int64_t rows, int64_t Dk, int64_t Dv, int ncs, int P,
+// ONE: one token per sequence (no offsets), Dk = 128 and 64-column slices (16 lanes x 4 columns
+// by 16 row groups of 8 rows): every index and bound is then known at compile time.
+template <int DT, bool VEC, int MAXR, bool ONE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1))) void gdr_step_bwd_kernel(
+    GdrArgs a, int64_t rows, int64_t Dk_, int64_t Dv, int ncs, int P_,
     const int32_t *__restrict__ cu, const float *state_in, const float *d_state, float *states,
     const void *d_out, void *dv_out, float *part, float *d_state_in) {
+    static_assert(!ONE || (VEC && MAXR == 8), "the one-token form is the 8-row vector one");
+    const int64_t Dk = ONE ? 128 : Dk_;
+    const int P = ONE ? 16 : P_;
     const int64_t H = a.H;
     const int g_dt = a.g_dt, beta_dt = a.beta_dt, l2norm = a.l2norm;
     const float scale = a.scale;
@@ -226,7 +231,7 @@ __global__ __launch_bounds__(256) void gdr_step_bwd_kernel(
     const int slice = blockIdx.x % ncs;
     const int64_t sh = blockIdx.x / ncs;
     const int64_t s = sh / H, h = sh % H;
-    const int64_t Dw = Dv / ncs, c0 = slice * Dw;
+    const int64_t Dw = ONE ? 64 : Dv / ncs, c0 = slice * Dw;
     const int tid = threadIdx.x;
     const int NKG = 256 / P;
     const int quad = tid % P, kg = tid / P;
@@ -241,7 +246,7 @@ __global__ __launch_bounds__(256) void gdr_step_bwd_kernel(
     float *red = ksh + Dk;     // [NKG][4 P] column partial sums
     __shared__ float w4[4];
 
-    const int64_t t0 = cu ? cu[s] : s, t1 = cu ? cu[s + 1] : s + 1;
+    const int64_t t0 = !ONE && cu ? cu[s] : s, t1 = !ONE && cu ? cu[s + 1] : s + 1;
     const int64_t DD = Dk * Dv;
 
     // the token's normalised rows: loads q and k into LDS, returns the multipliers of q (the
@@ -269,7 +274,7 @@ __global__ __launch_bounds__(256) void gdr_step_bwd_kernel(
             __syncthreads();
         }
     };
-    auto row_ok = [&](int rr) { return rr < rows_per && r0 + rr < Dk; };
+    auto row_ok = [&](int rr) { return ONE || (rr < rows_per && r0 + rr < Dk); };
     // the column sums of x[rr][c] * w[row] over the workgroup's rows, for this thread's columns
     auto col_sum = [&](float (*x)[4], const float *w, float wmul, float outv[4]) {
         float p4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(256) void gdr_step_bwd_kernel(
         const int64_t v_off = v_at(a, t, h) + c0, o_off = o_at(a, t, h) + c0;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const bool cv = cq + c < Dw;
+            const bool cv = ONE || cq + c < Dw;
             vv[c] = cv ? ld<DT>(v, v_off + cq + c) : 0.f;
             delta[c] = (vv[c] - kv[c]) * bt;
             dO[c] = cv && d_out ? ld<DT>(d_out, o_off + cq + c) : 0.f;
@@ -392,7 +397,7 @@ __global__ __launch_bounds__(256) void gdr_step_bwd_kernel(
             const int64_t dv_off = (t * H + h) * Dv + c0;
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                if (cq + c < Dw) st<DT>(dv_out, dv_off + cq + c, bt * dd[c]);
+                if (ONE || cq + c < Dw) st<DT>(dv_out, dv_off + cq + c, bt * dd[c]);
         }
         // dk = dS delta + S' dkv ; dS' = dS + k dkv^T ; dg = sum dS' o S' ; dP = a dS'
         float dg = 0.f;
@@ -616,15 +621,18 @@ extern "C" int dm_gdr_step_bwd(const dm_gdr_desc *d, const void *q, const void *
     float *part = (float *)((char *)workspace + w.states);
     const GdrArgs a = gdr_args(d, q, k, v, g, beta, true);
     const int64_t nrows = d->b;
-#define BWD(DT, V, R)                                                                        \
-    gdr_step_bwd_kernel<DT, V, R><<<(unsigned)blocks, 256, smem, st>>>(                      \
+    // one token per sequence at Dk = 128 in 64-column slices: the compile-time form
+    const bool one = !d->cu_seqlens && d->dk == 128 && dw == 64 && P == 16 && rows == 8 && vec;
+#define BWD(DT, V, R, O)                                                                     \
+    gdr_step_bwd_kernel<DT, V, R, O><<<(unsigned)blocks, 256, smem, st>>>(                   \
         a, nrows, d->dk, d->dv, ncs, P, d->cu_seqlens, state_in, d_state, states, d_out, dv, \
         part, d_state_in)
-#define BWD_V(DT, R)           \
-    if (vec) BWD(DT, true, R); \
-    else BWD(DT, false, R);
+#define BWD_V(DT, R)                  \
+    if (vec) BWD(DT, true, R, false); \
+    else BWD(DT, false, R, false);
 #define BWD_R(DT)                          \
     if (rows <= 4) { BWD_V(DT, 4) }        \
+    else if (one) { BWD(DT, true, 8, true); } \
     else if (rows <= 8) { BWD_V(DT, 8) }   \
     else if (rows <= 16) { BWD_V(DT, 16) } \
     else if (rows <= 32) { BWD_V(DT, 32) } \

@@ -53,6 +53,7 @@ CASES = [
     (4, 128, 128, [1, 7, 0, 40, 2]),  # two 64-column slices per (sequence, head)
     (1, 256, 256, [3, 1]),           # four slices, 16 rows a thread
     (2, 96, 200, [2, 4]),            # one slice of 200 columns
+    (3, 128, 256, None),             # one token per sequence at Dk = 128: the compile-time form
 ]
 
 
