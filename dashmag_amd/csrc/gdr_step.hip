@@ -41,10 +41,14 @@ __device__ __forceinline__ void st_cols(float *row, int cq, int64_t dw, const fl
 // Per token, with S the state (recurrent.rs:362-396):
 //   q, k <- l2norm (optional), q <- scale q;  S <- exp(g) S;  delta <- beta (v - S^T k);
 //   S <- S + k delta^T;  out <- S^T q.
-template <int DT, bool VEC, int MAXR>
-__global__ __launch_bounds__(256) void gdr_step_kernel(
-    GdrArgs a, int64_t nseq, int64_t Dk, int64_t Dv, int ncs, const int32_t *__restrict__ cu,
+// ONE: one token per sequence (no offsets), Dk = 128 and 64-column slices, every index and
+// bound known at compile time.
+template <int DT, bool VEC, int MAXR, bool ONE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1))) void gdr_step_kernel(
+    GdrArgs a, int64_t nseq, int64_t Dk_, int64_t Dv, int ncs, const int32_t *__restrict__ cu,
     const float *state_in, float *state_out, void *__restrict__ out) {
+    static_assert(!ONE || (VEC && MAXR == 8), "the one-token form is the 8-row vector one");
+    const int64_t Dk = ONE ? 128 : Dk_;
     const int64_t H = a.H;
     const int g_dt = a.g_dt, beta_dt = a.beta_dt, l2norm = a.l2norm;
     const float scale = a.scale;
@@ -53,7 +57,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     // taking Dv / ncs columns (every one recomputes the token's normalisation)
     const int64_t sh = blockIdx.x / ncs;
     const int64_t s = sh / H, h = sh % H;
-    const int64_t Dw = Dv / ncs, c0 = (blockIdx.x % ncs) * Dw;
+    const int64_t Dw = ONE ? 64 : Dv / ncs, c0 = (blockIdx.x % ncs) * Dw;
     const int tid = threadIdx.x;
     const int NQ = (int)((Dw + 3) / 4);  // column quads
     const int NKG = 256 / NQ;            // row groups
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(256) void gdr_step_kernel(
     __shared__ float norm2[2][4];  // the wavefronts' sums of q^2 and k^2
 
     int64_t t0, t1;
-    if (cu) {
+    if (!ONE && cu) {
         t0 = cu[s];
         t1 = cu[s + 1];
     } else {
@@ -555,14 +559,17 @@ extern "C" int dm_gdr_step(const dm_gdr_desc *d, const void *q, const void *k, c
     // 16-byte state rows: Dv a multiple of 4 and both state pointers aligned
     const bool vec = d->dv % 4 == 0 && aligned_16b(state_in) && aligned_16b(state_out);
     const GdrArgs a = gdr_args(d, q, k, v, g, beta, true);
-#define STEP(DT, V, R)                                                                       \
-    gdr_step_kernel<DT, V, R><<<(unsigned)blocks, 256, smem, st>>>(                          \
+    // one token per sequence at Dk = 128 in 64-column slices: the compile-time form
+    const bool one = !d->cu_seqlens && d->dk == 128 && dw == 64 && rows == 8 && vec;
+#define STEP(DT, V, R, O)                                                                    \
+    gdr_step_kernel<DT, V, R, O><<<(unsigned)blocks, 256, smem, st>>>(                       \
         a, nseq, d->dk, d->dv, ncs, d->cu_seqlens, state_in, state_out, out)
-#define STEP_V(DT, R)           \
-    if (vec) STEP(DT, true, R); \
-    else STEP(DT, false, R);
+#define STEP_V(DT, R)                  \
+    if (vec) STEP(DT, true, R, false); \
+    else STEP(DT, false, R, false);
 #define STEP_R(DT)                          \
     if (rows <= 4) { STEP_V(DT, 4) }        \
+    else if (one) { STEP(DT, true, 8, true); } \
     else if (rows <= 8) { STEP_V(DT, 8) }   \
     else if (rows <= 16) { STEP_V(DT, 16) } \
     else if (rows <= 32) { STEP_V(DT, 32) } \
