@@ -200,6 +200,10 @@ __device__ __forceinline__ float block_sum_256(float x, float *w4) {
     return (w4[0] + w4[1]) + (w4[2] + w4[3]);
 }
 
+// The per-slice partial sums' row: dq_s's Dk, dk's Dk, dg and dbeta, padded to whole 16-byte
+// pieces.
+__host__ __device__ inline int64_t step_pw(int64_t dk) { return (2 * dk + 2 + 3) & ~(int64_t)3; }
+
 // A sum over the P lanes of a row group (P a power of two dividing 64, the group aligned to P
 // lanes), in every lane of the group.
 __device__ __forceinline__ float group_sum(float x, int P) {
@@ -242,7 +246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
     const int cq = quad * 4;
     const int rows_per = (int)((Dk + NKG - 1) / NKG);
     const int r0 = kg * rows_per;
-    const int64_t PW = 2 * Dk + 2;
+    const int64_t PW = step_pw(Dk);
 
     extern __shared__ float sm[];
     float *qsh = sm;           // [Dk] the token's q, f32
@@ -300,6 +304,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
         __syncthreads();
     };
 
+    float racc[MAXR];    // the one-token form: a row group's sums, stored 4 at a time
     float Pst[MAXR][4];  // the state before the token
     float dS[MAXR][4];   // the gradient of the state after it
     const float *sin = state_in + sh * DD + c0;
@@ -385,9 +390,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
                 acc += (Pst[rr][c] + kr * delta[c]) * dO[c];
             }
             acc = group_sum(acc, P);
-            if (ok && quad == 0)
+            if (ONE) {
+                // the one-token form: a row group's sums in 16-byte stores of 4
+                racc[rr] = acc;
+                if (rr % 4 == 3 && quad == 0)
+                    *(float4 *)(part + ((int64_t)slice * rows * H + t * H + h) * PW + r0 + rr - 3) =
+                        make_float4(racc[rr - 3], racc[rr - 2], racc[rr - 1], racc[rr]);
+            } else if (ok && quad == 0) {
                 part[((int64_t)slice * rows * H + t * H + h) * PW + r0 + rr] = acc;
+            }
         }
+        // (the one-token form: a row group's 8 sums as two 16-byte stores)
+
         // ddelta = dS^T k
         float dd[4], dkv[4];
         col_sum(dS, ksh, kmul, dd);
@@ -418,9 +432,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
                 dS[rr][c] = decay * d1;
             }
             acc = group_sum(acc, P);
-            if (ok && quad == 0)
+            if (ONE) {
+                racc[rr] = acc;
+                if (rr % 4 == 3 && quad == 0)
+                    *(float4 *)(part + ((int64_t)slice * rows * H + t * H + h) * PW + Dk + r0 + rr - 3) =
+                        make_float4(racc[rr - 3], racc[rr - 2], racc[rr - 1], racc[rr]);
+            } else if (ok && quad == 0) {
                 part[((int64_t)slice * rows * H + t * H + h) * PW + Dk + r0 + rr] = acc;
+            }
         }
+
         dg = block_sum_256(dg, w4);
         db = block_sum_256(db, w4);
         if (tid == 0) {
@@ -443,7 +464,7 @@ template <int DT>
 __global__ __launch_bounds__(256) void gdr_step_bwd_finish(GdrArgs a, int64_t rows, int ncs,
                                                            const float *part, void *dq, void *dk,
                                                            void *dg, void *dbeta) {
-    const int64_t H = a.H, Dk = a.Dk, PW = 2 * Dk + 2;
+    const int64_t H = a.H, Dk = a.Dk, PW = step_pw(Dk);
     const int64_t th = blockIdx.x, t = th / H, h = th % H;
     const int tid = threadIdx.x;
     __shared__ float w4[4];
@@ -534,7 +555,7 @@ StepBwdWs step_bwd_ws(const dm_gdr_desc *d) {
     StepBwdWs w;
     const size_t rh = (size_t)d->b * (size_t)d->h;
     w.states = d->cu_seqlens ? up(rh * (size_t)d->dk * (size_t)d->dv * sizeof(float)) : 0;
-    w.part = up((size_t)step_slices(d) * rh * (size_t)(2 * d->dk + 2) * sizeof(float));
+    w.part = up((size_t)step_slices(d) * rh * (size_t)step_pw(d->dk) * sizeof(float));
     w.total = w.states + w.part;
     return w;
 }
