@@ -44,7 +44,7 @@ __device__ __forceinline__ void st_cols(float *row, int cq, int64_t dw, const fl
 // ONE: one token per sequence (no offsets), Dk = 128 and 64-column slices, every index and
 // bound known at compile time.
 template <int DT, bool VEC, int MAXR, bool ONE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1))) void gdr_step_kernel(
+__global__ __launch_bounds__(256) void gdr_step_kernel(
     GdrArgs a, int64_t nseq, int64_t Dk_, int64_t Dv, int ncs, const int32_t *__restrict__ cu,
     const float *state_in, float *state_out, void *__restrict__ out) {
     static_assert(!ONE || (VEC && MAXR == 8), "the one-token form is the 8-row vector one");
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1
     const int NKG = 256 / NQ;            // row groups
     const int quad = tid % NQ, kg = tid / NQ;
     const int cq = quad * 4;
-    const bool active = kg < NKG;
+    const bool active = ONE || kg < NKG;
     const int rows_per = (int)((Dk + NKG - 1) / NKG);
     const int r0 = kg * rows_per;
 
@@ -84,11 +84,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1
 
     float st_[MAXR][4];
     const float *sin = state_in + sh * Dk * Dv + c0;
+    // a row's offset from the slice's first, in 32 bits (Dk x Dv is at most 2^16; 64-bit
+    // products per row had doubled the registers of the one-token form)
+    const int dv32 = (int)Dv;
 #pragma unroll
     for (int rr = 0; rr < MAXR; rr++) {
         const int64_t row = r0 + rr;
-        if (active && rr < rows_per && row < Dk)
-            ld_cols<VEC>(sin + row * Dv, cq, Dw, st_[rr]);
+        if (ONE || (active && rr < rows_per && row < Dk))
+            ld_cols<VEC>(sin + r0 * dv32 + rr * dv32, cq, Dw, st_[rr]);
         else
             st_[rr][0] = st_[rr][1] = st_[rr][2] = st_[rr][3] = 0.f;
     }
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1
 #pragma unroll
         for (int rr = 0; rr < MAXR; rr++) {
             const int64_t row = r0 + rr;
-            const float kr = (active && rr < rows_per && row < Dk) ? ks[row] * kmul : 0.f;
+            const float kr = (ONE || (active && rr < rows_per && row < Dk)) ? ks[row] * kmul : 0.f;
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 st_[rr][c] *= decay;
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1
 #pragma unroll
         for (int rr = 0; rr < MAXR; rr++) {
             const int64_t row = r0 + rr;
-            const bool ok = active && rr < rows_per && row < Dk;
+            const bool ok = ONE || (active && rr < rows_per && row < Dk);
             const float kr = ok ? ks[row] * kmul : 0.f;
             const float qr = ok ? qs[row] * qmul * (l2norm ? scale : 1.f) : 0.f;
 #pragma unroll
@@ -182,7 +185,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1
 #pragma unroll
     for (int rr = 0; rr < MAXR; rr++) {
         const int64_t row = r0 + rr;
-        if (active && rr < rows_per && row < Dk) st_cols<VEC>(sout + row * Dv, cq, Dw, st_[rr]);
+        if (ONE || (active && rr < rows_per && row < Dk))
+            st_cols<VEC>(sout + r0 * dv32 + rr * dv32, cq, Dw, st_[rr]);
     }
 }
 
@@ -256,6 +260,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
 
     const int64_t t0 = !ONE && cu ? cu[s] : s, t1 = !ONE && cu ? cu[s + 1] : s + 1;
     const int64_t DD = Dk * Dv;
+    // a row's offset from the slice's first, in 32 bits (Dk x Dv is at most 2^16)
+    auto roff = [&](int rr) { return r0 * (int)Dv + rr * (int)Dv; };
 
     // the token's normalised rows: loads q and k into LDS, returns the multipliers of q (the
     // scale included) and k
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
 #pragma unroll
         for (int rr = 0; rr < MAXR; rr++) {
             if (row_ok(rr))
-                ld_cols<VEC>(base + (r0 + rr) * Dv, cq, Dw, Pst[rr]);
+                ld_cols<VEC>(base + roff(rr), cq, Dw, Pst[rr]);
             else
                 Pst[rr][0] = Pst[rr][1] = Pst[rr][2] = Pst[rr][3] = 0.f;
         }
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
 #pragma unroll
     for (int rr = 0; rr < MAXR; rr++) {
         if (d_state && row_ok(rr))
-            ld_cols<VEC>(d_state + sh * DD + c0 + (r0 + rr) * Dv, cq, Dw, dS[rr]);
+            ld_cols<VEC>(d_state + sh * DD + c0 + roff(rr), cq, Dw, dS[rr]);
         else
             dS[rr][0] = dS[rr][1] = dS[rr][2] = dS[rr][3] = 0.f;
     }
@@ -350,7 +356,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
             const float kr = ksh[r0 + rr] * kmul;
 #pragma unroll
             for (int c = 0; c < 4; c++) Pst[rr][c] += kr * delta[c];
-            st_cols<VEC>(dst + (r0 + rr) * Dv, cq, Dw, Pst[rr]);
+            st_cols<VEC>(dst + roff(rr), cq, Dw, Pst[rr]);
         }
         __syncthreads();
     }
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE ? 3 : 1
         float *dst = d_state_in + sh * DD + c0;
 #pragma unroll
         for (int rr = 0; rr < MAXR; rr++)
-            if (row_ok(rr)) st_cols<VEC>(dst + (r0 + rr) * Dv, cq, Dw, dS[rr]);
+            if (row_ok(rr)) st_cols<VEC>(dst + roff(rr), cq, Dw, dS[rr]);
     }
 }
 
