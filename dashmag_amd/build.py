@@ -30,7 +30,12 @@ FLAGS = [
 # wavefront per SIMD: with the products' accumulators in ordinary vector registers, the state's
 # decay and conversions work on them in place instead of moving every value out of and back into
 # the accumulator registers at each step.
-EXTRA = {"gdr_chunk_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# The attention kernels are scheduled with the strategy that keeps memory instructions together
+# (measured at head width 256, one wavefront per SIMD: forward 288 -> 262 us, dK/dV 759 -> 723 us,
+# dQ 359 -> 346 us on the reference's T = 6144 shape; the same at widths 64 and 128 within noise).
+EXTRA = {"gdr_chunk_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "attention_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+         "attention_mfma_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
 
 
 def sources():
