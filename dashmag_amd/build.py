@@ -32,10 +32,13 @@ FLAGS = [
 # the accumulator registers at each step.
 # The attention kernels are scheduled with the strategy that keeps memory instructions together
 # (measured at head width 256, one wavefront per SIMD: forward 288 -> 262 us, dK/dV 759 -> 723 us,
-# dQ 359 -> 346 us on the reference's T = 6144 shape; the same at widths 64 and 128 within noise).
+# dQ 359 -> 346 us on the reference's T = 6144 shape; the same at widths 64 and 128 within noise),
+# but for the head width 256 dK/dV kernel, whose occupancy-driven iterative scheduling took it to
+# 690 us.
 EXTRA = {"gdr_chunk_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
          "attention_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
-         "attention_mfma_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
+         "attention_mfma_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+         "attention_bwd_w4.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-maxocc"]}
 
 
 def sources():
