@@ -617,20 +617,24 @@ __global__ __launch_bounds__(kCv1Threads) void conv1d_update_kernel(
     int64_t B, int64_t C, int64_t K, int64_t W, int has_bias, int silu, const void *__restrict__ x,
     const void *__restrict__ wt, const void *__restrict__ bias, const float *state, void *__restrict__ out,
     float *next) {
-    const int64_t i = (int64_t)blockIdx.x * kCv1Threads + threadIdx.x;
-    if (i >= B * C) return;
-    const int64_t b = i / C, c = i % C;
-    const float xv = ld<DT>(x, i);
+    // the channel from the grid's first index, the row from its second; a row's state offsets in
+    // 32 bits (W x C is checked on the host)
+    const int c = blockIdx.x * kCv1Threads + threadIdx.x;
+    if (c >= C) return;
+    const int64_t b = blockIdx.y;
+    const int c32 = (int)C, k32 = (int)K, w32 = (int)W;
+    const float *sp = state + b * W * C + c;
+    float *np = next + b * W * C + c;
+    const float xv = ld<DT>(x, b * C + c);
     float y = 0.f;
-    for (int64_t j = 0; j < K; j++) {
-        const float v = j < K - 1 ? state[(b * W + W - (K - 1) + j) * C + c] : xv;
-        y = cv1_madd<DT>(y, v, ld<DT>(wt, c * K + j));
+    for (int j = 0; j < k32; j++) {
+        const float v = j < k32 - 1 ? sp[(w32 - (k32 - 1) + j) * c32] : xv;
+        y = cv1_madd<DT>(y, v, ld<DT>(wt, (int64_t)c * K + j));
     }
     if (has_bias) y = __fadd_rn(y, ld<DT>(bias, c));
     if (silu) y = cv1_silu<DT>(y);
-    st<DT>(out, i, y);
-    for (int64_t s = 0; s < W; s++)
-        next[(b * W + s) * C + c] = s + 1 < W ? state[(b * W + s + 1) * C + c] : xv;
+    st<DT>(out, b * C + c, y);
+    for (int t = 0; t < w32; t++) np[t * c32] = t + 1 < w32 ? sp[(t + 1) * c32] : xv;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -897,24 +901,35 @@ int dm_causal_conv1d_update(const dm_conv1d_desc *d, const void *x, const void *
     const char *op = "causal_conv1d_update";
     if (int rc = cv1_check(d, op, true)) return rc;
     if (d->has_bias && !bias) return refuse(std::string(op) + ": has_bias without a bias");
+    if (d->w * d->c >= (1ll << 31))
+        return refuse(std::string(op) + ": a row's state of 2^31 or more values is not implemented");
     hipStream_t st = (hipStream_t)stream;
     const int64_t n = d->b * d->c;
     if (n > 0) {
         KernelTimer timer(DM_KERNEL_CONV1D_UPDATE, st);
-        const unsigned blocks = (unsigned)((n + kCv1Threads - 1) / kCv1Threads);
         const int silu = d->activation == DM_ACT_SILU;
-#define CV1_UPD(DT)                                                                                \
-    conv1d_update_kernel<DT><<<blocks, kCv1Threads, 0, st>>>(d->b, d->c, d->k, d->w, d->has_bias, \
-                                                             silu, x, weight, bias, state, out,   \
-                                                             next_state)
-        if (d->dtype == DM_F32) {
-            CV1_UPD(DM_F32);
-        } else if (d->dtype == DM_BF16) {
-            CV1_UPD(DM_BF16);
-        } else {
-            CV1_UPD(DM_F16);
-        }
+        const size_t xb = dtype_bytes(d->dtype);
+        // the rows in launches of at most 65535 (the grid's second index)
+        for (int64_t b0 = 0; b0 < d->b; b0 += 65535) {
+            const int64_t nb = std::min<int64_t>(65535, d->b - b0);
+            const dim3 blocks((unsigned)((d->c + kCv1Threads - 1) / kCv1Threads), (unsigned)nb);
+            const void *xr = (const char *)x + (size_t)(b0 * d->c) * xb;
+            void *outr = (char *)out + (size_t)(b0 * d->c) * xb;
+            const float *sr = state + b0 * d->w * d->c;
+            float *nr = next_state + b0 * d->w * d->c;
+#define CV1_UPD(DT)                                                                              \
+    conv1d_update_kernel<DT><<<blocks, kCv1Threads, 0, st>>>(nb, d->c, d->k, d->w, d->has_bias, \
+                                                             silu, xr, weight, bias, sr, outr,   \
+                                                             nr)
+            if (d->dtype == DM_F32) {
+                CV1_UPD(DM_F32);
+            } else if (d->dtype == DM_BF16) {
+                CV1_UPD(DM_BF16);
+            } else {
+                CV1_UPD(DM_F16);
+            }
 #undef CV1_UPD
+        }
     }
     probe_add(DM_PROBE_CONV1D_UPDATE);
     DM_LAUNCH_CHECK("causal_conv1d_update: launch");

@@ -224,3 +224,23 @@ def test_refusals():
         dm.causal_conv1d(x, w, None, None, torch.tensor([0, 5]))
     with pytest.raises(dm.Unsupported, match="kernel widths above 16"):
         dm.causal_conv1d(x, torch.zeros(8, 17, dtype=torch.bfloat16, device="cuda"))
+
+
+def test_update_batch_above_one_launch():
+    """A decoding step over 70,000 rows: more rows than one launch's grid holds (65,535), so the
+    rows go in two launches; checked against the f64 oracle (1e-2) and the exact next state."""
+    b, c, k, w = 70000, 8, 3, 2
+    print(f"conv1d update b={b} c={c} k={k} w={w}", flush=True)
+    gen = torch.Generator().manual_seed(71)
+    x = torch.randn(b, c, generator=gen).to(torch.bfloat16)
+    wt = (0.5 * torch.randn(c, k, generator=gen)).to(torch.bfloat16)
+    bs = torch.randn(c, generator=gen).to(torch.bfloat16)
+    state = torch.randn(b, w, c, generator=gen)
+    opts = dm.CausalConv1dStepOptions(activation=dm.Activation.SILU)
+    out, nxt = dm.causal_conv1d_update(x.cuda(), wt.cuda(), bs.cuda(), state.cuda(), opts)
+    torch.cuda.synchronize()
+    eo, en = oracle.conv1d_update(x.float().numpy(), wt.float().numpy(), bs.float().numpy(),
+                                  state.numpy(), True, precision="f64")
+    _, rel = errors(_n(out), eo)
+    assert rel <= 1e-2, rel
+    np.testing.assert_array_equal(_n(nxt), en)
