@@ -141,3 +141,25 @@ def test_wide_step_packed_equals_token_by_token(dk):
             o1, state = dm.gated_delta_step(*(a[t:t + 1] for a in args), state, None, opts)
             assert torch.equal(o1[0], out[t]), (s, t)
         assert torch.equal(state[0], st[s]), s
+
+
+@pytest.mark.parametrize("l2norm", [True, False])
+def test_one_token_form_equals_the_general_form(l2norm):
+    """One token per sequence at Dk = 128 runs the compile-time form of the step and its backward;
+    the same rows as packed sequences of one token each run the general form. The arithmetic is
+    the same, in the same order: the results agree to the bit."""
+    b, h = 12, 3
+    x = inputs(505, None, h, 128, 128, torch.bfloat16, nseq=b)
+    args = [x[n] for n in ("q", "k", "v", "g", "beta")]
+    opts = dm.GatedDeltaStepOptions(qk_l2norm=l2norm, scale=None if l2norm else 0.45)
+    cut = torch.arange(b + 1, dtype=torch.int32)
+    print(f"one-token form against the general form, l2norm={l2norm}", flush=True)
+    o1, s1 = dm.gated_delta_step(*args, x["state"], None, opts)
+    o2, s2 = dm.gated_delta_step(*args, x["state"], cut, opts)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    g1 = dm.gated_delta_step_backward(*args, x["state"], None, x["d_out"], x["d_state"], opts)
+    g2 = dm.gated_delta_step_backward(*args, x["state"], cut, x["d_out"], x["d_state"], opts)
+    torch.cuda.synchronize()
+    for name, a, e in zip(["dq", "dk", "dv", "dg", "dbeta", "d_state"], g1, g2):
+        assert torch.equal(a, e), name
